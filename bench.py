@@ -1,0 +1,278 @@
+"""Benchmark of the MI355X attention stage (one GPU).
+
+Headline workload ("decode attn GB/s at 2K ctx"):
+  Llama-3.2-1B-shape batched decode step, fp16 KV cache: B=8 sequences with
+  2048 cached positions each, one new token per sequence (L = 2049),
+  Hq=32 / Hkv=8, D=64, RoPE theta 5e5, K/V ~ N(0, 0.5) (sigma 0.5).
+  One step = hl_rope_store_decode (RoPE of the new q/k, K/V write at column
+  2048) + hl_attn_decode (split-K attention + merge).  16 cache sets are
+  rotated (16 x 33.6 MB > the 256 MB Infinity Cache) so every step streams
+  its K/V from HBM.
+  value = algorithmic K+V bytes of one step / step time (GB/s).
+
+Extra objects on the same JSON line:
+  prefill: configs[3], Llama-3-8B-shape causal prefill, bf16, T=4096,
+    Hq32/Hkv8, D128, RoPE 5e5, KV cache written; TFLOP/s on causal FLOPs
+    4*Hq*D*T(T+1)/2 (prologue + flash kernel).
+  decode_c5: configs[4], Qwen3-30B-A3B-shape decode, bf16 KV, B=16, L=32769,
+    Hq32/Hkv4, D128, qkNorm + RoPE 1e6.
+  roofline: the decode attention call (split-K kernel + merge) timed with HIP
+    events on the stream it runs on.
+  cpu_baseline: the C oracle (single-threaded scalar fp32 restatement of the
+    reference's tensor.nim math) timed on this host on a bounded sample.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16/fp16 MFMA
+METRIC = "decode attn GB/s (%HBM peak) at 2K ctx; prefill attn TFLOP/s (%MFMA peak)"
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def event_time_ms(torch, fn, iters):
+    """Average ms per call of fn() from HIP events on torch's current stream
+    (the stream every library call is given)."""
+    st = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    for i in range(iters):
+        fn(i)
+    e1.record(st)
+    e1.synchronize()
+    return e0.elapsed_time(e1) / iters
+
+
+# ---------------------------------------------------------------------------
+# Decode (c3 headline, c5 extra)
+# ---------------------------------------------------------------------------
+class DecodeWorkload:
+    def __init__(self, torch, A, B, hq, hkv, d, prev, kv_dtype, sigma, base, n_sets, qknorm, seed):
+        self.t, self.A = torch, A
+        self.B, self.hq, self.hkv, self.d, self.prev = B, hq, hkv, d, prev
+        self.L = prev + 1
+        self.max_len = self.L
+        g = torch.Generator(device="cuda").manual_seed(seed)
+        n = B * hkv * d * self.max_len
+        self.kc = [(torch.randn(n, generator=g, device="cuda") * sigma).to(kv_dtype)
+                   for _ in range(n_sets)]
+        self.vc = [(torch.randn(n, generator=g, device="cuda") * sigma).to(kv_dtype)
+                   for _ in range(n_sets)]
+        self.q = torch.randn(B * hq * d, generator=g, device="cuda") * sigma
+        self.k = torch.randn(B * hkv * d, generator=g, device="cuda") * sigma
+        self.v = torch.randn(B * hkv * d, generator=g, device="cuda") * sigma
+        self.wq = self.wk = None
+        if qknorm:
+            self.wq = torch.rand(d, generator=g, device="cuda") + 0.5
+            self.wk = torch.rand(d, generator=g, device="cuda") + 0.5
+        self.base = base
+        self.out = torch.empty(B * hq * d, device="cuda")
+        self.args = [A.decode_args(self.q, kc, vc, self.out, hq, hkv, d, self.max_len, self.L)
+                     for kc, vc in zip(self.kc, self.vc)]
+        self.ws = A.workspace(A.decode_workspace_bytes(self.args[0]))
+        self.kv_bytes = 2 * B * hkv * d * self.L * self.kc[0].element_size()
+        self.flops = 4 * B * hq * d * self.L
+
+    def rope_store(self, i):
+        s = i % len(self.kc)
+        self.A.rope_store_decode(self.q, self.k, self.v, self.kc[s], self.vc[s], self.hq, self.hkv,
+                                 self.d, self.max_len, self.prev, self.base, q_norm_w=self.wq,
+                                 k_norm_w=self.wk, eps=1e-6)
+
+    def attend(self, i):
+        self.A.attn_decode(self.args[i % len(self.args)], self.ws)
+
+    def step(self, i):
+        self.rope_store(i)
+        self.attend(i)
+
+
+def bench_decode(torch, A, wl, steps, warmup):
+    for i in range(warmup):
+        wl.step(i)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        wl.step(i)
+    torch.cuda.synchronize()
+    step_ms = (time.perf_counter() - t0) * 1e3 / steps
+    attn_ms = event_time_ms(torch, wl.attend, max(steps, 50))
+    rs_ms = event_time_ms(torch, wl.rope_store, max(steps, 50))
+    return step_ms, attn_ms, rs_ms
+
+
+# ---------------------------------------------------------------------------
+# Prefill (c4)
+# ---------------------------------------------------------------------------
+class PrefillWorkload:
+    def __init__(self, torch, A, T=4096, hq=32, hkv=8, d=128, base=5e5, seed=7):
+        g = torch.Generator(device="cuda").manual_seed(seed)
+        bf = torch.bfloat16
+        self.q = torch.randn(hq * d, T, generator=g, device="cuda").to(bf)
+        self.k = torch.randn(hkv * d, T, generator=g, device="cuda").to(bf)
+        self.v = torch.randn(hkv * d, T, generator=g, device="cuda").to(bf)
+        self.kc = torch.empty(hkv * d, T, dtype=bf, device="cuda")
+        self.vc = torch.empty(hkv * d, T, dtype=bf, device="cuda")
+        self.out = torch.empty(hq * d, T, dtype=torch.float32, device="cuda")  # fp32 like act1
+        self.a = A.prefill_args(self.q, self.k, self.v, self.out, hq, hkv, d, T, apply_rope=True,
+                                rope_base=base, k_cache=self.kc, v_cache=self.vc, max_len=T)
+        self.ws = A.workspace(A.prefill_workspace_bytes(self.a))
+        self.A = A
+        self.flops = 4 * hq * d * T * (T + 1) // 2
+
+    def step(self, i):
+        self.A.attn_prefill(self.a, self.ws)
+
+
+# ---------------------------------------------------------------------------
+# CPU baseline: the C oracle on this host, one thread
+# ---------------------------------------------------------------------------
+def cpu_baseline(budget_s=12.0):
+    import oracle
+    oracle.lib()
+    B, hq, hkv, d, L = 8, 32, 8, 64, 2049
+    per = hkv * d * L
+    kb = oracle.to_storage(oracle.normal(B * per, 1, 0, 0.5), oracle.F16)
+    vb = oracle.to_storage(oracle.normal(B * per, 2, 0, 0.5), oracle.F16)
+    q = oracle.normal(B * hq * d, 3, 0, 0.5)
+    kf = oracle.upcast(kb, oracle.F16)
+    vf = oracle.upcast(vb, oracle.F16)
+    steps, t_total = 0, 0.0
+    while t_total < budget_s:
+        t0 = time.perf_counter()
+        for b in range(B):
+            oracle.attention_decode(q[b * hq * d:(b + 1) * hq * d], kf[b * per:(b + 1) * per],
+                                    vf[b * per:(b + 1) * per], hq, hkv, d, L, L)
+        t_total += time.perf_counter() - t0
+        steps += 1
+    kv_bytes = 2 * B * per * 2
+    return {
+        "value": round(kv_bytes * steps / t_total / 1e9, 4),
+        "unit": "GB/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": f"{steps} full c3 decode steps (8 seqs x 32 heads x 2049 cols, fp16 bits "
+                  f"upcast to fp32) through the scalar C oracle, {t_total:.1f} s on 1 thread",
+        "ms_per_step": round(t_total * 1e3 / steps, 3),
+        "host_nproc": os.cpu_count(),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--only", choices=["all", "decode", "prefill", "c5"], default="all")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
+                                   "(sharding is described in DESIGN.md, not built)"}))
+        sys.exit(2)
+
+    import torch
+    from hippo_leap_amd import attention as A
+    torch.cuda.init()
+    info = A.device_info()
+    log(f"device: {info['arch']} CUs={info['cu_count']} clk={info['clock_khz']} kHz")
+
+    result = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+              "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+              "data": "synthetic (seeded torch.randn on the GPU, random values of the "
+                      "configs' shapes/distributions)"}
+
+    if args.only in ("all", "decode"):
+        log("decode c3 ...")
+        wl = DecodeWorkload(torch, A, B=8, hq=32, hkv=8, d=64, prev=2048,
+                            kv_dtype=torch.float16, sigma=0.5, base=5e5, n_sets=16,
+                            qknorm=False, seed=3)
+        step_ms, attn_ms, rs_ms = bench_decode(torch, A, wl, args.steps, args.warmup)
+        value = wl.kv_bytes / (step_ms * 1e-3) / 1e9
+        achieved = wl.kv_bytes / (attn_ms * 1e-3) / 1e9
+        result.update({
+            "value": round(value, 2), "unit": "GB/s", "ms_per_step": round(step_ms, 5),
+            "dtype": "f16",
+            "config": {"workload": "c3: Llama-3.2-1B-shape batched decode, fp16 KV", "batch": 8,
+                       "cached_positions": 2048, "attn_len": 2049, "n_head": 32, "n_head_kv": 8,
+                       "head_dim": 64, "rope_theta": 5e5, "kv_sigma": 0.5,
+                       "rotating_cache_sets": 16, "step": "rope_store_decode + attn_decode"},
+            "roofline": {"bound": "hbm", "kernel": "decode_mfma_kernel + decode_merge_kernel",
+                         "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(achieved / HBM_PEAK_GBS, 4),
+                         "traffic": None, "algorithmic_bytes": wl.kv_bytes,
+                         "avg_us": round(attn_ms * 1e3, 3)},
+            "rope_store_us": round(rs_ms * 1e3, 3),
+        })
+        log(f"decode c3: step {step_ms*1e3:.2f} us, attention {attn_ms*1e3:.2f} us "
+            f"({achieved:.0f} GB/s), rope+store {rs_ms*1e3:.2f} us")
+        del wl
+        torch.cuda.empty_cache()
+
+    if args.only in ("all", "prefill"):
+        log("prefill c4 ...")
+        pw = PrefillWorkload(torch, A)
+        for i in range(max(2, args.warmup // 2)):
+            pw.step(i)
+        torch.cuda.synchronize()
+        iters = max(10, args.steps // 5)
+        ms = event_time_ms(torch, pw.step, iters)
+        tf = pw.flops / (ms * 1e-3) / 1e12
+        result["prefill"] = {
+            "workload": "c4: Llama-3-8B-shape causal prefill bf16, T=4096, Hq32/Hkv8, D128, "
+                        "RoPE 5e5, KV cache written",
+            "dtype": "bf16 in, fp16 MFMA operands, fp32 accumulation and output",
+            "value": round(tf, 2), "unit": "TFLOP/s", "ms_per_step": round(ms, 4),
+            "roofline": {"bound": "mfma", "kernel": "prologue_kernel + prefill_mfma_kernel",
+                         "achieved": round(tf, 2), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(tf / BF16_PEAK_TFLOPS, 4), "traffic": None,
+                         "algorithmic_flops": pw.flops},
+        }
+        log(f"prefill c4: {ms:.3f} ms, {tf:.1f} TFLOP/s")
+        del pw
+        torch.cuda.empty_cache()
+
+    if args.only in ("all", "c5"):
+        log("decode c5 ...")
+        wl = DecodeWorkload(torch, A, B=16, hq=32, hkv=4, d=128, prev=32768,
+                            kv_dtype=torch.bfloat16, sigma=1.0, base=1e6, n_sets=1,
+                            qknorm=True, seed=5)
+        step_ms, attn_ms, rs_ms = bench_decode(torch, A, wl, max(10, args.steps // 4), 3)
+        ach = wl.kv_bytes / (attn_ms * 1e-3) / 1e9
+        result["decode_c5"] = {
+            "workload": "c5: Qwen3-30B-A3B-shape decode, bf16 KV, B=16, L=32769, Hq32/Hkv4, "
+                        "D128, qkNorm + RoPE 1e6",
+            "value": round(wl.kv_bytes / (step_ms * 1e-3) / 1e9, 2), "unit": "GB/s",
+            "ms_per_step": round(step_ms, 5),
+            "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),
+                         "algorithmic_bytes": wl.kv_bytes, "avg_us": round(attn_ms * 1e3, 3)},
+        }
+        log(f"decode c5: step {step_ms*1e3:.1f} us, attention {attn_ms*1e3:.1f} us ({ach:.0f} GB/s)")
+        del wl
+        torch.cuda.empty_cache()
+
+    if not args.no_cpu:
+        log("cpu baseline ...")
+        result["cpu_baseline"] = cpu_baseline()
+        if "value" in result:
+            result["cpu_baseline"]["gpu_over_cpu"] = round(result["value"] /
+                                                           result["cpu_baseline"]["value"], 1)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

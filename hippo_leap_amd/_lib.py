@@ -1,0 +1,131 @@
+"""ctypes binding of libhl_attn.so (declarations mirror include/hl_attn.h).
+
+The library is loaded from this package directory only; a missing library is
+an error (there is no CPU fallback for any entry point).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(PKG_DIR, "libhl_attn.so")
+
+HL_OK, HL_EINVAL, HL_ECAPACITY, HL_EUNSUPPORTED, HL_EHIP = 0, -1, -2, -3, -4
+HL_F32, HL_F16, HL_BF16 = 0, 1, 2
+HL_ROPE_HALF_SPLIT, HL_ROPE_INTERLEAVED = 0, 1
+
+c_int, c_float, c_void_p, c_size_t, c_longlong = (
+    ctypes.c_int, ctypes.c_float, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_longlong)
+
+
+class HLError(ValueError):
+    """Raised for a negative status; the reference raises ValueError for the
+    same preconditions (backends/naive.nim:3969-3976, 4594-4599)."""
+
+    def __init__(self, code: int, msg: str):
+        super().__init__(msg)
+        self.code = code
+
+
+class DeviceInfo(ctypes.Structure):
+    _fields_ = [
+        ("device", c_int), ("cu_count", c_int), ("clock_khz", c_int),
+        ("mem_clock_khz", c_int), ("l2_bytes", c_int), ("hbm_bytes", c_size_t),
+        ("hbm_peak_gbs", ctypes.c_double), ("bf16_dense_tflops", ctypes.c_double),
+        ("fp32_tflops", ctypes.c_double), ("arch", ctypes.c_char * 64),
+    ]
+
+
+class DecodeArgs(ctypes.Structure):
+    _fields_ = [
+        ("batch", c_int), ("n_head", c_int), ("n_head_kv", c_int), ("head_dim", c_int),
+        ("kv_dtype", c_int), ("max_len", c_int), ("seq_len", c_int),
+        ("seq_lens", c_void_p), ("cache_batch_stride", c_longlong),
+        ("q", c_void_p), ("k_cache", c_void_p), ("v_cache", c_void_p), ("out", c_void_p),
+        ("scale", c_float), ("num_splits", c_int),
+    ]
+
+
+class RopeStoreArgs(ctypes.Structure):
+    _fields_ = [
+        ("batch", c_int), ("n_head_q", c_int), ("n_head_kv", c_int), ("head_dim", c_int),
+        ("rope_dim", c_int), ("rope_style", c_int), ("rope_base", c_float),
+        ("use_installed_theta", c_int), ("kv_dtype", c_int), ("max_len", c_int),
+        ("cache_batch_stride", c_longlong),
+        ("q", c_void_p), ("k", c_void_p), ("v", c_void_p),
+        ("k_cache", c_void_p), ("v_cache", c_void_p),
+        ("positions", c_void_p), ("pos", c_int),
+        ("q_norm_w", c_void_p), ("k_norm_w", c_void_p), ("eps", c_float),
+    ]
+
+
+class PrefillArgs(ctypes.Structure):
+    _fields_ = [
+        ("n_head", c_int), ("n_head_kv", c_int), ("head_dim", c_int), ("seq_len", c_int),
+        ("io_dtype", c_int),
+        ("q", c_void_p), ("k", c_void_p), ("v", c_void_p), ("out", c_void_p),
+        ("q_norm_w", c_void_p), ("k_norm_w", c_void_p), ("eps", c_float),
+        ("apply_rope", c_int), ("rope_dim", c_int), ("rope_style", c_int),
+        ("rope_base", c_float), ("use_installed_theta", c_int),
+        ("k_cache", c_void_p), ("v_cache", c_void_p), ("kv_dtype", c_int),
+        ("max_len", c_int), ("start_pos", c_int), ("scale", c_float),
+        ("write_back_qk", c_int), ("out_dtype", c_int),
+    ]
+
+
+# name -> (restype, argtypes); every symbol include/hl_attn.h declares.
+SIGNATURES = {
+    "hl_last_error": (ctypes.c_char_p, []),
+    "hl_abi_version": (c_int, []),
+    "hl_device_info_get": (c_int, [ctypes.POINTER(DeviceInfo)]),
+    "hl_rope_theta_table": (c_int, [ctypes.POINTER(c_float), c_int, c_float]),
+    "hl_set_rope_theta": (c_int, [c_int, c_float]),
+    "hl_gpu_qk_norm": (c_int, [c_void_p, c_void_p, c_int, c_int, c_float, c_void_p]),
+    "hl_gpu_qk_norm_prefill": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_float, c_void_p]),
+    "hl_gpu_rope_at_pos": (c_int, [c_void_p, c_int, c_int, c_int, c_float, c_int, c_int, c_void_p]),
+    "hl_gpu_rope_at_pos_theta": (c_int, [c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p]),
+    "hl_gpu_rope_qk_decode": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_float, c_int,
+                                      c_void_p]),
+    "hl_gpu_fused_rope_store_kv": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int,
+                                           c_int, c_int, c_int, c_int, c_int, c_int, c_void_p]),
+    "hl_gpu_store_kv": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_void_p]),
+    "hl_gpu_store_kv_pair": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int,
+                                     c_int, c_void_p]),
+    "hl_gpu_attention_decode": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int,
+                                        c_int, c_int, c_void_p]),
+    "hl_gpu_attention_prefill": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int,
+                                         c_int, c_void_p]),
+    "hl_attn_decode_workspace_bytes": (c_size_t, [ctypes.POINTER(DecodeArgs)]),
+    "hl_attn_decode": (c_int, [ctypes.POINTER(DecodeArgs), c_void_p, c_size_t, c_void_p]),
+    "hl_rope_store_decode": (c_int, [ctypes.POINTER(RopeStoreArgs), c_void_p]),
+    "hl_attn_prefill_workspace_bytes": (c_size_t, [ctypes.POINTER(PrefillArgs)]),
+    "hl_attn_prefill": (c_int, [ctypes.POINTER(PrefillArgs), c_void_p, c_size_t, c_void_p]),
+    "hl_kv_cache_to_f32": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p]),
+}
+
+_lib = None
+
+
+def load() -> ctypes.CDLL:
+    """Loads libhl_attn.so from the package directory (raises if it is absent)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(
+            f"{LIB_PATH} is missing: build it with `python -m hippo_leap_amd.build` "
+            "(the attention stage has no CPU fallback)")
+    lib = ctypes.CDLL(LIB_PATH)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def check(rc: int) -> None:
+    if rc != HL_OK:
+        msg = load().hl_last_error().decode(errors="replace")
+        raise HLError(rc, msg)

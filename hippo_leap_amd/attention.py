@@ -1,0 +1,222 @@
+"""Host-side mirror of the reference's attention-stage procs over torch tensors.
+
+Each function keeps the name (snake_case), argument order and meaning of the
+Nim proc it replaces in backends/naive.nim and calls the matching C-ABI entry
+point of libhl_attn.so on torch's current HIP stream.  Torch supplies device
+memory and the stream only; all arithmetic runs in the HIP kernels.
+
+Reference procs mirrored:
+  gpu_qk_norm              gpuQkNorm              naive.nim:2918-2926
+  gpu_qk_norm_prefill      gpuQkNormPrefill       naive.nim:2962-2971
+  gpu_rope_at_pos          gpuRopeAtPos           naive.nim:3088-3101
+  gpu_rope_at_pos_theta    gpuRopeAtPosTheta      naive.nim:3133-3144
+  gpu_rope_qk_decode       gpuRopeQKDecode        naive.nim:3075-3086
+  gpu_fused_rope_store_kv  gpuFusedRopeStoreKV    naive.nim:3203-3223
+  gpu_store_kv             gpuStoreKV             naive.nim:3241-3253
+  gpu_store_kv_pair        gpuStoreKVPair         naive.nim:3273-3285
+  gpu_attention_decode     gpuAttentionDecode     naive.nim:3369-3383
+  gpu_attention_prefill    gpuAttentionPrefill    naive.nim:3450-3464
+Errors raise HLError (a ValueError), as the reference raises ValueError.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+from ._lib import (HL_BF16, HL_F16, HL_F32, HL_ROPE_HALF_SPLIT, DecodeArgs, PrefillArgs,
+                   RopeStoreArgs, check)
+
+_DT = {torch.float32: HL_F32, torch.float16: HL_F16, torch.bfloat16: HL_BF16}
+
+
+def dtype_code(t: torch.Tensor) -> int:
+    try:
+        return _DT[t.dtype]
+    except KeyError:
+        raise _lib.HLError(_lib.HL_EINVAL, f"unsupported dtype {t.dtype}") from None
+
+
+def _p(t):
+    """Device pointer of a tensor (or None)."""
+    if t is None:
+        return None
+    if not t.is_cuda:
+        raise _lib.HLError(_lib.HL_EINVAL, "tensor must live on the GPU")
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(stream=None):
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return ctypes.c_void_p(s.cuda_stream)
+
+
+# ---------------------------------------------------------------------------
+# Reference-signature wrappers (fp32, one sequence)
+# ---------------------------------------------------------------------------
+def gpu_qk_norm(x, weight, n_head, head_dim, eps, stream=None):
+    check(_lib.load().hl_gpu_qk_norm(_p(x), _p(weight), n_head, head_dim, eps, _stream(stream)))
+
+
+def gpu_qk_norm_prefill(x, weight, n_head, head_dim, seq_len, eps, stream=None):
+    check(_lib.load().hl_gpu_qk_norm_prefill(_p(x), _p(weight), n_head, head_dim, seq_len, eps,
+                                             _stream(stream)))
+
+
+def gpu_rope_at_pos(x, n_head, head_dim, rope_dim, rope_base, pos, seq_len, stream=None):
+    check(_lib.load().hl_gpu_rope_at_pos(_p(x), n_head, head_dim, rope_dim, rope_base, pos,
+                                         seq_len, _stream(stream)))
+
+
+def gpu_rope_at_pos_theta(x, n_head, head_dim, rope_dim, pos, seq_len, stream=None):
+    check(_lib.load().hl_gpu_rope_at_pos_theta(_p(x), n_head, head_dim, rope_dim, pos, seq_len,
+                                               _stream(stream)))
+
+
+def gpu_rope_qk_decode(q, k, n_head_q, n_head_k, head_dim, rope_dim, rope_base, pos, stream=None):
+    check(_lib.load().hl_gpu_rope_qk_decode(_p(q), _p(k), n_head_q, n_head_k, head_dim, rope_dim,
+                                            rope_base, pos, _stream(stream)))
+
+
+def gpu_fused_rope_store_kv(q, k, v, k_cache, v_cache, n_head_q, n_head_k, head_dim, rope_dim,
+                            kv_dim, cache_cols, pos, stream=None):
+    check(_lib.load().hl_gpu_fused_rope_store_kv(
+        _p(q), _p(k), _p(v), _p(k_cache), _p(v_cache), n_head_q, n_head_k, head_dim, rope_dim,
+        kv_dim, cache_cols, pos, _stream(stream)))
+
+
+def gpu_store_kv(cache, src, rows, src_cols, cache_cols, start_pos, stream=None):
+    check(_lib.load().hl_gpu_store_kv(_p(cache), _p(src), rows, src_cols, cache_cols, start_pos,
+                                      _stream(stream)))
+
+
+def gpu_store_kv_pair(k_cache, k_src, v_cache, v_src, rows, src_cols, cache_cols, start_pos,
+                      stream=None):
+    check(_lib.load().hl_gpu_store_kv_pair(_p(k_cache), _p(k_src), _p(v_cache), _p(v_src), rows,
+                                           src_cols, cache_cols, start_pos, _stream(stream)))
+
+
+def gpu_attention_decode(dst, q, k_cache, v_cache, n_head, n_head_kv, head_dim, cur_len,
+                         cache_cols, stream=None):
+    check(_lib.load().hl_gpu_attention_decode(_p(dst), _p(q), _p(k_cache), _p(v_cache), n_head,
+                                              n_head_kv, head_dim, cur_len, cache_cols,
+                                              _stream(stream)))
+
+
+def gpu_attention_prefill(dst, q, k, v, n_head, n_head_kv, head_dim, seq_len, stream=None):
+    check(_lib.load().hl_gpu_attention_prefill(_p(dst), _p(q), _p(k), _p(v), n_head, n_head_kv,
+                                               head_dim, seq_len, _stream(stream)))
+
+
+def set_rope_theta(rope_dim: int, rope_base: float) -> None:
+    """Installs the theta table (naive.nim:3850-3861) used by the *_theta procs."""
+    check(_lib.load().hl_set_rope_theta(rope_dim, rope_base))
+
+
+def rope_theta_table(rope_dim: int, rope_base: float) -> list[float]:
+    buf = (ctypes.c_float * (rope_dim // 2))()
+    check(_lib.load().hl_rope_theta_table(buf, rope_dim, rope_base))
+    return list(buf)
+
+
+def kv_cache_to_f32(cache, rows, max_len, col0, ncols, stream=None) -> torch.Tensor:
+    out = torch.empty(rows, ncols, dtype=torch.float32, device=cache.device)
+    check(_lib.load().hl_kv_cache_to_f32(_p(out), _p(cache), dtype_code(cache), rows, max_len, col0,
+                                         ncols, _stream(stream)))
+    return out
+
+
+def device_info() -> dict:
+    info = _lib.DeviceInfo()
+    check(_lib.load().hl_device_info_get(ctypes.byref(info)))
+    return {name: (getattr(info, name).decode() if name == "arch" else getattr(info, name))
+            for name, _ in _lib.DeviceInfo._fields_}
+
+
+# ---------------------------------------------------------------------------
+# Batched / typed API
+# ---------------------------------------------------------------------------
+def decode_args(q, k_cache, v_cache, out, n_head, n_head_kv, head_dim, max_len, seq_len,
+                seq_lens=None, cache_batch_stride=0, scale=0.0, num_splits=0) -> DecodeArgs:
+    a = DecodeArgs()
+    a.batch = q.numel() // (n_head * head_dim)
+    a.n_head, a.n_head_kv, a.head_dim = n_head, n_head_kv, head_dim
+    a.kv_dtype = dtype_code(k_cache)
+    a.max_len, a.seq_len = max_len, seq_len
+    a.seq_lens = seq_lens.data_ptr() if seq_lens is not None else None
+    a.cache_batch_stride = cache_batch_stride
+    a.q, a.k_cache, a.v_cache, a.out = q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), out.data_ptr()
+    a.scale, a.num_splits = scale, num_splits
+    return a
+
+
+def decode_workspace_bytes(args: DecodeArgs) -> int:
+    return int(_lib.load().hl_attn_decode_workspace_bytes(ctypes.byref(args)))
+
+
+def attn_decode(args: DecodeArgs, workspace=None, stream=None) -> None:
+    """Batched split-K decode (hl_attn_decode); workspace is a uint8 device tensor."""
+    ws = workspace.data_ptr() if workspace is not None else None
+    nbytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    check(_lib.load().hl_attn_decode(ctypes.byref(args), ws, nbytes, _stream(stream)))
+
+
+def rope_store_decode(q, k, v, k_cache, v_cache, n_head_q, n_head_kv, head_dim, max_len, pos,
+                      rope_base, rope_dim=0, rope_style=HL_ROPE_HALF_SPLIT, positions=None,
+                      q_norm_w=None, k_norm_w=None, eps=1e-6, cache_batch_stride=0,
+                      use_installed_theta=False, stream=None) -> None:
+    a = RopeStoreArgs()
+    a.batch = q.numel() // (n_head_q * head_dim)
+    a.n_head_q, a.n_head_kv, a.head_dim = n_head_q, n_head_kv, head_dim
+    a.rope_dim, a.rope_style, a.rope_base = rope_dim, rope_style, rope_base
+    a.use_installed_theta = int(use_installed_theta)
+    a.kv_dtype, a.max_len, a.cache_batch_stride = dtype_code(k_cache), max_len, cache_batch_stride
+    a.q, a.k, a.v = q.data_ptr(), k.data_ptr(), v.data_ptr()
+    a.k_cache, a.v_cache = k_cache.data_ptr(), v_cache.data_ptr()
+    a.positions = positions.data_ptr() if positions is not None else None
+    a.pos = pos
+    a.q_norm_w = q_norm_w.data_ptr() if q_norm_w is not None else None
+    a.k_norm_w = k_norm_w.data_ptr() if k_norm_w is not None else None
+    a.eps = eps
+    check(_lib.load().hl_rope_store_decode(ctypes.byref(a), _stream(stream)))
+
+
+def prefill_args(q, k, v, out, n_head, n_head_kv, head_dim, seq_len, rope_base=0.0,
+                 apply_rope=False, rope_dim=0, rope_style=HL_ROPE_HALF_SPLIT, q_norm_w=None,
+                 k_norm_w=None, eps=1e-6, k_cache=None, v_cache=None, max_len=0, start_pos=0,
+                 scale=0.0, write_back_qk=False, use_installed_theta=False) -> PrefillArgs:
+    """Arguments of hl_attn_prefill; the output dtype is taken from `out`."""
+    a = PrefillArgs()
+    a.n_head, a.n_head_kv, a.head_dim, a.seq_len = n_head, n_head_kv, head_dim, seq_len
+    a.io_dtype = dtype_code(q)
+    a.q, a.k, a.v, a.out = q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr()
+    a.q_norm_w = q_norm_w.data_ptr() if q_norm_w is not None else None
+    a.k_norm_w = k_norm_w.data_ptr() if k_norm_w is not None else None
+    a.eps = eps
+    a.apply_rope, a.rope_dim, a.rope_style, a.rope_base = int(apply_rope), rope_dim, rope_style, rope_base
+    a.use_installed_theta = int(use_installed_theta)
+    a.k_cache = k_cache.data_ptr() if k_cache is not None else None
+    a.v_cache = v_cache.data_ptr() if v_cache is not None else None
+    a.kv_dtype = dtype_code(k_cache) if k_cache is not None else HL_F32
+    a.max_len, a.start_pos, a.scale = max_len, start_pos, scale
+    a.write_back_qk = int(write_back_qk)
+    a.out_dtype = dtype_code(out)
+    return a
+
+
+def prefill_workspace_bytes(args: PrefillArgs) -> int:
+    return int(_lib.load().hl_attn_prefill_workspace_bytes(ctypes.byref(args)))
+
+
+def attn_prefill(args: PrefillArgs, workspace=None, stream=None) -> None:
+    ws = workspace.data_ptr() if workspace is not None else None
+    nbytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    check(_lib.load().hl_attn_prefill(ctypes.byref(args), ws, nbytes, _stream(stream)))
+
+
+def workspace(nbytes: int, device="cuda") -> torch.Tensor | None:
+    """Allocates a caller-owned workspace (GpuContext.attnScratch's role)."""
+    if nbytes <= 0:
+        return None
+    return torch.empty(nbytes, dtype=torch.uint8, device=device)

@@ -1,0 +1,648 @@
+// C ABI of libhl_attn.so: argument checks, workspace planning and dispatch.
+//
+// Error behaviour mirrors the reference's host prechecks, which raise
+// ValueError with these messages (backends/naive.nim):
+//   "GQA requires head_count divisible by head_count_kv"   :3971-3972, 4596-4597
+//   "prefill requires at least one token"                   :3973-3974
+//   "prefill exceeds KV cache capacity"                     :3975-3976
+//   "KV cache full"                                         :4598-4599
+// Each becomes a negative status plus the same text from hl_last_error().
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <mutex>
+#include <vector>
+
+#include "common.h"
+#include "launch.h"
+
+using namespace hl;
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  return fail(HL_EHIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+inline hipStream_t as_stream(void* s) { return (hipStream_t)s; }
+
+std::mutex g_mu;
+bool g_theta_set = false;
+int g_theta_dim = 0;
+ThetaTable g_theta;
+
+// Library-owned split-K workspace for the reference-signature decode entry
+// point (the reference keeps such scratch in its module-global GpuContext).
+struct DevWs {
+  void* ptr = nullptr;
+  size_t bytes = 0;
+};
+std::vector<DevWs> g_ws;
+
+void build_theta(ThetaTable& t, int rope_dim, float base) {
+  memset(&t, 0, sizeof(t));
+  for (int i = 0; i < rope_dim / 2; ++i)
+    t.t[i] = powf(1.0f / base, (2.0f * (float)i) / (float)rope_dim);
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+int check_gqa(int n_head, int n_head_kv) {
+  if (n_head <= 0 || n_head_kv <= 0)
+    return fail(HL_EINVAL, "head counts must be positive (n_head=%d, n_head_kv=%d)", n_head, n_head_kv);
+  if (n_head % n_head_kv != 0)
+    return fail(HL_EINVAL, "GQA requires head_count divisible by head_count_kv");
+  return HL_OK;
+}
+
+int check_dtype(int dt, const char* what) {
+  if (dt != HL_F32 && dt != HL_F16 && dt != HL_BF16)
+    return fail(HL_EINVAL, "%s: unknown dtype %d", what, dt);
+  return HL_OK;
+}
+
+int check_rope(int head_dim, int rope_dim, int style) {
+  if (rope_dim <= 0 || rope_dim > head_dim || (rope_dim & 1) || rope_dim > HL_MAX_ROPE_DIM)
+    return fail(HL_EINVAL, "rope_dim %d must be even and in [2, head_dim=%d]", rope_dim, head_dim);
+  if (style != HL_ROPE_HALF_SPLIT && style != HL_ROPE_INTERLEAVED)
+    return fail(HL_EINVAL, "unknown rope_style %d", style);
+  return HL_OK;
+}
+
+// Theta for an op: installed table (must match rope_dim) or built from base.
+int theta_for(int use_installed, int rope_dim, float base, ThetaTable& out) {
+  if (use_installed) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (!g_theta_set) return fail(HL_EINVAL, "no RoPE theta table installed (hl_set_rope_theta)");
+    if (g_theta_dim != rope_dim)
+      return fail(HL_EINVAL, "installed theta table has rope_dim %d, call uses %d", g_theta_dim, rope_dim);
+    out = g_theta;
+    return HL_OK;
+  }
+  if (!(base > 0.f)) return fail(HL_EINVAL, "rope_base must be > 0");
+  build_theta(out, rope_dim, base);
+  return HL_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* hl_last_error(void) { return g_err; }
+
+int hl_abi_version(void) { return 1; }
+
+int hl_device_info_get(hl_device_info* info) {
+  if (!info) return fail(HL_EINVAL, "info is null");
+  memset(info, 0, sizeof(*info));
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  hipDeviceProp_t pr;
+  e = hipGetDeviceProperties(&pr, dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDeviceProperties");
+  info->device = dev;
+  info->cu_count = pr.multiProcessorCount;
+  info->clock_khz = pr.clockRate;
+  info->mem_clock_khz = pr.memoryClockRate;
+  info->l2_bytes = pr.l2CacheSize;
+  info->hbm_bytes = pr.totalGlobalMem;
+  info->hbm_peak_gbs = 8000.0;
+  info->bf16_dense_tflops = (double)pr.multiProcessorCount * (pr.clockRate * 1e3) * 4096.0 / 1e12;
+  info->fp32_tflops = 157.3;
+  strncpy(info->arch, pr.gcnArchName, sizeof(info->arch) - 1);
+  return HL_OK;
+}
+
+int hl_rope_theta_table(float* theta_out, int rope_dim, float rope_base) {
+  if (!theta_out) return fail(HL_EINVAL, "theta_out is null");
+  if (rope_dim <= 0 || (rope_dim & 1) || rope_dim > HL_MAX_ROPE_DIM)
+    return fail(HL_EINVAL, "rope_dim %d must be even and <= %d", rope_dim, HL_MAX_ROPE_DIM);
+  if (!(rope_base > 0.f)) return fail(HL_EINVAL, "rope_base must be > 0");
+  ThetaTable t;
+  build_theta(t, rope_dim, rope_base);
+  memcpy(theta_out, t.t, sizeof(float) * (rope_dim / 2));
+  return HL_OK;
+}
+
+int hl_set_rope_theta(int rope_dim, float rope_base) {
+  if (rope_dim <= 0 || (rope_dim & 1) || rope_dim > HL_MAX_ROPE_DIM)
+    return fail(HL_EINVAL, "rope_dim %d must be even and <= %d", rope_dim, HL_MAX_ROPE_DIM);
+  if (!(rope_base > 0.f)) return fail(HL_EINVAL, "rope_base must be > 0");
+  std::lock_guard<std::mutex> lk(g_mu);
+  build_theta(g_theta, rope_dim, rope_base);
+  g_theta_dim = rope_dim;
+  g_theta_set = true;
+  return HL_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Reference-signature drop-ins
+// ---------------------------------------------------------------------------
+int hl_gpu_qk_norm(float* x, const float* weight, int n_head, int head_dim, float eps,
+                   void* stream) {
+  if (!x || !weight) return fail(HL_EINVAL, "qk_norm: null pointer");
+  if (n_head <= 0 || head_dim <= 0 || head_dim > HL_MAX_HEAD_DIM)
+    return fail(HL_EINVAL, "qk_norm: bad shape n_head=%d head_dim=%d", n_head, head_dim);
+  HeadVecOp op;
+  memset(&op, 0, sizeof(op));
+  op.q = x;
+  op.q_norm_w = weight;
+  op.eps = eps;
+  op.batch = 1;
+  op.n_head_q = n_head;
+  op.head_dim = head_dim;
+  op.rope_dim = 0;
+  hipError_t e = headvec_launch(op, as_stream(stream));
+  return e == hipSuccess ? HL_OK : hip_fail(e, "qk_norm launch");
+}
+
+int hl_gpu_qk_norm_prefill(float* x, const float* weight, int n_head, int head_dim, int seq_len,
+                           float eps, void* stream) {
+  if (!x || !weight) return fail(HL_EINVAL, "qk_norm_prefill: null pointer");
+  if (n_head <= 0 || head_dim <= 0 || head_dim > HL_MAX_HEAD_DIM || seq_len <= 0)
+    return fail(HL_EINVAL, "qk_norm_prefill: bad shape");
+  PrologueOp op;
+  memset(&op, 0, sizeof(op));
+  op.q = x;
+  op.q_inplace = x;
+  op.io_dtype = HL_F32;
+  op.q_norm_w = weight;
+  op.eps = eps;
+  op.n_head = n_head;
+  op.n_head_kv = 0;
+  op.head_dim = head_dim;
+  op.seq_len = seq_len;
+  op.t_pad = seq_len;
+  op.kv_dtype = HL_F32;
+  hipError_t e = prologue_launch(op, as_stream(stream));
+  return e == hipSuccess ? HL_OK : hip_fail(e, "qk_norm_prefill launch");
+}
+
+static int rope_cols_common(float* x, int n_head, int head_dim, int rope_dim, int pos0,
+                            int seq_len, const ThetaTable& th, void* stream) {
+  PrologueOp op;
+  memset(&op, 0, sizeof(op));
+  op.q = x;
+  op.q_inplace = x;
+  op.io_dtype = HL_F32;
+  op.n_head = n_head;
+  op.head_dim = head_dim;
+  op.seq_len = seq_len;
+  op.t_pad = seq_len;
+  op.do_rope = 1;
+  op.rope_dim = rope_dim;
+  op.rope_style = HL_ROPE_HALF_SPLIT;
+  op.start_pos = pos0;
+  op.kv_dtype = HL_F32;
+  op.theta = th;
+  hipError_t e = prologue_launch(op, as_stream(stream));
+  return e == hipSuccess ? HL_OK : hip_fail(e, "rope launch");
+}
+
+static int rope_vec_common(float* q, float* k, int n_head_q, int n_head_k, int head_dim,
+                           int rope_dim, int pos, const ThetaTable& th, void* stream) {
+  HeadVecOp op;
+  memset(&op, 0, sizeof(op));
+  op.q = q;
+  op.k = k;
+  op.batch = 1;
+  op.n_head_q = n_head_q;
+  op.n_head_kv = k ? n_head_k : 0;
+  op.head_dim = head_dim;
+  op.rope_dim = rope_dim;
+  op.rope_style = HL_ROPE_HALF_SPLIT;
+  op.do_rope = 1;
+  op.rope_q = 1;
+  op.rope_k = 1;
+  op.pos = pos;
+  op.theta = th;
+  hipError_t e = headvec_launch(op, as_stream(stream));
+  return e == hipSuccess ? HL_OK : hip_fail(e, "rope launch");
+}
+
+int hl_gpu_rope_at_pos(float* x, int n_head, int head_dim, int rope_dim, float rope_base, int pos,
+                       int seq_len, void* stream) {
+  if (!x) return fail(HL_EINVAL, "rope_at_pos: null pointer");
+  if (n_head <= 0 || head_dim <= 0 || head_dim > HL_MAX_HEAD_DIM || seq_len <= 0)
+    return fail(HL_EINVAL, "rope_at_pos: bad shape");
+  int rc = check_rope(head_dim, rope_dim, HL_ROPE_HALF_SPLIT);
+  if (rc) return rc;
+  ThetaTable th;
+  if ((rc = theta_for(0, rope_dim, rope_base, th))) return rc;
+  if (seq_len == 1) return rope_vec_common(x, nullptr, n_head, 0, head_dim, rope_dim, pos, th, stream);
+  // seq_len > 1: column p rotated at position p (the reference ignores pos)
+  return rope_cols_common(x, n_head, head_dim, rope_dim, 0, seq_len, th, stream);
+}
+
+int hl_gpu_rope_at_pos_theta(float* x, int n_head, int head_dim, int rope_dim, int pos,
+                             int seq_len, void* stream) {
+  if (!x) return fail(HL_EINVAL, "rope_at_pos_theta: null pointer");
+  if (n_head <= 0 || head_dim <= 0 || head_dim > HL_MAX_HEAD_DIM || seq_len <= 0)
+    return fail(HL_EINVAL, "rope_at_pos_theta: bad shape");
+  int rc = check_rope(head_dim, rope_dim, HL_ROPE_HALF_SPLIT);
+  if (rc) return rc;
+  ThetaTable th;
+  if ((rc = theta_for(1, rope_dim, 0.f, th))) return rc;
+  if (seq_len == 1) return rope_vec_common(x, nullptr, n_head, 0, head_dim, rope_dim, pos, th, stream);
+  return rope_cols_common(x, n_head, head_dim, rope_dim, pos, seq_len, th, stream);
+}
+
+int hl_gpu_rope_qk_decode(float* q, float* k, int n_head_q, int n_head_k, int head_dim,
+                          int rope_dim, float rope_base, int pos, void* stream) {
+  if (!q || !k) return fail(HL_EINVAL, "rope_qk_decode: null pointer");
+  if (n_head_q <= 0 || n_head_k <= 0 || head_dim <= 0 || head_dim > HL_MAX_HEAD_DIM)
+    return fail(HL_EINVAL, "rope_qk_decode: bad shape");
+  int rc = check_rope(head_dim, rope_dim, HL_ROPE_HALF_SPLIT);
+  if (rc) return rc;
+  ThetaTable th;
+  bool installed;
+  {
+    std::lock_guard<std::mutex> lk(g_mu);
+    installed = g_theta_set && g_theta_dim == rope_dim;
+  }
+  if ((rc = theta_for(installed ? 1 : 0, rope_dim, rope_base, th))) return rc;
+  return rope_vec_common(q, k, n_head_q, n_head_k, head_dim, rope_dim, pos, th, stream);
+}
+
+int hl_gpu_fused_rope_store_kv(float* q, float* k, const float* v, float* k_cache, float* v_cache,
+                               int n_head_q, int n_head_k, int head_dim, int rope_dim, int kv_dim,
+                               int cache_cols, int pos, void* stream) {
+  if (!q || !k || !v || !k_cache || !v_cache) return fail(HL_EINVAL, "fused_rope_store_kv: null pointer");
+  if (n_head_q <= 0 || n_head_k <= 0 || head_dim <= 0 || head_dim > HL_MAX_HEAD_DIM)
+    return fail(HL_EINVAL, "fused_rope_store_kv: bad shape");
+  if (kv_dim != n_head_k * head_dim)
+    return fail(HL_EINVAL, "fused_rope_store_kv: kv_dim %d != n_head_k*head_dim %d", kv_dim,
+                n_head_k * head_dim);
+  if (pos < 0 || pos >= cache_cols) return fail(HL_ECAPACITY, "KV cache full");
+  int rc = check_rope(head_dim, rope_dim, HL_ROPE_HALF_SPLIT);
+  if (rc) return rc;
+  ThetaTable th;
+  if ((rc = theta_for(1, rope_dim, 0.f, th))) return rc;
+  HeadVecOp op;
+  memset(&op, 0, sizeof(op));
+  op.q = q;
+  op.k = k;
+  op.v = v;
+  op.k_cache = k_cache;
+  op.v_cache = v_cache;
+  op.batch = 1;
+  op.n_head_q = n_head_q;
+  op.n_head_kv = n_head_k;
+  op.head_dim = head_dim;
+  op.rope_dim = rope_dim;
+  op.rope_style = HL_ROPE_HALF_SPLIT;
+  op.do_rope = 1;
+  op.rope_q = 1;
+  op.rope_k = 1;
+  op.kv_dtype = HL_F32;
+  op.max_len = cache_cols;
+  op.batch_stride = (long long)kv_dim * cache_cols;
+  op.pos = pos;
+  op.theta = th;
+  hipError_t e = headvec_launch(op, as_stream(stream));
+  return e == hipSuccess ? HL_OK : hip_fail(e, "fused_rope_store_kv launch");
+}
+
+int hl_gpu_store_kv(float* cache, const float* src, int rows, int src_cols, int cache_cols,
+                    int start_pos, void* stream) {
+  if (!cache || !src) return fail(HL_EINVAL, "store_kv: null pointer");
+  if (rows <= 0 || src_cols <= 0 || start_pos < 0) return fail(HL_EINVAL, "store_kv: bad shape");
+  if (start_pos + src_cols > cache_cols) return fail(HL_ECAPACITY, "prefill exceeds KV cache capacity");
+  hipError_t e = store_cols_launch(cache, src, nullptr, nullptr, rows, src_cols, cache_cols,
+                                   start_pos, HL_F32, as_stream(stream));
+  return e == hipSuccess ? HL_OK : hip_fail(e, "store_kv launch");
+}
+
+int hl_gpu_store_kv_pair(float* k_cache, const float* k_src, float* v_cache, const float* v_src,
+                         int rows, int src_cols, int cache_cols, int start_pos, void* stream) {
+  if (!k_cache || !k_src || !v_cache || !v_src) return fail(HL_EINVAL, "store_kv_pair: null pointer");
+  if (rows <= 0 || src_cols <= 0 || start_pos < 0) return fail(HL_EINVAL, "store_kv_pair: bad shape");
+  if (start_pos + src_cols > cache_cols) return fail(HL_ECAPACITY, "KV cache full");
+  hipError_t e = store_cols_launch(k_cache, k_src, v_cache, v_src, rows, src_cols, cache_cols,
+                                   start_pos, HL_F32, as_stream(stream));
+  return e == hipSuccess ? HL_OK : hip_fail(e, "store_kv_pair launch");
+}
+
+// ---------------------------------------------------------------------------
+// Decode attention
+// ---------------------------------------------------------------------------
+static int validate_decode(const hl_decode_args* a) {
+  if (!a) return fail(HL_EINVAL, "decode: args is null");
+  int rc = check_gqa(a->n_head, a->n_head_kv);
+  if (rc) return rc;
+  if ((rc = check_dtype(a->kv_dtype, "decode kv_dtype"))) return rc;
+  if (a->batch <= 0) return fail(HL_EINVAL, "decode: batch must be >= 1");
+  if (a->head_dim != 64 && a->head_dim != 128)
+    return fail(HL_EUNSUPPORTED, "decode: head_dim %d not built (64, 128)", a->head_dim);
+  if (!a->q || !a->k_cache || !a->v_cache || !a->out) return fail(HL_EINVAL, "decode: null pointer");
+  if (a->seq_len <= 0) return fail(HL_EINVAL, "decode: attention length must be >= 1");
+  if (a->seq_len > a->max_len) return fail(HL_ECAPACITY, "KV cache full");
+  if (a->num_splits < 0 || a->num_splits > 1024) return fail(HL_EINVAL, "decode: num_splits must be in [0, 1024]");
+  if (!aligned16(a->q)) return fail(HL_EINVAL, "decode: q must be 16-byte aligned");
+  const long long dense = (long long)a->n_head_kv * a->head_dim * a->max_len;
+  if (a->cache_batch_stride != 0 && a->cache_batch_stride < dense)
+    return fail(HL_EINVAL, "decode: cache_batch_stride smaller than one sequence's cache");
+  return HL_OK;
+}
+
+size_t hl_attn_decode_workspace_bytes(const hl_decode_args* a) {
+  if (validate_decode(a)) return 0;
+  DecodePlan plan;
+  decode_plan(a, &plan);
+  return plan.ws_bytes;
+}
+
+int hl_attn_decode(const hl_decode_args* a, void* workspace, size_t ws_bytes, void* stream) {
+  int rc = validate_decode(a);
+  if (rc) return rc;
+  DecodePlan plan;
+  decode_plan(a, &plan);
+  if (plan.ws_bytes > 0 && (!workspace || ws_bytes < plan.ws_bytes))
+    return fail(HL_EINVAL, "decode: workspace of %zu bytes needed, %zu given", plan.ws_bytes, ws_bytes);
+  const long long stride = a->cache_batch_stride ? a->cache_batch_stride
+                                                 : (long long)a->n_head_kv * a->head_dim * a->max_len;
+  const bool vec_ok = a->kv_dtype != HL_F32 && (a->max_len % 8 == 0) && (stride % 8 == 0) &&
+                      aligned16(a->k_cache) && aligned16(a->v_cache);
+  hipError_t e = decode_launch(a, &plan, workspace, as_stream(stream), vec_ok);
+  return e == hipSuccess ? HL_OK : hip_fail(e, "decode launch");
+}
+
+int hl_gpu_attention_decode(float* dst, const float* q, const float* k_cache, const float* v_cache,
+                            int n_head, int n_head_kv, int head_dim, int cur_len, int cache_cols,
+                            void* stream) {
+  hl_decode_args a;
+  memset(&a, 0, sizeof(a));
+  a.batch = 1;
+  a.n_head = n_head;
+  a.n_head_kv = n_head_kv;
+  a.head_dim = head_dim;
+  a.kv_dtype = HL_F32;
+  a.max_len = cache_cols;
+  a.seq_len = cur_len;
+  a.q = q;
+  a.k_cache = k_cache;
+  a.v_cache = v_cache;
+  a.out = dst;
+  int rc = validate_decode(&a);
+  if (rc) return rc;
+  DecodePlan plan;
+  decode_plan(&a, &plan);
+  void* ws = nullptr;
+  if (plan.ws_bytes > 0) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    std::lock_guard<std::mutex> lk(g_mu);
+    if ((int)g_ws.size() <= dev) g_ws.resize(dev + 1);
+    DevWs& w = g_ws[dev];
+    if (w.bytes < plan.ws_bytes) {
+      if (w.ptr) {
+        e = hipDeviceSynchronize();  // an earlier launch may still read it
+        if (e != hipSuccess) return hip_fail(e, "hipDeviceSynchronize");
+        hipFree(w.ptr);
+        w.ptr = nullptr;
+        w.bytes = 0;
+      }
+      size_t bytes = plan.ws_bytes < (1u << 20) ? (1u << 20) : plan.ws_bytes;
+      e = hipMalloc(&w.ptr, bytes);
+      if (e != hipSuccess) return hip_fail(e, "hipMalloc(decode workspace)");
+      w.bytes = bytes;
+    }
+    ws = w.ptr;
+  }
+  hipError_t e = decode_launch(&a, &plan, ws, as_stream(stream), false);
+  return e == hipSuccess ? HL_OK : hip_fail(e, "decode launch");
+}
+
+// ---------------------------------------------------------------------------
+// Decode-side fused qkNorm + RoPE + KV store
+// ---------------------------------------------------------------------------
+int hl_rope_store_decode(const hl_rope_store_args* a, void* stream) {
+  if (!a) return fail(HL_EINVAL, "rope_store: args is null");
+  int rc = check_gqa(a->n_head_q, a->n_head_kv);
+  if (rc) return rc;
+  if ((rc = check_dtype(a->kv_dtype, "rope_store kv_dtype"))) return rc;
+  if (a->batch <= 0 || a->head_dim <= 0 || a->head_dim > HL_MAX_HEAD_DIM || (a->head_dim & 1))
+    return fail(HL_EINVAL, "rope_store: bad shape");
+  if (!a->q || !a->k || !a->v || !a->k_cache || !a->v_cache) return fail(HL_EINVAL, "rope_store: null pointer");
+  if (!a->positions && (a->pos < 0 || a->pos >= a->max_len)) return fail(HL_ECAPACITY, "KV cache full");
+  const int rope_dim = a->rope_dim ? a->rope_dim : a->head_dim;
+  if ((rc = check_rope(a->head_dim, rope_dim, a->rope_style))) return rc;
+  const long long dense = (long long)a->n_head_kv * a->head_dim * a->max_len;
+  if (a->cache_batch_stride != 0 && a->cache_batch_stride < dense)
+    return fail(HL_EINVAL, "rope_store: cache_batch_stride smaller than one sequence's cache");
+  HeadVecOp op;
+  memset(&op, 0, sizeof(op));
+  if ((rc = theta_for(a->use_installed_theta, rope_dim, a->rope_base, op.theta))) return rc;
+  op.q = a->q;
+  op.k = a->k;
+  op.v = a->v;
+  op.k_cache = a->k_cache;
+  op.v_cache = a->v_cache;
+  op.positions = a->positions;
+  op.pos = a->pos;
+  op.batch = a->batch;
+  op.n_head_q = a->n_head_q;
+  op.n_head_kv = a->n_head_kv;
+  op.head_dim = a->head_dim;
+  op.rope_dim = rope_dim;
+  op.rope_style = a->rope_style;
+  op.do_rope = 1;
+  op.rope_q = 1;
+  op.rope_k = 1;
+  op.kv_dtype = a->kv_dtype;
+  op.max_len = a->max_len;
+  op.batch_stride = a->cache_batch_stride ? a->cache_batch_stride : dense;
+  op.q_norm_w = a->q_norm_w;
+  op.k_norm_w = a->k_norm_w;
+  op.eps = a->eps;
+  hipError_t e = headvec_launch(op, as_stream(stream));
+  return e == hipSuccess ? HL_OK : hip_fail(e, "rope_store launch");
+}
+
+// ---------------------------------------------------------------------------
+// Prefill
+// ---------------------------------------------------------------------------
+struct PrefillPlan {
+  bool mfma;
+  int t_pad;
+  size_t off_q, off_k, off_v, bytes;
+};
+
+static int validate_prefill(const hl_prefill_args* a, PrefillPlan* pl) {
+  if (!a) return fail(HL_EINVAL, "prefill: args is null");
+  int rc = check_gqa(a->n_head, a->n_head_kv);
+  if (rc) return rc;
+  if ((rc = check_dtype(a->io_dtype, "prefill io_dtype"))) return rc;
+  if (a->seq_len <= 0) return fail(HL_EINVAL, "prefill requires at least one token");
+  if (a->head_dim != 64 && a->head_dim != 128)
+    return fail(HL_EUNSUPPORTED, "prefill: head_dim %d not built (64, 128)", a->head_dim);
+  if (!a->q || !a->k || !a->v || !a->out) return fail(HL_EINVAL, "prefill: null pointer");
+  if (a->k_cache || a->v_cache) {
+    if (!a->k_cache || !a->v_cache) return fail(HL_EINVAL, "prefill: give both caches or neither");
+    if ((rc = check_dtype(a->kv_dtype, "prefill kv_dtype"))) return rc;
+    if (a->start_pos < 0) return fail(HL_EINVAL, "prefill: start_pos < 0");
+    if ((long long)a->start_pos + a->seq_len > a->max_len)
+      return fail(HL_ECAPACITY, "prefill exceeds KV cache capacity");
+  }
+  if (a->apply_rope) {
+    const int rd = a->rope_dim ? a->rope_dim : a->head_dim;
+    if ((rc = check_rope(a->head_dim, rd, a->rope_style))) return rc;
+  }
+  if ((rc = check_dtype(a->out_dtype, "prefill out_dtype"))) return rc;
+  if (a->io_dtype == HL_F32 && a->out_dtype != HL_F32)
+    return fail(HL_EUNSUPPORTED, "prefill: fp32 activations produce fp32 output");
+  if (a->write_back_qk && a->io_dtype != HL_F32)
+    return fail(HL_EUNSUPPORTED, "prefill: write_back_qk needs fp32 activations");
+  const size_t D = a->head_dim, T = a->seq_len;
+  pl->mfma = a->io_dtype != HL_F32;
+  if (pl->mfma) {
+    pl->t_pad = prefill_mfma_tpad(a->seq_len);
+    const size_t tp = pl->t_pad;
+    pl->off_q = 0;
+    pl->off_k = pl->off_q + (size_t)a->n_head * tp * D * 2;
+    pl->off_v = pl->off_k + (size_t)a->n_head_kv * tp * D * 2;
+    pl->bytes = pl->off_v + (size_t)a->n_head_kv * tp * D * 2;
+  } else {
+    pl->t_pad = a->seq_len;
+    const bool pre = a->apply_rope || a->q_norm_w || a->k_norm_w;
+    pl->off_q = 0;
+    pl->off_k = (pre && !a->write_back_qk) ? (size_t)a->n_head * T * D * 4 : 0;
+    pl->off_v = 0;
+    pl->bytes = (pre && !a->write_back_qk) ? pl->off_k + (size_t)a->n_head_kv * T * D * 4 : 0;
+  }
+  return HL_OK;
+}
+
+size_t hl_attn_prefill_workspace_bytes(const hl_prefill_args* a) {
+  PrefillPlan pl;
+  if (validate_prefill(a, &pl)) return 0;
+  return pl.bytes;
+}
+
+int hl_attn_prefill(const hl_prefill_args* a, void* workspace, size_t ws_bytes, void* stream) {
+  PrefillPlan pl;
+  int rc = validate_prefill(a, &pl);
+  if (rc) return rc;
+  if (pl.bytes > 0 && (!workspace || ws_bytes < pl.bytes))
+    return fail(HL_EINVAL, "prefill: workspace of %zu bytes needed, %zu given", pl.bytes, ws_bytes);
+  if (pl.bytes > 0 && !aligned16(workspace)) return fail(HL_EINVAL, "prefill: workspace must be 16-byte aligned");
+  const int rope_dim = a->rope_dim ? a->rope_dim : a->head_dim;
+  PrologueOp op;
+  memset(&op, 0, sizeof(op));
+  if (a->apply_rope && (rc = theta_for(a->use_installed_theta, rope_dim, a->rope_base, op.theta)))
+    return rc;
+  const float scale = a->scale != 0.f ? a->scale : 1.0f / sqrtf((float)a->head_dim);
+  char* ws = (char*)workspace;
+  hipStream_t st = as_stream(stream);
+  op.q = a->q;
+  op.k = a->k;
+  op.v = a->v;
+  op.io_dtype = a->io_dtype;
+  op.k_cache = a->k_cache;
+  op.v_cache = a->v_cache;
+  op.kv_dtype = a->kv_dtype;
+  op.max_len = a->max_len;
+  op.start_pos = a->start_pos;
+  op.n_head = a->n_head;
+  op.n_head_kv = a->n_head_kv;
+  op.head_dim = a->head_dim;
+  op.seq_len = a->seq_len;
+  op.do_rope = a->apply_rope;
+  op.rope_dim = rope_dim;
+  op.rope_style = a->rope_style;
+  op.q_norm_w = a->q_norm_w;
+  op.k_norm_w = a->k_norm_w;
+  op.eps = a->eps;
+  op.t_pad = pl.t_pad;
+
+  PrefillLaunch pf;
+  memset(&pf, 0, sizeof(pf));
+  pf.out = a->out;
+  pf.out_dtype = a->out_dtype;
+  pf.n_head = a->n_head;
+  pf.n_head_kv = a->n_head_kv;
+  pf.head_dim = a->head_dim;
+  pf.seq_len = a->seq_len;
+  pf.t_pad = pl.t_pad;
+  hipError_t e;
+  if (pl.mfma) {
+    op.qt = (uint16_t*)(ws + pl.off_q);
+    op.kt = (uint16_t*)(ws + pl.off_k);
+    op.vt = (uint16_t*)(ws + pl.off_v);
+    op.qt_scale = scale * kLog2e;
+    if ((e = prologue_launch(op, st)) != hipSuccess) return hip_fail(e, "prefill prologue launch");
+    pf.qt = op.qt;
+    pf.kt = op.kt;
+    pf.vt = op.vt;
+    e = prefill_mfma_launch(pf, st);
+    return e == hipSuccess ? HL_OK : hip_fail(e, "prefill launch");
+  }
+  // fp32: normed/roped q,k either in place or in the workspace
+  const bool pre = a->apply_rope || a->q_norm_w || a->k_norm_w;
+  const float* qsrc = (const float*)a->q;
+  const float* ksrc = (const float*)a->k;
+  if (pre) {
+    float* qd = a->write_back_qk ? (float*)a->q : (float*)(ws + pl.off_q);
+    float* kd = a->write_back_qk ? (float*)a->k : (float*)(ws + pl.off_k);
+    op.q_inplace = qd;
+    op.k_inplace = kd;
+    qsrc = qd;
+    ksrc = kd;
+  } else {
+    op.q = nullptr;  // nothing to do for q; k only feeds the cache
+    if (!a->k_cache) op.k = nullptr;
+  }
+  if (!a->k_cache) op.v = nullptr;
+  if (op.q || op.k || op.v) {
+    if ((e = prologue_launch(op, st)) != hipSuccess) return hip_fail(e, "prefill prologue launch");
+  }
+  pf.q = qsrc;
+  pf.k = ksrc;
+  pf.v = (const float*)a->v;
+  pf.scale_log2 = scale * kLog2e;
+  e = prefill_f32_launch(pf, st);
+  return e == hipSuccess ? HL_OK : hip_fail(e, "prefill launch");
+}
+
+int hl_gpu_attention_prefill(float* dst, const float* q, const float* k, const float* v, int n_head,
+                             int n_head_kv, int head_dim, int seq_len, void* stream) {
+  hl_prefill_args a;
+  memset(&a, 0, sizeof(a));
+  a.n_head = n_head;
+  a.n_head_kv = n_head_kv;
+  a.head_dim = head_dim;
+  a.seq_len = seq_len;
+  a.io_dtype = HL_F32;
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.out = dst;
+  return hl_attn_prefill(&a, nullptr, 0, stream);
+}
+
+int hl_kv_cache_to_f32(float* dst, const void* cache, int kv_dtype, int rows, int max_len, int col0,
+                       int ncols, void* stream) {
+  if (!dst || !cache) return fail(HL_EINVAL, "cache_to_f32: null pointer");
+  int rc = check_dtype(kv_dtype, "cache_to_f32");
+  if (rc) return rc;
+  if (rows <= 0 || ncols <= 0 || col0 < 0 || col0 + ncols > max_len)
+    return fail(HL_EINVAL, "cache_to_f32: bad range");
+  hipError_t e = cache_to_f32_launch(dst, cache, kv_dtype, rows, max_len, col0, ncols, as_stream(stream));
+  return e == hipSuccess ? HL_OK : hip_fail(e, "cache_to_f32 launch");
+}
+
+}  // extern "C"

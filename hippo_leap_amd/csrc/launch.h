@@ -1,0 +1,102 @@
+// Internal host-side launchers shared between the kernel translation units
+// and the C-ABI layer (api.hip).  Validation happens in api.hip; these assume
+// arguments already checked.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "common.h"
+
+namespace hl {
+
+// ---- decode attention (decode.hip) ----------------------------------------
+struct DecodePlan {
+  int head_chunk, n_chunks, num_splits, split_len;
+  size_t ws_bytes;
+};
+void decode_plan(const hl_decode_args* a, DecodePlan* plan);
+hipError_t decode_launch(const hl_decode_args* a, const DecodePlan* plan, void* ws,
+                         hipStream_t stream, bool vec_ok);
+
+// ---- per-token head-vector ops (rope_store.hip) ---------------------------
+// One launch over B sequences x (Hq + 2*Hkv) head vectors of the new token:
+// optional RMSNorm, optional RoPE at the sequence's position, optional store
+// of k / v into the cache column.
+struct HeadVecOp {
+  float* q;            // [B][Hq*D] or null
+  float* k;            // [B][Hkv*D] or null
+  const float* v;      // [B][Hkv*D] or null
+  void* k_cache;       // null: no store
+  void* v_cache;
+  const int* positions;
+  int pos;
+  int batch, n_head_q, n_head_kv, head_dim, rope_dim, rope_style, do_rope, kv_dtype, max_len;
+  long long batch_stride;
+  const float* q_norm_w;
+  const float* k_norm_w;
+  float eps;
+  int rope_q, rope_k;  // which tensors get RoPE
+  ThetaTable theta;
+};
+hipError_t headvec_launch(const HeadVecOp& op, hipStream_t stream);
+
+// ---- column-major prologue (rope_store.hip) --------------------------------
+// Works on col-major [H*D, T] activations, one (head, 64-column tile) per
+// workgroup, for the Q heads, K heads and V heads of a prefill:
+//   Q: norm?, RoPE?, then write back in place (fp32) and/or to the MFMA
+//      layout qt[Hq][T][D] (fp16, pre-scaled by scale*log2 e)
+//   K: norm?, RoPE?, write back / kt[Hkv][T][D] fp16 / cache column
+//   V: vt[Hkv][D][T] fp16 and/or cache column
+struct PrologueOp {
+  const void* q;
+  const void* k;
+  const void* v;
+  int io_dtype;
+  float* q_inplace;   // fp32 write-back targets (may alias q/k) or null
+  float* k_inplace;
+  uint16_t* qt;       // MFMA layouts (fp16 bits) or null
+  uint16_t* kt;
+  uint16_t* vt;
+  void* k_cache;
+  void* v_cache;
+  int kv_dtype, max_len, start_pos;
+  int n_head, n_head_kv, head_dim, seq_len;
+  int do_rope, rope_dim, rope_style;
+  const float* q_norm_w;
+  const float* k_norm_w;
+  float eps;
+  float qt_scale;     // multiplier folded into qt
+  int t_pad;          // row count of qt/kt/vt (seq_len rounded up); pad rows zeroed
+  ThetaTable theta;
+};
+hipError_t prologue_launch(const PrologueOp& op, hipStream_t stream);
+
+// Plain column copy with dtype conversion: cache[r*cache_cols + start + c] =
+// src[r*src_cols + c] (two tensors when src2 != null).
+hipError_t store_cols_launch(void* cache, const float* src, void* cache2, const float* src2,
+                             int rows, int src_cols, int cache_cols, int start_pos, int kv_dtype,
+                             hipStream_t stream);
+
+hipError_t cache_to_f32_launch(float* dst, const void* cache, int kv_dtype, int rows, int max_len,
+                               int col0, int ncols, hipStream_t stream);
+
+// ---- prefill attention (prefill.hip) --------------------------------------
+struct PrefillLaunch {
+  // fp32 path: col-major q/k/v/out [H*D, T]
+  const float* q;
+  const float* k;
+  const float* v;
+  // MFMA path: qt [Hq][Tp][D], kt [Hkv][Tp][D], vt [Hkv][D][Tp] (fp16 bits)
+  const uint16_t* qt;
+  const uint16_t* kt;
+  const uint16_t* vt;
+  void* out;
+  int out_dtype;
+  int n_head, n_head_kv, head_dim, seq_len, t_pad;
+  float scale_log2;   // fp32 path only (MFMA path has it folded into qt)
+};
+hipError_t prefill_f32_launch(const PrefillLaunch& p, hipStream_t stream);
+hipError_t prefill_mfma_launch(const PrefillLaunch& p, hipStream_t stream);
+int prefill_mfma_tpad(int seq_len);
+
+}  // namespace hl

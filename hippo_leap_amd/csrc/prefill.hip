@@ -1,0 +1,393 @@
+// Causal prefill attention for gfx950 (flash-style, online softmax).
+//
+// Semantics: attentionPrefillKernel / gpuAttentionPrefill (backends/naive.nim:
+// 3385-3464): for query row i of head h, scores s_j = (q_i . k_j) * scale for
+// j <= i, p = softmax(s), o_i = sum_j p_j v_j; kv head = h / (Hq/Hkv).  The
+// reference materialises the whole causal row in a 4096-float LDS array (so
+// T <= 4096) and re-reads K/V for every query row; here K/V tiles are staged
+// once per workgroup and reused by every query row and every head of the GQA
+// group it holds, with no length cap.
+//
+// Two kernels:
+//  * prefill_mfma_kernel: fp16 MFMA (v_mfma_f32_32x32x16_f16) on operands
+//    prepared by prologue_kernel: qt[Hq][Tp][D] (q pre-scaled by
+//    scale*log2 e), kt[Hkv][Tp][D], vt[Hkv][D][Tp].  fp16 operands keep 11
+//    significant bits (bf16 has 8), which keeps the result within 2e-3 of the
+//    fp32 reference; P is rounded to fp16, accumulation is fp32.
+//  * prefill_f32_kernel: fp32 vector-ALU flash kernel on the reference's
+//    col-major fp32 tensors (the 1e-4 path).
+#include "common.h"
+#include "launch.h"
+
+namespace hl {
+
+// ===========================================================================
+// MFMA path
+// ===========================================================================
+namespace {
+constexpr int BN = 64;          // key columns per tile
+constexpr int QR = 32;          // query rows per wave
+}  // namespace
+
+int prefill_mfma_tpad(int seq_len) { return (seq_len + BN - 1) / BN * BN; }
+
+struct MfmaPrefillParams {
+  const uint16_t* qt;
+  const uint16_t* kt;
+  const uint16_t* vt;
+  void* out;
+  int n_head, n_head_kv, group, T, Tp;
+  int nh;          // heads per workgroup (waves split nh x (4/nh) row blocks)
+  int rows_wg;     // query rows per workgroup = 32 * (4/nh)
+  int n_qblk;      // query row blocks of rows_wg
+  int n_hgrp;      // head groups of nh per kv head
+};
+
+__device__ __forceinline__ f32x16 mma32(f16x8 a, f16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+template <int D, int ODT>
+__global__ __launch_bounds__(256, 2) void prefill_mfma_kernel(MfmaPrefillParams p) {
+  constexpr int KP = D + 8;        // K tile row pitch (fp16 elements)
+  constexpr int VP = BN + 8;       // V tile row pitch
+  constexpr int KSTEPS = D / 16;   // QK^T k-steps
+  constexpr int DB = D / 32;       // 32-dim blocks of O^T
+  __shared__ __attribute__((aligned(16))) uint16_t ks[BN * KP];
+  __shared__ __attribute__((aligned(16))) uint16_t vs[D * VP];
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int hh = lane >> 5, ln = lane & 31;
+
+  // Work item: heaviest (last) query blocks first; within a query block the
+  // kv head varies fastest, so with the hardware's round-robin of workgroups
+  // over the 8 XCDs a given kv head keeps landing on the same XCD (and L2)
+  // whenever Hkv * head groups is a multiple of 8.
+  const int per_q = p.n_head_kv * p.n_hgrp;
+  const int item = blockIdx.x;
+  const int qblk = p.n_qblk - 1 - item / per_q;
+  const int kvh = (item % per_q) / p.n_hgrp;
+  const int hgrp = (item % per_q) % p.n_hgrp;
+  const int hq = kvh * p.group + hgrp * p.nh + (wave % p.nh);
+  const int r0 = qblk * p.rows_wg + (wave / p.nh) * QR;  // this wave's first row
+  const int wg_last_row = min(p.T - 1, qblk * p.rows_wg + p.rows_wg - 1);
+  const int n_tiles = wg_last_row / BN + 1;
+
+  // Q^T operand: lane holds q[t = r0 + ln][16*ks + 8*hh .. +7]
+  f16x8 qf[KSTEPS];
+  {
+    const int t = min(r0 + ln, p.Tp - 1);
+    const uint16_t* qrow = p.qt + ((long long)hq * p.Tp + t) * D;
+#pragma unroll
+    for (int k = 0; k < KSTEPS; ++k) qf[k] = *(const f16x8*)(qrow + 16 * k + 8 * hh);
+  }
+
+  const uint16_t* kbase = p.kt + (long long)kvh * p.Tp * D;
+  const uint16_t* vbase = p.vt + (long long)kvh * D * p.Tp;
+
+  // Register prefetch of one K tile (BN*D halves) and one V tile.
+  constexpr int KCH = BN * D / 8 / 256;  // 16-byte chunks per thread
+  constexpr int VCH = D * BN / 8 / 256;
+  u16x8 kreg[KCH], vreg[VCH];
+  auto load_tile = [&](int j0) {
+#pragma unroll
+    for (int c = 0; c < KCH; ++c) {
+      const int ch = tid + 256 * c;  // chunk index within the contiguous tile
+      kreg[c] = *(const u16x8*)(kbase + (long long)j0 * D + 8 * ch);
+    }
+#pragma unroll
+    for (int c = 0; c < VCH; ++c) {
+      const int ch = tid + 256 * c;
+      const int d = ch / (BN / 8), jc = ch % (BN / 8);
+      vreg[c] = *(const u16x8*)(vbase + (long long)d * p.Tp + j0 + 8 * jc);
+    }
+  };
+  auto store_tile = [&]() {
+#pragma unroll
+    for (int c = 0; c < KCH; ++c) {
+      const int ch = tid + 256 * c;
+      const int j = ch / (D / 8), dc = ch % (D / 8);
+      *(u16x8*)(ks + j * KP + 8 * dc) = kreg[c];
+    }
+#pragma unroll
+    for (int c = 0; c < VCH; ++c) {
+      const int ch = tid + 256 * c;
+      const int d = ch / (BN / 8), jc = ch % (BN / 8);
+      // columns 8*jc .. +7: j = 16q + 8a + e; slot(16q + 8a + 4b + e') = 16q + 8b + 4a + e'
+      const int q16 = jc >> 1, a = jc & 1;
+      uint16_t* row = vs + d * VP + 16 * q16 + 4 * a;
+      const u16x8 v = vreg[c];
+      typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
+      *(u16x4*)(row) = u16x4{v[0], v[1], v[2], v[3]};
+      *(u16x4*)(row + 8) = u16x4{v[4], v[5], v[6], v[7]};
+    }
+  };
+
+  f32x16 o[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) o[db][i] = 0.f;
+  float m_run = -INFINITY, l_run = 0.f;
+  const int t_abs = r0 + ln;
+
+  load_tile(0);
+  for (int tile = 0; tile < n_tiles; ++tile) {
+    const int j0 = tile * BN;
+    __syncthreads();
+    store_tile();
+    __syncthreads();
+    if (tile + 1 < n_tiles) load_tile(j0 + BN);
+
+    // skip tiles entirely above this wave's rows (causal)
+    if (j0 > r0 + QR - 1 || r0 >= p.T) continue;
+
+    // S^T[j][t] for j in two 32-blocks
+    f32x16 s[2];
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) s[mb][i] = 0.f;
+      const uint16_t* krow = ks + (32 * mb + ln) * KP + 8 * hh;
+#pragma unroll
+      for (int k = 0; k < KSTEPS; ++k) {
+        const f16x8 a = *(const f16x8*)(krow + 16 * k);
+        s[mb] = mma32(a, qf[k], s[mb]);
+      }
+    }
+    // causal mask on the diagonal tile: j > t -> -inf
+    const bool diag = j0 + BN - 1 > r0;
+    float mt = -INFINITY;
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int j = j0 + 32 * mb + 8 * (i >> 2) + 4 * hh + (i & 3);
+        if (diag && j > t_abs) s[mb][i] = -INFINITY;
+        mt = fmaxf(mt, s[mb][i]);
+      }
+    mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+    const float mn = fmaxf(m_run, mt);
+    // mn is finite: column j0 <= t_abs is always unmasked for rows < T; rows
+    // >= T (padding) see their own finite scores of the zero pad.
+    const float alpha = fast_exp2(m_run - mn);
+    m_run = mn;
+    float ps = 0.f;
+    f16x8 pf[4];  // B operand of O^T = V^T P^T, one per 16-column k-step
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float pv = fast_exp2(s[mb][8 * u + e] - mn);
+          ps += pv;
+          pf[2 * mb + u][e] = (_Float16)pv;
+        }
+    l_run = l_run * alpha + ps;
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) o[db][i] *= alpha;
+      const uint16_t* vrow = vs + (32 * db + ln) * VP + 8 * hh;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const f16x8 a = *(const f16x8*)(vrow + 16 * k);
+        o[db] = mma32(a, pf[k], o[db]);
+      }
+    }
+  }
+
+  if (r0 >= p.T) return;
+  const float l = l_run + __shfl_xor(l_run, 32, 64);
+  const float inv = 1.0f / l;
+  if (t_abs < p.T) {
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int d = 32 * db + 8 * (i >> 2) + 4 * hh + (i & 3);
+        store_elem<ODT>(p.out, ((long long)hq * D + d) * p.T + t_abs, o[db][i] * inv);
+      }
+  }
+}
+
+hipError_t prefill_mfma_launch(const PrefillLaunch& a, hipStream_t stream) {
+  MfmaPrefillParams p;
+  p.qt = a.qt;
+  p.kt = a.kt;
+  p.vt = a.vt;
+  p.out = a.out;
+  p.n_head = a.n_head;
+  p.n_head_kv = a.n_head_kv;
+  p.group = a.n_head / a.n_head_kv;
+  p.T = a.seq_len;
+  p.Tp = a.t_pad;
+  p.nh = (p.group % 4 == 0) ? 4 : ((p.group % 2 == 0) ? 2 : 1);
+  p.rows_wg = QR * (4 / p.nh);
+  p.n_qblk = (p.T + p.rows_wg - 1) / p.rows_wg;
+  p.n_hgrp = p.group / p.nh;
+  dim3 grid(a.n_head_kv * p.n_hgrp * p.n_qblk);
+#define HL_PF(DD, OD) hipLaunchKernelGGL((prefill_mfma_kernel<DD, OD>), grid, dim3(256), 0, stream, p)
+  if (a.head_dim == 64) {
+    if (a.out_dtype == HL_F16) HL_PF(64, HL_F16);
+    else if (a.out_dtype == HL_BF16) HL_PF(64, HL_BF16);
+    else HL_PF(64, HL_F32);
+  } else if (a.head_dim == 128) {
+    if (a.out_dtype == HL_F16) HL_PF(128, HL_F16);
+    else if (a.out_dtype == HL_BF16) HL_PF(128, HL_BF16);
+    else HL_PF(128, HL_F32);
+  } else {
+    return hipErrorInvalidValue;
+  }
+#undef HL_PF
+  return hipGetLastError();
+}
+
+// ===========================================================================
+// fp32 path: 32 query rows x 64 key columns per step, 256 threads.
+// Thread (rg = tid/16, cg = tid%16) owns score rows {2rg, 2rg+1} x columns
+// {4cg..4cg+3} and output rows {2rg, 2rg+1} x dims {4cg + 64u + 0..3}.
+// ===========================================================================
+template <int D>
+__global__ __launch_bounds__(256) void prefill_f32_kernel(PrefillLaunch p) {
+  constexpr int BM = 32, BNF = 64, DU = D / 64;
+  __shared__ __attribute__((aligned(16))) float sq[D][BM];        // Q tile, [d][row]
+  __shared__ __attribute__((aligned(16))) float skv[BNF * (D + 4)];  // K as [d][col], then V as [col][d]
+  __shared__ __attribute__((aligned(16))) float sp[BM][BNF + 4];
+
+  const int tid = threadIdx.x;
+  const int rg = tid >> 4, cg = tid & 15;
+  const int T = p.seq_len;
+  const int nq = (T + BM - 1) / BM;
+  const int h = blockIdx.y;
+  const int qb = nq - 1 - blockIdx.x;  // heavy blocks first
+  const int i0 = qb * BM;
+  const int kvh = h / (p.n_head / p.n_head_kv);
+  const float* Q = p.q + (long long)h * D * T;
+  const float* K = p.k + (long long)kvh * D * T;
+  const float* V = p.v + (long long)kvh * D * T;
+
+  for (int idx = tid; idx < D * BM; idx += 256) {
+    const int d = idx / BM, r = idx % BM;
+    sq[d][r] = (i0 + r < T) ? Q[(long long)d * T + i0 + r] : 0.f;
+  }
+
+  float o[2][4 * DU];
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int b = 0; b < 4 * DU; ++b) o[a][b] = 0.f;
+  float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};
+  const int last_row = min(T - 1, i0 + BM - 1);
+  const int n_tiles = last_row / BNF + 1;
+
+  for (int tile = 0; tile < n_tiles; ++tile) {
+    const int j0 = tile * BNF;
+    __syncthreads();
+    // K tile as [d][col] (pitch BNF+4)
+    for (int idx = tid; idx < D * BNF; idx += 256) {
+      const int d = idx / BNF, c = idx % BNF;
+      skv[d * (BNF + 4) + c] = (j0 + c < T) ? K[(long long)d * T + j0 + c] : 0.f;
+    }
+    __syncthreads();
+    float s[2][4];
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int b = 0; b < 4; ++b) s[a][b] = 0.f;
+    for (int d = 0; d < D; ++d) {
+      const float q0 = sq[d][2 * rg], q1 = sq[d][2 * rg + 1];
+      const f32x4 kv = *(const f32x4*)&skv[d * (BNF + 4) + 4 * cg];
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        s[0][b] = fmaf(q0, kv[b], s[0][b]);
+        s[1][b] = fmaf(q1, kv[b], s[1][b]);
+      }
+    }
+    // scale (naive.nim:3415), causal mask, online softmax per row
+    float alpha[2];
+#pragma unroll
+    for (int a = 0; a < 2; ++a) {
+      const int i = i0 + 2 * rg + a;
+      float mt = -INFINITY;
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const int j = j0 + 4 * cg + b;
+        s[a][b] = (j <= i && j < T) ? s[a][b] * p.scale_log2 : -INFINITY;
+        mt = fmaxf(mt, s[a][b]);
+      }
+#pragma unroll
+      for (int off = 8; off > 0; off >>= 1) mt = fmaxf(mt, __shfl_xor(mt, off, 16));
+      const float mn = fmaxf(m_run[a], mt);
+      if (mn == -INFINITY) {  // row entirely masked in this tile and before
+        alpha[a] = 1.f;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) sp[2 * rg + a][4 * cg + b] = 0.f;
+        continue;
+      }
+      alpha[a] = fast_exp2(m_run[a] - mn);
+      m_run[a] = mn;
+      float ps = 0.f;
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const float pv = fast_exp2(s[a][b] - mn);
+        ps += pv;
+        sp[2 * rg + a][4 * cg + b] = pv;
+      }
+      l_run[a] = l_run[a] * alpha[a] + ps;
+    }
+    __syncthreads();
+    // V tile as [col][d] (pitch D+4)
+    for (int idx = tid; idx < D * BNF; idx += 256) {
+      const int d = idx / BNF, c = idx % BNF;
+      skv[c * (D + 4) + d] = (j0 + c < T) ? V[(long long)d * T + j0 + c] : 0.f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int b = 0; b < 4 * DU; ++b) o[a][b] *= alpha[a];
+    const int ncols = min(BNF, T - j0);
+    for (int c = 0; c < ncols; ++c) {
+      const float p0 = sp[2 * rg][c], p1 = sp[2 * rg + 1][c];
+#pragma unroll
+      for (int u = 0; u < DU; ++u) {
+        const f32x4 vv = *(const f32x4*)&skv[c * (D + 4) + 4 * cg + 64 * u];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          o[0][4 * u + e] = fmaf(p0, vv[e], o[0][4 * u + e]);
+          o[1][4 * u + e] = fmaf(p1, vv[e], o[1][4 * u + e]);
+        }
+      }
+    }
+  }
+
+  float* O = (float*)p.out + (long long)h * D * T;
+#pragma unroll
+  for (int a = 0; a < 2; ++a) {
+    float l = l_run[a];
+#pragma unroll
+    for (int off = 8; off > 0; off >>= 1) l += __shfl_xor(l, off, 16);
+    const int i = i0 + 2 * rg + a;
+    if (i < T) {
+      const float inv = 1.0f / l;
+#pragma unroll
+      for (int u = 0; u < DU; ++u)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) O[(long long)(4 * cg + 64 * u + e) * T + i] = o[a][4 * u + e] * inv;
+    }
+  }
+}
+
+hipError_t prefill_f32_launch(const PrefillLaunch& p, hipStream_t stream) {
+  dim3 grid((p.seq_len + 31) / 32, p.n_head);
+  switch (p.head_dim) {
+    case 64: hipLaunchKernelGGL(prefill_f32_kernel<64>, grid, dim3(256), 0, stream, p); break;
+    case 128: hipLaunchKernelGGL(prefill_f32_kernel<128>, grid, dim3(256), 0, stream, p); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace hl

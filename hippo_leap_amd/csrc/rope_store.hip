@@ -1,0 +1,329 @@
+// qkNorm, RoPE and KV-cache store kernels for gfx950.
+//
+// Reference kernels replaced (backends/naive.nim):
+//   qkNormKernel / qkNormPrefillKernel          :2887-2971
+//   ropeAtPosKernel / ropeQKDecodeKernel /
+//   ropeAtPosThetaKernel                        :3006-3144
+//   fusedRopeStoreKVKernel                      :3149-3223
+//   storeKVKernel / storeKVPairKernel           :3228-3285
+// The reference launches one of these per tensor per layer (up to six per
+// attention layer); here one launch covers every head vector of a decode
+// step (headvec_kernel) or every (head, 32-token tile) of a prefill
+// (prologue_kernel), with the cache write and the conversion to the MFMA
+// operand layout done while the data is in registers/LDS.
+//
+// Formulas kept from the reference:
+//   RMSNorm   x * (1/sqrtf(sum(x^2)/D + eps)) * w[d]          (:2910, :2915)
+//   RoPE      angle = float(pos) * theta[i];                    (:3065-3073)
+//             (v0, v1) -> (v0*c - v1*s, v0*s + v1*c)
+//             half-split pairs (i, i+rope_dim/2), or interleaved (2i, 2i+1)
+//             as in tensor.nim:156-166; dims >= rope_dim pass through
+//   theta[i]  powf(1/base, 2i/rope_dim) on the host (:3850-3861), passed to
+//             the kernel by value.
+#include "common.h"
+#include "launch.h"
+
+namespace hl {
+
+__device__ __forceinline__ void rope_pair_index(int i, int half, int style, int& i0, int& i1) {
+  if (style == HL_ROPE_HALF_SPLIT) {
+    i0 = i;
+    i1 = i + half;
+  } else {
+    i0 = 2 * i;
+    i1 = 2 * i + 1;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Decode side: one wave per head vector of the new token.
+// blockIdx.x in [0, Hq): q heads; [Hq, Hq+Hkv): k heads; [Hq+Hkv, Hq+2Hkv): v.
+// ---------------------------------------------------------------------------
+template <int KDT>
+__global__ __launch_bounds__(64) void headvec_kernel(HeadVecOp op) {
+  __shared__ float sx[HL_MAX_HEAD_DIM];
+  const int lane = threadIdx.x;
+  const int b = blockIdx.y;
+  const int D = op.head_dim;
+  int hv = blockIdx.x;
+  int kind;  // 0 q, 1 k, 2 v
+  if (hv < op.n_head_q) {
+    kind = 0;
+  } else if (hv < op.n_head_q + op.n_head_kv) {
+    kind = 1;
+    hv -= op.n_head_q;
+  } else {
+    kind = 2;
+    hv -= op.n_head_q + op.n_head_kv;
+  }
+  float* x = nullptr;
+  const float* xin = nullptr;
+  const float* nw = nullptr;
+  int rope = 0;
+  void* cache = nullptr;
+  if (kind == 0) {
+    if (!op.q) return;
+    x = op.q + ((long long)b * op.n_head_q + hv) * D;
+    xin = x;
+    nw = op.q_norm_w;
+    rope = op.rope_q;
+  } else if (kind == 1) {
+    if (!op.k) return;
+    x = op.k + ((long long)b * op.n_head_kv + hv) * D;
+    xin = x;
+    nw = op.k_norm_w;
+    rope = op.rope_k;
+    cache = op.k_cache;
+  } else {
+    if (!op.v) return;
+    xin = op.v + ((long long)b * op.n_head_kv + hv) * D;
+    cache = op.v_cache;
+  }
+
+  for (int d = lane; d < D; d += 64) sx[d] = xin[d];
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+  if (nw) {
+    float ss = 0.f;
+    for (int d = lane; d < D; d += 64) ss += sx[d] * sx[d];
+    ss = wave_sum(ss);
+    const float inv = 1.0f / sqrtf(ss / (float)D + op.eps);
+    for (int d = lane; d < D; d += 64) sx[d] = sx[d] * inv * nw[d];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+  if (rope && op.do_rope) {
+    const int pos = op.positions ? op.positions[b] : op.pos;
+    const int half = op.rope_dim / 2;
+    for (int i = lane; i < half; i += 64) {
+      int i0, i1;
+      rope_pair_index(i, half, op.rope_style, i0, i1);
+      const float angle = (float)pos * op.theta.t[i];
+      const float c = cosf(angle), s = sinf(angle);
+      const float v0 = sx[i0], v1 = sx[i1];
+      sx[i0] = v0 * c - v1 * s;
+      sx[i1] = v0 * s + v1 * c;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+  if (x && (nw || (rope && op.do_rope)))
+    for (int d = lane; d < D; d += 64) x[d] = sx[d];
+  if (cache) {
+    const int pos = op.positions ? op.positions[b] : op.pos;
+    const long long base = (long long)b * op.batch_stride + (long long)hv * D * op.max_len + pos;
+    for (int d = lane; d < D; d += 64) store_elem<KDT>(cache, base + (long long)d * op.max_len, sx[d]);
+  }
+}
+
+hipError_t headvec_launch(const HeadVecOp& op, hipStream_t stream) {
+  dim3 grid(op.n_head_q + 2 * op.n_head_kv, op.batch);
+  switch (op.kv_dtype) {
+    case HL_F32: hipLaunchKernelGGL(headvec_kernel<HL_F32>, grid, dim3(64), 0, stream, op); break;
+    case HL_F16: hipLaunchKernelGGL(headvec_kernel<HL_F16>, grid, dim3(64), 0, stream, op); break;
+    default: hipLaunchKernelGGL(headvec_kernel<HL_BF16>, grid, dim3(64), 0, stream, op); break;
+  }
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Prefill side: one workgroup per (head vector, 32-token tile) of col-major
+// [H*D, T] activations.  blockIdx.y: q heads, then k heads, then v heads.
+// ---------------------------------------------------------------------------
+constexpr int kPT = 32;  // tokens per tile (LDS tile [256][33] floats = 33 KB)
+
+template <int IODT, int KDT>
+__global__ __launch_bounds__(256) void prologue_kernel(PrologueOp op) {
+  __shared__ float sx[HL_MAX_HEAD_DIM][kPT + 1];
+  __shared__ float sred[8][kPT];
+  __shared__ float sinv[kPT];
+  const int tid = threadIdx.x;
+  const int T = op.seq_len, D = op.head_dim;
+  const int t0 = blockIdx.x * kPT;
+  int hv = blockIdx.y;
+  int kind;
+  if (hv < op.n_head) {
+    kind = 0;
+  } else if (hv < op.n_head + op.n_head_kv) {
+    kind = 1;
+    hv -= op.n_head;
+  } else {
+    kind = 2;
+    hv -= op.n_head + op.n_head_kv;
+  }
+  const void* src = kind == 0 ? op.q : (kind == 1 ? op.k : op.v);
+  if (!src) return;
+  const float* nw = kind == 0 ? op.q_norm_w : (kind == 1 ? op.k_norm_w : nullptr);
+  const bool rope = op.do_rope && kind < 2;
+  const long long hbase = (long long)hv * D * T;
+
+  // load the [D, 32] tile (coalesced along tokens)
+  const int tc = tid & (kPT - 1), part = tid / kPT;  // 8 parts
+  const int t = t0 + tc;
+  for (int d = part; d < D; d += 8)
+    sx[d][tc] = (t < T) ? load_elem<IODT>(src, hbase + (long long)d * T + t) : 0.f;
+  __syncthreads();
+
+  if (nw) {
+    float ss = 0.f;
+    for (int d = part; d < D; d += 8) ss += sx[d][tc] * sx[d][tc];
+    sred[part][tc] = ss;
+    __syncthreads();
+    if (part == 0) {
+      float tot = 0.f;
+      for (int q = 0; q < 8; ++q) tot += sred[q][tc];
+      sinv[tc] = 1.0f / sqrtf(tot / (float)D + op.eps);
+    }
+    __syncthreads();
+    const float inv = sinv[tc];
+    for (int d = part; d < D; d += 8) sx[d][tc] = sx[d][tc] * inv * nw[d];
+    __syncthreads();
+  }
+  if (rope) {
+    const int half = op.rope_dim / 2;
+    const float pos = (float)(op.start_pos + t);
+    for (int i = part; i < half; i += 8) {
+      int i0, i1;
+      rope_pair_index(i, half, op.rope_style, i0, i1);
+      const float angle = pos * op.theta.t[i];
+      const float c = cosf(angle), s = sinf(angle);
+      const float v0 = sx[i0][tc], v1 = sx[i1][tc];
+      sx[i0][tc] = v0 * c - v1 * s;
+      sx[i1][tc] = v0 * s + v1 * c;
+    }
+    __syncthreads();
+  }
+
+  // fp32 write-back in place (the reference's in-place semantics)
+  float* inplace = kind == 0 ? op.q_inplace : (kind == 1 ? op.k_inplace : nullptr);
+  if (inplace && t < T)
+    for (int d = part; d < D; d += 8) inplace[hbase + (long long)d * T + t] = sx[d][tc];
+
+  // KV-cache write, columns start_pos + t
+  void* cache = kind == 1 ? op.k_cache : (kind == 2 ? op.v_cache : nullptr);
+  if (cache && t < T) {
+    const long long cb = (long long)hv * D * op.max_len + op.start_pos + t;
+    for (int d = part; d < D; d += 8) store_elem<KDT>(cache, cb + (long long)d * op.max_len, sx[d][tc]);
+  }
+
+  // MFMA operand layouts (fp16 bits), pad rows t >= T written as zeros
+  if (kind < 2) {
+    uint16_t* dst = kind == 0 ? op.qt : op.kt;
+    if (dst) {
+      const float mul = kind == 0 ? op.qt_scale : 1.0f;
+      const int chunks = D / 8;
+      for (int idx = tid; idx < kPT * chunks; idx += 256) {
+        const int tt = idx / chunks, ch = idx % chunks;
+        const int tg = t0 + tt;
+        if (tg >= op.t_pad) continue;
+        u16x8 w;
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          w[e] = tg < T ? f32_to_f16_bits(sx[8 * ch + e][tt] * mul) : (uint16_t)0;
+        *(u16x8*)(dst + ((long long)hv * op.t_pad + tg) * D + 8 * ch) = w;
+      }
+    }
+  } else if (op.vt) {
+    const int tp = t0 + tc;
+    if (tp < op.t_pad)
+      for (int d = part; d < D; d += 8)
+        op.vt[((long long)hv * D + d) * op.t_pad + tp] = tp < T ? f32_to_f16_bits(sx[d][tc]) : 0;
+  }
+}
+
+hipError_t prologue_launch(const PrologueOp& op, hipStream_t stream) {
+  const int cols = op.t_pad > op.seq_len ? op.t_pad : op.seq_len;
+  dim3 grid((cols + kPT - 1) / kPT, op.n_head + 2 * op.n_head_kv);
+#define HL_PRO(IO, KD) hipLaunchKernelGGL((prologue_kernel<IO, KD>), grid, dim3(256), 0, stream, op)
+#define HL_PRO_IO(IO)                      \
+  switch (op.kv_dtype) {                   \
+    case HL_F32: HL_PRO(IO, HL_F32); break; \
+    case HL_F16: HL_PRO(IO, HL_F16); break; \
+    default: HL_PRO(IO, HL_BF16); break;    \
+  }
+  switch (op.io_dtype) {
+    case HL_F32: HL_PRO_IO(HL_F32); break;
+    case HL_F16: HL_PRO_IO(HL_F16); break;
+    default: HL_PRO_IO(HL_BF16); break;
+  }
+#undef HL_PRO_IO
+#undef HL_PRO
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// storeKV / storeKVPair: [rows, src_cols] fp32 -> cache columns start_pos..
+// ---------------------------------------------------------------------------
+template <int KDT>
+__global__ __launch_bounds__(256) void store_cols_kernel(void* cache, const float* src, void* cache2,
+                                                         const float* src2, int rows, int src_cols,
+                                                         int cache_cols, int start_pos) {
+  const long long total = (long long)rows * src_cols;
+  long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
+  const bool second = idx >= total;
+  if (second) {
+    if (!src2) return;
+    idx -= total;
+    if (idx >= total) return;
+  }
+  const int r = (int)(idx / src_cols), c = (int)(idx % src_cols);
+  const float v = (second ? src2 : src)[idx];
+  store_elem<KDT>(second ? cache2 : cache, (long long)r * cache_cols + start_pos + c, v);
+}
+
+hipError_t store_cols_launch(void* cache, const float* src, void* cache2, const float* src2,
+                             int rows, int src_cols, int cache_cols, int start_pos, int kv_dtype,
+                             hipStream_t stream) {
+  const long long total = (long long)rows * src_cols * (src2 ? 2 : 1);
+  dim3 grid((unsigned)((total + 255) / 256));
+  switch (kv_dtype) {
+    case HL_F32:
+      hipLaunchKernelGGL(store_cols_kernel<HL_F32>, grid, dim3(256), 0, stream, cache, src, cache2,
+                         src2, rows, src_cols, cache_cols, start_pos);
+      break;
+    case HL_F16:
+      hipLaunchKernelGGL(store_cols_kernel<HL_F16>, grid, dim3(256), 0, stream, cache, src, cache2,
+                         src2, rows, src_cols, cache_cols, start_pos);
+      break;
+    default:
+      hipLaunchKernelGGL(store_cols_kernel<HL_BF16>, grid, dim3(256), 0, stream, cache, src, cache2,
+                         src2, rows, src_cols, cache_cols, start_pos);
+      break;
+  }
+  return hipGetLastError();
+}
+
+template <int KDT>
+__global__ __launch_bounds__(256) void cache_to_f32_kernel(float* dst, const void* cache, int rows,
+                                                           int max_len, int col0, int ncols) {
+  const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (long long)rows * ncols) return;
+  const int r = (int)(idx / ncols), c = (int)(idx % ncols);
+  dst[idx] = load_elem<KDT>(cache, (long long)r * max_len + col0 + c);
+}
+
+hipError_t cache_to_f32_launch(float* dst, const void* cache, int kv_dtype, int rows, int max_len,
+                               int col0, int ncols, hipStream_t stream) {
+  dim3 grid((unsigned)(((long long)rows * ncols + 255) / 256));
+  switch (kv_dtype) {
+    case HL_F32:
+      hipLaunchKernelGGL(cache_to_f32_kernel<HL_F32>, grid, dim3(256), 0, stream, dst, cache, rows,
+                         max_len, col0, ncols);
+      break;
+    case HL_F16:
+      hipLaunchKernelGGL(cache_to_f32_kernel<HL_F16>, grid, dim3(256), 0, stream, dst, cache, rows,
+                         max_len, col0, ncols);
+      break;
+    default:
+      hipLaunchKernelGGL(cache_to_f32_kernel<HL_BF16>, grid, dim3(256), 0, stream, dst, cache, rows,
+                         max_len, col0, ncols);
+      break;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace hl

@@ -1,0 +1,282 @@
+/*
+ * hl_attn.h — C ABI of the MI355X (gfx950) attention stage for HippoLeap.
+ *
+ * The library (libhl_attn.so) replaces the attention sub-sequence of the
+ * reference's naive backend: per-head RMSNorm (qkNorm) -> RoPE -> KV-cache
+ * store -> attention.  Reference files are cited relative to the
+ * monofuel/hippo_leap repository root.
+ *
+ * Conventions shared by every entry point
+ *  - Plain pointers and sizes only; `stream` is a hipStream_t passed as void*
+ *    (NULL = the null stream).  All work is enqueued asynchronously on that
+ *    stream; nothing synchronises, nothing allocates device memory except
+ *    hl_gpu_attention_decode's library-owned split-K workspace (grown once).
+ *  - The caller owns every device buffer (naive.nim:171-182).
+ *  - Return value: HL_OK (0) or a negative HL_E* code.  hl_last_error()
+ *    returns a thread-local message for the last failing call, mirroring the
+ *    reference's `raise newException(ValueError, msg)` (naive.nim:3969-3976,
+ *    4594-4599).
+ *  - Layouts follow the reference ("ggml column-major"): a `[R, C]` tensor
+ *    stores element (r, c) at r*C + c, so the column index (token / cache
+ *    position) is fastest.
+ *      decode vectors q/k/v/out : [B][H*D]           (naive.nim:4697-4717)
+ *      prefill activations      : [H*D, T]           (naive.nim:4064-4078)
+ *      KV cache (one layer)     : [Hkv*D, max_len]   (naive.nim:3565-3567)
+ *    For B > 1, sequence b's cache starts cache_batch_stride elements after
+ *    sequence b-1's (0 = dense: Hkv*D*max_len).
+ */
+#ifndef HL_ATTN_H
+#define HL_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ------------------------------------------------------ */
+enum {
+  HL_OK = 0,
+  HL_EINVAL = -1,        /* bad shape / pointer / GQA divisibility          */
+  HL_ECAPACITY = -2,     /* KV cache full, prefill longer than max_len      */
+  HL_EUNSUPPORTED = -3,  /* dtype / head_dim combination not built          */
+  HL_EHIP = -4           /* HIP runtime error (launch, device query)         */
+};
+
+/* ---- element types of activations and KV cache ------------------------- */
+enum { HL_F32 = 0, HL_F16 = 1, HL_BF16 = 2 };
+
+/* ---- RoPE pairing ------------------------------------------------------- */
+enum {
+  HL_ROPE_HALF_SPLIT = 0,  /* pairs (i, i+rope_dim/2): every GPU kernel of the
+                              reference (naive.nim:3020-3030, 3066-3073)     */
+  HL_ROPE_INTERLEAVED = 1  /* pairs (2i, 2i+1): tensor.nim:141-166           */
+};
+
+#define HL_MAX_HEAD_DIM 256
+#define HL_MAX_ROPE_DIM 256
+
+/* ------------------------------------------------------------------------ */
+/* Library state and diagnostics                                             */
+/* ------------------------------------------------------------------------ */
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* hl_last_error(void);
+
+/* ABI version: bumped when a struct below changes. */
+int hl_abi_version(void);
+
+typedef struct hl_device_info {
+  int device;
+  int cu_count;
+  int clock_khz;             /* peak engine clock                         */
+  int mem_clock_khz;
+  int l2_bytes;
+  size_t hbm_bytes;
+  double hbm_peak_gbs;       /* published MI355X HBM3E peak (8000 GB/s)   */
+  double bf16_dense_tflops;  /* CUs x clk x 4096 flop/clk/CU (dense MFMA) */
+  double fp32_tflops;        /* published vector fp32 peak                */
+  char arch[64];             /* e.g. "gfx950:sramecc+:xnack-"             */
+} hl_device_info;
+
+/* Fills *info for the current HIP device.  Replaces nothing in the
+ * reference (which has no roofline reporting); used by the benchmark.     */
+int hl_device_info_get(hl_device_info* info);
+
+/* Host-side RoPE theta table: theta[i] = powf(1/base, 2i/rope_dim) for
+ * i < rope_dim/2, computed in fp32 exactly as naive.nim:3850-3861.       */
+int hl_rope_theta_table(float* theta_out, int rope_dim, float rope_base);
+
+/* Installs the process-wide theta table used by the entry points that, in
+ * the reference, read modelPtrs.ropeTheta (gpuRopeQKDecode,
+ * gpuRopeAtPosTheta, gpuFusedRopeStoreKV).  Mirrors the table build inside
+ * ensureModelGpuPtrs / loadModelBackend (naive.nim:3850-3861, 3956-3958).
+ * The table travels to the GPU as a kernel argument: no device memory.   */
+int hl_set_rope_theta(int rope_dim, float rope_base);
+
+/* ------------------------------------------------------------------------ */
+/* Drop-ins with the reference's exact call contract (fp32, one sequence).   */
+/* Argument order and meaning follow the Nim procs cited on each line.       */
+/* ------------------------------------------------------------------------ */
+
+/* gpuQkNorm (naive.nim:2918-2926): per-head RMSNorm of x[nHead*headDim] in
+ * place, x * (1/sqrtf(sum(x^2)/headDim + eps)) * w[d].                     */
+int hl_gpu_qk_norm(float* x, const float* weight, int n_head, int head_dim,
+                   float eps, void* stream);
+
+/* gpuQkNormPrefill (naive.nim:2962-2971): same on col-major [nHead*headDim,
+ * seqLen], one normalisation per (head, column).                          */
+int hl_gpu_qk_norm_prefill(float* x, const float* weight, int n_head,
+                           int head_dim, int seq_len, float eps, void* stream);
+
+/* gpuRopeAtPos (naive.nim:3088-3101): half-split RoPE in place.  seq_len==1:
+ * x is [nHead*headDim] at position `pos`; seq_len>1: x is col-major
+ * [nHead*headDim, seqLen] and column p is rotated at position p (the
+ * reference ignores `pos` there, naive.nim:3036-3037).  Theta is
+ * powf(1/ropeBase, 2i/ropeDim) evaluated on the host.                      */
+int hl_gpu_rope_at_pos(float* x, int n_head, int head_dim, int rope_dim,
+                       float rope_base, int pos, int seq_len, void* stream);
+
+/* gpuRopeAtPosTheta (naive.nim:3133-3144): as above with the installed theta
+ * table; for seq_len>1 column p is rotated at position pos+p.              */
+int hl_gpu_rope_at_pos_theta(float* x, int n_head, int head_dim, int rope_dim,
+                             int pos, int seq_len, void* stream);
+
+/* gpuRopeQKDecode (naive.nim:3075-3086): RoPE of q[nHeadQ*headDim] and
+ * k[nHeadK*headDim] at `pos` in one launch with the installed theta table
+ * (the reference ignores ropeBase; so does this entry point when a table is
+ * installed, otherwise the table is built from rope_base).               */
+int hl_gpu_rope_qk_decode(float* q, float* k, int n_head_q, int n_head_k,
+                          int head_dim, int rope_dim, float rope_base, int pos,
+                          void* stream);
+
+/* gpuFusedRopeStoreKV (naive.nim:3203-3223): RoPE q,k at `pos` in place,
+ * then write rotated k and v into column `pos` of the fp32 caches
+ * [kvDim, cacheCols]; dims >= ropeDim of k are copied unrotated.          */
+int hl_gpu_fused_rope_store_kv(float* q, float* k, const float* v,
+                               float* k_cache, float* v_cache, int n_head_q,
+                               int n_head_k, int head_dim, int rope_dim,
+                               int kv_dim, int cache_cols, int pos,
+                               void* stream);
+
+/* gpuStoreKV (naive.nim:3241-3253): cache[r*cacheCols + startPos + c] =
+ * src[r*srcCols + c] for r < rows, c < srcCols.                          */
+int hl_gpu_store_kv(float* cache, const float* src, int rows, int src_cols,
+                    int cache_cols, int start_pos, void* stream);
+
+/* gpuStoreKVPair (naive.nim:3273-3285): gpuStoreKV of K and V in one launch. */
+int hl_gpu_store_kv_pair(float* k_cache, const float* k_src, float* v_cache,
+                         const float* v_src, int rows, int src_cols,
+                         int cache_cols, int start_pos, void* stream);
+
+/* gpuAttentionDecode (naive.nim:3369-3383): dst[nHead*headDim] =
+ * softmax(q_h . K^T / sqrt(headDim)) . V over cache columns [0, curLen) of
+ * the fp32 caches [nHeadKv*headDim, cacheCols], kv head = h / (nHead /
+ * nHeadKv).  Split-K over the context with a library-owned workspace.     */
+int hl_gpu_attention_decode(float* dst, const float* q, const float* k_cache,
+                            const float* v_cache, int n_head, int n_head_kv,
+                            int head_dim, int cur_len, int cache_cols,
+                            void* stream);
+
+/* gpuAttentionPrefill (naive.nim:3450-3464): causal attention over the
+ * col-major fp32 projections q[nHead*headDim, seqLen], k/v[nHeadKv*headDim,
+ * seqLen]; dst is col-major [nHead*headDim, seqLen].  No 4096-token cap.  */
+int hl_gpu_attention_prefill(float* dst, const float* q, const float* k,
+                             const float* v, int n_head, int n_head_kv,
+                             int head_dim, int seq_len, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Batched / typed API (extends the reference: B sequences, fp16/bf16 KV)   */
+/* ------------------------------------------------------------------------ */
+
+typedef struct hl_decode_args {
+  int batch;                    /* B >= 1                                        */
+  int n_head;                   /* Hq                                            */
+  int n_head_kv;                /* Hkv, Hq % Hkv == 0                             */
+  int head_dim;                 /* D                                             */
+  int kv_dtype;                 /* HL_F32 | HL_F16 | HL_BF16                      */
+  int max_len;                  /* cache columns (cacheCols)                     */
+  int seq_len;                  /* attention length L = pos+1 (max over B when
+                                   seq_lens is given)                           */
+  const int* seq_lens;          /* optional device int[B] of per-sequence L       */
+  long long cache_batch_stride; /* elements between sequences (0 = dense)        */
+  const float* q;               /* device [B][Hq*D] fp32                         */
+  const void* k_cache;          /* device [B][Hkv*D, max_len] kv_dtype           */
+  const void* v_cache;
+  float* out;                   /* device [B][Hq*D] fp32                         */
+  float scale;                  /* 0 -> 1/sqrtf(D) (naive.nim:3374)              */
+  int num_splits;               /* 0 -> chosen to fill the GPU                   */
+} hl_decode_args;
+
+/* Workspace bytes hl_attn_decode needs for these args (split-K partials:
+ * running max, sum and D accumulators per split per query head).        */
+size_t hl_attn_decode_workspace_bytes(const hl_decode_args* a);
+
+/* Decode attention for B sequences (the batched form of
+ * gpuAttentionDecode, naive.nim:3369-3383).  `workspace` is device memory
+ * of at least hl_attn_decode_workspace_bytes(a) bytes (in HippoLeap:
+ * GpuContext.attnScratch, backend_types.nim:125-126).                    */
+int hl_attn_decode(const hl_decode_args* a, void* workspace, size_t ws_bytes,
+                   void* stream);
+
+typedef struct hl_rope_store_args {
+  int batch, n_head_q, n_head_kv, head_dim;
+  int rope_dim;                 /* 0 -> head_dim; dims >= rope_dim pass through */
+  int rope_style;               /* HL_ROPE_HALF_SPLIT | HL_ROPE_INTERLEAVED      */
+  float rope_base;              /* theta base, used when use_installed_theta==0  */
+  int use_installed_theta;      /* 1 -> table from hl_set_rope_theta            */
+  int kv_dtype, max_len;
+  long long cache_batch_stride; /* 0 = dense                                     */
+  float* q;                     /* device [B][Hq*D] fp32, rotated in place       */
+  float* k;                     /* device [B][Hkv*D] fp32, normed+rotated in place*/
+  const float* v;               /* device [B][Hkv*D] fp32                        */
+  void* k_cache;                /* device [B][Hkv*D, max_len]                   */
+  void* v_cache;
+  const int* positions;         /* optional device int[B]; else `pos` for all   */
+  int pos;
+  const float* q_norm_w;        /* optional device [D]: qkNorm before RoPE       */
+  const float* k_norm_w;        /* optional device [D]                           */
+  float eps;
+} hl_rope_store_args;
+
+/* One launch for the new token of B sequences: optional qkNorm of q and k
+ * (naive.nim:4697-4700), RoPE at the position (naive.nim:3046-3073), and
+ * the write of k and v into cache column `pos` in kv_dtype with
+ * round-to-nearest-even (the drop-in for gpuQkNorm + gpuFusedRopeStoreKV,
+ * naive.nim:2918-2926, 3149-3223).  Fails with HL_ECAPACITY when a
+ * position is >= max_len (the "KV cache full" check, naive.nim:4598-4599,
+ * for the host `pos`; device positions are not inspected).               */
+int hl_rope_store_decode(const hl_rope_store_args* a, void* stream);
+
+typedef struct hl_prefill_args {
+  int n_head, n_head_kv, head_dim, seq_len;
+  int io_dtype;                 /* dtype of q/k/v/out: HL_F32|HL_F16|HL_BF16     */
+  const void* q;                /* device col-major [Hq*D, T]                    */
+  const void* k;                /* device col-major [Hkv*D, T]                   */
+  const void* v;
+  void* out;                    /* device col-major [Hq*D, T] out_dtype          */
+  /* fused before attention (naive.nim:4067-4076)                              */
+  const float* q_norm_w;        /* optional [D] (qkNorm, Qwen3)                  */
+  const float* k_norm_w;
+  float eps;
+  int apply_rope;               /* 1 -> RoPE of q and k at positions start_pos+p */
+  int rope_dim;                 /* 0 -> head_dim                                 */
+  int rope_style;
+  float rope_base;
+  int use_installed_theta;
+  /* fused KV-cache write (naive.nim:4075-4076); k_cache == NULL skips it      */
+  void* k_cache;
+  void* v_cache;
+  int kv_dtype;
+  int max_len;
+  int start_pos;
+  float scale;                  /* 0 -> 1/sqrtf(D)                               */
+  int write_back_qk;            /* 1 (fp32 only): leave normed+roped q,k in the
+                                   q/k buffers, as the reference's in-place ops do*/
+  int out_dtype;                /* dtype of `out`: HL_F32 (default, the
+                                   reference's fp32 act1) or, for fp16/bf16
+                                   io, HL_F16 / HL_BF16 (RNE of the fp32 value) */
+} hl_prefill_args;
+
+size_t hl_attn_prefill_workspace_bytes(const hl_prefill_args* a);
+
+/* Causal prefill with the pre-attention ops fused: qkNorm -> RoPE -> KV
+ * cache write -> flash attention (bf16/fp16: MFMA; fp32: vector ALU).
+ * Replaces naive.nim:4067-4078 for one attention layer.  Errors:
+ * HL_EINVAL for shapes / GQA, HL_ECAPACITY for start_pos+T > max_len
+ * (naive.nim:3975-3976).                                                  */
+int hl_attn_prefill(const hl_prefill_args* a, void* workspace, size_t ws_bytes,
+                    void* stream);
+
+/* Reads cache columns [col0, col0+ncols) of a [rows, max_len] cache of
+ * kv_dtype into fp32 dst[rows, ncols] (exact upcast; halfToFloat semantics,
+ * quant.nim:78-96).  Debug / host-mirror helper (KvCache.k, types:41-49). */
+int hl_kv_cache_to_f32(float* dst, const void* cache, int kv_dtype, int rows,
+                       int max_len, int col0, int ncols, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HL_ATTN_H */

@@ -1,0 +1,371 @@
+/*
+ * hl_oracle.c — CPU restatement of the reference's attention-stage math.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This file is the checker for the HIP kernels:
+ * only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg load
+ * it.  The product library never links or calls it.
+ *
+ * Sources restated (monofuel/hippo_leap, paths relative to src/hippo_leap):
+ *   tensor.nim:63-81    matmul        i -> j -> p loop, fp32 accumulator
+ *   tensor.nim:83-100   rmsnorm       ss sum, inv = 1/sqrt(ss/dim + eps)
+ *   tensor.nim:102-118  rmsnormCols   same per column of a col-major tensor
+ *   tensor.nim:120-139  softmaxLastDim  max from element 0, exp, sum, *1/sum
+ *   tensor.nim:141-166  ropeInplace   interleaved pairs (2i, 2i+1)
+ *   tensor.nim:42-54    add / mul     scale and mask glue
+ *   quant.nim:78-96     halfToFloat   exact IEEE half decode
+ *   quant.nim:98-107    floatToHalf   truncating, flush-to-zero (not used for
+ *                                     caches; kept to document the difference)
+ * and the semantics tensor.nim leaves to the GPU backend (backends/naive.nim):
+ *   :3307-3308, 3400-3401  GQA mapping kvh = h / (Hq/Hkv)
+ *   :3328, 3374            score = dot * (1/sqrtf(D)), scale after the dot
+ *   :3403                  causal extent j <= i
+ *   :3020-3030, 3066-3073  half-split RoPE (i, i+ropeDim/2); dims >= ropeDim pass
+ *   :3850-3861             theta table powf(1/base, 2i/ropeDim) in fp32
+ *   :3565-3567, 3239       cache layout [kvDim, maxLen], column = position
+ *   :4066-4074             qkNorm before RoPE
+ *
+ * Every routine is single-threaded scalar fp32 code (built -O2, no
+ * fast-math), like the reference's CPU path.  fp16/bf16 inputs enter as
+ * their stored bits and are upcast exactly.
+ *
+ * Pinning status (what checks each function; see tests/test_oracle.py):
+ *   matmul, softmax, rmsnorm(+Cols), rope (both styles), theta table,
+ *   attention decode/prefill: fp64 brute force + closed forms + torch
+ *   scaled_dot_product_attention (fp64) through the golden fixtures.
+ *   halfToFloat: the reference KAT tests/test_quant.nim:5-15.
+ *   f32->f16/bf16 RNE: numpy / torch conversions (exhaustive over a sweep).
+ *   Device transcendental functions of the reference (hippo's expf, powf,
+ *   cosf, sinf) are not pinned by any reference test: parity unpinned at
+ *   that boundary; tolerance-based only.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#define ORC_F32 0
+#define ORC_F16 1
+#define ORC_BF16 2
+
+/* ---------------------------------------------------------------------- */
+/* Seeded input generator (shared by tests, fixtures and the CPU baseline) */
+/* ---------------------------------------------------------------------- */
+
+static uint64_t splitmix64(uint64_t x) {
+  x += 0x9E3779B97F4A7C15ull;
+  x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
+  x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
+  return x ^ (x >> 31);
+}
+
+/* uniform in [0,1) with 24 random bits, counter-based on (seed, i) */
+static double u01(uint64_t seed, uint64_t i) {
+  uint64_t r = splitmix64(seed * 0x100000001B3ull ^ splitmix64(i));
+  return (double)(r >> 40) * (1.0 / 16777216.0);
+}
+
+void orc_fill_uniform(float* out, int64_t n, uint64_t seed, float lo, float hi) {
+  for (int64_t i = 0; i < n; ++i)
+    out[i] = (float)(lo + (hi - lo) * u01(seed, (uint64_t)i));
+}
+
+/* Box-Muller on counter pairs: element i uses counters (2*(i/2), +1). */
+void orc_fill_normal(float* out, int64_t n, uint64_t seed, float mean, float std) {
+  for (int64_t i = 0; i < n; ++i) {
+    uint64_t c = (uint64_t)(i & ~(int64_t)1);
+    double u1 = u01(seed, c) + (1.0 / 33554432.0); /* (0,1] */
+    double u2 = u01(seed, c + 1);
+    double r = sqrt(-2.0 * log(u1));
+    double z = (i & 1) ? r * sin(6.283185307179586 * u2) : r * cos(6.283185307179586 * u2);
+    out[i] = (float)(mean + std * z);
+  }
+}
+
+/* ---------------------------------------------------------------------- */
+/* Storage-type conversions                                               */
+/* ---------------------------------------------------------------------- */
+
+static uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+static float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+
+/* quant.nim:78-96 halfToFloat: exact decode, written from its branches. */
+float orc_half_to_float(uint16_t h) {
+  uint32_t s = (h >> 15) & 1u, e = (h >> 10) & 0x1Fu, f = h & 0x3FFu;
+  if (e == 0) {
+    if (f == 0) return s ? -0.0f : 0.0f;
+    return (s ? -1.0f : 1.0f) * powf(2.0f, -14.0f) * ((float)f / 1024.0f);
+  } else if (e == 31) {
+    if (f == 0) return s ? -INFINITY : INFINITY;
+    return NAN;
+  }
+  float mant = 1.0f + (float)f / 1024.0f;
+  return (s ? -1.0f : 1.0f) * mant * powf(2.0f, (float)((int)e - 15));
+}
+
+/* quant.nim:98-107 floatToHalf: truncates the mantissa and flushes |x| <
+ * 2^-14 to signed zero.  Documented only; caches use orc_float_to_half_rne. */
+uint16_t orc_float_to_half_trunc(float f) {
+  uint32_t bits = f2u(f);
+  uint16_t s = (uint16_t)((bits >> 16) & 0x8000u);
+  int e = (int)((bits >> 23) & 0xFFu) - 127;
+  uint32_t m = bits & 0x7FFFFFu;
+  if (e <= -15) return s;
+  if (e > 15) return s | 0x7C00u;
+  return s | (uint16_t)((e + 15) << 10) | (uint16_t)(m >> 13);
+}
+
+/* IEEE binary16 round-to-nearest-even with subnormals, inf and NaN. */
+uint16_t orc_float_to_half_rne(float f) {
+  uint32_t x = f2u(f);
+  uint16_t sign = (uint16_t)((x >> 16) & 0x8000u);
+  uint32_t ax = x & 0x7FFFFFFFu;
+  if (ax >= 0x7F800000u) /* inf / nan */
+    return sign | (ax > 0x7F800000u ? 0x7E00u : 0x7C00u);
+  if (ax >= 0x477FF000u) return sign | 0x7C00u; /* rounds to >= 65520 -> inf */
+  if (ax < 0x38800000u) { /* below 2^-14: subnormal or zero */
+    /* value = ax as float; half subnormal unit = 2^-24 */
+    float a = u2f(ax);
+    float scaled = a * 16777216.0f; /* exact: multiply by 2^24 */
+    /* round half to even in integer units */
+    float r = nearbyintf(scaled);  /* default rounding mode is RNE */
+    return sign | (uint16_t)r;
+  }
+  uint32_t mant = ax & 0x7FFFFFu;
+  int e = (int)(ax >> 23) - 127 + 15;
+  uint32_t h = ((uint32_t)e << 10) | (mant >> 13);
+  uint32_t rem = mant & 0x1FFFu;
+  if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) h += 1; /* may carry into exp */
+  return sign | (uint16_t)h;
+}
+
+float orc_bf16_to_float(uint16_t b) { return u2f((uint32_t)b << 16); }
+
+uint16_t orc_float_to_bf16_rne(float f) {
+  uint32_t x = f2u(f);
+  if ((x & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((x >> 16) | 0x40u); /* quiet NaN */
+  uint32_t lsb = (x >> 16) & 1u;
+  x += 0x7FFFu + lsb;
+  return (uint16_t)(x >> 16);
+}
+
+void orc_convert_from_f32(int dtype, const float* src, void* dst, int64_t n) {
+  if (dtype == ORC_F32) { memcpy(dst, src, (size_t)n * 4); return; }
+  uint16_t* d = (uint16_t*)dst;
+  for (int64_t i = 0; i < n; ++i)
+    d[i] = dtype == ORC_F16 ? orc_float_to_half_rne(src[i]) : orc_float_to_bf16_rne(src[i]);
+}
+
+void orc_upcast_to_f32(int dtype, const void* src, float* dst, int64_t n) {
+  if (dtype == ORC_F32) { memcpy(dst, src, (size_t)n * 4); return; }
+  const uint16_t* s = (const uint16_t*)src;
+  for (int64_t i = 0; i < n; ++i)
+    dst[i] = dtype == ORC_F16 ? orc_half_to_float(s[i]) : orc_bf16_to_float(s[i]);
+}
+
+/* ---------------------------------------------------------------------- */
+/* tensor.nim restatements                                                */
+/* ---------------------------------------------------------------------- */
+
+/* tensor.nim:63-81: c[m,n] = a[m,k] * b[k,n], row-major, loop i, j, p. */
+void orc_matmul(const float* a, const float* b, float* c, int m, int k, int n) {
+  for (int i = 0; i < m; ++i) {
+    const float* arow = a + (int64_t)i * k;
+    for (int j = 0; j < n; ++j) {
+      float acc = 0.0f;
+      for (int p = 0; p < k; ++p) acc += arow[p] * b[(int64_t)p * n + j];
+      c[(int64_t)i * n + j] = acc;
+    }
+  }
+}
+
+/* tensor.nim:120-139: softmax over the last dim, written to out. */
+void orc_softmax_last_dim(const float* x, float* out, int64_t outer, int dim) {
+  for (int64_t o = 0; o < outer; ++o) {
+    const float* xr = x + o * dim;
+    float* yr = out + o * dim;
+    float maxv = xr[0];
+    for (int i = 1; i < dim; ++i) maxv = fmaxf(maxv, xr[i]);
+    float sum = 0.0f;
+    for (int i = 0; i < dim; ++i) {
+      float v = expf(xr[i] - maxv);
+      yr[i] = v;
+      sum += v;
+    }
+    float inv = 1.0f / sum;
+    for (int i = 0; i < dim; ++i) yr[i] *= inv;
+  }
+}
+
+/* tensor.nim:83-100: RMSNorm of each length-dim row. */
+void orc_rmsnorm(const float* x, const float* w, float* out, int64_t outer, int dim, float eps) {
+  for (int64_t o = 0; o < outer; ++o) {
+    const float* xr = x + o * dim;
+    float ss = 0.0f;
+    for (int i = 0; i < dim; ++i) ss += xr[i] * xr[i];
+    float inv = 1.0f / sqrtf(ss / (float)dim + eps);
+    for (int i = 0; i < dim; ++i) out[o * dim + i] = xr[i] * inv * w[i];
+  }
+}
+
+/* tensor.nim:102-118: RMSNorm over rows for each column of [dim, seq]. */
+void orc_rmsnorm_cols(const float* x, const float* w, float* out, int dim, int seq, float eps) {
+  for (int s = 0; s < seq; ++s) {
+    float ss = 0.0f;
+    for (int r = 0; r < dim; ++r) { float v = x[(int64_t)r * seq + s]; ss += v * v; }
+    float inv = 1.0f / sqrtf(ss / (float)dim + eps);
+    for (int r = 0; r < dim; ++r)
+      out[(int64_t)r * seq + s] = x[(int64_t)r * seq + s] * inv * w[r];
+  }
+}
+
+/* tensor.nim:141-166: interleaved RoPE on [outer, seq, dim] row-major. */
+void orc_rope_inplace(float* x, int64_t outer, int seq, int dim, float base, int start_pos) {
+  float inv_base = 1.0f / base;
+  for (int64_t o = 0; o < outer; ++o)
+    for (int p = 0; p < seq; ++p) {
+      float pos = (float)(start_pos + p);
+      float* row = x + (o * seq + p) * dim;
+      for (int i = 0; i < dim / 2; ++i) {
+        float theta = powf(inv_base, (float)(2 * i) / (float)dim);
+        float angle = pos * theta;
+        float c = cosf(angle), s = sinf(angle);
+        float v0 = row[2 * i], v1 = row[2 * i + 1];
+        row[2 * i] = v0 * c - v1 * s;
+        row[2 * i + 1] = v0 * s + v1 * c;
+      }
+    }
+}
+
+/* ---------------------------------------------------------------------- */
+/* naive.nim semantics                                                    */
+/* ---------------------------------------------------------------------- */
+
+/* naive.nim:3850-3861: theta[i] = pow(1/base, 2i/ropeDim), fp32. */
+void orc_rope_theta_table(float* theta, int rope_dim, float base) {
+  for (int i = 0; i < rope_dim / 2; ++i)
+    theta[i] = powf(1.0f / base, (2.0f * (float)i) / (float)rope_dim);
+}
+
+/* One head vector x[head_dim] (stride `stride` between dims) rotated at
+ * `pos`.  style 0: half-split pairs (i, i+rope_dim/2) (naive.nim:3066-3073);
+ * style 1: interleaved (2i, 2i+1) (tensor.nim:156-166).  Dims >= rope_dim
+ * are untouched (naive.nim:3200-3201).  angle = float(pos) * theta[i].   */
+static void rope_vec(float* x, int64_t stride, int rope_dim, const float* theta, int pos, int style) {
+  int half = rope_dim / 2;
+  for (int i = 0; i < half; ++i) {
+    float angle = (float)pos * theta[i];
+    float c = cosf(angle), s = sinf(angle);
+    int64_t i0 = style == 0 ? i : 2 * i;
+    int64_t i1 = style == 0 ? i + half : 2 * i + 1;
+    float v0 = x[i0 * stride], v1 = x[i1 * stride];
+    x[i0 * stride] = v0 * c - v1 * s;
+    x[i1 * stride] = v0 * s + v1 * c;
+  }
+}
+
+/* Decode-side RoPE of x[n_head*head_dim] at pos (ropeQKDecodeKernel,
+ * naive.nim:3046-3073, for one of q / k). */
+void orc_rope_heads(float* x, int n_head, int head_dim, int rope_dim, const float* theta,
+                    int pos, int style) {
+  for (int h = 0; h < n_head; ++h) rope_vec(x + (int64_t)h * head_dim, 1, rope_dim, theta, pos, style);
+}
+
+/* Prefill-side RoPE of col-major x[n_head*head_dim, seq]: column p at
+ * position pos0 + p (ropeAtPosThetaKernel naive.nim:3116-3131; with pos0 = 0
+ * this is ropeAtPosKernel's prefill branch naive.nim:3031-3044). */
+void orc_rope_cols(float* x, int n_head, int head_dim, int seq, int rope_dim, const float* theta,
+                   int pos0, int style) {
+  for (int h = 0; h < n_head; ++h)
+    for (int p = 0; p < seq; ++p)
+      rope_vec(x + (int64_t)h * head_dim * seq + p, seq, rope_dim, theta, pos0 + p, style);
+}
+
+/* qkNormKernel (naive.nim:2887-2916): per-head RMSNorm in place; the
+ * formula is tensor.nim:92-100's. */
+void orc_qk_norm(float* x, const float* w, int n_head, int head_dim, float eps) {
+  orc_rmsnorm(x, w, x, n_head, head_dim, eps);
+}
+
+/* qkNormPrefillKernel (naive.nim:2928-2960): per (head, column) on
+ * col-major [n_head*head_dim, seq]. */
+void orc_qk_norm_cols(float* x, const float* w, int n_head, int head_dim, int seq, float eps) {
+  for (int h = 0; h < n_head; ++h) {
+    float* xh = x + (int64_t)h * head_dim * seq;
+    orc_rmsnorm_cols(xh, w, xh, head_dim, seq, eps);
+  }
+}
+
+/* storeKVKernel (naive.nim:3228-3239): cache[r*cols + start + c] = src[r*src_cols + c],
+ * written in the cache dtype with RNE. */
+void orc_store_kv(void* cache, int dtype, const float* src, int rows, int src_cols, int cache_cols,
+                  int start_pos) {
+  for (int r = 0; r < rows; ++r)
+    for (int c = 0; c < src_cols; ++c) {
+      int64_t di = (int64_t)r * cache_cols + start_pos + c;
+      float v = src[(int64_t)r * src_cols + c];
+      if (dtype == ORC_F32) ((float*)cache)[di] = v;
+      else if (dtype == ORC_F16) ((uint16_t*)cache)[di] = orc_float_to_half_rne(v);
+      else ((uint16_t*)cache)[di] = orc_float_to_bf16_rne(v);
+    }
+}
+
+/* Decode attention (attentionDecodeKernel's math, naive.nim:3292-3367,
+ * composed from tensor.nim ops): for each query head h,
+ *   scores[1,L] = matmul(q_h[1,D], K_kvh[D,L]) * scale      (tensor.nim:63-81, 49-54)
+ *   p = softmaxLastDim(scores)                              (tensor.nim:120-139)
+ *   o_h[1,D] = matmul(p[1,L], V_kvh^T[L,D])
+ * K_kvh / V_kvh are rows kvh*D .. kvh*D+D-1 of the fp32 caches
+ * [Hkv*D, max_len], columns 0..L-1.  `scores` is caller scratch [L]. */
+void orc_attention_decode(const float* q, const float* kc, const float* vc, float* out, int n_head,
+                          int n_head_kv, int head_dim, int L, int max_len, float scale,
+                          float* scores) {
+  int group = n_head / n_head_kv;
+  for (int h = 0; h < n_head; ++h) {
+    int kvh = h / group;
+    const float* qh = q + (int64_t)h * head_dim;
+    const float* K = kc + (int64_t)kvh * head_dim * max_len;
+    const float* V = vc + (int64_t)kvh * head_dim * max_len;
+    for (int j = 0; j < L; ++j) {
+      float acc = 0.0f;
+      for (int p = 0; p < head_dim; ++p) acc += qh[p] * K[(int64_t)p * max_len + j];
+      scores[j] = acc * scale;
+    }
+    orc_softmax_last_dim(scores, scores, 1, L);
+    for (int d = 0; d < head_dim; ++d) {
+      float acc = 0.0f;
+      for (int p = 0; p < L; ++p) acc += scores[p] * V[(int64_t)d * max_len + p];
+      out[(int64_t)h * head_dim + d] = acc;
+    }
+  }
+}
+
+/* Causal prefill attention (attentionPrefillKernel's math, naive.nim:3385-3447)
+ * over col-major Q[Hq*D, T], K/V[Hkv*D, T]; O col-major [Hq*D, T].  Row i of
+ * head h attends to j <= i.  Only heads [h0,h1) and rows r0, r0+rstep, ... < r1
+ * are written, so a test can check sampled rows of a large case.  `scores`
+ * is caller scratch [T]. */
+void orc_attention_prefill(const float* Q, const float* K, const float* V, float* O, int n_head,
+                           int n_head_kv, int head_dim, int T, float scale, int h0, int h1,
+                           int r0, int r1, int rstep, float* scores) {
+  int group = n_head / n_head_kv;
+  for (int h = h0; h < h1; ++h) {
+    int kvh = h / group;
+    const float* Qh = Q + (int64_t)h * head_dim * T;
+    const float* Kh = K + (int64_t)kvh * head_dim * T;
+    const float* Vh = V + (int64_t)kvh * head_dim * T;
+    for (int i = r0; i < r1; i += rstep) {
+      int n = i + 1;
+      for (int j = 0; j < n; ++j) {
+        float acc = 0.0f;
+        for (int p = 0; p < head_dim; ++p) acc += Qh[(int64_t)p * T + i] * Kh[(int64_t)p * T + j];
+        scores[j] = acc * scale;
+      }
+      orc_softmax_last_dim(scores, scores, 1, n);
+      for (int d = 0; d < head_dim; ++d) {
+        float acc = 0.0f;
+        for (int p = 0; p < n; ++p) acc += scores[p] * Vh[(int64_t)d * T + p];
+        O[((int64_t)h * head_dim + d) * T + i] = acc;
+      }
+    }
+  }
+}

@@ -1,0 +1,155 @@
+"""C-ABI checks that need no GPU: exports match include/hl_attn.h, and the
+argument validation that runs before any HIP call reproduces the reference's
+host prechecks (backends/naive.nim:3969-3976, 4594-4599) as status codes."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+from hippo_leap_amd import _lib
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include",
+                      "hl_attn.h")
+FAKE = 1 << 20  # a non-null, 16-byte aligned pointer value; validation never dereferences it
+
+
+def header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return set(re.findall(r"\b(hl_\w+)\s*\(", text))
+
+
+def test_exports_match_header(hl):
+    declared = header_functions()
+    assert declared == set(_lib.SIGNATURES), declared ^ set(_lib.SIGNATURES)
+    for name in declared:
+        assert hasattr(hl, name), name
+
+
+def test_abi_version(hl):
+    assert hl.hl_abi_version() == 1
+
+
+def _err(hl):
+    return hl.hl_last_error().decode()
+
+
+def _decode_args(**kw):
+    a = _lib.DecodeArgs()
+    a.batch, a.n_head, a.n_head_kv, a.head_dim = 1, 32, 8, 64
+    a.kv_dtype, a.max_len, a.seq_len = _lib.HL_F16, 2049, 2049
+    a.q = a.k_cache = a.v_cache = a.out = FAKE
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+def test_decode_gqa_divisibility(hl):
+    a = _decode_args(n_head=6, n_head_kv=4)
+    assert hl.hl_attn_decode(ctypes.byref(a), None, 0, None) == _lib.HL_EINVAL
+    assert _err(hl) == "GQA requires head_count divisible by head_count_kv"
+
+
+def test_decode_cache_full(hl):
+    a = _decode_args(seq_len=2050)
+    assert hl.hl_attn_decode(ctypes.byref(a), None, 0, None) == _lib.HL_ECAPACITY
+    assert _err(hl) == "KV cache full"
+    assert hl.hl_gpu_attention_decode(FAKE, FAKE, FAKE, FAKE, 32, 4, 64, 513, 512, None) == \
+        _lib.HL_ECAPACITY
+
+
+def test_decode_unsupported_head_dim(hl):
+    a = _decode_args(head_dim=96)
+    assert hl.hl_attn_decode(ctypes.byref(a), None, 0, None) == _lib.HL_EUNSUPPORTED
+
+
+def test_decode_workspace_required(hl):
+    a = _decode_args()
+    need = hl.hl_attn_decode_workspace_bytes(ctypes.byref(a))
+    assert need > 0
+    assert hl.hl_attn_decode(ctypes.byref(a), None, 0, None) == _lib.HL_EINVAL
+    assert "workspace" in _err(hl)
+    # partials: (D + 2) floats per split per query head per sequence
+    assert need % ((64 + 2) * 4 * 32) == 0
+
+
+def test_decode_null_pointer(hl):
+    a = _decode_args(q=None)
+    assert hl.hl_attn_decode(ctypes.byref(a), None, 0, None) == _lib.HL_EINVAL
+
+
+def _prefill_args(**kw):
+    a = _lib.PrefillArgs()
+    a.n_head, a.n_head_kv, a.head_dim, a.seq_len = 32, 8, 128, 4096
+    a.io_dtype = _lib.HL_BF16
+    a.q = a.k = a.v = a.out = FAKE
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+def test_prefill_empty(hl):
+    a = _prefill_args(seq_len=0)
+    assert hl.hl_attn_prefill(ctypes.byref(a), None, 0, None) == _lib.HL_EINVAL
+    assert _err(hl) == "prefill requires at least one token"
+
+
+def test_prefill_exceeds_cache(hl):
+    a = _prefill_args(k_cache=FAKE, v_cache=FAKE, kv_dtype=_lib.HL_BF16, max_len=4095)
+    assert hl.hl_attn_prefill(ctypes.byref(a), None, 0, None) == _lib.HL_ECAPACITY
+    assert _err(hl) == "prefill exceeds KV cache capacity"
+    a = _prefill_args(k_cache=FAKE, v_cache=FAKE, kv_dtype=_lib.HL_BF16, max_len=5000,
+                      start_pos=1000)
+    assert hl.hl_attn_prefill(ctypes.byref(a), None, 0, None) == _lib.HL_ECAPACITY
+
+
+def test_prefill_gqa(hl):
+    a = _prefill_args(n_head=30)
+    assert hl.hl_attn_prefill(ctypes.byref(a), None, 0, None) == _lib.HL_EINVAL
+    assert _err(hl) == "GQA requires head_count divisible by head_count_kv"
+
+
+def test_prefill_workspace_size(hl):
+    a = _prefill_args()
+    # qt [Hq][T][D] + kt [Hkv][T][D] + vt [Hkv][D][T] fp16
+    assert hl.hl_attn_prefill_workspace_bytes(ctypes.byref(a)) == (32 + 8 + 8) * 4096 * 128 * 2
+    f = _prefill_args(io_dtype=_lib.HL_F32)
+    assert hl.hl_attn_prefill_workspace_bytes(ctypes.byref(f)) == 0  # no fused ops: none needed
+
+
+def test_rope_store_cache_full(hl):
+    a = _lib.RopeStoreArgs()
+    a.batch, a.n_head_q, a.n_head_kv, a.head_dim = 1, 32, 4, 128
+    a.rope_base, a.kv_dtype, a.max_len, a.pos = 1e6, _lib.HL_BF16, 100, 100
+    a.q = a.k = a.v = a.k_cache = a.v_cache = FAKE
+    assert hl.hl_rope_store_decode(ctypes.byref(a), None) == _lib.HL_ECAPACITY
+    assert _err(hl) == "KV cache full"
+    assert hl.hl_gpu_fused_rope_store_kv(FAKE, FAKE, FAKE, FAKE, FAKE, 32, 4, 64, 64, 256, 512,
+                                         512, None) == _lib.HL_ECAPACITY
+
+
+def test_rope_dim_checks(hl):
+    assert hl.hl_gpu_rope_at_pos(FAKE, 4, 64, 63, 1e4, 0, 1, None) == _lib.HL_EINVAL
+    assert hl.hl_gpu_rope_at_pos(FAKE, 4, 64, 66, 1e4, 0, 1, None) == _lib.HL_EINVAL
+
+
+def test_theta_table_matches_oracle(hl, orc):
+    for rd, base in ((64, 1e4), (64, 5e5), (128, 1e6)):
+        buf = (ctypes.c_float * (rd // 2))()
+        assert hl.hl_rope_theta_table(buf, rd, base) == 0
+        assert np.array_equal(np.array(buf, np.float32), orc.theta_table(rd, base))
+
+
+def test_installed_theta_dim_mismatch(hl):
+    assert hl.hl_set_rope_theta(64, 1e4) == 0
+    assert hl.hl_gpu_rope_at_pos_theta(FAKE, 4, 128, 128, 0, 1, None) == _lib.HL_EINVAL
+    assert "theta" in _err(hl)
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    monkeypatch.setattr(_lib, "_lib", None)
+    monkeypatch.setattr(_lib, "LIB_PATH", str(tmp_path / "libhl_attn.so"))
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        _lib.load()

@@ -1,0 +1,178 @@
+"""GPU parity: causal prefill with fused qkNorm / RoPE / KV-cache write
+(hl_attn_prefill, hl_gpu_attention_prefill) against the CPU oracle."""
+import numpy as np
+import pytest
+import torch
+
+from util import TOL_F32, TOL_LOWP, golden, rel_err
+
+pytestmark = pytest.mark.gpu
+
+TDT = {0: torch.float32, 1: torch.float16, 2: torch.bfloat16}
+
+
+def to_dev(x, dt):
+    return torch.from_numpy(np.ascontiguousarray(x, np.float32)).cuda().to(TDT[dt])
+
+
+def from_dev(t):
+    return t.float().cpu().numpy()
+
+
+def run_prefill(q, k, v, hq, hkv, d, T, out_dtype=torch.float32, **kw):
+    from hippo_leap_amd import attention as A
+    out = torch.full(q.shape, float("nan"), dtype=out_dtype, device="cuda")
+    a = A.prefill_args(q, k, v, out, hq, hkv, d, T, **kw)
+    ws = A.workspace(A.prefill_workspace_bytes(a))
+    A.attn_prefill(a, ws)
+    torch.cuda.synchronize()
+    return out
+
+
+def oracle_prefill(orc, q, k, v, hq, hkv, d, T, base=None, style=0, wq=None, wk=None, eps=1e-6,
+                   heads=None, rows=None, rope_dim=None):
+    q, k = q.copy(), k.copy()
+    if wq is not None:
+        q = orc.qk_norm_cols(q, wq, hq, d, T, eps)
+        k = orc.qk_norm_cols(k, wk, hkv, d, T, eps)
+    if base is not None:
+        rd = rope_dim or d
+        th = orc.theta_table(rd, base)
+        q = orc.rope_cols(q, hq, d, T, rd, th, 0, style)
+        k = orc.rope_cols(k, hkv, d, T, rd, th, 0, style)
+    return orc.attention_prefill(q, k, v, hq, hkv, d, T, heads=heads, rows=rows), q, k
+
+
+@pytest.mark.parametrize("name", ["prefill_f32_halfsplit", "prefill_f32_interleaved"])
+def test_prefill_golden_fp32(hl, name):
+    g = golden(name)
+    hq, hkv, d, T, style = (int(v) for v in g["shape"])
+    out = run_prefill(to_dev(g["q"], 0), to_dev(g["k"], 0), to_dev(g["v"], 0), hq, hkv, d, T,
+                      apply_rope=True, rope_base=float(g["base"][0]), rope_style=style)
+    assert rel_err(from_dev(out), g["expected"]) < TOL_F32 / 10
+
+
+def test_prefill_reference_dropin(hl, orc):
+    """gpuAttentionPrefill signature: already-roped fp32 projections."""
+    from hippo_leap_amd import attention as A
+    hq, hkv, d, T = 32, 4, 64, 300
+    q = orc.normal(hq * d * T, 11).reshape(hq * d, T)
+    k = orc.normal(hkv * d * T, 12).reshape(hkv * d, T)
+    v = orc.normal(hkv * d * T, 13).reshape(hkv * d, T)
+    ref = orc.attention_prefill(q, k, v, hq, hkv, d, T)
+    dst = torch.empty(hq * d, T, device="cuda")
+    A.gpu_attention_prefill(dst, to_dev(q, 0), to_dev(k, 0), to_dev(v, 0), hq, hkv, d, T)
+    torch.cuda.synchronize()
+    assert rel_err(from_dev(dst), ref) < TOL_F32
+
+
+def test_prefill_c2_full(hl, orc):
+    """Config 2: T=512, Hq32/Hkv4, D64 fp32, RoPE 1e4 on q,k, KV cache written."""
+    hq, hkv, d, T, max_len = 32, 4, 64, 512, 600
+    q = orc.normal(hq * d * T, 21).reshape(hq * d, T)
+    k = orc.normal(hkv * d * T, 22).reshape(hkv * d, T)
+    v = orc.normal(hkv * d * T, 23).reshape(hkv * d, T)
+    ref, qr, kr = oracle_prefill(orc, q, k, v, hq, hkv, d, T, base=1e4)
+    kc = torch.full((hkv * d, max_len), 7.0, device="cuda")
+    vc = torch.full((hkv * d, max_len), 7.0, device="cuda")
+    qd, kd = to_dev(q, 0), to_dev(k, 0)
+    out = run_prefill(qd, kd, to_dev(v, 0), hq, hkv, d, T, apply_rope=True, rope_base=1e4,
+                      k_cache=kc, v_cache=vc, max_len=max_len, write_back_qk=True)
+    err = rel_err(from_dev(out), ref)
+    print(f"c2 rel err {err:.3e}")
+    assert err < TOL_F32
+    # in-place semantics of the reference: q, k hold the roped values
+    assert rel_err(from_dev(qd), qr) < 1e-5 and rel_err(from_dev(kd), kr) < 1e-5
+    kcn, vcn = kc.cpu().numpy(), vc.cpu().numpy()
+    assert rel_err(kcn[:, :T], kr) < 1e-5
+    assert np.array_equal(vcn[:, :T], v)                  # V stored bit-exactly
+    assert np.all(kcn[:, T:] == 7.0) and np.all(vcn[:, T:] == 7.0)  # canary untouched
+
+
+@pytest.mark.parametrize("T", [1, 2, 31, 32, 33, 63, 64, 65, 127, 200])
+def test_prefill_fp32_lengths(hl, orc, T):
+    hq, hkv, d = 8, 2, 128
+    q = orc.normal(hq * d * T, 30 + T).reshape(hq * d, T)
+    k = orc.normal(hkv * d * T, 31 + T).reshape(hkv * d, T)
+    v = orc.normal(hkv * d * T, 32 + T).reshape(hkv * d, T)
+    ref, _, _ = oracle_prefill(orc, q, k, v, hq, hkv, d, T, base=5e5)
+    out = run_prefill(to_dev(q, 0), to_dev(k, 0), to_dev(v, 0), hq, hkv, d, T, apply_rope=True,
+                      rope_base=5e5)
+    assert rel_err(from_dev(out), ref) < TOL_F32
+
+
+@pytest.mark.parametrize("dt", [1, 2])
+@pytest.mark.parametrize("T", [1, 17, 32, 64, 65, 100, 257])
+@pytest.mark.parametrize("hq,hkv,d", [(8, 2, 128), (4, 4, 64), (16, 2, 64), (6, 3, 128)])
+def test_prefill_mfma_shapes(hl, orc, dt, T, hq, hkv, d):
+    qs = orc.to_storage(orc.normal(hq * d * T, 40 + T), dt)
+    ks = orc.to_storage(orc.normal(hkv * d * T, 41 + T), dt)
+    vs = orc.to_storage(orc.normal(hkv * d * T, 42 + T), dt)
+    q, k, v = (orc.upcast(x, dt).reshape(-1, T) for x in (qs, ks, vs))
+    ref, _, _ = oracle_prefill(orc, q, k, v, hq, hkv, d, T, base=5e5)
+    out = run_prefill(to_dev(q, dt), to_dev(k, dt), to_dev(v, dt), hq, hkv, d, T,
+                      apply_rope=True, rope_base=5e5)
+    assert rel_err(from_dev(out), ref) < TOL_LOWP
+
+
+@pytest.mark.parametrize("dt", [1, 2])
+def test_prefill_mfma_qknorm_interleaved_partial_rope_cache(hl, orc, dt):
+    hq, hkv, d, T, max_len, rd = 16, 4, 128, 150, 160, 64
+    q, k, v = (orc.upcast(orc.to_storage(orc.normal(h * d * T, 50 + i), dt), dt).reshape(-1, T)
+               for i, h in enumerate((hq, hkv, hkv)))
+    wq, wk = orc.uniform(d, 53, 0.5, 1.5), orc.uniform(d, 54, 0.5, 1.5)
+    ref, _, kr = oracle_prefill(orc, q, k, v, hq, hkv, d, T, base=1e6, style=1, wq=wq, wk=wk,
+                                rope_dim=rd)
+    kc = torch.zeros(hkv * d, max_len, dtype=TDT[dt], device="cuda")
+    vc = torch.zeros(hkv * d, max_len, dtype=TDT[dt], device="cuda")
+    out = run_prefill(to_dev(q, dt), to_dev(k, dt), to_dev(v, dt), hq, hkv, d, T,
+                      apply_rope=True, rope_base=1e6, rope_style=1, rope_dim=rd,
+                      q_norm_w=torch.from_numpy(wq).cuda(), k_norm_w=torch.from_numpy(wk).cuda(),
+                      k_cache=kc, v_cache=vc, max_len=max_len)
+    assert rel_err(from_dev(out), ref) < TOL_LOWP
+    # cache: V bit-exact conversion; K within one storage ulp of the oracle's roped K
+    assert np.array_equal(from_dev(vc)[:, :T], v)
+    assert rel_err(from_dev(kc)[:, :T], kr) < 2 ** -7
+
+
+def test_prefill_c4_full_size_sampled(hl, orc):
+    """Config 4 at full size (T=4096, Hq32/Hkv8, D128, bf16, RoPE 5e5, cache
+    write); the oracle checks 4 heads x 48 sampled rows incl. first/last."""
+    hq, hkv, d, T, dt = 32, 8, 128, 4096, 2
+    gen = torch.Generator(device="cuda").manual_seed(60)
+    qd = torch.randn(hq * d, T, generator=gen, device="cuda").to(torch.bfloat16)
+    kd = torch.randn(hkv * d, T, generator=gen, device="cuda").to(torch.bfloat16)
+    vd = torch.randn(hkv * d, T, generator=gen, device="cuda").to(torch.bfloat16)
+    kc = torch.zeros(hkv * d, T, dtype=torch.bfloat16, device="cuda")
+    vc = torch.zeros(hkv * d, T, dtype=torch.bfloat16, device="cuda")
+    out = from_dev(run_prefill(qd, kd, vd, hq, hkv, d, T, apply_rope=True, rope_base=5e5,
+                               k_cache=kc, v_cache=vc, max_len=T))
+    q, k, v = from_dev(qd), from_dev(kd), from_dev(vd)
+    th = orc.theta_table(d, 5e5)
+    qr = orc.rope_cols(q, hq, d, T, d, th)
+    kr = orc.rope_cols(k, hkv, d, T, d, th)
+    # rows 0, 97, 194, ... and the last 5 rows of every 16th near the end (incl. 4095)
+    samples = [(0, T, 97), (T - 65, T, 16)]
+    for h in (0, 5, 17, 31):
+        blk = slice(h * d, (h + 1) * d)
+        for r0, r1, rs in samples:
+            ref = orc.attention_prefill(qr, kr, v, hq, hkv, d, T, heads=(h, h + 1),
+                                        rows=(r0, r1, rs))
+            err = rel_err(out[blk, r0:r1:rs], ref[blk, r0:r1:rs])
+            print(f"c4 head {h} rows {r0}:{r1}:{rs} rel err {err:.3e}")
+            assert err < TOL_LOWP
+    assert np.array_equal(from_dev(vc), v)
+    assert rel_err(from_dev(kc), kr) < 2 ** -7
+
+
+@pytest.mark.parametrize("dt", [1, 2])
+def test_prefill_lowp_output_is_rne_of_fp32_output(hl, orc, dt):
+    """fp16/bf16 output = round-to-nearest-even of the fp32 output, bit for bit."""
+    hq, hkv, d, T = 8, 2, 128, 130
+    q, k, v = (orc.upcast(orc.to_storage(orc.normal(h * d * T, 70 + i), dt), dt).reshape(-1, T)
+               for i, h in enumerate((hq, hkv, hkv)))
+    args = (to_dev(q, dt), to_dev(k, dt), to_dev(v, dt), hq, hkv, d, T)
+    o32 = run_prefill(*args, apply_rope=True, rope_base=5e5)
+    olp = run_prefill(*args, out_dtype=TDT[dt], apply_rope=True, rope_base=5e5)
+    exp = orc.to_storage(from_dev(o32), dt)
+    assert np.array_equal(olp.view(torch.int16).cpu().numpy().view(np.uint16), exp)

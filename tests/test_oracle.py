@@ -1,0 +1,287 @@
+"""Pins the CPU oracle (oracle/hl_oracle.c) before it is trusted as the checker.
+
+Each oracle function is checked against something other than its own formula:
+the reference's known-answer test, the committed golden fixtures (fp64,
+cross-checked with torch SDPA when written), NumPy/torch library routines,
+closed forms and invariants chosen so that a dropped term, wrong sign, wrong
+index or transposed operand fails.
+"""
+import numpy as np
+import pytest
+import torch
+
+from util import golden, rel_err
+
+pytestmark = pytest.mark.filterwarnings("ignore::RuntimeWarning")
+
+
+# ---------------------------------------------------------------------------
+# fp16 / bf16 storage
+# ---------------------------------------------------------------------------
+def test_half_to_float_reference_kat(orc):
+    """tests/test_quant.nim:5-15 of the reference, value for value."""
+    assert orc.half_to_float(0x0000) == 0.0
+    assert orc.half_to_float(0x3C00) == 1.0
+    assert orc.half_to_float(0xBC00) == -1.0
+    assert orc.half_to_float(0x4000) == 2.0
+    assert orc.half_to_float(0x3800) == 0.5
+    assert orc.half_to_float(0x7C00) == float("inf")
+    assert orc.half_to_float(0xFC00) == float("-inf")
+    assert np.isnan(orc.half_to_float(0x7C01))
+
+
+def test_half_to_float_exhaustive(orc):
+    bits = np.arange(65536, dtype=np.uint16)
+    got = orc.upcast(bits, orc.F16)
+    ref = bits.view(np.float16).astype(np.float32)
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+
+
+def _sweep():
+    rng = np.random.default_rng(5)
+    x = np.concatenate([
+        rng.standard_normal(20000).astype(np.float32) * 10,
+        rng.standard_normal(5000).astype(np.float32) * 1e-5,      # fp16 subnormals
+        np.float32(2.0) ** rng.integers(-30, 20, 2000).astype(np.float32),
+        np.array([65504, 65519, 65520, 70000, -65520, 6.1035156e-05, 5.96e-08, 2.98e-08,
+                  1 + 2**-11, 1 + 3 * 2**-11, 1 + 2**-8, 1 + 3 * 2**-8, 0.0, -0.0,
+                  np.inf, -np.inf], dtype=np.float32),
+    ])
+    return x
+
+
+def test_float_to_half_rne_matches_numpy(orc):
+    x = _sweep()
+    got = orc.to_storage(x, orc.F16)
+    ref = x.astype(np.float16).view(np.uint16)
+    assert np.array_equal(got, ref)
+
+
+def test_float_to_bf16_rne_matches_torch(orc):
+    x = _sweep()
+    got = orc.to_storage(x, orc.BF16)
+    ref = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(got, ref)
+    back = orc.upcast(got, orc.BF16)
+    assert np.array_equal(back, torch.from_numpy(x).to(torch.bfloat16).float().numpy())
+
+
+def test_reference_float_to_half_truncates(orc):
+    """quant.nim:98-107 truncates and flushes; the caches use RNE instead."""
+    x = np.float32(1 + 3 * 2**-11)  # halfway case: RNE rounds up, truncation down
+    assert orc.float_to_half_trunc(float(x)) == 0x3C01
+    assert int(orc.to_storage(np.array([x]), orc.F16)[0]) == 0x3C02
+    assert orc.float_to_half_trunc(3e-5) == 0  # below 2^-14: flushed
+    assert int(orc.to_storage(np.array([3e-5], np.float32), orc.F16)[0]) != 0
+
+
+# ---------------------------------------------------------------------------
+# tensor.nim ops
+# ---------------------------------------------------------------------------
+def test_matmul(orc):
+    a = orc.normal(7 * 13, 1).reshape(7, 13)
+    b = orc.normal(13 * 5, 2).reshape(13, 5)
+    assert rel_err(orc.matmul(a, b), a.astype(np.float64) @ b) < 1e-6
+    assert np.array_equal(orc.matmul(np.eye(7, dtype=np.float32), a), a)
+    # (a b)^T = b^T a^T catches a transposed operand
+    assert rel_err(orc.matmul(b.T, a.T), orc.matmul(a, b).T) < 1e-6
+
+
+def test_softmax(orc):
+    x = orc.normal(4 * 33, 3, 0, 5).reshape(4, 33)
+    y = orc.softmax_last_dim(x)
+    e = np.exp(x.astype(np.float64) - x.max(-1, keepdims=True))
+    assert rel_err(y, e / e.sum(-1, keepdims=True)) < 1e-6
+    assert np.allclose(y.sum(-1), 1.0, atol=1e-6)
+    assert rel_err(orc.softmax_last_dim(x + 7.5), y) < 1e-5  # shift invariance
+    assert np.all(orc.softmax_last_dim(np.zeros((1, 9), np.float32)) == np.float32(1 / 9))
+
+
+def test_rmsnorm(orc):
+    w = orc.uniform(64, 4, 0.5, 1.5)
+    c, eps = 0.75, 1e-6
+    got = orc.rmsnorm(np.full((2, 64), c, np.float32), w, eps)
+    assert rel_err(got[0], w * c / np.sqrt(c * c + eps)) < 1e-6  # closed form
+    x = orc.normal(3 * 64, 5).reshape(3, 64)
+    ref = x / np.sqrt((x.astype(np.float64) ** 2).mean(-1, keepdims=True) + eps) * w
+    assert rel_err(orc.rmsnorm(x, w, eps), ref) < 1e-6
+    # column form on the transpose
+    assert rel_err(orc.rmsnorm_cols(np.ascontiguousarray(x.T), w, eps), ref.T) < 1e-6
+
+
+# ---------------------------------------------------------------------------
+# RoPE
+# ---------------------------------------------------------------------------
+def test_theta_table(orc):
+    for rd, base in ((64, 1e4), (128, 5e5), (128, 1e6)):
+        th = orc.theta_table(rd, base)
+        i = np.arange(rd // 2, dtype=np.float64)
+        ref = (1.0 / base) ** (2 * i / rd)
+        assert np.all(np.abs(th - ref) <= 2 * np.spacing(th.astype(np.float32)))
+        assert th[0] == 1.0
+
+
+def test_rope_identity_norm_composition(orc):
+    H, D = 3, 64
+    th = orc.theta_table(D, 1e4)
+    x = orc.normal(H * D, 6)
+    assert np.array_equal(orc.rope_heads(x, H, D, D, th, 0), x)  # pos 0 = identity
+    for style in (0, 1):
+        y = orc.rope_heads(x, H, D, D, th, 17, style)
+        xr, yr = x.reshape(H, D).astype(np.float64), y.reshape(H, D).astype(np.float64)
+        half = D // 2
+        if style == 0:
+            px, py = xr[:, :half] ** 2 + xr[:, half:] ** 2, yr[:, :half] ** 2 + yr[:, half:] ** 2
+        else:
+            px, py = xr[:, 0::2] ** 2 + xr[:, 1::2] ** 2, yr[:, 0::2] ** 2 + yr[:, 1::2] ** 2
+        assert np.allclose(px, py, rtol=1e-5)  # rotation preserves each pair's norm
+        y2 = orc.rope_heads(orc.rope_heads(x, H, D, D, th, 5, style), H, D, D, th, 12, style)
+        assert rel_err(y2, y) < 1e-5  # R(5) R(12) = R(17)
+        assert rel_err(y, x) > 1e-2  # and it does rotate
+
+
+def test_rope_half_split_vs_interleaved_permutation(orc):
+    H, D = 2, 16
+    th = orc.theta_table(D, 1e4)
+    x = orc.normal(H * D, 7).reshape(H, D)
+    perm = np.empty(D, np.int64)  # interleaved slot 2i <- i, 2i+1 <- i+D/2
+    perm[0::2], perm[1::2] = np.arange(D // 2), np.arange(D // 2) + D // 2
+    a = orc.rope_heads(x.reshape(-1), H, D, D, th, 9, 0).reshape(H, D)
+    b = orc.rope_heads(x[:, perm].reshape(-1), H, D, D, th, 9, 1).reshape(H, D)
+    assert np.array_equal(a[:, perm], b)
+
+
+def test_rope_partial_rotary_passthrough(orc):
+    H, D, rd = 2, 64, 32
+    th = orc.theta_table(rd, 1e4)
+    x = orc.normal(H * D, 8)
+    y = orc.rope_heads(x, H, D, rd, th, 11).reshape(H, D)
+    assert np.array_equal(y[:, rd:], x.reshape(H, D)[:, rd:])
+
+
+def test_rope_inplace_tensor_nim_matches_interleaved_cols(orc):
+    """tensor.nim ropeInplace ([outer, seq, dim]) == the interleaved column form."""
+    H, D, T = 2, 32, 9
+    x = orc.normal(H * T * D, 9).reshape(H, T, D)
+    a = orc.rope_inplace(x, 1e4, 3)
+    th = orc.theta_table(D, 1e4)
+    cols = np.ascontiguousarray(x.transpose(0, 2, 1)).reshape(H * D, T)
+    b = orc.rope_cols(cols, H, D, T, D, th, 3, 1).reshape(H, D, T).transpose(0, 2, 1)
+    assert rel_err(a, b) < 1e-6
+
+
+@pytest.mark.parametrize("name", ["prefill_f32_halfsplit", "prefill_f32_interleaved"])
+def test_rope_cols_golden(orc, name):
+    g = golden(name)
+    hq, hkv, d, T, style = (int(v) for v in g["shape"])
+    th = orc.theta_table(d, float(g["base"][0]))
+    assert rel_err(orc.rope_cols(g["q"], hq, d, T, d, th, 0, style), g["q_roped"]) < 1e-5
+    assert rel_err(orc.rope_cols(g["k"], hkv, d, T, d, th, 0, style), g["k_roped"]) < 1e-5
+
+
+# ---------------------------------------------------------------------------
+# Attention
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("name", ["decode_f32", "decode_f16", "decode_bf16"])
+def test_decode_golden(orc, name):
+    g = golden(name)
+    hq, hkv, d, L, max_len, dt = (int(v) for v in g["shape"])
+    kc, vc = orc.upcast(g["k_cache"], dt), orc.upcast(g["v_cache"], dt)
+    out = orc.attention_decode(g["q"], kc, vc, hq, hkv, d, L, max_len)
+    assert rel_err(out, g["expected"]) < 1e-5
+
+
+@pytest.mark.parametrize("name", ["prefill_f32_halfsplit", "prefill_f32_interleaved"])
+def test_prefill_golden(orc, name):
+    g = golden(name)
+    hq, hkv, d, T, style = (int(v) for v in g["shape"])
+    out = orc.attention_prefill(g["q_roped"], g["k_roped"], g["v"], hq, hkv, d, T)
+    assert rel_err(out, g["expected"]) < 1e-5
+
+
+def test_decode_closed_forms(orc):
+    hq, hkv, d, M = 4, 2, 64, 40
+    q = orc.uniform(hq * d, 30)
+    kc = orc.uniform(hkv * d * M, 31).reshape(hkv, d, M)
+    vc = orc.uniform(hkv * d * M, 32).reshape(hkv, d, M)
+    g = hq // hkv
+    # L = 1: output is v_0 of the head's kv head
+    o = orc.attention_decode(q, kc, vc, hq, hkv, d, 1, M).reshape(hq, d)
+    for h in range(hq):
+        assert np.array_equal(o[h], vc[h // g, :, 0])
+    # identical K columns: uniform weights -> mean of V over L
+    kc_same = np.repeat(kc[:, :, :1], M, axis=2)
+    o = orc.attention_decode(q, kc_same, vc, hq, hkv, d, 23, M).reshape(hq, d)
+    for h in range(hq):
+        assert rel_err(o[h], vc[h // g, :, :23].astype(np.float64).mean(-1)) < 1e-5
+    # q = 0: same mean
+    o = orc.attention_decode(np.zeros_like(q), kc, vc, hq, hkv, d, 23, M).reshape(hq, d)
+    assert rel_err(o[1], vc[0, :, :23].astype(np.float64).mean(-1)) < 1e-5
+    # GQA mapping: replicating kv heads to MHA gives the same result
+    o_gqa = orc.attention_decode(q, kc, vc, hq, hkv, d, 31, M)
+    o_mha = orc.attention_decode(q, np.repeat(kc, g, 0), np.repeat(vc, g, 0), hq, hq, d, 31, M)
+    assert np.array_equal(o_gqa, o_mha)
+    # a wrong group mapping (h % Hkv) would differ
+    assert rel_err(o_gqa.reshape(hq, d)[1], o_gqa.reshape(hq, d)[2]) > 1e-3
+
+
+def test_prefill_closed_forms_and_causality(orc):
+    hq, hkv, d, T = 4, 2, 64, 40
+    q = orc.normal(hq * d * T, 40).reshape(hq * d, T)
+    k = orc.normal(hkv * d * T, 41).reshape(hkv * d, T)
+    v = orc.normal(hkv * d * T, 42).reshape(hkv * d, T)
+    o = orc.attention_prefill(q, k, v, hq, hkv, d, T)
+    g = hq // hkv
+    o3, v3 = o.reshape(hq, d, T), v.reshape(hkv, d, T)
+    for h in range(hq):
+        assert np.array_equal(o3[h, :, 0], v3[h // g, :, 0])  # row 0 = v_0
+    # last row equals decode with L = T over the same K/V
+    dec = orc.attention_decode(np.ascontiguousarray(q[:, T - 1]), k, v, hq, hkv, d, T, T)
+    assert rel_err(o[:, T - 1], dec) < 1e-6
+    # causality: perturbing K/V at j > i leaves row i unchanged
+    i = 17
+    k2, v2 = k.copy(), v.copy()
+    k2[:, i + 1:] += 3.0
+    v2[:, i + 1:] -= 2.0
+    o2 = orc.attention_prefill(q, k2, v2, hq, hkv, d, T)
+    assert np.array_equal(o2[:, :i + 1], o[:, :i + 1])
+    assert not np.allclose(o2[:, i + 1:], o[:, i + 1:])
+    # row subsets reproduce the full computation
+    sub = orc.attention_prefill(q, k, v, hq, hkv, d, T, heads=(1, 3), rows=(3, T, 7))
+    assert np.array_equal(sub[64:192, 3::7], o[64:192, 3::7])
+
+
+def test_decode_step_golden(orc):
+    for name in ("decode_step_bf16_qknorm", "decode_step_f16_qknorm"):
+        g = golden(name)
+        hq, hkv, d, prev, max_len, dt = (int(v) for v in g["shape"])
+        eps, base = float(g["eps"][0]), float(g["base"][0])
+        th = orc.theta_table(d, base)
+        qn = orc.rope_heads(orc.qk_norm(g["q"], g["wq"], hq, d, eps), hq, d, d, th, prev)
+        kn = orc.rope_heads(orc.qk_norm(g["k"], g["wk"], hkv, d, eps), hkv, d, d, th, prev)
+        assert rel_err(qn, g["q_rot"]) < 1e-5 and rel_err(kn, g["k_rot"]) < 1e-5
+        kc, vc = g["k_cache"].copy(), g["v_cache"].copy()
+        orc.store_kv(kc, dt, kn, hkv * d, 1, max_len, prev)
+        orc.store_kv(vc, dt, g["v"], hkv * d, 1, max_len, prev)
+        out = orc.attention_decode(qn, orc.upcast(kc, dt), orc.upcast(vc, dt), hq, hkv, d,
+                                   prev + 1, max_len)
+        assert rel_err(out, g["expected"]) < 1e-5
+
+
+def test_decode_fp64_brute_force(orc):
+    rng = np.random.default_rng(0)
+    for hq, hkv, d, L in ((6, 3, 64, 5), (8, 1, 128, 129)):
+        M = L + 3
+        q = rng.standard_normal(hq * d).astype(np.float32)
+        kc = rng.standard_normal(hkv * d * M).astype(np.float32)
+        vc = rng.standard_normal(hkv * d * M).astype(np.float32)
+        out = orc.attention_decode(q, kc, vc, hq, hkv, d, L, M).reshape(hq, d)
+        K = kc.reshape(hkv, d, M).astype(np.float64)
+        V = vc.reshape(hkv, d, M).astype(np.float64)
+        for h in range(hq):
+            kv = h // (hq // hkv)
+            s = q.reshape(hq, d)[h].astype(np.float64) @ K[kv, :, :L] / np.sqrt(d)
+            p = np.exp(s - s.max())
+            assert rel_err(out[h], V[kv, :, :L] @ (p / p.sum())) < 1e-5
