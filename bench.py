@@ -5,7 +5,8 @@ Headline workload ("decode attn GB/s at 2K ctx"):
   2048 cached positions each, one new token per sequence (L = 2049),
   Hq=32 / Hkv=8, D=64, RoPE theta 5e5, K/V ~ N(0, 0.5) (sigma 0.5).
   One step = hl_rope_store_decode (RoPE of the new q/k, K/V write at column
-  2048) + hl_attn_decode (split-K attention + merge).  16 cache sets are
+  2048) + hl_attn_decode (split-K attention + merge); the W warmup and K timed
+  steps each run as one captured HIP graph.  16 cache sets are
   rotated (16 x 33.6 MB > the 256 MB Infinity Cache) so every step streams
   its K/V from HBM.
   value = algorithmic K+V bytes of one step / step time (GB/s).
@@ -45,7 +46,8 @@ def log(msg):
 
 def event_time_ms(torch, fn, iters):
     """Average ms per call of fn() from HIP events on torch's current stream
-    (the stream every library call is given)."""
+    (the stream every library call is given).  Eager launches: includes the
+    host's launch rate when kernels are shorter than a Python call."""
     st = torch.cuda.current_stream()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(st)
@@ -56,6 +58,38 @@ def event_time_ms(torch, fn, iters):
     return e0.elapsed_time(e1) / iters
 
 
+def capture(torch, fn, n, first=0):
+    """Captures n calls fn(first), fn(first+1), ... into one HIP graph."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn(first)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(n):
+            fn(first + i)
+    torch.cuda.synchronize()
+    return g
+
+
+def graph_time_ms(torch, fn, n_inner=64, replays=8):
+    """Average ms per fn() call: n_inner calls captured in a HIP graph, the
+    graph replayed `replays` times between HIP events on the current stream."""
+    g = capture(torch, fn, n_inner)
+    g.replay()
+    torch.cuda.synchronize()
+    st = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    for _ in range(replays):
+        g.replay()
+    e1.record(st)
+    e1.synchronize()
+    return e0.elapsed_time(e1) / (replays * n_inner)
+
+
 # ---------------------------------------------------------------------------
 # Decode (c3 headline, c5 extra)
 # ---------------------------------------------------------------------------
@@ -64,7 +98,7 @@ class DecodeWorkload:
         self.t, self.A = torch, A
         self.B, self.hq, self.hkv, self.d, self.prev = B, hq, hkv, d, prev
         self.L = prev + 1
-        self.max_len = self.L
+        self.max_len = (self.L + 63) // 64 * 64  # cache columns: allocation rounded to 64
         g = torch.Generator(device="cuda").manual_seed(seed)
         n = B * hkv * d * self.max_len
         self.kc = [(torch.randn(n, generator=g, device="cuda") * sigma).to(kv_dtype)
@@ -83,7 +117,7 @@ class DecodeWorkload:
         self.args = [A.decode_args(self.q, kc, vc, self.out, hq, hkv, d, self.max_len, self.L)
                      for kc, vc in zip(self.kc, self.vc)]
         self.ws = A.workspace(A.decode_workspace_bytes(self.args[0]))
-        self.kv_bytes = 2 * B * hkv * d * self.L * self.kc[0].element_size()
+        self.kv_bytes = 2 * B * hkv * d * self.L * self.kc[0].element_size()  # columns < L
         self.flops = 4 * B * hq * d * self.L
 
     def rope_store(self, i):
@@ -101,17 +135,23 @@ class DecodeWorkload:
 
 
 def bench_decode(torch, A, wl, steps, warmup):
-    for i in range(warmup):
-        wl.step(i)
+    """Returns (step ms, attention ms, rope+store ms, eager step ms).
+
+    The W warmup and K timed steps are each captured into a HIP graph (as a
+    serving loop would run them); the timed graph is bracketed by
+    synchronize() on both sides and timed with the host clock."""
+    gw = capture(torch, wl.step, warmup)
+    gt = capture(torch, wl.step, steps, first=warmup)
+    gw.replay()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for i in range(steps):
-        wl.step(i)
+    gt.replay()
     torch.cuda.synchronize()
     step_ms = (time.perf_counter() - t0) * 1e3 / steps
-    attn_ms = event_time_ms(torch, wl.attend, max(steps, 50))
-    rs_ms = event_time_ms(torch, wl.rope_store, max(steps, 50))
-    return step_ms, attn_ms, rs_ms
+    attn_ms = graph_time_ms(torch, wl.attend)
+    rs_ms = graph_time_ms(torch, wl.rope_store)
+    eager_ms = event_time_ms(torch, wl.step, 20)
+    return step_ms, attn_ms, rs_ms, eager_ms
 
 
 # ---------------------------------------------------------------------------
@@ -200,7 +240,7 @@ def main():
         wl = DecodeWorkload(torch, A, B=8, hq=32, hkv=8, d=64, prev=2048,
                             kv_dtype=torch.float16, sigma=0.5, base=5e5, n_sets=16,
                             qknorm=False, seed=3)
-        step_ms, attn_ms, rs_ms = bench_decode(torch, A, wl, args.steps, args.warmup)
+        step_ms, attn_ms, rs_ms, eager_ms = bench_decode(torch, A, wl, args.steps, args.warmup)
         value = wl.kv_bytes / (step_ms * 1e-3) / 1e9
         achieved = wl.kv_bytes / (attn_ms * 1e-3) / 1e9
         result.update({
@@ -216,6 +256,7 @@ def main():
                          "traffic": None, "algorithmic_bytes": wl.kv_bytes,
                          "avg_us": round(attn_ms * 1e3, 3)},
             "rope_store_us": round(rs_ms * 1e3, 3),
+            "eager_ms_per_step": round(eager_ms, 5),
         })
         log(f"decode c3: step {step_ms*1e3:.2f} us, attention {attn_ms*1e3:.2f} us "
             f"({achieved:.0f} GB/s), rope+store {rs_ms*1e3:.2f} us")
@@ -228,8 +269,7 @@ def main():
         for i in range(max(2, args.warmup // 2)):
             pw.step(i)
         torch.cuda.synchronize()
-        iters = max(10, args.steps // 5)
-        ms = event_time_ms(torch, pw.step, iters)
+        ms = graph_time_ms(torch, pw.step, n_inner=8, replays=max(2, args.steps // 20))
         tf = pw.flops / (ms * 1e-3) / 1e12
         result["prefill"] = {
             "workload": "c4: Llama-3-8B-shape causal prefill bf16, T=4096, Hq32/Hkv8, D128, "
@@ -250,7 +290,7 @@ def main():
         wl = DecodeWorkload(torch, A, B=16, hq=32, hkv=4, d=128, prev=32768,
                             kv_dtype=torch.bfloat16, sigma=1.0, base=1e6, n_sets=1,
                             qknorm=True, seed=5)
-        step_ms, attn_ms, rs_ms = bench_decode(torch, A, wl, max(10, args.steps // 4), 3)
+        step_ms, attn_ms, rs_ms, _ = bench_decode(torch, A, wl, max(10, args.steps // 4), 3)
         ach = wl.kv_bytes / (attn_ms * 1e-3) / 1e9
         result["decode_c5"] = {
             "workload": "c5: Qwen3-30B-A3B-shape decode, bf16 KV, B=16, L=32769, Hq32/Hkv4, "

@@ -47,6 +47,10 @@ __device__ __forceinline__ float load_elem(const void* p, int64_t i) {
 }
 template <int DT>
 __device__ __forceinline__ void store_elem(void* p, int64_t i, float v) {
+  // Materialise the fp32 value first: without the barrier the compiler may
+  // fuse the producing multiply into a mixed-precision op that rounds once
+  // to 16 bits, which is not the RNE of the fp32 result.
+  if constexpr (DT != HL_F32) __asm__ volatile("" : "+v"(v));
   if constexpr (DT == HL_F32) ((float*)p)[i] = v;
   else if constexpr (DT == HL_F16) ((uint16_t*)p)[i] = f32_to_f16_bits(v);
   else ((uint16_t*)p)[i] = f32_to_bf16_bits(v);

@@ -253,7 +253,9 @@ template <int D>
 __global__ __launch_bounds__(256) void prefill_f32_kernel(PrefillLaunch p) {
   constexpr int BM = 32, BNF = 64, DU = D / 64;
   __shared__ __attribute__((aligned(16))) float sq[D][BM];        // Q tile, [d][row]
-  __shared__ __attribute__((aligned(16))) float skv[BNF * (D + 4)];  // K as [d][col], then V as [col][d]
+  // K tile as [d][col] (D x (BNF+4)), then V tile as [col][d] (BNF x (D+4))
+  constexpr int KV_FLOATS = D * (BNF + 4) > BNF * (D + 4) ? D * (BNF + 4) : BNF * (D + 4);
+  __shared__ __attribute__((aligned(16))) float skv[KV_FLOATS];
   __shared__ __attribute__((aligned(16))) float sp[BM][BNF + 4];
 
   const int tid = threadIdx.x;
