@@ -372,11 +372,9 @@ int hl_attn_decode(const hl_decode_args* a, void* workspace, size_t ws_bytes, vo
   decode_plan(a, &plan);
   if (plan.ws_bytes > 0 && (!workspace || ws_bytes < plan.ws_bytes))
     return fail(HL_EINVAL, "decode: workspace of %zu bytes needed, %zu given", plan.ws_bytes, ws_bytes);
-  const long long stride = a->cache_batch_stride ? a->cache_batch_stride
-                                                 : (long long)a->n_head_kv * a->head_dim * a->max_len;
-  const bool vec_ok = a->kv_dtype != HL_F32 && (a->max_len % 8 == 0) && (stride % 8 == 0) &&
-                      aligned16(a->k_cache) && aligned16(a->v_cache);
-  hipError_t e = decode_launch(a, &plan, workspace, as_stream(stream), vec_ok);
+  if (plan.ws_bytes > 0 && ((uintptr_t)workspace & 7) != 0)
+    return fail(HL_EINVAL, "decode: workspace must be 8-byte aligned");
+  hipError_t e = decode_launch(a, &plan, workspace, as_stream(stream));
   return e == hipSuccess ? HL_OK : hip_fail(e, "decode launch");
 }
 
@@ -423,7 +421,7 @@ int hl_gpu_attention_decode(float* dst, const float* q, const float* k_cache, co
     }
     ws = w.ptr;
   }
-  hipError_t e = decode_launch(&a, &plan, ws, as_stream(stream), false);
+  hipError_t e = decode_launch(&a, &plan, ws, as_stream(stream));
   return e == hipSuccess ? HL_OK : hip_fail(e, "decode launch");
 }
 

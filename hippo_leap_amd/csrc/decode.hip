@@ -11,46 +11,79 @@
 // Work split: grid = (num_splits, Hkv * head_chunks, B), 256 threads = 4
 // waves.  The split's columns are dealt to the waves in 32- (MFMA path) or
 // 64-column (fp32 path) tiles; each wave keeps its own online-softmax state
-// (running max m, sum l, accumulators o) in registers, the four waves merge
-// through LDS, and the workgroup writes one partial (m, l, o[D]) per query
-// head.  decode_merge_kernel folds the partials of all splits.
+// (running max m, sum l, accumulators o) in registers and prefetches its next
+// tile while computing the current one.  The four waves merge through LDS and
+// the workgroup writes one partial (m, l, o[D]) per query head.  The last
+// workgroup of a (sequence, kv head, head chunk) to finish folds the partials
+// of all splits and writes the output, so one launch does the whole step.
 //
-// Softmax runs in base 2: q is pre-multiplied by scale*log2(e), so
+// Softmax runs in base 2 (scores pre-multiplied by scale*log2 e), so
 // p = exp2(s - m) equals the reference's expf(score - max).
+#include <atomic>
+#include <map>
+#include <mutex>
+
 #include "common.h"
 #include "launch.h"
 
 namespace hl {
 
-// Partial layout in the workspace: for (b, hq, split):
-//   ws_o [((b*Hq + hq)*S + split)*D + d]   unnormalised sum p*v
-//   ws_ml[((b*Hq + hq)*S + split)*2 + {0,1}]  running max (log2 units), sum
+// Workspace layout (num_splits > 1):
+//   ws_o  [((b*Hq + hq)*S + split)*D + d]     unnormalised sum p*v
+//   ws_ml [((b*Hq + hq)*S + split)*2 + {0,1}] running max (log2 units), sum
+//   slots [(b*Hkv + kvh)*n_chunks + chunk]    uint64 arrival counters
+// A counter holds (generation << 32 | arrivals).  The generation is a
+// per-call value that is never 0; the last arrival resets the counter to 0,
+// so the workspace needs no initialisation and graph replays (which repeat
+// the generation) start from 0 again.
 struct DecodeParams {
   const float* q;
   const void* k;
   const void* v;
-  float* out;      // final output when direct != 0
+  float* out;
   float* ws_o;
   float* ws_ml;
+  unsigned long long* slots;
   const int* seq_lens;
   long long batch_stride;
   int n_head, n_head_kv, head_dim, group, head_chunk, n_chunks;
   int max_len, seq_len, split_len, num_splits;
-  int direct;      // 1: num_splits == 1, normalise and write out directly
+  unsigned int gen;
   float scale_log2;
 };
 
-// ---------------------------------------------------------------------------
-// Workgroup epilogue shared by both kernels: merge the 4 waves' states held
-// in LDS and write the split's partial (or the final output).
-//   sm_m[w][h], sm_l[w][h], sm_o[w][h][D] for h < hc (heads of this chunk).
-// ---------------------------------------------------------------------------
+constexpr int kMaxFusedSplits = 256;
+
+// Registers this workgroup's partial; returns true in the last arrival.
+__device__ __forceinline__ bool arrive_last(unsigned long long* slot, unsigned int gen, int S) {
+  __shared__ int s_last;
+  __threadfence();  // partials written by every thread are visible device-wide
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    unsigned long long v = __hip_atomic_load(slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    unsigned long long nv;
+    while (true) {
+      nv = ((unsigned int)(v >> 32) == gen) ? v + 1 : (((unsigned long long)gen << 32) | 1ull);
+      unsigned long long prev = atomicCAS(slot, v, nv);
+      if (prev == v) break;
+      v = prev;
+    }
+    s_last = (int)(nv & 0xFFFFFFFFull) >= S;
+  }
+  __syncthreads();
+  return s_last != 0;
+}
+
+// Workgroup epilogue shared by both kernels.  sm_m[w][h], sm_l[w][h] and
+// sm_o[w][h][D] hold the 4 waves' states for the hc heads of this chunk.
+// `lds_w` is scratch for the fused merge (>= 16 * kMaxFusedSplits floats,
+// may alias sm_*: it is used after they are consumed).
 template <int D>
-__device__ __forceinline__ void merge_waves_and_store(const DecodeParams& p, const float* sm_m,
-                                                      const float* sm_l, const float* sm_o,
-                                                      int hc, int b, int hq0, int split,
-                                                      int hstride) {
+__device__ void finish_workgroup(const DecodeParams& p, const float* sm_m, const float* sm_l,
+                                 const float* sm_o, int hc, int b, int kvh, int chunk, int hq0,
+                                 int split, int hstride, float* lds_w) {
   const int tid = threadIdx.x;
+  const int S = p.num_splits;
   for (int idx = tid; idx < hc * D; idx += 256) {
     const int h = idx / D, d = idx % D;
     float M = -INFINITY;
@@ -65,12 +98,11 @@ __device__ __forceinline__ void merge_waves_and_store(const DecodeParams& p, con
         l += f * sm_l[w * hstride + h];
       }
     }
-    const int hq = hq0 + h;
-    const long long row = (long long)b * p.n_head + hq;
-    if (p.direct) {
+    const long long row = (long long)b * p.n_head + hq0 + h;
+    if (S == 1) {
       p.out[row * D + d] = o / l;
     } else {
-      const long long pi = row * p.num_splits + split;
+      const long long pi = row * S + split;
       p.ws_o[pi * D + d] = o;
       if (d == 0) {
         p.ws_ml[pi * 2 + 0] = M;
@@ -78,6 +110,41 @@ __device__ __forceinline__ void merge_waves_and_store(const DecodeParams& p, con
       }
     }
   }
+  if (S == 1) return;
+  unsigned long long* slot = p.slots + ((long long)b * p.n_head_kv + kvh) * p.n_chunks + chunk;
+  if (!arrive_last(slot, p.gen, S)) return;
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+
+  // Fold all splits: weights w[h][s] = exp2(m_s - M_h) in LDS, then o[h][d].
+  float* sw = lds_w;                          // [16][S]
+  float* sinv = lds_w + 16 * kMaxFusedSplits;  // [16]
+  for (int h = tid >> 4; h < hc; h += 16) {   // 16 threads per head
+    const long long row = (long long)b * p.n_head + hq0 + h;
+    const float* ml = p.ws_ml + row * S * 2;
+    float M = -INFINITY;
+    for (int s = tid & 15; s < S; s += 16) M = fmaxf(M, ml[2 * s]);
+#pragma unroll
+    for (int o = 8; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 16));
+    float l = 0.f;
+    for (int s = tid & 15; s < S; s += 16) {
+      const float w = M == -INFINITY ? 0.f : fast_exp2(ml[2 * s] - M);
+      sw[h * kMaxFusedSplits + s] = w;
+      l += w * ml[2 * s + 1];
+    }
+#pragma unroll
+    for (int o = 8; o > 0; o >>= 1) l += __shfl_xor(l, o, 16);
+    if ((tid & 15) == 0) sinv[h] = 1.0f / l;
+  }
+  __syncthreads();
+  for (int idx = tid; idx < hc * D; idx += 256) {
+    const int h = idx / D, d = idx % D;
+    const long long row = (long long)b * p.n_head + hq0 + h;
+    const float* wo = p.ws_o + row * S * D + d;
+    float o = 0.f;
+    for (int s = 0; s < S; ++s) o += sw[h * kMaxFusedSplits + s] * wo[(long long)s * D];
+    p.out[row * D + d] = o * sinv[h];
+  }
+  if (tid == 0) __hip_atomic_store(slot, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---------------------------------------------------------------------------
@@ -89,10 +156,12 @@ template <int D>
 __global__ __launch_bounds__(256) void decode_f32_kernel(DecodeParams p) {
   constexpr int HC = 16;  // max heads per chunk
   constexpr int DPL = (D + 63) / 64;  // output dims per lane
+  constexpr int MERGE_FLOATS = 4 * HC * (D + 2);
+  constexpr int FUSE_FLOATS = 16 * kMaxFusedSplits + 16;
+  constexpr int SM_FLOATS = MERGE_FLOATS > FUSE_FLOATS ? MERGE_FLOATS : FUSE_FLOATS;
   __shared__ __attribute__((aligned(16))) float sq[HC * D];
   __shared__ float sp[4][HC][64];
-  __shared__ float sm_m[4 * HC], sm_l[4 * HC];
-  __shared__ float sm_o[4 * HC * D];
+  __shared__ __attribute__((aligned(16))) float sm[SM_FLOATS];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int b = blockIdx.z;
@@ -187,6 +256,9 @@ __global__ __launch_bounds__(256) void decode_f32_kernel(DecodeParams p) {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   }
 
+  float* sm_m = sm;
+  float* sm_l = sm_m + 4 * HC;
+  float* sm_o = sm_l + 4 * HC;
 #pragma unroll
   for (int h = 0; h < HC; ++h) {
     const float l = wave_sum(l_run[h]);
@@ -201,7 +273,7 @@ __global__ __launch_bounds__(256) void decode_f32_kernel(DecodeParams p) {
     }
   }
   __syncthreads();
-  merge_waves_and_store<D>(p, sm_m, sm_l, sm_o, hc, b, hq0, split, HC);
+  finish_workgroup<D>(p, sm_m, sm_l, sm_o, hc, b, kvh, chunk, hq0, split, HC, sm);
 }
 
 // ---------------------------------------------------------------------------
@@ -271,15 +343,18 @@ __device__ __forceinline__ u16x8 load_row8(const uint16_t* row, int col, int lim
 }
 
 template <int D, int DT, bool VEC>
-__global__ __launch_bounds__(256, 2) void decode_mfma_kernel(DecodeParams p) {
+__global__ __launch_bounds__(256, D == 64 ? 2 : 1) void decode_mfma_kernel(DecodeParams p) {
   typedef typename MfmaT<DT>::vec vec;
   constexpr int KS = D / 32;      // k-steps of the QK^T product
   constexpr int NB = D / 16;      // 16-dim output blocks
+  constexpr int KR = D / 16;      // 16-byte K loads per lane per tile
   constexpr int PITCH = 40;       // LDS row pitch (elements) of a 32-column K tile
   constexpr int HS = 16;          // head slots of the merge buffers
-  constexpr int KT_ELEMS = 4 * D * PITCH;              // 4 wave tiles (uint16)
-  constexpr int MERGE_FLOATS = 4 * HS * (D + 2);
-  constexpr int LDS_BYTES = (KT_ELEMS * 2 > MERGE_FLOATS * 4) ? KT_ELEMS * 2 : MERGE_FLOATS * 4;
+  constexpr int KT_BYTES = 4 * D * PITCH * 2;                   // 4 wave tiles (uint16)
+  constexpr int MERGE_BYTES = 4 * HS * (D + 2) * 4;
+  constexpr int FUSE_BYTES = (16 * kMaxFusedSplits + 16) * 4;
+  constexpr int LDS_A = KT_BYTES > MERGE_BYTES ? KT_BYTES : MERGE_BYTES;
+  constexpr int LDS_BYTES = LDS_A > FUSE_BYTES ? LDS_A : FUSE_BYTES;
   __shared__ __attribute__((aligned(16))) unsigned char lds_raw[LDS_BYTES];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -292,6 +367,29 @@ __global__ __launch_bounds__(256, 2) void decode_mfma_kernel(DecodeParams p) {
   const int L = p.seq_lens ? p.seq_lens[b] : p.seq_len;
   const int s0 = split * p.split_len;
   const int s1 = min(L, s0 + p.split_len);
+
+  const long long base = (long long)b * p.batch_stride + (long long)kvh * D * p.max_len;
+  const uint16_t* K = (const uint16_t*)p.k + base;
+  const uint16_t* V = (const uint16_t*)p.v + base;
+  uint16_t* kt = (uint16_t*)lds_raw + wave * D * PITCH;
+
+  // K tile: row = lane/4 + 16*r, 8 columns at 8*(lane&3); V operand: row
+  // 16*nb + c, columns t0+8g .. +7.
+  auto load_tile = [&](int t0, u16x8* kr, u16x8* vr) {
+#pragma unroll
+    for (int r = 0; r < KR; ++r) {
+      const int row = (lane >> 2) + 16 * r;
+      kr[r] = load_row8<VEC>(K + (long long)row * p.max_len, t0 + 8 * (lane & 3), s1);
+    }
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+      vr[nb] = load_row8<VEC>(V + (long long)(16 * nb + c) * p.max_len, t0 + 8 * g, s1);
+  };
+
+  // Issue the first tile's loads before anything else.
+  int t0 = s0 + wave * 32;
+  u16x8 kr[KR], vr[NB];
+  if (t0 < s1) load_tile(t0, kr, vr);
 
   // Q^T operand: lane (g, c) holds q[head c][32*ks + 8g + e], scaled, hi/lo.
   vec qh[KS], ql[KS];
@@ -312,32 +410,19 @@ __global__ __launch_bounds__(256, 2) void decode_mfma_kernel(DecodeParams p) {
     }
   }
 
-  const long long base = (long long)b * p.batch_stride + (long long)kvh * D * p.max_len;
-  const uint16_t* K = (const uint16_t*)p.k + base;
-  const uint16_t* V = (const uint16_t*)p.v + base;
-  uint16_t* kt = (uint16_t*)lds_raw + wave * D * PITCH;
-
   f32x4 o[NB];
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) o[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m_run = -INFINITY, l_run = 0.f;
 
-  for (int t0 = s0 + wave * 32; t0 < s1; t0 += 128) {
-    // Issue K tile loads (row = lane/4 + 16*r, 8 columns at 8*(lane&3)) and
-    // the V operand loads (row 16*nb + c, columns t0+8g .. +7).
-    u16x8 kr[D / 16];
-#pragma unroll
-    for (int r = 0; r < D / 16; ++r) {
-      const int row = (lane >> 2) + 16 * r;
-      kr[r] = load_row8<VEC>(K + (long long)row * p.max_len, t0 + 8 * (lane & 3), s1);
-    }
-    u16x8 vr[NB];
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb)
-      vr[nb] = load_row8<VEC>(V + (long long)(16 * nb + c) * p.max_len, t0 + 8 * g, s1);
+  for (; t0 < s1; t0 += 128) {
+    // prefetch the next tile of this wave
+    u16x8 krn[KR], vrn[NB];
+    const bool more = t0 + 128 < s1;
+    if (more) load_tile(t0 + 128, krn, vrn);
 
 #pragma unroll
-    for (int r = 0; r < D / 16; ++r) {
+    for (int r = 0; r < KR; ++r) {
       const int row = (lane >> 2) + 16 * r;
       *(u16x8*)(kt + row * PITCH + 8 * (lane & 3)) = kr[r];
     }
@@ -403,6 +488,13 @@ __global__ __launch_bounds__(256, 2) void decode_mfma_kernel(DecodeParams p) {
       o[nb] = MfmaT<DT>::mma(ph, bv, o[nb]);
       o[nb] = MfmaT<DT>::mma(pl, bv, o[nb]);
     }
+
+    if (more) {
+#pragma unroll
+      for (int r = 0; r < KR; ++r) kr[r] = krn[r];
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) vr[nb] = vrn[nb];
+    }
   }
 
   // Wave state -> LDS, then the 4-wave merge.
@@ -421,71 +513,93 @@ __global__ __launch_bounds__(256, 2) void decode_mfma_kernel(DecodeParams p) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) sm_o[(wave * HS + 4 * g + i) * D + 16 * nb + c] = o[nb][i];
   __syncthreads();
-  merge_waves_and_store<D>(p, sm_m, sm_l, sm_o, hc, b, hq0, split, HS);
-}
-
-// Folds the partials of all splits: one workgroup per (query head, sequence).
-__global__ __launch_bounds__(256) void decode_merge_kernel(DecodeParams p) {
-  const int hq = blockIdx.x, b = blockIdx.y;
-  const int D = p.head_dim, S = p.num_splits;
-  const long long row = (long long)b * p.n_head + hq;
-  const float* ml = p.ws_ml + row * S * 2;
-  __shared__ float sf[1024];
-  __shared__ float sinvl;
-  float M = -INFINITY;
-  for (int s = 0; s < S; ++s) M = fmaxf(M, ml[2 * s]);
-  // per-split weights (S <= 1024 enforced on the host)
-  for (int s = threadIdx.x; s < S; s += blockDim.x)
-    sf[s] = (M == -INFINITY) ? 0.f : fast_exp2(ml[2 * s] - M);
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    float l = 0.f;
-    for (int s = 0; s < S; ++s) l += sf[s] * ml[2 * s + 1];
-    sinvl = 1.f / l;
-  }
-  __syncthreads();
-  const float* wo = p.ws_o + row * S * D;
-  for (int d = threadIdx.x; d < D; d += blockDim.x) {
-    float o = 0.f;
-    for (int s = 0; s < S; ++s) o += sf[s] * wo[(long long)s * D + d];
-    p.out[row * D + d] = o * sinvl;
-  }
+  finish_workgroup<D>(p, sm_m, sm_l, sm_o, hc, b, kvh, chunk, hq0, split, HS, (float*)lds_raw);
 }
 
 // ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
-static int pick_splits(const hl_decode_args* a, int n_chunks, int tile_cols) {
-  if (a->num_splits > 0) return a->num_splits;
-  const int cols_per_iter = 4 * tile_cols;  // 4 waves
-  const long long units = (long long)a->batch * a->n_head_kv * n_chunks;
-  const int target = 2048;  // ~8 workgroups per CU on 256 CUs
-  int s = (int)((target + units - 1) / units);
-  const int max_s = (a->seq_len + cols_per_iter - 1) / cols_per_iter;
-  if (s > max_s) s = max_s;
-  if (s < 1) s = 1;
-  if (s > 1024) s = 1024;
-  return s;
+namespace {
+
+typedef void (*KernelFn)(DecodeParams);
+
+KernelFn pick_kernel(int kv_dtype, int D, bool vec) {
+  if (kv_dtype == HL_F32) return D == 64 ? decode_f32_kernel<64> : decode_f32_kernel<128>;
+  if (kv_dtype == HL_F16) {
+    if (D == 64) return vec ? decode_mfma_kernel<64, HL_F16, true> : decode_mfma_kernel<64, HL_F16, false>;
+    return vec ? decode_mfma_kernel<128, HL_F16, true> : decode_mfma_kernel<128, HL_F16, false>;
+  }
+  if (D == 64) return vec ? decode_mfma_kernel<64, HL_BF16, true> : decode_mfma_kernel<64, HL_BF16, false>;
+  return vec ? decode_mfma_kernel<128, HL_BF16, true> : decode_mfma_kernel<128, HL_BF16, false>;
 }
+
+// Resident workgroups of a kernel on the whole device (cached).
+int capacity(KernelFn fn) {
+  static std::mutex mu;
+  static std::map<std::pair<int, KernelFn>, int> cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 512;
+  std::lock_guard<std::mutex> lk(mu);
+  auto key = std::make_pair(dev, fn);
+  auto it = cache.find(key);
+  if (it != cache.end()) return it->second;
+  int per_cu = 0, cus = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void*)fn, 256, 0) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      per_cu <= 0 || cus <= 0) {
+    (void)hipGetLastError();
+    return 512;
+  }
+  cache[key] = per_cu * cus;
+  return per_cu * cus;
+}
+
+bool vec_path(const hl_decode_args* a) {
+  const long long stride = a->cache_batch_stride ? a->cache_batch_stride
+                                                 : (long long)a->n_head_kv * a->head_dim * a->max_len;
+  return a->kv_dtype != HL_F32 && (a->max_len % 8 == 0) && (stride % 8 == 0) &&
+         ((uintptr_t)a->k_cache & 15) == 0 && ((uintptr_t)a->v_cache & 15) == 0;
+}
+
+std::atomic<unsigned int> g_gen{0};
+
+}  // namespace
 
 void decode_plan(const hl_decode_args* a, DecodePlan* plan) {
   const int G = a->n_head / a->n_head_kv;
   plan->head_chunk = G < 16 ? G : 16;
   plan->n_chunks = (G + plan->head_chunk - 1) / plan->head_chunk;
+  plan->vec = vec_path(a);
   const int tile = a->kv_dtype == HL_F32 ? 64 : 32;
-  plan->num_splits = pick_splits(a, plan->n_chunks, tile);
-  const int per = 4 * tile;
-  int split_len = (a->seq_len + plan->num_splits - 1) / plan->num_splits;
-  split_len = (split_len + per - 1) / per * per;
-  plan->split_len = split_len;
-  plan->num_splits = (a->seq_len + split_len - 1) / split_len;
-  plan->ws_bytes = plan->num_splits > 1
-                       ? (size_t)a->batch * a->n_head * plan->num_splits * (a->head_dim + 2) * 4
-                       : 0;
+  const int tiles = (a->seq_len + tile - 1) / tile;
+  const long long units = (long long)a->batch * a->n_head_kv * plan->n_chunks;
+  int S;
+  if (a->num_splits > 0) {
+    S = a->num_splits;
+  } else {
+    // one full round of resident workgroups
+    const int cap = capacity(pick_kernel(a->kv_dtype, a->head_dim, plan->vec));
+    S = (int)(cap / units);
+    if (S < 1) S = 1;
+  }
+  if (S > tiles) S = tiles;
+  if (S > kMaxFusedSplits) S = kMaxFusedSplits;
+  const int tiles_per_split = (tiles + S - 1) / S;
+  plan->split_len = tiles_per_split * tile;
+  plan->num_splits = (a->seq_len + plan->split_len - 1) / plan->split_len;
+  if (plan->num_splits > 1) {
+    const size_t partial = (size_t)a->batch * a->n_head * plan->num_splits * (a->head_dim + 2) * 4;
+    const size_t slots_off = (partial + 7) / 8 * 8;
+    plan->slots_offset = slots_off;
+    plan->ws_bytes = slots_off + (size_t)units * 8;
+  } else {
+    plan->slots_offset = 0;
+    plan->ws_bytes = 0;
+  }
 }
 
 hipError_t decode_launch(const hl_decode_args* a, const DecodePlan* plan, void* ws,
-                         hipStream_t stream, bool vec_ok) {
+                         hipStream_t stream) {
   DecodeParams p;
   const int D = a->head_dim;
   p.q = a->q;
@@ -494,6 +608,7 @@ hipError_t decode_launch(const hl_decode_args* a, const DecodePlan* plan, void* 
   p.out = a->out;
   p.ws_o = (float*)ws;
   p.ws_ml = ws ? (float*)ws + (size_t)a->batch * a->n_head * plan->num_splits * D : nullptr;
+  p.slots = ws ? (unsigned long long*)((char*)ws + plan->slots_offset) : nullptr;
   p.seq_lens = a->seq_lens;
   p.batch_stride = a->cache_batch_stride ? a->cache_batch_stride
                                          : (long long)a->n_head_kv * D * a->max_len;
@@ -507,43 +622,17 @@ hipError_t decode_launch(const hl_decode_args* a, const DecodePlan* plan, void* 
   p.seq_len = a->seq_len;
   p.split_len = plan->split_len;
   p.num_splits = plan->num_splits;
-  p.direct = plan->num_splits == 1;
+  unsigned int gen;
+  do {
+    gen = g_gen.fetch_add(1) + 1;
+  } while (gen == 0);
+  p.gen = gen;
   const float scale = a->scale != 0.f ? a->scale : 1.0f / sqrtf((float)D);
   p.scale_log2 = scale * kLog2e;
 
   dim3 grid(plan->num_splits, a->n_head_kv * plan->n_chunks, a->batch);
-  dim3 block(256);
-#define HL_DEC_F32(DD) \
-  case DD: hipLaunchKernelGGL(decode_f32_kernel<DD>, grid, block, 0, stream, p); break;
-#define HL_DEC_MFMA(DD, DTT)                                                                 \
-  case DD:                                                                                   \
-    if (vec_ok) hipLaunchKernelGGL((decode_mfma_kernel<DD, DTT, true>), grid, block, 0, stream, p); \
-    else hipLaunchKernelGGL((decode_mfma_kernel<DD, DTT, false>), grid, block, 0, stream, p);      \
-    break;
-  if (a->kv_dtype == HL_F32) {
-    switch (D) {
-      HL_DEC_F32(64)
-      HL_DEC_F32(128)
-      default: return hipErrorInvalidValue;
-    }
-  } else if (a->kv_dtype == HL_F16) {
-    switch (D) {
-      HL_DEC_MFMA(64, HL_F16)
-      HL_DEC_MFMA(128, HL_F16)
-      default: return hipErrorInvalidValue;
-    }
-  } else {
-    switch (D) {
-      HL_DEC_MFMA(64, HL_BF16)
-      HL_DEC_MFMA(128, HL_BF16)
-      default: return hipErrorInvalidValue;
-    }
-  }
-#undef HL_DEC_F32
-#undef HL_DEC_MFMA
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess || p.direct) return e;
-  hipLaunchKernelGGL(decode_merge_kernel, dim3(a->n_head, a->batch), dim3(128), 0, stream, p);
+  KernelFn fn = pick_kernel(a->kv_dtype, D, plan->vec);
+  hipLaunchKernelGGL(fn, grid, dim3(256), 0, stream, p);
   return hipGetLastError();
 }
 

@@ -8,7 +8,7 @@
 //   storeKVKernel / storeKVPairKernel           :3228-3285
 // The reference launches one of these per tensor per layer (up to six per
 // attention layer); here one launch covers every head vector of a decode
-// step (headvec_kernel) or every (head, 32-token tile) of a prefill
+// step (headvec_kernel) or every (32-token tile, group of heads) of a prefill
 // (prologue_kernel), with the cache write and the conversion to the MFMA
 // operand layout done while the data is in registers/LDS.
 //
@@ -131,113 +131,205 @@ hipError_t headvec_launch(const HeadVecOp& op, hipStream_t stream) {
 }
 
 // ---------------------------------------------------------------------------
-// Prefill side: one workgroup per (head vector, 32-token tile) of col-major
-// [H*D, T] activations.  blockIdx.y: q heads, then k heads, then v heads.
+// Prefill side: one workgroup per (32-token tile, group of kHPG head vectors)
+// of col-major [H*D, T] activations.  Head vectors are numbered q heads, then
+// k heads, then v heads.  The workgroup evaluates cos/sin of its 32 positions
+// once (an LDS table of rope_dim/2 x 32 entries) and reuses it for every q/k
+// head of its group: RoPE's trigonometry is per (position, pair), not per
+// head, and with angles up to ~T rad it is the costly part of this kernel.
 // ---------------------------------------------------------------------------
-constexpr int kPT = 32;  // tokens per tile (LDS tile [256][33] floats = 33 KB)
+constexpr int kPT = 32;   // tokens per tile
+constexpr int kHPG = 8;   // head vectors per workgroup
+constexpr int kTabHalf = 64;  // largest rope_dim/2 served from the LDS table
+
+// 8 consecutive elements [t, t+8) of one activation row as fp32; t >= lim -> 0.
+template <int DT>
+__device__ __forceinline__ void load_row8_f32(const void* base, long long off, int t, int lim,
+                                              float* x) {
+  const int esz = DT == HL_F32 ? 4 : 2;
+  if (t + 8 <= lim && (((uintptr_t)base + (uintptr_t)off * esz) & 15) == 0) {
+    if constexpr (DT == HL_F32) {
+      const f32x4 a = *(const f32x4*)((const float*)base + off);
+      const f32x4 b = *(const f32x4*)((const float*)base + off + 4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        x[e] = a[e];
+        x[e + 4] = b[e];
+      }
+    } else {
+      const u16x8 v = *(const u16x8*)((const uint16_t*)base + off);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = from_bits<DT>(v[e]);
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = (t + e < lim) ? load_elem<DT>(base, off + e) : 0.f;
+  }
+}
+
+// Stores 8 consecutive elements [t, t+8) of one row; elements >= lim skipped.
+template <int DT>
+__device__ __forceinline__ void store_row8(void* base, long long off, int t, int lim,
+                                           const float* x) {
+  const int esz = DT == HL_F32 ? 4 : 2;
+  if (t + 8 <= lim && (((uintptr_t)base + (uintptr_t)off * esz) & 15) == 0) {
+    if constexpr (DT == HL_F32) {
+      *(f32x4*)((float*)base + off) = f32x4{x[0], x[1], x[2], x[3]};
+      *(f32x4*)((float*)base + off + 4) = f32x4{x[4], x[5], x[6], x[7]};
+    } else {
+      u16x8 v;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = to_bits<DT>(x[e]);
+      *(u16x8*)((uint16_t*)base + off) = v;
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      if (t + e < lim) store_elem<DT>(base, off + e, x[e]);
+  }
+}
 
 template <int IODT, int KDT>
 __global__ __launch_bounds__(256) void prologue_kernel(PrologueOp op) {
   __shared__ float sx[HL_MAX_HEAD_DIM][kPT + 1];
+  __shared__ float scos[kTabHalf][kPT], ssin[kTabHalf][kPT];
   __shared__ float sred[8][kPT];
   __shared__ float sinv[kPT];
   const int tid = threadIdx.x;
   const int T = op.seq_len, D = op.head_dim;
   const int t0 = blockIdx.x * kPT;
-  int hv = blockIdx.y;
-  int kind;
-  if (hv < op.n_head) {
-    kind = 0;
-  } else if (hv < op.n_head + op.n_head_kv) {
-    kind = 1;
-    hv -= op.n_head;
-  } else {
-    kind = 2;
-    hv -= op.n_head + op.n_head_kv;
-  }
-  const void* src = kind == 0 ? op.q : (kind == 1 ? op.k : op.v);
-  if (!src) return;
-  const float* nw = kind == 0 ? op.q_norm_w : (kind == 1 ? op.k_norm_w : nullptr);
-  const bool rope = op.do_rope && kind < 2;
-  const long long hbase = (long long)hv * D * T;
-
-  // load the [D, 32] tile (coalesced along tokens)
-  const int tc = tid & (kPT - 1), part = tid / kPT;  // 8 parts
+  const int n_vec = op.n_head + 2 * op.n_head_kv;
+  const int hv0 = blockIdx.y * kHPG;
+  const int hv1 = min(n_vec, hv0 + kHPG);
+  const int tc = tid & (kPT - 1), part = tid / kPT;  // 8 parts of 32 lanes
   const int t = t0 + tc;
-  for (int d = part; d < D; d += 8)
-    sx[d][tc] = (t < T) ? load_elem<IODT>(src, hbase + (long long)d * T + t) : 0.f;
-  __syncthreads();
+  const int half = op.rope_dim / 2;
+  const bool tab = op.do_rope && half <= kTabHalf && hv0 < op.n_head + op.n_head_kv;
 
-  if (nw) {
-    float ss = 0.f;
-    for (int d = part; d < D; d += 8) ss += sx[d][tc] * sx[d][tc];
-    sred[part][tc] = ss;
-    __syncthreads();
-    if (part == 0) {
-      float tot = 0.f;
-      for (int q = 0; q < 8; ++q) tot += sred[q][tc];
-      sinv[tc] = 1.0f / sqrtf(tot / (float)D + op.eps);
-    }
-    __syncthreads();
-    const float inv = sinv[tc];
-    for (int d = part; d < D; d += 8) sx[d][tc] = sx[d][tc] * inv * nw[d];
-    __syncthreads();
-  }
-  if (rope) {
-    const int half = op.rope_dim / 2;
+  if (tab) {
     const float pos = (float)(op.start_pos + t);
     for (int i = part; i < half; i += 8) {
-      int i0, i1;
-      rope_pair_index(i, half, op.rope_style, i0, i1);
       const float angle = pos * op.theta.t[i];
-      const float c = cosf(angle), s = sinf(angle);
-      const float v0 = sx[i0][tc], v1 = sx[i1][tc];
-      sx[i0][tc] = v0 * c - v1 * s;
-      sx[i1][tc] = v0 * s + v1 * c;
+      scos[i][tc] = cosf(angle);
+      ssin[i][tc] = sinf(angle);
+    }
+  }
+
+  for (int hv = hv0; hv < hv1; ++hv) {
+    int kind, h;
+    if (hv < op.n_head) {
+      kind = 0;
+      h = hv;
+    } else if (hv < op.n_head + op.n_head_kv) {
+      kind = 1;
+      h = hv - op.n_head;
+    } else {
+      kind = 2;
+      h = hv - op.n_head - op.n_head_kv;
+    }
+    const void* src = kind == 0 ? op.q : (kind == 1 ? op.k : op.v);
+    if (!src) continue;  // uniform across the workgroup
+    const float* nw = kind == 0 ? op.q_norm_w : (kind == 1 ? op.k_norm_w : nullptr);
+    const bool rope = op.do_rope && kind < 2;
+    const long long hbase = (long long)h * D * T;
+
+    __syncthreads();  // previous head's readers of sx are done
+    // load [D, 32]: thread -> (row, 8-token chunk), 64 rows per pass
+    for (int r = tid >> 2; r < D; r += 64) {
+      const int c8 = (tid & 3) * 8;
+      float x[8];
+      load_row8_f32<IODT>(src, hbase + (long long)r * T + t0 + c8, t0 + c8, T, x);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sx[r][c8 + e] = x[e];
     }
     __syncthreads();
-  }
 
-  // fp32 write-back in place (the reference's in-place semantics)
-  float* inplace = kind == 0 ? op.q_inplace : (kind == 1 ? op.k_inplace : nullptr);
-  if (inplace && t < T)
-    for (int d = part; d < D; d += 8) inplace[hbase + (long long)d * T + t] = sx[d][tc];
+    if (nw) {
+      float ss = 0.f;
+      for (int d = part; d < D; d += 8) ss += sx[d][tc] * sx[d][tc];
+      sred[part][tc] = ss;
+      __syncthreads();
+      if (part == 0) {
+        float tot = 0.f;
+        for (int q = 0; q < 8; ++q) tot += sred[q][tc];
+        sinv[tc] = 1.0f / sqrtf(tot / (float)D + op.eps);
+      }
+      __syncthreads();
+      const float inv = sinv[tc];
+      for (int d = part; d < D; d += 8) sx[d][tc] = sx[d][tc] * inv * nw[d];
+      __syncthreads();
+    }
+    if (rope) {
+      const float pos = (float)(op.start_pos + t);
+      for (int i = part; i < half; i += 8) {
+        int i0, i1;
+        rope_pair_index(i, half, op.rope_style, i0, i1);
+        float c, s;
+        if (tab) {
+          c = scos[i][tc];
+          s = ssin[i][tc];
+        } else {
+          const float angle = pos * op.theta.t[i];
+          c = cosf(angle);
+          s = sinf(angle);
+        }
+        const float v0 = sx[i0][tc], v1 = sx[i1][tc];
+        sx[i0][tc] = v0 * c - v1 * s;
+        sx[i1][tc] = v0 * s + v1 * c;
+      }
+      __syncthreads();
+    }
 
-  // KV-cache write, columns start_pos + t
-  void* cache = kind == 1 ? op.k_cache : (kind == 2 ? op.v_cache : nullptr);
-  if (cache && t < T) {
-    const long long cb = (long long)hv * D * op.max_len + op.start_pos + t;
-    for (int d = part; d < D; d += 8) store_elem<KDT>(cache, cb + (long long)d * op.max_len, sx[d][tc]);
-  }
-
-  // MFMA operand layouts (fp16 bits), pad rows t >= T written as zeros
-  if (kind < 2) {
-    uint16_t* dst = kind == 0 ? op.qt : op.kt;
-    if (dst) {
-      const float mul = kind == 0 ? op.qt_scale : 1.0f;
-      const int chunks = D / 8;
-      for (int idx = tid; idx < kPT * chunks; idx += 256) {
-        const int tt = idx / chunks, ch = idx % chunks;
-        const int tg = t0 + tt;
-        if (tg >= op.t_pad) continue;
-        u16x8 w;
+    // row-wise outputs: fp32 write-back in place, KV-cache columns start_pos + t
+    float* inplace = kind == 0 ? op.q_inplace : (kind == 1 ? op.k_inplace : nullptr);
+    void* cache = kind == 1 ? op.k_cache : (kind == 2 ? op.v_cache : nullptr);
+    if (inplace || cache) {
+      for (int r = tid >> 2; r < D; r += 64) {
+        const int c8 = (tid & 3) * 8;
+        float x[8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e)
-          w[e] = tg < T ? f32_to_f16_bits(sx[8 * ch + e][tt] * mul) : (uint16_t)0;
-        *(u16x8*)(dst + ((long long)hv * op.t_pad + tg) * D + 8 * ch) = w;
+        for (int e = 0; e < 8; ++e) x[e] = sx[r][c8 + e];
+        if (inplace) store_row8<HL_F32>(inplace, hbase + (long long)r * T + t0 + c8, t0 + c8, T, x);
+        if (cache)
+          store_row8<KDT>(cache, ((long long)h * D + r) * op.max_len + op.start_pos + t0 + c8,
+                          t0 + c8, T, x);
       }
     }
-  } else if (op.vt) {
-    const int tp = t0 + tc;
-    if (tp < op.t_pad)
-      for (int d = part; d < D; d += 8)
-        op.vt[((long long)hv * D + d) * op.t_pad + tp] = tp < T ? f32_to_f16_bits(sx[d][tc]) : 0;
+
+    // MFMA operand layouts (fp16 bits); pad rows t >= T are written as zeros
+    if (kind < 2) {
+      uint16_t* dst = kind == 0 ? op.qt : op.kt;
+      if (dst) {
+        const float mul = kind == 0 ? op.qt_scale : 1.0f;
+        const int chunks = D / 8;
+        for (int idx = tid; idx < kPT * chunks; idx += 256) {
+          const int tt = idx / chunks, ch = idx % chunks;
+          const int tg = t0 + tt;
+          if (tg >= op.t_pad) continue;
+          u16x8 w;
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            w[e] = tg < T ? f32_to_f16_bits(sx[8 * ch + e][tt] * mul) : (uint16_t)0;
+          *(u16x8*)(dst + ((long long)h * op.t_pad + tg) * D + 8 * ch) = w;
+        }
+      }
+    } else if (op.vt) {
+      for (int r = tid >> 2; r < D; r += 64) {
+        const int c8 = (tid & 3) * 8;
+        if (t0 + c8 >= op.t_pad) continue;
+        float x[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] = (t0 + c8 + e < T) ? sx[r][c8 + e] : 0.f;
+        store_row8<HL_F16>(op.vt, ((long long)h * D + r) * op.t_pad + t0 + c8, t0 + c8, op.t_pad, x);
+      }
+    }
   }
 }
 
 hipError_t prologue_launch(const PrologueOp& op, hipStream_t stream) {
   const int cols = op.t_pad > op.seq_len ? op.t_pad : op.seq_len;
-  dim3 grid((cols + kPT - 1) / kPT, op.n_head + 2 * op.n_head_kv);
+  const int n_vec = op.n_head + 2 * op.n_head_kv;
+  dim3 grid((cols + kPT - 1) / kPT, (n_vec + kHPG - 1) / kHPG);
 #define HL_PRO(IO, KD) hipLaunchKernelGGL((prologue_kernel<IO, KD>), grid, dim3(256), 0, stream, op)
 #define HL_PRO_IO(IO)                      \
   switch (op.kv_dtype) {                   \

@@ -189,8 +189,11 @@ typedef struct hl_decode_args {
   int num_splits;               /* 0 -> chosen to fill the GPU                   */
 } hl_decode_args;
 
-/* Workspace bytes hl_attn_decode needs for these args (split-K partials:
- * running max, sum and D accumulators per split per query head).        */
+/* Workspace bytes hl_attn_decode needs for these args: split-K partials
+ * (running max, sum and D accumulators per split per query head) and one
+ * 8-byte arrival counter per (sequence, kv head, 16-head chunk).  The
+ * contents need no initialisation and may be reused by other work between
+ * calls; calls that overlap in time must not share a workspace.          */
 size_t hl_attn_decode_workspace_bytes(const hl_decode_args* a);
 
 /* Decode attention for B sequences (the batched form of

@@ -198,3 +198,42 @@ def test_decode_reference_dropin_matches_batched(hl, orc):
     A.gpu_attention_decode(dst, qd, kd, vd, hq, hkv, d, L, max_len)
     torch.cuda.synchronize()
     assert rel_err(dst.cpu().numpy(), run_decode(qd, kd, vd, 1, hq, hkv, d, L, max_len)) < 1e-6
+
+
+@pytest.mark.parametrize("dt", [0, 2])
+def test_decode_workspace_garbage_reuse_and_graph_replay(hl, orc, dt):
+    """The fused split merge keeps arrival counters in the workspace: they need
+    no initialisation (garbage bytes), survive reuse with other split counts,
+    and graph replays (which repeat a call's generation) stay correct."""
+    from hippo_leap_amd import attention as A
+    B, hq, hkv, d, L, max_len = 3, 16, 4, 64, 900, 960
+    q, kb, vb = make_case(orc, B, hq, hkv, d, L, max_len, dt, 1000)
+    ref = oracle_decode(orc, q, kb, vb, B, hq, hkv, d, [L] * B, max_len, dt)
+    qd, kd, vd = torch.from_numpy(q).cuda(), dev_bits(kb, dt), dev_bits(vb, dt)
+    out = torch.full((B * hq * d,), float("nan"), device="cuda")
+    args = {ns: A.decode_args(qd, kd, vd, out, hq, hkv, d, max_len, L, num_splits=ns)
+            for ns in (5, 11, 0)}
+    nbytes = max(A.decode_workspace_bytes(a) for a in args.values())
+    ws = torch.full((nbytes,), 0xAB, dtype=torch.uint8, device="cuda")
+    tol = TOL_F32 if dt == 0 else TOL_LOWP
+    for ns in (5, 11, 0, 5):
+        out.fill_(float("nan"))
+        A.attn_decode(args[ns], ws)
+        torch.cuda.synchronize()
+        assert rel_err(out.cpu().numpy(), ref) < tol, ns
+        ws[: nbytes // 2].fill_(0x5C)  # clobber between calls (other work reusing it)
+    g = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        A.attn_decode(args[11], ws)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g):
+        A.attn_decode(args[11], ws)
+    for _ in range(4):
+        out.fill_(float("nan"))  # eager work between replays
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert rel_err(out.cpu().numpy(), ref) < tol
