@@ -477,7 +477,7 @@ int hl_rope_store_decode(const hl_rope_store_args* a, void* stream) {
 struct PrefillPlan {
   bool mfma;
   int t_pad;
-  size_t off_q, off_k, off_v, bytes;
+  size_t off_q, off_k, off_v, off_tab, bytes;
 };
 
 static int validate_prefill(const hl_prefill_args* a, PrefillPlan* pl) {
@@ -513,13 +513,19 @@ static int validate_prefill(const hl_prefill_args* a, PrefillPlan* pl) {
     pl->off_q = 0;
     pl->off_k = pl->off_q + (size_t)a->n_head * tp * D * 2;
     pl->off_v = pl->off_k + (size_t)a->n_head_kv * tp * D * 2;
-    pl->bytes = pl->off_v + (size_t)a->n_head_kv * tp * D * 2;
+    pl->off_tab = pl->off_v + (size_t)a->n_head_kv * tp * D * 2;
+    pl->bytes = pl->off_tab;
+    if (a->apply_rope) {  // (cos, sin) table [T][rope_dim/2]
+      const int rd = a->rope_dim ? a->rope_dim : a->head_dim;
+      pl->bytes += (size_t)T * (rd / 2) * 8;
+    }
   } else {
     pl->t_pad = a->seq_len;
     const bool pre = a->apply_rope || a->q_norm_w || a->k_norm_w;
     pl->off_q = 0;
     pl->off_k = (pre && !a->write_back_qk) ? (size_t)a->n_head * T * D * 4 : 0;
     pl->off_v = 0;
+    pl->off_tab = 0;
     pl->bytes = (pre && !a->write_back_qk) ? pl->off_k + (size_t)a->n_head_kv * T * D * 4 : 0;
   }
   return HL_OK;
@@ -582,6 +588,12 @@ int hl_attn_prefill(const hl_prefill_args* a, void* workspace, size_t ws_bytes, 
     op.kt = (uint16_t*)(ws + pl.off_k);
     op.vt = (uint16_t*)(ws + pl.off_v);
     op.qt_scale = scale * kLog2e;
+    if (a->apply_rope && rope_dim / 2 <= 64) {
+      float2* tab = (float2*)(ws + pl.off_tab);
+      if ((e = rope_table_launch(tab, op.theta, a->start_pos, a->seq_len, rope_dim / 2, st)) != hipSuccess)
+        return hip_fail(e, "rope table launch");
+      op.rope_tab = tab;
+    }
     if ((e = prologue_launch(op, st)) != hipSuccess) return hip_fail(e, "prefill prologue launch");
     pf.qt = op.qt;
     pf.kt = op.kt;

@@ -54,30 +54,53 @@ struct DecodeParams {
 
 constexpr int kMaxFusedSplits = 256;
 
+// Cross-workgroup exchange of the split partials.  The partials are small, so
+// they are written and read with relaxed agent-scope atomic stores/loads
+// (write-through / cache-bypassing accesses that are coherent across the
+// XCDs' separate L2s) instead of release/acquire fences, which on gfx950
+// write back and invalidate the whole L2 of the XCD for every workgroup.
+// Ordering: each thread waits for its partial stores to complete
+// (s_waitcnt vmcnt(0)) before the workgroup barrier that precedes the
+// arrival RMW; the merging workgroup issues its loads only after the RMW has
+// returned "last".
+__device__ __forceinline__ void store_agent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_agent(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void wait_stores() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);  // no compiler reordering across
+  __builtin_amdgcn_s_waitcnt(0x0F70);        // s_waitcnt vmcnt(0)
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
 // Registers this workgroup's partial; returns true in the last arrival.
 __device__ __forceinline__ bool arrive_last(unsigned long long* slot, unsigned int gen, int S) {
   __shared__ int s_last;
-  __threadfence();  // partials written by every thread are visible device-wide
+  wait_stores();
   __syncthreads();
   if (threadIdx.x == 0) {
     unsigned long long v = __hip_atomic_load(slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     unsigned long long nv;
     while (true) {
       nv = ((unsigned int)(v >> 32) == gen) ? v + 1 : (((unsigned long long)gen << 32) | 1ull);
-      unsigned long long prev = atomicCAS(slot, v, nv);
-      if (prev == v) break;
-      v = prev;
+      unsigned long long expected = v;
+      if (__hip_atomic_compare_exchange_strong(slot, &expected, nv, __ATOMIC_RELAXED,
+                                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
+        break;
+      v = expected;
     }
     s_last = (int)(nv & 0xFFFFFFFFull) >= S;
   }
   __syncthreads();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
   return s_last != 0;
 }
 
 // Workgroup epilogue shared by both kernels.  sm_m[w][h], sm_l[w][h] and
 // sm_o[w][h][D] hold the 4 waves' states for the hc heads of this chunk.
-// `lds_w` is scratch for the fused merge (>= 16 * kMaxFusedSplits floats,
-// may alias sm_*: it is used after they are consumed).
+// `lds_w` is unused scratch kept for the call signature.
 template <int D>
 __device__ void finish_workgroup(const DecodeParams& p, const float* sm_m, const float* sm_l,
                                  const float* sm_o, int hc, int b, int kvh, int chunk, int hq0,
@@ -103,46 +126,55 @@ __device__ void finish_workgroup(const DecodeParams& p, const float* sm_m, const
       p.out[row * D + d] = o / l;
     } else {
       const long long pi = row * S + split;
-      p.ws_o[pi * D + d] = o;
+      store_agent(&p.ws_o[pi * D + d], o);
       if (d == 0) {
-        p.ws_ml[pi * 2 + 0] = M;
-        p.ws_ml[pi * 2 + 1] = l;
+        store_agent(&p.ws_ml[pi * 2 + 0], M);
+        store_agent(&p.ws_ml[pi * 2 + 1], l);
       }
     }
   }
   if (S == 1) return;
   unsigned long long* slot = p.slots + ((long long)b * p.n_head_kv + kvh) * p.n_chunks + chunk;
   if (!arrive_last(slot, p.gen, S)) return;
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
 
-  // Fold all splits: weights w[h][s] = exp2(m_s - M_h) in LDS, then o[h][d].
-  float* sw = lds_w;                          // [16][S]
-  float* sinv = lds_w + 16 * kMaxFusedSplits;  // [16]
-  for (int h = tid >> 4; h < hc; h += 16) {   // 16 threads per head
-    const long long row = (long long)b * p.n_head + hq0 + h;
-    const float* ml = p.ws_ml + row * S * 2;
-    float M = -INFINITY;
-    for (int s = tid & 15; s < S; s += 16) M = fmaxf(M, ml[2 * s]);
-#pragma unroll
-    for (int o = 8; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 16));
-    float l = 0.f;
-    for (int s = tid & 15; s < S; s += 16) {
-      const float w = M == -INFINITY ? 0.f : fast_exp2(ml[2 * s] - M);
-      sw[h * kMaxFusedSplits + s] = w;
-      l += w * ml[2 * s + 1];
-    }
-#pragma unroll
-    for (int o = 8; o > 0; o >>= 1) l += __shfl_xor(l, o, 16);
-    if ((tid & 15) == 0) sinv[h] = 1.0f / l;
-  }
-  __syncthreads();
+  // Fold all splits, 8 at a time: each chunk's m, l and o loads are issued
+  // together (one memory round trip per 8 splits), then merged into a
+  // running (max, sum, accumulator) per output element.
+  (void)lds_w;
   for (int idx = tid; idx < hc * D; idx += 256) {
     const int h = idx / D, d = idx % D;
     const long long row = (long long)b * p.n_head + hq0 + h;
+    const float* ml = p.ws_ml + row * S * 2;
     const float* wo = p.ws_o + row * S * D + d;
-    float o = 0.f;
-    for (int s = 0; s < S; ++s) o += sw[h * kMaxFusedSplits + s] * wo[(long long)s * D];
-    p.out[row * D + d] = o * sinv[h];
+    float M = -INFINITY, lsum = 0.f, osum = 0.f;
+    for (int s0 = 0; s0 < S; s0 += 8) {
+      float m[8], l[8], x[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int sp = min(s0 + u, S - 1);
+        m[u] = load_agent(&ml[2 * sp]);
+        l[u] = load_agent(&ml[2 * sp + 1]);
+        x[u] = load_agent(&wo[(long long)sp * D]);
+      }
+      float mc = M;
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (s0 + u < S) mc = fmaxf(mc, m[u]);
+      if (mc == -INFINITY) continue;  // no columns so far (empty splits)
+      const float r = fast_exp2(M - mc);
+      lsum *= r;
+      osum *= r;
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        if (s0 + u < S) {
+          const float w = fast_exp2(m[u] - mc);
+          lsum += w * l[u];
+          osum += w * x[u];
+        }
+      }
+      M = mc;
+    }
+    p.out[row * D + d] = osum / lsum;
   }
   if (tid == 0) __hip_atomic_store(slot, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -330,15 +362,23 @@ __device__ __forceinline__ void split_hi_lo(const float* x, typename MfmaT<DT>::
 
 // Loads 8 consecutive 16-bit cache elements [col, col+8) of one row; columns
 // >= lim read as zero.  VEC: the 8 elements are 16-byte aligned.
+// VEC (rows 16-byte aligned, max_len % 8 == 0): one unconditional 16-byte
+// load at a column clamped into the row, so every wave issues the same loads
+// and the compiler can wait on exact counts; masking happens after the load.
 template <bool VEC>
-__device__ __forceinline__ u16x8 load_row8(const uint16_t* row, int col, int lim) {
+__device__ __forceinline__ u16x8 load_row8(const uint16_t* row, int col, int lim, int max_len) {
   u16x8 r;
-  if (VEC && col + 8 <= lim) {
-    r = *(const u16x8*)(row + col);
+  if (VEC) {
+    r = *(const u16x8*)(row + min(col, max_len - 8));
   } else {
 #pragma unroll
     for (int e = 0; e < 8; ++e) r[e] = (col + e < lim) ? row[col + e] : (uint16_t)0;
   }
+  return r;
+}
+__device__ __forceinline__ u16x8 mask_row8(u16x8 r, int col, int lim) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) r[e] = (col + e < lim) ? r[e] : (uint16_t)0;
   return r;
 }
 
@@ -379,17 +419,17 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void decode_mfma_kernel(Decod
 #pragma unroll
     for (int r = 0; r < KR; ++r) {
       const int row = (lane >> 2) + 16 * r;
-      kr[r] = load_row8<VEC>(K + (long long)row * p.max_len, t0 + 8 * (lane & 3), s1);
+      kr[r] = load_row8<VEC>(K + (long long)row * p.max_len, t0 + 8 * (lane & 3), s1, p.max_len);
     }
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb)
-      vr[nb] = load_row8<VEC>(V + (long long)(16 * nb + c) * p.max_len, t0 + 8 * g, s1);
+      vr[nb] = load_row8<VEC>(V + (long long)(16 * nb + c) * p.max_len, t0 + 8 * g, s1, p.max_len);
   };
 
   // Issue the first tile's loads before anything else.
   int t0 = s0 + wave * 32;
-  u16x8 kr[KR], vr[NB];
-  if (t0 < s1) load_tile(t0, kr, vr);
+  u16x8 ka[KR], va[NB], kb[KR], vb[NB];
+  if (t0 < s1) load_tile(t0, ka, va);
 
   // Q^T operand: lane (g, c) holds q[head c][32*ks + 8g + e], scaled, hi/lo.
   vec qh[KS], ql[KS];
@@ -415,12 +455,14 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void decode_mfma_kernel(Decod
   for (int nb = 0; nb < NB; ++nb) o[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m_run = -INFINITY, l_run = 0.f;
 
-  for (; t0 < s1; t0 += 128) {
-    // prefetch the next tile of this wave
-    u16x8 krn[KR], vrn[NB];
-    const bool more = t0 + 128 < s1;
-    if (more) load_tile(t0 + 128, krn, vrn);
-
+  // One 32-column tile whose K/V registers have been loaded.
+  auto compute = [&](int t0, u16x8* kr, u16x8* vr) {
+    if (VEC && t0 + 32 > s1) {  // boundary tile (wave-uniform): zero columns >= s1
+#pragma unroll
+      for (int r = 0; r < KR; ++r) kr[r] = mask_row8(kr[r], t0 + 8 * (lane & 3), s1);
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) vr[nb] = mask_row8(vr[nb], t0 + 8 * g, s1);
+    }
 #pragma unroll
     for (int r = 0; r < KR; ++r) {
       const int row = (lane >> 2) + 16 * r;
@@ -488,12 +530,29 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void decode_mfma_kernel(Decod
       o[nb] = MfmaT<DT>::mma(ph, bv, o[nb]);
       o[nb] = MfmaT<DT>::mma(pl, bv, o[nb]);
     }
+  };
 
-    if (more) {
-#pragma unroll
-      for (int r = 0; r < KR; ++r) kr[r] = krn[r];
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb) vr[nb] = vrn[nb];
+  // Two-stage pipeline over this wave's tiles (t0, t0+128, ...): buffers a and
+  // b alternate, and each branch below is uniform across the wave, so the
+  // loads of the next tile stay in flight while the current one computes.
+  if (t0 < s1) {
+    while (true) {
+      if (t0 + 128 < s1) {
+        load_tile(t0 + 128, kb, vb);
+        compute(t0, ka, va);
+        t0 += 128;
+      } else {
+        compute(t0, ka, va);
+        break;
+      }
+      if (t0 + 128 < s1) {
+        load_tile(t0 + 128, ka, va);
+        compute(t0, kb, vb);
+        t0 += 128;
+      } else {
+        compute(t0, kb, vb);
+        break;
+      }
     }
   }
 

@@ -70,8 +70,15 @@ struct PrologueOp {
   float qt_scale;     // multiplier folded into qt
   int t_pad;          // row count of qt/kt/vt (seq_len rounded up); pad rows zeroed
   ThetaTable theta;
+  const float2* rope_tab;  // optional [seq_len][rope_dim/2] (cos, sin) of positions start_pos + t
 };
 hipError_t prologue_launch(const PrologueOp& op, hipStream_t stream);
+
+// (cos, sin) of angle = float(start_pos + t) * theta[i] for t < T, i < half,
+// written as tab[t * half + i]; one evaluation per (position, pair) shared by
+// every head of a prefill.
+hipError_t rope_table_launch(float2* tab, const ThetaTable& theta, int start_pos, int T, int half,
+                             hipStream_t stream);
 
 // Plain column copy with dtype conversion: cache[r*cache_cols + start + c] =
 // src[r*src_cols + c] (two tensors when src2 != null).

@@ -27,6 +27,10 @@ namespace hl {
 namespace {
 constexpr int BN = 64;          // key columns per tile
 constexpr int QR = 32;          // query rows per wave
+// Lazy rescale: exponents are taken against a reference max that is only
+// raised when a row's max exceeds it by more than kRescale (log2 units), so
+// P <= 2^kRescale stays well inside fp16 and the O rescale is rare.
+constexpr float kRescale = 8.0f;
 }  // namespace
 
 int prefill_mfma_tpad(int seq_len) { return (seq_len + BN - 1) / BN * BN; }
@@ -47,14 +51,53 @@ __device__ __forceinline__ f32x16 mma32(f16x8 a, f16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) const void global_cvoid_t;
+
+// One 16-byte global -> LDS copy per lane; the LDS destination is
+// dst + 16 * lane (dst uniform across the wave).  No VGPRs are involved and
+// completion is tracked by vmcnt.
+__device__ __forceinline__ void copy16_to_lds(const void* src, void* dst_uniform) {
+  __builtin_amdgcn_global_load_lds((global_cvoid_t*)src, (lds_void_t*)dst_uniform, 16, 0, 0);
+}
+
+// MFMA output row m of a 32-row S^T block holds key sigma(m), where sigma
+// permutes groups of 4 rows: with m = 8a + 4h + e,
+// sigma(m) = 16*(a>>1) + 8h + 4*(a&1) + e.  The 32x32 MFMA output gives lane
+// half h the rows {8a + 4h + e}; under sigma those become, for each 16-key
+// k-step u (a = 2u, 2u+1), the 8 consecutive keys 16u + 8h .. 16u + 8h + 7,
+// which is exactly one 16-byte chunk of a V row: the P^T operand and the V
+// operand need no further shuffling.
+__device__ __forceinline__ int sigma_row(int m) {
+  const int a = m >> 3, h = (m >> 2) & 1, e = m & 3;
+  return 16 * (a >> 1) + 8 * h + 4 * (a & 1) + e;
+}
+
+// Each wave owns 32 query rows of one head.  Per 64-key tile:
+//   S^T[j][t] = K[j][:] . Q^T[:][t]     (v_mfma_f32_32x32x16_f16, K from LDS,
+//                                        Q^T in registers)
+//   online softmax over j for each row t (row t = lane % 32: in-lane plus one
+//                                        xor-32 exchange)
+//   O^T[d][t] += V^T[d][j] . P^T[j][t]  (V from LDS, P^T straight from the
+//                                        S^T registers as fp16)
+// The O^T formulation keeps each row's rescale factor a per-lane scalar.
+// K/V tiles go global -> LDS with direct (VGPR-free) copies into two stages;
+// tile i+2 is requested right after the one barrier that ends tile i.
+// LDS rows are stored with their 16-byte chunks XOR-swizzled by the row so
+// that the fragment reads (32 rows, one chunk each) hit distinct banks.
 template <int D, int ODT>
 __global__ __launch_bounds__(256, 2) void prefill_mfma_kernel(MfmaPrefillParams p) {
-  constexpr int KP = D + 8;        // K tile row pitch (fp16 elements)
-  constexpr int VP = BN + 8;       // V tile row pitch
-  constexpr int KSTEPS = D / 16;   // QK^T k-steps
-  constexpr int DB = D / 32;       // 32-dim blocks of O^T
-  __shared__ __attribute__((aligned(16))) uint16_t ks[BN * KP];
-  __shared__ __attribute__((aligned(16))) uint16_t vs[D * VP];
+  constexpr int KSTEPS = D / 16;    // QK^T k-steps
+  constexpr int DB = D / 32;        // 32-dim blocks of O^T
+  constexpr int KCPR = D / 8;       // 16-byte chunks per K row (key j: D dims)
+  constexpr int VCPR = BN / 8;      // 16-byte chunks per V row (dim d: BN keys)
+  constexpr int KT = BN * D;        // K stage elements
+  constexpr int VT = D * BN;        // V stage elements
+  constexpr int STAGE = KT + VT;
+  constexpr int KI = KT / 8 / 64 / 4;  // direct copies per wave per tile (K)
+  constexpr int VI = VT / 8 / 64 / 4;  // (V)
+  __shared__ __attribute__((aligned(1024))) uint16_t lds[2 * STAGE];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int hh = lane >> 5, ln = lane & 31;
@@ -72,8 +115,36 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma_kernel(MfmaPrefillParams 
   const int r0 = qblk * p.rows_wg + (wave / p.nh) * QR;  // this wave's first row
   const int wg_last_row = min(p.T - 1, qblk * p.rows_wg + p.rows_wg - 1);
   const int n_tiles = wg_last_row / BN + 1;
+  const bool live = r0 < p.T;
+  const int wave_tiles = live ? min(n_tiles, (r0 + QR - 1) / BN + 1) : 0;
 
-  // Q^T operand: lane holds q[t = r0 + ln][16*ks + 8*hh .. +7]
+  const uint16_t* kbase = p.kt + (long long)kvh * p.Tp * D;
+  const uint16_t* vbase = p.vt + (long long)kvh * D * p.Tp;
+
+  // Tile j0 -> stage: every wave copies KI + VI KB of the 2*BN*D*2-byte tile.
+  auto request_tile = [&](int j0, uint16_t* st) {
+#pragma unroll
+    for (int r = 0; r < KI; ++r) {
+      const int blk = wave * KI + r;            // 1 KB block of the K stage
+      const int j = blk * (64 / KCPR) + lane / KCPR;
+      const int slot = lane % KCPR;
+      const int c = slot ^ (j % KCPR);
+      copy16_to_lds(kbase + (long long)(j0 + j) * D + 8 * c, st + blk * 512);
+    }
+#pragma unroll
+    for (int r = 0; r < VI; ++r) {
+      const int blk = wave * VI + r;            // 1 KB block of the V stage
+      const int d = blk * (64 / VCPR) + lane / VCPR;
+      const int slot = lane % VCPR;
+      const int c = slot ^ (d % VCPR);
+      copy16_to_lds(vbase + (long long)d * p.Tp + j0 + 8 * c, st + KT + blk * 512);
+    }
+  };
+
+  request_tile(0, lds);
+  if (n_tiles > 1) request_tile(BN, lds + STAGE);
+
+  // Q^T operand: lane holds q[t = r0 + ln][16*k + 8*hh .. +7]
   f16x8 qf[KSTEPS];
   {
     const int t = min(r0 + ln, p.Tp - 1);
@@ -82,123 +153,126 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma_kernel(MfmaPrefillParams 
     for (int k = 0; k < KSTEPS; ++k) qf[k] = *(const f16x8*)(qrow + 16 * k + 8 * hh);
   }
 
-  const uint16_t* kbase = p.kt + (long long)kvh * p.Tp * D;
-  const uint16_t* vbase = p.vt + (long long)kvh * D * p.Tp;
-
-  // Register prefetch of one K tile (BN*D halves) and one V tile.
-  constexpr int KCH = BN * D / 8 / 256;  // 16-byte chunks per thread
-  constexpr int VCH = D * BN / 8 / 256;
-  u16x8 kreg[KCH], vreg[VCH];
-  auto load_tile = [&](int j0) {
-#pragma unroll
-    for (int c = 0; c < KCH; ++c) {
-      const int ch = tid + 256 * c;  // chunk index within the contiguous tile
-      kreg[c] = *(const u16x8*)(kbase + (long long)j0 * D + 8 * ch);
-    }
-#pragma unroll
-    for (int c = 0; c < VCH; ++c) {
-      const int ch = tid + 256 * c;
-      const int d = ch / (BN / 8), jc = ch % (BN / 8);
-      vreg[c] = *(const u16x8*)(vbase + (long long)d * p.Tp + j0 + 8 * jc);
-    }
-  };
-  auto store_tile = [&]() {
-#pragma unroll
-    for (int c = 0; c < KCH; ++c) {
-      const int ch = tid + 256 * c;
-      const int j = ch / (D / 8), dc = ch % (D / 8);
-      *(u16x8*)(ks + j * KP + 8 * dc) = kreg[c];
-    }
-#pragma unroll
-    for (int c = 0; c < VCH; ++c) {
-      const int ch = tid + 256 * c;
-      const int d = ch / (BN / 8), jc = ch % (BN / 8);
-      // columns 8*jc .. +7: j = 16q + 8a + e; slot(16q + 8a + 4b + e') = 16q + 8b + 4a + e'
-      const int q16 = jc >> 1, a = jc & 1;
-      uint16_t* row = vs + d * VP + 16 * q16 + 4 * a;
-      const u16x8 v = vreg[c];
-      typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
-      *(u16x4*)(row) = u16x4{v[0], v[1], v[2], v[3]};
-      *(u16x4*)(row + 8) = u16x4{v[4], v[5], v[6], v[7]};
-    }
-  };
-
   f32x16 o[DB];
 #pragma unroll
   for (int db = 0; db < DB; ++db)
 #pragma unroll
     for (int i = 0; i < 16; ++i) o[db][i] = 0.f;
   float m_run = -INFINITY, l_run = 0.f;
+  const f16x2 ones = {(_Float16)1.0f, (_Float16)1.0f};
   const int t_abs = r0 + ln;
 
-  load_tile(0);
+  // Per-lane LDS offsets (elements) of the fragments this lane reads.
+  int koff[2], voff[DB];
+#pragma unroll
+  for (int mb = 0; mb < 2; ++mb) {
+    const int j = 32 * mb + sigma_row(ln);
+    koff[mb] = j * D;  // chunk (2k + hh) ^ (j % KCPR) added per k-step
+  }
+#pragma unroll
+  for (int db = 0; db < DB; ++db) voff[db] = KT + (32 * db + ln) * BN;
+  const int kswz[2] = {(32 * 0 + sigma_row(ln)) % KCPR, (32 * 1 + sigma_row(ln)) % KCPR};
+  const int vswz = ln % VCPR;  // (32*db + ln) % 8 == ln % 8
+
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): tile 0 (and 1) landed for this wave
+  __syncthreads();
+
   for (int tile = 0; tile < n_tiles; ++tile) {
     const int j0 = tile * BN;
-    __syncthreads();
-    store_tile();
-    __syncthreads();
-    if (tile + 1 < n_tiles) load_tile(j0 + BN);
+    const uint16_t* st = lds + (tile & 1) * STAGE;
 
-    // skip tiles entirely above this wave's rows (causal)
-    if (j0 > r0 + QR - 1 || r0 >= p.T) continue;
+    if (tile < wave_tiles) {
+      // All K fragments first, then the two key-block MFMA chains interleaved.
+      f32x16 s[2];
+      f16x8 kf[2][KSTEPS];
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+        for (int k = 0; k < KSTEPS; ++k)
+          kf[mb][k] = *(const f16x8*)(st + koff[mb] + 8 * ((2 * k + hh) ^ kswz[mb]));
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) s[mb][i] = 0.f;
+#pragma unroll
+      for (int k = 0; k < KSTEPS; ++k)
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb) s[mb] = mma32(kf[mb][k], qf[k], s[mb]);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2 * KSTEPS, 0);  // LDS reads first
+      __builtin_amdgcn_sched_group_barrier(0x008, 2 * KSTEPS, 0);  // then the MFMAs
 
-    // S^T[j][t] for j in two 32-blocks
-    f32x16 s[2];
+      // causal mask on the diagonal tile only: key j > row t -> -inf
+      if (j0 + BN - 1 > r0) {
 #pragma unroll
-    for (int mb = 0; mb < 2; ++mb) {
+        for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) s[mb][i] = 0.f;
-      const uint16_t* krow = ks + (32 * mb + ln) * KP + 8 * hh;
-#pragma unroll
-      for (int k = 0; k < KSTEPS; ++k) {
-        const f16x8 a = *(const f16x8*)(krow + 16 * k);
-        s[mb] = mma32(a, qf[k], s[mb]);
+          for (int i = 0; i < 16; ++i) {
+            const int a = i >> 2;
+            const int j = j0 + 32 * mb + 16 * (a >> 1) + 8 * hh + 4 * (a & 1) + (i & 3);
+            s[mb][i] = j > t_abs ? -INFINITY : s[mb][i];
+          }
       }
-    }
-    // causal mask on the diagonal tile: j > t -> -inf
-    const bool diag = j0 + BN - 1 > r0;
-    float mt = -INFINITY;
+
+      float mt = -INFINITY;
 #pragma unroll
-    for (int mb = 0; mb < 2; ++mb)
+      for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int j = j0 + 32 * mb + 8 * (i >> 2) + 4 * hh + (i & 3);
-        if (diag && j > t_abs) s[mb][i] = -INFINITY;
-        mt = fmaxf(mt, s[mb][i]);
-      }
-    mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
-    const float mn = fmaxf(m_run, mt);
-    // mn is finite: column j0 <= t_abs is always unmasked for rows < T; rows
-    // >= T (padding) see their own finite scores of the zero pad.
-    const float alpha = fast_exp2(m_run - mn);
-    m_run = mn;
-    float ps = 0.f;
-    f16x8 pf[4];  // B operand of O^T = V^T P^T, one per 16-column k-step
+        for (int i = 0; i < 16; ++i) mt = fmaxf(mt, s[mb][i]);
+      mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+      // Every row t < T has an unmasked key j0 <= t in each tile it visits;
+      // rows >= T (padding) score their zero-padded q, so mt is finite.
+      const bool grew = mt > m_run + kRescale;
+      const float mn = grew ? mt : m_run;
+      f16x8 pf[4];  // P^T operands: k-step 2*mb + u holds keys 16(2mb+u) + 8hh + 0..7
+      float ps = 0.f;
 #pragma unroll
-    for (int mb = 0; mb < 2; ++mb)
+      for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-      for (int u = 0; u < 2; ++u)
+        for (int u = 0; u < 2; ++u) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float pv = fast_exp2(s[mb][8 * u + e] - mn);
-          ps += pv;
-          pf[2 * mb + u][e] = (_Float16)pv;
+          for (int e = 0; e < 8; ++e)
+            pf[2 * mb + u][e] = (_Float16)fast_exp2(s[mb][8 * u + e] - mn);
+          // row sum from the same fp16 values the MFMA consumes
+#pragma unroll
+          for (int e = 0; e < 8; e += 2) {
+            const f16x2 pr = {pf[2 * mb + u][e], pf[2 * mb + u][e + 1]};
+            ps = __builtin_amdgcn_fdot2(pr, ones, ps, false);
+          }
         }
-    l_run = l_run * alpha + ps;
+      // rescale only when some row's reference max moved (uniform test
+      // across the wave); on the first tile o and l are still zero
+      if (tile > 0 && __builtin_amdgcn_ballot_w64(grew) != 0) {
+        const float alpha = fast_exp2(m_run - mn);
+        l_run *= alpha;
 #pragma unroll
-    for (int db = 0; db < DB; ++db) {
+        for (int db = 0; db < DB; ++db)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) o[db][i] *= alpha;
-      const uint16_t* vrow = vs + (32 * db + ln) * VP + 8 * hh;
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const f16x8 a = *(const f16x8*)(vrow + 16 * k);
-        o[db] = mma32(a, pf[k], o[db]);
+          for (int i = 0; i < 16; ++i) o[db][i] *= alpha;
       }
+      m_run = mn;
+      l_run += ps;
+
+      // All V fragments, then DB independent MFMA chains interleaved.
+      f16x8 va[DB][4];
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+          va[db][u] = *(const f16x8*)(st + voff[db] + 8 * ((2 * u + hh) ^ vswz));
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int db = 0; db < DB; ++db) o[db] = mma32(va[db][u], pf[u], o[db]);
     }
+
+    // End of tile: every wave is done with this stage and its copies of the
+    // next tile have landed; then the stage is refilled with tile + 2.
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    __syncthreads();
+    if (tile + 2 < n_tiles) request_tile(j0 + 2 * BN, lds + (tile & 1) * STAGE);
   }
 
-  if (r0 >= p.T) return;
+  if (!live) return;
   const float l = l_run + __shfl_xor(l_run, 32, 64);
   const float inv = 1.0f / l;
   if (t_abs < p.T) {

@@ -207,16 +207,24 @@ __global__ __launch_bounds__(256) void prologue_kernel(PrologueOp op) {
   const bool tab = op.do_rope && half <= kTabHalf && hv0 < op.n_head + op.n_head_kv;
 
   if (tab) {
-    const float pos = (float)(op.start_pos + t);
-    for (int i = part; i < half; i += 8) {
-      const float angle = pos * op.theta.t[i];
-      scos[i][tc] = cosf(angle);
-      ssin[i][tc] = sinf(angle);
+    if (op.rope_tab) {  // precomputed by rope_table_kernel
+      for (int i = part; i < half; i += 8) {
+        const float2 cs = t < T ? op.rope_tab[(long long)t * half + i] : make_float2(1.f, 0.f);
+        scos[i][tc] = cs.x;
+        ssin[i][tc] = cs.y;
+      }
+    } else {
+      const float pos = (float)(op.start_pos + t);
+      for (int i = part; i < half; i += 8) {
+        const float angle = pos * op.theta.t[i];
+        scos[i][tc] = cosf(angle);
+        ssin[i][tc] = sinf(angle);
+      }
     }
   }
 
-  for (int hv = hv0; hv < hv1; ++hv) {
-    int kind, h;
+  // Head vector hv -> (kind, head index, source); kind 0 q, 1 k, 2 v.
+  auto decode_hv = [&](int hv, int& kind, int& h) {
     if (hv < op.n_head) {
       kind = 0;
       h = hv;
@@ -227,21 +235,57 @@ __global__ __launch_bounds__(256) void prologue_kernel(PrologueOp op) {
       kind = 2;
       h = hv - op.n_head - op.n_head_kv;
     }
-    const void* src = kind == 0 ? op.q : (kind == 1 ? op.k : op.v);
-    if (!src) continue;  // uniform across the workgroup
+  };
+  auto src_of = [&](int kind) { return kind == 0 ? op.q : (kind == 1 ? op.k : op.v); };
+  // Loads head hv's [D, 32] tile into registers: thread -> (row, 8-token
+  // chunk), 64 rows per pass, D <= 256 -> at most 4 passes.
+  constexpr int kPass = HL_MAX_HEAD_DIM / 64;
+  const int c8 = (tid & 3) * 8;
+  auto load_regs = [&](int hv, float (*x)[8]) {
+    int kind, h;
+    decode_hv(hv, kind, h);
+    const void* src = src_of(kind);
+    if (!src) return;
+    const long long hbase = (long long)h * D * T;
+#pragma unroll
+    for (int ps = 0; ps < kPass; ++ps) {
+      const int r = (tid >> 2) + 64 * ps;
+      if (r < D) load_row8_f32<IODT>(src, hbase + (long long)r * T + t0 + c8, t0 + c8, T, x[ps]);
+    }
+  };
+  float xa[kPass][8], xb[kPass][8];
+  if (hv0 < hv1) load_regs(hv0, xa);
+
+  for (int hv = hv0; hv < hv1; ++hv) {
+    int kind, h;
+    decode_hv(hv, kind, h);
+    const void* src = src_of(kind);
+    // prefetch the next head's tile while this one is processed
+    if (hv + 1 < hv1) load_regs(hv + 1, xb);
+    if (!src) {  // uniform across the workgroup
+#pragma unroll
+      for (int ps = 0; ps < kPass; ++ps)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) xa[ps][e] = xb[ps][e];
+      continue;
+    }
     const float* nw = kind == 0 ? op.q_norm_w : (kind == 1 ? op.k_norm_w : nullptr);
     const bool rope = op.do_rope && kind < 2;
     const long long hbase = (long long)h * D * T;
 
     __syncthreads();  // previous head's readers of sx are done
-    // load [D, 32]: thread -> (row, 8-token chunk), 64 rows per pass
-    for (int r = tid >> 2; r < D; r += 64) {
-      const int c8 = (tid & 3) * 8;
-      float x[8];
-      load_row8_f32<IODT>(src, hbase + (long long)r * T + t0 + c8, t0 + c8, T, x);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) sx[r][c8 + e] = x[e];
+    for (int ps = 0; ps < kPass; ++ps) {
+      const int r = (tid >> 2) + 64 * ps;
+      if (r < D) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sx[r][c8 + e] = xa[ps][e];
+      }
     }
+#pragma unroll
+    for (int ps = 0; ps < kPass; ++ps)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) xa[ps][e] = xb[ps][e];
     __syncthreads();
 
     if (nw) {
@@ -285,7 +329,6 @@ __global__ __launch_bounds__(256) void prologue_kernel(PrologueOp op) {
     void* cache = kind == 1 ? op.k_cache : (kind == 2 ? op.v_cache : nullptr);
     if (inplace || cache) {
       for (int r = tid >> 2; r < D; r += 64) {
-        const int c8 = (tid & 3) * 8;
         float x[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) x[e] = sx[r][c8 + e];
@@ -315,7 +358,6 @@ __global__ __launch_bounds__(256) void prologue_kernel(PrologueOp op) {
       }
     } else if (op.vt) {
       for (int r = tid >> 2; r < D; r += 64) {
-        const int c8 = (tid & 3) * 8;
         if (t0 + c8 >= op.t_pad) continue;
         float x[8];
 #pragma unroll
@@ -344,6 +386,23 @@ hipError_t prologue_launch(const PrologueOp& op, hipStream_t stream) {
   }
 #undef HL_PRO_IO
 #undef HL_PRO
+  return hipGetLastError();
+}
+
+__global__ __launch_bounds__(256) void rope_table_kernel(float2* tab, ThetaTable theta, int start_pos,
+                                                         int T, int half) {
+  const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (long long)T * half) return;
+  const int t = (int)(idx / half), i = (int)(idx % half);
+  const float angle = (float)(start_pos + t) * theta.t[i];
+  tab[idx] = make_float2(cosf(angle), sinf(angle));
+}
+
+hipError_t rope_table_launch(float2* tab, const ThetaTable& theta, int start_pos, int T, int half,
+                             hipStream_t stream) {
+  const long long n = (long long)T * half;
+  hipLaunchKernelGGL(rope_table_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, tab,
+                     theta, start_pos, T, half);
   return hipGetLastError();
 }
 

@@ -116,6 +116,10 @@ def test_prefill_workspace_size(hl):
     a = _prefill_args()
     # qt [Hq][T][D] + kt [Hkv][T][D] + vt [Hkv][D][T] fp16
     assert hl.hl_attn_prefill_workspace_bytes(ctypes.byref(a)) == (32 + 8 + 8) * 4096 * 128 * 2
+    # with RoPE: plus the (cos, sin) table [T][rope_dim/2] of float2
+    r = _prefill_args(apply_rope=1, rope_base=5e5)
+    assert hl.hl_attn_prefill_workspace_bytes(ctypes.byref(r)) == \
+        (32 + 8 + 8) * 4096 * 128 * 2 + 4096 * 64 * 8
     f = _prefill_args(io_dtype=_lib.HL_F32)
     assert hl.hl_attn_prefill_workspace_bytes(ctypes.byref(f)) == 0  # no fused ops: none needed
 
