@@ -116,7 +116,7 @@ class DecodeWorkload:
         self.out = torch.empty(B * hq * d, device="cuda")
         self.args = [A.decode_args(self.q, kc, vc, self.out, hq, hkv, d, self.max_len, self.L)
                      for kc, vc in zip(self.kc, self.vc)]
-        self.ws = A.workspace(A.decode_workspace_bytes(self.args[0]))
+        self.ws = A.decode_workspace(self.args[0])
         self.kv_bytes = 2 * B * hkv * d * self.L * self.kc[0].element_size()  # columns < L
         self.flops = 4 * B * hq * d * self.L
 

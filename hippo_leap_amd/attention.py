@@ -155,6 +155,16 @@ def decode_workspace_bytes(args: DecodeArgs) -> int:
     return int(_lib.load().hl_attn_decode_workspace_bytes(ctypes.byref(args)))
 
 
+def decode_workspace(args: DecodeArgs, device="cuda", stream=None):
+    """Allocates and zero-initialises a decode workspace (None if not needed)."""
+    nbytes = decode_workspace_bytes(args)
+    if nbytes <= 0:
+        return None
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
+    check(_lib.load().hl_attn_decode_workspace_init(ws.data_ptr(), nbytes, _stream(stream)))
+    return ws
+
+
 def attn_decode(args: DecodeArgs, workspace=None, stream=None) -> None:
     """Batched split-K decode (hl_attn_decode); workspace is a uint8 device tensor."""
     ws = workspace.data_ptr() if workspace is not None else None

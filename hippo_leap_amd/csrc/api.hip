@@ -48,6 +48,7 @@ ThetaTable g_theta;
 struct DevWs {
   void* ptr = nullptr;
   size_t bytes = 0;
+  size_t zero_prefix = 0;  // leading bytes known to hold zero arrival counters
 };
 std::vector<DevWs> g_ws;
 
@@ -372,10 +373,17 @@ int hl_attn_decode(const hl_decode_args* a, void* workspace, size_t ws_bytes, vo
   decode_plan(a, &plan);
   if (plan.ws_bytes > 0 && (!workspace || ws_bytes < plan.ws_bytes))
     return fail(HL_EINVAL, "decode: workspace of %zu bytes needed, %zu given", plan.ws_bytes, ws_bytes);
-  if (plan.ws_bytes > 0 && ((uintptr_t)workspace & 7) != 0)
-    return fail(HL_EINVAL, "decode: workspace must be 8-byte aligned");
+  if (plan.ws_bytes > 0 && ((uintptr_t)workspace & 3) != 0)
+    return fail(HL_EINVAL, "decode: workspace must be 4-byte aligned");
   hipError_t e = decode_launch(a, &plan, workspace, as_stream(stream));
   return e == hipSuccess ? HL_OK : hip_fail(e, "decode launch");
+}
+
+int hl_attn_decode_workspace_init(void* workspace, size_t bytes, void* stream) {
+  if (bytes == 0) return HL_OK;
+  if (!workspace) return fail(HL_EINVAL, "decode workspace init: null pointer");
+  hipError_t e = zero_fill_launch(workspace, bytes, as_stream(stream));
+  return e == hipSuccess ? HL_OK : hip_fail(e, "workspace init launch");
 }
 
 int hl_gpu_attention_decode(float* dst, const float* q, const float* k_cache, const float* v_cache,
@@ -417,8 +425,18 @@ int hl_gpu_attention_decode(float* dst, const float* q, const float* k_cache, co
       size_t bytes = plan.ws_bytes < (1u << 20) ? (1u << 20) : plan.ws_bytes;
       e = hipMalloc(&w.ptr, bytes);
       if (e != hipSuccess) return hip_fail(e, "hipMalloc(decode workspace)");
+      e = hipMemset(w.ptr, 0, bytes);  // arrival counters start at zero
+      if (e != hipSuccess) return hip_fail(e, "hipMemset(decode workspace)");
       w.bytes = bytes;
+      w.zero_prefix = bytes;
     }
+    // Bytes past the previous call's counters held its partials: a call with
+    // a longer counter region clears the difference first.
+    if (plan.counters_bytes > w.zero_prefix) {
+      e = zero_fill_launch(w.ptr, plan.counters_bytes, as_stream(stream));
+      if (e != hipSuccess) return hip_fail(e, "decode workspace clear");
+    }
+    w.zero_prefix = plan.counters_bytes;
     ws = w.ptr;
   }
   hipError_t e = decode_launch(&a, &plan, ws, as_stream(stream));

@@ -19,7 +19,6 @@
 //
 // Softmax runs in base 2 (scores pre-multiplied by scale*log2 e), so
 // p = exp2(s - m) equals the reference's expf(score - max).
-#include <atomic>
 #include <map>
 #include <mutex>
 
@@ -29,13 +28,12 @@
 namespace hl {
 
 // Workspace layout (num_splits > 1):
+//   slots [(b*Hkv + kvh)*n_chunks + chunk]    uint32 arrival counters (first)
 //   ws_o  [((b*Hq + hq)*S + split)*D + d]     unnormalised sum p*v
 //   ws_ml [((b*Hq + hq)*S + split)*2 + {0,1}] running max (log2 units), sum
-//   slots [(b*Hkv + kvh)*n_chunks + chunk]    uint64 arrival counters
-// A counter holds (generation << 32 | arrivals).  The generation is a
-// per-call value that is never 0; the last arrival resets the counter to 0,
-// so the workspace needs no initialisation and graph replays (which repeat
-// the generation) start from 0 again.
+// The counters must be zero before the first call (hl_attn_decode_workspace_init);
+// the last arrival of every (sequence, kv head, chunk) resets its counter to
+// 0, so the workspace is ready for the next call (and for graph replays).
 struct DecodeParams {
   const float* q;
   const void* k;
@@ -43,12 +41,11 @@ struct DecodeParams {
   float* out;
   float* ws_o;
   float* ws_ml;
-  unsigned long long* slots;
+  unsigned int* slots;
   const int* seq_lens;
   long long batch_stride;
   int n_head, n_head_kv, head_dim, group, head_chunk, n_chunks;
   int max_len, seq_len, split_len, num_splits;
-  unsigned int gen;
   float scale_log2;
 };
 
@@ -76,22 +73,13 @@ __device__ __forceinline__ void wait_stores() {
 }
 
 // Registers this workgroup's partial; returns true in the last arrival.
-__device__ __forceinline__ bool arrive_last(unsigned long long* slot, unsigned int gen, int S) {
+__device__ __forceinline__ bool arrive_last(unsigned int* slot, int S) {
   __shared__ int s_last;
   wait_stores();
   __syncthreads();
   if (threadIdx.x == 0) {
-    unsigned long long v = __hip_atomic_load(slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    unsigned long long nv;
-    while (true) {
-      nv = ((unsigned int)(v >> 32) == gen) ? v + 1 : (((unsigned long long)gen << 32) | 1ull);
-      unsigned long long expected = v;
-      if (__hip_atomic_compare_exchange_strong(slot, &expected, nv, __ATOMIC_RELAXED,
-                                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
-        break;
-      v = expected;
-    }
-    s_last = (int)(nv & 0xFFFFFFFFull) >= S;
+    const unsigned int old = __hip_atomic_fetch_add(slot, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = old == (unsigned int)(S - 1);
   }
   __syncthreads();
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
@@ -134,8 +122,8 @@ __device__ void finish_workgroup(const DecodeParams& p, const float* sm_m, const
     }
   }
   if (S == 1) return;
-  unsigned long long* slot = p.slots + ((long long)b * p.n_head_kv + kvh) * p.n_chunks + chunk;
-  if (!arrive_last(slot, p.gen, S)) return;
+  unsigned int* slot = p.slots + ((long long)b * p.n_head_kv + kvh) * p.n_chunks + chunk;
+  if (!arrive_last(slot, S)) return;
 
   // Fold all splits, 8 at a time: each chunk's m, l and o loads are issued
   // together (one memory round trip per 8 splits), then merged into a
@@ -176,7 +164,7 @@ __device__ void finish_workgroup(const DecodeParams& p, const float* sm_m, const
     }
     p.out[row * D + d] = osum / lsum;
   }
-  if (tid == 0) __hip_atomic_store(slot, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (tid == 0) __hip_atomic_store(slot, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---------------------------------------------------------------------------
@@ -203,7 +191,7 @@ __global__ __launch_bounds__(256) void decode_f32_kernel(DecodeParams p) {
   const int split = blockIdx.x;
   const int L = p.seq_lens ? p.seq_lens[b] : p.seq_len;
   const int s0 = split * p.split_len;
-  const int s1 = min(L, s0 + p.split_len);
+  const int s1 = split == p.num_splits - 1 ? L : min(L, s0 + p.split_len);  // last split takes the rest
 
   const float* qb = p.q + ((long long)b * p.n_head + hq0) * D;
   for (int i = tid; i < HC * D; i += 256) {
@@ -382,8 +370,8 @@ __device__ __forceinline__ u16x8 mask_row8(u16x8 r, int col, int lim) {
   return r;
 }
 
-template <int D, int DT, bool VEC>
-__global__ __launch_bounds__(256, D == 64 ? 2 : 1) void decode_mfma_kernel(DecodeParams p) {
+template <int D, int DT, bool VEC, bool PIPE>
+__global__ __launch_bounds__(256, PIPE ? (D == 64 ? 2 : 1) : 4) void decode_mfma_kernel(DecodeParams p) {
   typedef typename MfmaT<DT>::vec vec;
   constexpr int KS = D / 32;      // k-steps of the QK^T product
   constexpr int NB = D / 16;      // 16-dim output blocks
@@ -406,7 +394,7 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void decode_mfma_kernel(Decod
   const int split = blockIdx.x;
   const int L = p.seq_lens ? p.seq_lens[b] : p.seq_len;
   const int s0 = split * p.split_len;
-  const int s1 = min(L, s0 + p.split_len);
+  const int s1 = split == p.num_splits - 1 ? L : min(L, s0 + p.split_len);  // last split takes the rest
 
   const long long base = (long long)b * p.batch_stride + (long long)kvh * D * p.max_len;
   const uint16_t* K = (const uint16_t*)p.k + base;
@@ -532,10 +520,20 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void decode_mfma_kernel(Decod
     }
   };
 
-  // Two-stage pipeline over this wave's tiles (t0, t0+128, ...): buffers a and
-  // b alternate, and each branch below is uniform across the wave, so the
-  // loads of the next tile stay in flight while the current one computes.
-  if (t0 < s1) {
+  // PIPE: two-stage pipeline over this wave's tiles (t0, t0+128, ...):
+  // buffers a and b alternate, and each branch below is uniform across the
+  // wave, so the loads of the next tile stay in flight while the current one
+  // computes.  !PIPE (about one tile per wave): no second buffer, fewer
+  // registers, more resident waves.
+  if (!PIPE) {
+    if (t0 < s1) {
+      compute(t0, ka, va);
+      for (t0 += 128; t0 < s1; t0 += 128) {
+        load_tile(t0, ka, va);
+        compute(t0, ka, va);
+      }
+    }
+  } else if (t0 < s1) {
     while (true) {
       if (t0 + 128 < s1) {
         load_tile(t0 + 128, kb, vb);
@@ -575,6 +573,25 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void decode_mfma_kernel(Decod
   finish_workgroup<D>(p, sm_m, sm_l, sm_o, hc, b, kvh, chunk, hq0, split, HS, (float*)lds_raw);
 }
 
+// Zero-fills a workspace (a kernel rather than a memset node, so that it can
+// be captured in a HIP graph).
+__global__ __launch_bounds__(256) void zero_fill_kernel(unsigned int* p, size_t n_words, unsigned char* tail,
+                                                        int n_tail) {
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n_words; i += (size_t)gridDim.x * 256) p[i] = 0u;
+  if (blockIdx.x == 0 && (int)threadIdx.x < n_tail) tail[threadIdx.x] = 0;
+}
+
+hipError_t zero_fill_launch(void* ws, size_t bytes, hipStream_t stream) {
+  const size_t words = bytes / 4;
+  const int n_tail = (int)(bytes % 4);
+  unsigned int blocks = (unsigned int)((words + 255) / 256);
+  if (blocks == 0) blocks = 1;
+  if (blocks > 4096) blocks = 4096;
+  hipLaunchKernelGGL(zero_fill_kernel, dim3(blocks), dim3(256), 0, stream, (unsigned int*)ws, words,
+                     (unsigned char*)ws + words * 4, n_tail);
+  return hipGetLastError();
+}
+
 // ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
@@ -582,14 +599,16 @@ namespace {
 
 typedef void (*KernelFn)(DecodeParams);
 
-KernelFn pick_kernel(int kv_dtype, int D, bool vec) {
+template <int D, int DT>
+KernelFn pick_mfma(bool vec, bool pipe) {
+  if (vec) return pipe ? decode_mfma_kernel<D, DT, true, true> : decode_mfma_kernel<D, DT, true, false>;
+  return pipe ? decode_mfma_kernel<D, DT, false, true> : decode_mfma_kernel<D, DT, false, false>;
+}
+
+KernelFn pick_kernel(int kv_dtype, int D, bool vec, bool pipe) {
   if (kv_dtype == HL_F32) return D == 64 ? decode_f32_kernel<64> : decode_f32_kernel<128>;
-  if (kv_dtype == HL_F16) {
-    if (D == 64) return vec ? decode_mfma_kernel<64, HL_F16, true> : decode_mfma_kernel<64, HL_F16, false>;
-    return vec ? decode_mfma_kernel<128, HL_F16, true> : decode_mfma_kernel<128, HL_F16, false>;
-  }
-  if (D == 64) return vec ? decode_mfma_kernel<64, HL_BF16, true> : decode_mfma_kernel<64, HL_BF16, false>;
-  return vec ? decode_mfma_kernel<128, HL_BF16, true> : decode_mfma_kernel<128, HL_BF16, false>;
+  if (kv_dtype == HL_F16) return D == 64 ? pick_mfma<64, HL_F16>(vec, pipe) : pick_mfma<128, HL_F16>(vec, pipe);
+  return D == 64 ? pick_mfma<64, HL_BF16>(vec, pipe) : pick_mfma<128, HL_BF16>(vec, pipe);
 }
 
 // Resident workgroups of a kernel on the whole device (cached).
@@ -620,8 +639,6 @@ bool vec_path(const hl_decode_args* a) {
          ((uintptr_t)a->k_cache & 15) == 0 && ((uintptr_t)a->v_cache & 15) == 0;
 }
 
-std::atomic<unsigned int> g_gen{0};
-
 }  // namespace
 
 void decode_plan(const hl_decode_args* a, DecodePlan* plan) {
@@ -629,30 +646,36 @@ void decode_plan(const hl_decode_args* a, DecodePlan* plan) {
   plan->head_chunk = G < 16 ? G : 16;
   plan->n_chunks = (G + plan->head_chunk - 1) / plan->head_chunk;
   plan->vec = vec_path(a);
-  const int tile = a->kv_dtype == HL_F32 ? 64 : 32;
+  const bool mfma = a->kv_dtype != HL_F32;
+  const int tile = mfma ? 32 : 64;
   const int tiles = (a->seq_len + tile - 1) / tile;
   const long long units = (long long)a->batch * a->n_head_kv * plan->n_chunks;
-  int S;
-  if (a->num_splits > 0) {
-    S = a->num_splits;
-  } else {
-    // one full round of resident workgroups
-    const int cap = capacity(pick_kernel(a->kv_dtype, a->head_dim, plan->vec));
-    S = (int)(cap / units);
-    if (S < 1) S = 1;
-  }
+  // Splits fill one round of resident workgroups.  When that leaves about one
+  // tile per wave, the register-light kernel (no prefetch buffer, more
+  // resident waves) is used.
+  auto splits_for = [&](bool pipe) {
+    if (a->num_splits > 0) return a->num_splits;
+    const int cap = capacity(pick_kernel(a->kv_dtype, a->head_dim, plan->vec, pipe));
+    int S = (int)(cap / units);
+    return S < 1 ? 1 : S;
+  };
+  int S = splits_for(false);
+  plan->pipe = !mfma ? false : (tiles / (S < tiles ? S : tiles) > 5);
+  if (plan->pipe) S = splits_for(true);
   if (S > tiles) S = tiles;
   if (S > kMaxFusedSplits) S = kMaxFusedSplits;
-  const int tiles_per_split = (tiles + S - 1) / S;
+  const int tiles_per_split = tiles / S;  // the last split also takes the remainder
   plan->split_len = tiles_per_split * tile;
-  plan->num_splits = (a->seq_len + plan->split_len - 1) / plan->split_len;
+  plan->num_splits = S;
   if (plan->num_splits > 1) {
+    // Counters first, so their place depends only on (batch, kv heads, head
+    // chunks) and not on the split count: a workspace shared by calls with
+    // different split counts keeps them where the previous call left them (zero).
+    plan->counters_bytes = ((size_t)units * 4 + 255) / 256 * 256;
     const size_t partial = (size_t)a->batch * a->n_head * plan->num_splits * (a->head_dim + 2) * 4;
-    const size_t slots_off = (partial + 7) / 8 * 8;
-    plan->slots_offset = slots_off;
-    plan->ws_bytes = slots_off + (size_t)units * 8;
+    plan->ws_bytes = plan->counters_bytes + partial;
   } else {
-    plan->slots_offset = 0;
+    plan->counters_bytes = 0;
     plan->ws_bytes = 0;
   }
 }
@@ -665,9 +688,9 @@ hipError_t decode_launch(const hl_decode_args* a, const DecodePlan* plan, void* 
   p.k = a->k_cache;
   p.v = a->v_cache;
   p.out = a->out;
-  p.ws_o = (float*)ws;
-  p.ws_ml = ws ? (float*)ws + (size_t)a->batch * a->n_head * plan->num_splits * D : nullptr;
-  p.slots = ws ? (unsigned long long*)((char*)ws + plan->slots_offset) : nullptr;
+  p.slots = (unsigned int*)ws;
+  p.ws_o = ws ? (float*)((char*)ws + plan->counters_bytes) : nullptr;
+  p.ws_ml = ws ? p.ws_o + (size_t)a->batch * a->n_head * plan->num_splits * D : nullptr;
   p.seq_lens = a->seq_lens;
   p.batch_stride = a->cache_batch_stride ? a->cache_batch_stride
                                          : (long long)a->n_head_kv * D * a->max_len;
@@ -681,16 +704,11 @@ hipError_t decode_launch(const hl_decode_args* a, const DecodePlan* plan, void* 
   p.seq_len = a->seq_len;
   p.split_len = plan->split_len;
   p.num_splits = plan->num_splits;
-  unsigned int gen;
-  do {
-    gen = g_gen.fetch_add(1) + 1;
-  } while (gen == 0);
-  p.gen = gen;
   const float scale = a->scale != 0.f ? a->scale : 1.0f / sqrtf((float)D);
   p.scale_log2 = scale * kLog2e;
 
   dim3 grid(plan->num_splits, a->n_head_kv * plan->n_chunks, a->batch);
-  KernelFn fn = pick_kernel(a->kv_dtype, D, plan->vec);
+  KernelFn fn = pick_kernel(a->kv_dtype, D, plan->vec, plan->pipe);
   hipLaunchKernelGGL(fn, grid, dim3(256), 0, stream, p);
   return hipGetLastError();
 }

@@ -13,12 +13,14 @@ namespace hl {
 struct DecodePlan {
   int head_chunk, n_chunks, num_splits, split_len;
   bool vec;             // 16-byte cache loads (fp16/bf16, aligned rows)
-  size_t slots_offset;  // byte offset of the arrival counters in the workspace
+  bool pipe;            // prefetching kernel (several tiles per wave)
+  size_t counters_bytes;  // arrival counters at the workspace start, partials after
   size_t ws_bytes;
 };
 void decode_plan(const hl_decode_args* a, DecodePlan* plan);
 hipError_t decode_launch(const hl_decode_args* a, const DecodePlan* plan, void* ws,
                          hipStream_t stream);
+hipError_t zero_fill_launch(void* ws, size_t bytes, hipStream_t stream);
 
 // ---- per-token head-vector ops (rope_store.hip) ---------------------------
 // One launch over B sequences x (Hq + 2*Hkv) head vectors of the new token:

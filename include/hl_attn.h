@@ -189,12 +189,24 @@ typedef struct hl_decode_args {
   int num_splits;               /* 0 -> chosen to fill the GPU                   */
 } hl_decode_args;
 
-/* Workspace bytes hl_attn_decode needs for these args: split-K partials
- * (running max, sum and D accumulators per split per query head) and one
- * 8-byte arrival counter per (sequence, kv head, 16-head chunk).  The
- * contents need no initialisation and may be reused by other work between
- * calls; calls that overlap in time must not share a workspace.          */
+/* Workspace bytes hl_attn_decode needs for these args: one 4-byte arrival
+ * counter per (sequence, kv head, 16-head chunk), rounded up to 256 bytes,
+ * then the split-K partials (running max, sum and D accumulators per split
+ * per query head).  The counters must be zero before the first call
+ * (hl_attn_decode_workspace_init on the freshly allocated workspace); every
+ * call leaves its counters zero again, so the workspace may be reused by
+ * calls with any split count as long as it holds no other data in between.
+ * A call whose counter region (batch x kv heads x head chunks) is larger than
+ * the previous call's on the same workspace needs another init first.
+ * Calls that overlap in time must not share a workspace.  Returns 0 when the
+ * plan needs no workspace (a single split).                              */
 size_t hl_attn_decode_workspace_bytes(const hl_decode_args* a);
+
+/* Zero-fills `bytes` of workspace on `stream` (a kernel, not a memset, so it
+ * may be captured in a HIP graph).  Call once after allocating a decode
+ * workspace.  No counterpart in the reference (its decode has no split-K
+ * workspace).                                                             */
+int hl_attn_decode_workspace_init(void* workspace, size_t bytes, void* stream);
 
 /* Decode attention for B sequences (the batched form of
  * gpuAttentionDecode, naive.nim:3369-3383).  `workspace` is device memory

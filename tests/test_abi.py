@@ -71,9 +71,9 @@ def test_decode_workspace_required(hl):
     assert need > 0
     assert hl.hl_attn_decode(ctypes.byref(a), None, 0, None) == _lib.HL_EINVAL
     assert "workspace" in _err(hl)
-    # partials: (D + 2) floats per split per query head per sequence, then one
-    # 8-byte arrival counter per (sequence, kv head)
-    assert (need - 8 * 8) % ((64 + 2) * 4 * 32) == 0
+    # one 4-byte arrival counter per (sequence, kv head), padded to 256 bytes,
+    # then (D + 2) floats per split per query head per sequence
+    assert (need - 256) % ((64 + 2) * 4 * 32) == 0
 
 
 def test_decode_null_pointer(hl):

@@ -27,7 +27,7 @@ def run_decode(q, kc, vc, B, hq, hkv, d, L, max_len, seq_lens=None, num_splits=0
     out = torch.full((B * hq * d,), float("nan"), device="cuda")
     a = A.decode_args(q, kc, vc, out, hq, hkv, d, max_len, L, seq_lens=seq_lens,
                       cache_batch_stride=stride, num_splits=num_splits)
-    ws = A.workspace(A.decode_workspace_bytes(a))
+    ws = A.decode_workspace(a)
     A.attn_decode(a, ws)
     torch.cuda.synchronize()
     return out.cpu().numpy()
@@ -201,10 +201,11 @@ def test_decode_reference_dropin_matches_batched(hl, orc):
 
 
 @pytest.mark.parametrize("dt", [0, 2])
-def test_decode_workspace_garbage_reuse_and_graph_replay(hl, orc, dt):
-    """The fused split merge keeps arrival counters in the workspace: they need
-    no initialisation (garbage bytes), survive reuse with other split counts,
-    and graph replays (which repeat a call's generation) stay correct."""
+def test_decode_workspace_reuse_and_graph_replay(hl, orc, dt):
+    """The fused split merge keeps arrival counters in the workspace: after
+    hl_attn_decode_workspace_init (the partials may hold garbage) every call
+    leaves them zero, so reuse with other split counts and graph replays stay
+    correct."""
     from hippo_leap_amd import attention as A
     B, hq, hkv, d, L, max_len = 3, 16, 4, 64, 900, 960
     q, kb, vb = make_case(orc, B, hq, hkv, d, L, max_len, dt, 1000)
@@ -212,16 +213,20 @@ def test_decode_workspace_garbage_reuse_and_graph_replay(hl, orc, dt):
     qd, kd, vd = torch.from_numpy(q).cuda(), dev_bits(kb, dt), dev_bits(vb, dt)
     out = torch.full((B * hq * d,), float("nan"), device="cuda")
     args = {ns: A.decode_args(qd, kd, vd, out, hq, hkv, d, max_len, L, num_splits=ns)
-            for ns in (5, 11, 0)}
+            for ns in (5, 11, 0, 16)}
     nbytes = max(A.decode_workspace_bytes(a) for a in args.values())
     ws = torch.full((nbytes,), 0xAB, dtype=torch.uint8, device="cuda")
+    hl.hl_attn_decode_workspace_init(ws.data_ptr(), nbytes, None)
+    torch.cuda.synchronize()
+    assert int(ws.sum()) == 0
     tol = TOL_F32 if dt == 0 else TOL_LOWP
-    for ns in (5, 11, 0, 5):
+    for ns in (5, 11, 0, 16, 5):
         out.fill_(float("nan"))
         A.attn_decode(args[ns], ws)
         torch.cuda.synchronize()
         assert rel_err(out.cpu().numpy(), ref) < tol, ns
-        ws[: nbytes // 2].fill_(0x5C)  # clobber between calls (other work reusing it)
+    # every call left the counters (the workspace head) at zero
+    assert int(ws[:B * hkv * 4].sum()) == 0
     g = torch.cuda.CUDAGraph()
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
@@ -237,3 +242,20 @@ def test_decode_workspace_garbage_reuse_and_graph_replay(hl, orc, dt):
         g.replay()
         torch.cuda.synchronize()
         assert rel_err(out.cpu().numpy(), ref) < tol
+
+
+def test_decode_dropin_shape_changes_share_library_workspace(hl, orc):
+    """The drop-in keeps one library workspace per device: a call with more
+    kv heads (a longer arrival-counter region) after calls whose partials
+    covered that region must still merge correctly, and so must the small
+    shape after it."""
+    from hippo_leap_amd import attention as A
+    d, L, max_len = 64, 900, 960
+    for hq, hkv in ((16, 2), (128, 128), (16, 2), (128, 128)):
+        q, kb, vb = make_case(orc, 1, hq, hkv, d, L, max_len, 0, 1100 + hkv)
+        dst = torch.full((hq * d,), float("nan"), device="cuda")
+        A.gpu_attention_decode(dst, *(torch.from_numpy(x).cuda() for x in (q, kb, vb)), hq, hkv,
+                               d, L, max_len)
+        torch.cuda.synchronize()
+        ref = oracle_decode(orc, q, kb, vb, 1, hq, hkv, d, [L], max_len, 0)
+        assert rel_err(dst.cpu().numpy(), ref) < TOL_F32, (hq, hkv)

@@ -155,7 +155,7 @@ def test_decode_step_golden(hl, orc, name):
                         q_norm_w=dev(g["wq"]), k_norm_w=dev(g["wk"]), eps=float(g["eps"][0]))
     out = torch.empty(hq * d, device="cuda")
     a = A.decode_args(qd, kc, vc, out, hq, hkv, d, M, prev + 1)
-    A.attn_decode(a, A.workspace(A.decode_workspace_bytes(a)))
+    A.attn_decode(a, A.decode_workspace(a))
     torch.cuda.synchronize()
     assert rel_err(host(out), g["expected"]) < 2e-4
 
