@@ -117,6 +117,10 @@ class DecodeWorkload:
         self.args = [A.decode_args(self.q, kc, vc, self.out, hq, hkv, d, self.max_len, self.L)
                      for kc, vc in zip(self.kc, self.vc)]
         self.ws = A.decode_workspace(self.args[0])
+        self.rs = [A.rope_store_args(self.q, self.k, self.v, kc, vc, hq, hkv, d, self.max_len, prev,
+                                     base, q_norm_w=self.wq, k_norm_w=self.wk, eps=1e-6)
+                   for kc, vc in zip(self.kc, self.vc)]
+        self.step_ws = A.decode_step_workspace(self.rs[0], self.args[0])
         self.kv_bytes = 2 * B * hkv * d * self.L * self.kc[0].element_size()  # columns < L
         self.flops = 4 * B * hq * d * self.L
 
@@ -129,13 +133,20 @@ class DecodeWorkload:
     def attend(self, i):
         self.A.attn_decode(self.args[i % len(self.args)], self.ws)
 
-    def step(self, i):
+    def two_calls(self, i):
         self.rope_store(i)
         self.attend(i)
 
+    def step(self, i):
+        """One fused launch: qkNorm + RoPE + cache store + attention."""
+        s = i % len(self.args)
+        self.A.decode_step(self.rs[s], self.args[s], self.step_ws)
+
 
 def bench_decode(torch, A, wl, steps, warmup):
-    """Returns (step ms, attention ms, rope+store ms, eager step ms).
+    """Returns a dict of ms: the timed step (host clock), the step kernel
+    (HIP events over a graph of steps), attention alone, rope+store alone,
+    the two-call step, and the eager step.
 
     The W warmup and K timed steps are each captured into a HIP graph (as a
     serving loop would run them); the timed graph is bracketed by
@@ -148,10 +159,10 @@ def bench_decode(torch, A, wl, steps, warmup):
     gt.replay()
     torch.cuda.synchronize()
     step_ms = (time.perf_counter() - t0) * 1e3 / steps
-    attn_ms = graph_time_ms(torch, wl.attend)
-    rs_ms = graph_time_ms(torch, wl.rope_store)
-    eager_ms = event_time_ms(torch, wl.step, 20)
-    return step_ms, attn_ms, rs_ms, eager_ms
+    return {"step": step_ms, "kernel": graph_time_ms(torch, wl.step),
+            "attn": graph_time_ms(torch, wl.attend), "rope_store": graph_time_ms(torch, wl.rope_store),
+            "two_calls": graph_time_ms(torch, wl.two_calls),
+            "eager": event_time_ms(torch, wl.step, 20)}
 
 
 # ---------------------------------------------------------------------------
@@ -240,26 +251,32 @@ def main():
         wl = DecodeWorkload(torch, A, B=8, hq=32, hkv=8, d=64, prev=2048,
                             kv_dtype=torch.float16, sigma=0.5, base=5e5, n_sets=16,
                             qknorm=False, seed=3)
-        step_ms, attn_ms, rs_ms, eager_ms = bench_decode(torch, A, wl, args.steps, args.warmup)
+        t = bench_decode(torch, A, wl, args.steps, args.warmup)
+        step_ms = t["step"]
         value = wl.kv_bytes / (step_ms * 1e-3) / 1e9
-        achieved = wl.kv_bytes / (attn_ms * 1e-3) / 1e9
+        achieved = wl.kv_bytes / (t["kernel"] * 1e-3) / 1e9
         result.update({
             "value": round(value, 2), "unit": "GB/s", "ms_per_step": round(step_ms, 5),
             "dtype": "f16",
             "config": {"workload": "c3: Llama-3.2-1B-shape batched decode, fp16 KV", "batch": 8,
                        "cached_positions": 2048, "attn_len": 2049, "n_head": 32, "n_head_kv": 8,
                        "head_dim": 64, "rope_theta": 5e5, "kv_sigma": 0.5,
-                       "rotating_cache_sets": 16, "step": "rope_store_decode + attn_decode"},
-            "roofline": {"bound": "hbm", "kernel": "decode_mfma_kernel + decode_merge_kernel",
+                       "rotating_cache_sets": 16,
+                       "step": "hl_decode_step (qkNorm/RoPE + KV store + split-K attention, "
+                               "one launch)"},
+            "roofline": {"bound": "hbm", "kernel": "decode_mfma_kernel (fused step)",
                          "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(achieved / HBM_PEAK_GBS, 4),
                          "traffic": None, "algorithmic_bytes": wl.kv_bytes,
-                         "avg_us": round(attn_ms * 1e3, 3)},
-            "rope_store_us": round(rs_ms * 1e3, 3),
-            "eager_ms_per_step": round(eager_ms, 5),
+                         "avg_us": round(t["kernel"] * 1e3, 3)},
+            "attention_only_us": round(t["attn"] * 1e3, 3),
+            "rope_store_only_us": round(t["rope_store"] * 1e3, 3),
+            "two_call_step_us": round(t["two_calls"] * 1e3, 3),
+            "eager_ms_per_step": round(t["eager"], 5),
         })
-        log(f"decode c3: step {step_ms*1e3:.2f} us, attention {attn_ms*1e3:.2f} us "
-            f"({achieved:.0f} GB/s), rope+store {rs_ms*1e3:.2f} us")
+        log(f"decode c3: step {step_ms*1e3:.2f} us, step kernel {t['kernel']*1e3:.2f} us "
+            f"({achieved:.0f} GB/s), attention alone {t['attn']*1e3:.2f} us, rope+store "
+            f"{t['rope_store']*1e3:.2f} us, two calls {t['two_calls']*1e3:.2f} us")
         del wl
         torch.cuda.empty_cache()
 
@@ -290,8 +307,9 @@ def main():
         wl = DecodeWorkload(torch, A, B=16, hq=32, hkv=4, d=128, prev=32768,
                             kv_dtype=torch.bfloat16, sigma=1.0, base=1e6, n_sets=1,
                             qknorm=True, seed=5)
-        step_ms, attn_ms, rs_ms, _ = bench_decode(torch, A, wl, max(10, args.steps // 4), 3)
-        ach = wl.kv_bytes / (attn_ms * 1e-3) / 1e9
+        t = bench_decode(torch, A, wl, max(10, args.steps // 4), 3)
+        step_ms = t["step"]
+        ach = wl.kv_bytes / (t["kernel"] * 1e-3) / 1e9
         result["decode_c5"] = {
             "workload": "c5: Qwen3-30B-A3B-shape decode, bf16 KV, B=16, L=32769, Hq32/Hkv4, "
                         "D128, qkNorm + RoPE 1e6",
@@ -299,9 +317,12 @@ def main():
             "ms_per_step": round(step_ms, 5),
             "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS,
                          "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),
-                         "algorithmic_bytes": wl.kv_bytes, "avg_us": round(attn_ms * 1e3, 3)},
+                         "algorithmic_bytes": wl.kv_bytes, "avg_us": round(t["kernel"] * 1e3, 3)},
+            "attention_only_us": round(t["attn"] * 1e3, 3),
+            "two_call_step_us": round(t["two_calls"] * 1e3, 3),
         }
-        log(f"decode c5: step {step_ms*1e3:.1f} us, attention {attn_ms*1e3:.1f} us ({ach:.0f} GB/s)")
+        log(f"decode c5: step {step_ms*1e3:.1f} us, step kernel {t['kernel']*1e3:.1f} us "
+            f"({ach:.0f} GB/s), attention alone {t['attn']*1e3:.1f} us")
         del wl
         torch.cuda.empty_cache()
 

@@ -100,6 +100,10 @@ SIGNATURES = {
     "hl_attn_decode": (c_int, [ctypes.POINTER(DecodeArgs), c_void_p, c_size_t, c_void_p]),
     "hl_attn_decode_workspace_init": (c_int, [c_void_p, c_size_t, c_void_p]),
     "hl_rope_store_decode": (c_int, [ctypes.POINTER(RopeStoreArgs), c_void_p]),
+    "hl_decode_step_workspace_bytes": (c_size_t, [ctypes.POINTER(RopeStoreArgs),
+                                                  ctypes.POINTER(DecodeArgs)]),
+    "hl_decode_step": (c_int, [ctypes.POINTER(RopeStoreArgs), ctypes.POINTER(DecodeArgs), c_void_p,
+                               c_size_t, c_void_p]),
     "hl_attn_prefill_workspace_bytes": (c_size_t, [ctypes.POINTER(PrefillArgs)]),
     "hl_attn_prefill": (c_int, [ctypes.POINTER(PrefillArgs), c_void_p, c_size_t, c_void_p]),
     "hl_kv_cache_to_f32": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p]),

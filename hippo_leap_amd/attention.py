@@ -148,6 +148,7 @@ def decode_args(q, k_cache, v_cache, out, n_head, n_head_kv, head_dim, max_len, 
     a.cache_batch_stride = cache_batch_stride
     a.q, a.k_cache, a.v_cache, a.out = q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), out.data_ptr()
     a.scale, a.num_splits = scale, num_splits
+    a._tensors = (q, k_cache, v_cache, out, seq_lens)  # the struct holds raw pointers into these
     return a
 
 
@@ -172,10 +173,10 @@ def attn_decode(args: DecodeArgs, workspace=None, stream=None) -> None:
     check(_lib.load().hl_attn_decode(ctypes.byref(args), ws, nbytes, _stream(stream)))
 
 
-def rope_store_decode(q, k, v, k_cache, v_cache, n_head_q, n_head_kv, head_dim, max_len, pos,
-                      rope_base, rope_dim=0, rope_style=HL_ROPE_HALF_SPLIT, positions=None,
-                      q_norm_w=None, k_norm_w=None, eps=1e-6, cache_batch_stride=0,
-                      use_installed_theta=False, stream=None) -> None:
+def rope_store_args(q, k, v, k_cache, v_cache, n_head_q, n_head_kv, head_dim, max_len, pos,
+                    rope_base, rope_dim=0, rope_style=HL_ROPE_HALF_SPLIT, positions=None,
+                    q_norm_w=None, k_norm_w=None, eps=1e-6, cache_batch_stride=0,
+                    use_installed_theta=False) -> RopeStoreArgs:
     a = RopeStoreArgs()
     a.batch = q.numel() // (n_head_q * head_dim)
     a.n_head_q, a.n_head_kv, a.head_dim = n_head_q, n_head_kv, head_dim
@@ -189,7 +190,33 @@ def rope_store_decode(q, k, v, k_cache, v_cache, n_head_q, n_head_kv, head_dim, 
     a.q_norm_w = q_norm_w.data_ptr() if q_norm_w is not None else None
     a.k_norm_w = k_norm_w.data_ptr() if k_norm_w is not None else None
     a.eps = eps
+    a._tensors = (q, k, v, k_cache, v_cache, positions, q_norm_w, k_norm_w)
+    return a
+
+
+def rope_store_decode(*args, stream=None, **kw) -> None:
+    """hl_rope_store_decode; arguments as rope_store_args."""
+    a = rope_store_args(*args, **kw)
     check(_lib.load().hl_rope_store_decode(ctypes.byref(a), _stream(stream)))
+
+
+def decode_step_workspace(rs: RopeStoreArgs, at: DecodeArgs, device="cuda", stream=None):
+    """Allocates and zero-initialises the workspace of hl_decode_step (None if not needed)."""
+    lib = _lib.load()
+    nbytes = int(lib.hl_decode_step_workspace_bytes(ctypes.byref(rs), ctypes.byref(at)))
+    if nbytes <= 0:
+        return None
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
+    check(lib.hl_attn_decode_workspace_init(ws.data_ptr(), nbytes, _stream(stream)))
+    return ws
+
+
+def decode_step(rs: RopeStoreArgs, at: DecodeArgs, workspace=None, stream=None) -> None:
+    """hl_decode_step: qkNorm + RoPE + KV store + attention for the new token."""
+    ws = workspace.data_ptr() if workspace is not None else None
+    nbytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    check(_lib.load().hl_decode_step(ctypes.byref(rs), ctypes.byref(at), ws, nbytes,
+                                     _stream(stream)))
 
 
 def prefill_args(q, k, v, out, n_head, n_head_kv, head_dim, seq_len, rope_base=0.0,
@@ -212,6 +239,7 @@ def prefill_args(q, k, v, out, n_head, n_head_kv, head_dim, seq_len, rope_base=0
     a.max_len, a.start_pos, a.scale = max_len, start_pos, scale
     a.write_back_qk = int(write_back_qk)
     a.out_dtype = dtype_code(out)
+    a._tensors = (q, k, v, out, q_norm_w, k_norm_w, k_cache, v_cache)
     return a
 
 

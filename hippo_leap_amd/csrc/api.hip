@@ -446,7 +446,7 @@ int hl_gpu_attention_decode(float* dst, const float* q, const float* k_cache, co
 // ---------------------------------------------------------------------------
 // Decode-side fused qkNorm + RoPE + KV store
 // ---------------------------------------------------------------------------
-int hl_rope_store_decode(const hl_rope_store_args* a, void* stream) {
+static int rope_store_op(const hl_rope_store_args* a, HeadVecOp& op) {
   if (!a) return fail(HL_EINVAL, "rope_store: args is null");
   int rc = check_gqa(a->n_head_q, a->n_head_kv);
   if (rc) return rc;
@@ -460,7 +460,6 @@ int hl_rope_store_decode(const hl_rope_store_args* a, void* stream) {
   const long long dense = (long long)a->n_head_kv * a->head_dim * a->max_len;
   if (a->cache_batch_stride != 0 && a->cache_batch_stride < dense)
     return fail(HL_EINVAL, "rope_store: cache_batch_stride smaller than one sequence's cache");
-  HeadVecOp op;
   memset(&op, 0, sizeof(op));
   if ((rc = theta_for(a->use_installed_theta, rope_dim, a->rope_base, op.theta))) return rc;
   op.q = a->q;
@@ -485,8 +484,77 @@ int hl_rope_store_decode(const hl_rope_store_args* a, void* stream) {
   op.q_norm_w = a->q_norm_w;
   op.k_norm_w = a->k_norm_w;
   op.eps = a->eps;
+  return HL_OK;
+}
+
+int hl_rope_store_decode(const hl_rope_store_args* a, void* stream) {
+  HeadVecOp op;
+  int rc = rope_store_op(a, op);
+  if (rc) return rc;
   hipError_t e = headvec_launch(op, as_stream(stream));
   return e == hipSuccess ? HL_OK : hip_fail(e, "rope_store launch");
+}
+
+// ---------------------------------------------------------------------------
+// Fused decode step: rope_store + attention in one launch (fp16/bf16 KV)
+// ---------------------------------------------------------------------------
+static int validate_step(const hl_rope_store_args* rs, const hl_decode_args* at, HeadVecOp& op) {
+  int rc = rope_store_op(rs, op);
+  if (rc) return rc;
+  if ((rc = validate_decode(at))) return rc;
+  if (rs->batch != at->batch || rs->n_head_q != at->n_head || rs->n_head_kv != at->n_head_kv ||
+      rs->head_dim != at->head_dim || rs->kv_dtype != at->kv_dtype || rs->max_len != at->max_len ||
+      rs->cache_batch_stride != at->cache_batch_stride || rs->q != at->q ||
+      rs->k_cache != at->k_cache || rs->v_cache != at->v_cache)
+    return fail(HL_EINVAL, "decode_step: rope_store and decode args describe different tensors");
+  if (at->seq_lens) return fail(HL_EINVAL, "decode_step: lengths come from the positions (seq_lens must be null)");
+  if (!rs->positions && at->seq_len != rs->pos + 1)
+    return fail(HL_EINVAL, "decode_step: seq_len must be pos + 1");
+  return HL_OK;
+}
+
+static DecodeStep step_of(const HeadVecOp& op) {
+  DecodeStep st;
+  st.k = op.k;
+  st.v = op.v;
+  st.q_norm_w = op.q_norm_w;
+  st.k_norm_w = op.k_norm_w;
+  st.eps = op.eps;
+  st.rope_dim = op.rope_dim;
+  st.rope_style = op.rope_style;
+  st.pos = op.pos;
+  st.positions = op.positions;
+  st.theta = op.theta;
+  return st;
+}
+
+size_t hl_decode_step_workspace_bytes(const hl_rope_store_args* rs, const hl_decode_args* at) {
+  HeadVecOp op;
+  if (validate_step(rs, at, op)) return 0;
+  DecodePlan plan;
+  decode_plan(at, &plan, true);
+  return plan.ws_bytes;
+}
+
+int hl_decode_step(const hl_rope_store_args* rs, const hl_decode_args* at, void* workspace,
+                   size_t ws_bytes, void* stream) {
+  HeadVecOp op;
+  int rc = validate_step(rs, at, op);
+  if (rc) return rc;
+  DecodePlan plan;
+  decode_plan(at, &plan, true);
+  if (plan.ws_bytes > 0 && (!workspace || ws_bytes < plan.ws_bytes))
+    return fail(HL_EINVAL, "decode_step: workspace of %zu bytes needed, %zu given", plan.ws_bytes, ws_bytes);
+  if (plan.ws_bytes > 0 && ((uintptr_t)workspace & 3) != 0)
+    return fail(HL_EINVAL, "decode_step: workspace must be 4-byte aligned");
+  const hipStream_t s = as_stream(stream);
+  const DecodeStep st = step_of(op);
+  if (!plan.step) {  // fp32 KV: the stand-alone kernels, back to back
+    hipError_t e = headvec_launch(op, s);
+    if (e != hipSuccess) return hip_fail(e, "decode_step rope_store launch");
+  }
+  hipError_t e = decode_launch(at, &plan, workspace, s, &st);
+  return e == hipSuccess ? HL_OK : hip_fail(e, "decode_step launch");
 }
 
 // ---------------------------------------------------------------------------

@@ -19,10 +19,12 @@
 //
 // Softmax runs in base 2 (scores pre-multiplied by scale*log2 e), so
 // p = exp2(s - m) equals the reference's expf(score - max).
+#include <cstring>
 #include <map>
 #include <mutex>
 
 #include "common.h"
+#include "headvec.h"
 #include "launch.h"
 
 namespace hl {
@@ -47,9 +49,27 @@ struct DecodeParams {
   int n_head, n_head_kv, head_dim, group, head_chunk, n_chunks;
   int max_len, seq_len, split_len, num_splits;
   float scale_log2;
+  // Fused decode step (STEP kernels only): q above is the raw new-token
+  // activation; k_act / v_act are the new token's k and v.  The kernel applies
+  // qkNorm + RoPE at column pos = L - 1, writes k / v into that cache column
+  // and attends over [0, L), L = (positions ? positions[b] : pos) + 1.
+  const float* k_act;
+  const float* v_act;
+  const float* q_norm_w;
+  const float* k_norm_w;
+  float eps;
+  int rope_dim, rope_style, pos;
+  const int* positions;
+  ThetaTable theta;
 };
 
 constexpr int kMaxFusedSplits = 256;
+
+// Attention length of sequence b: the new token's column + 1 in a decode
+// step with per-sequence positions, else seq_lens[b] or seq_len.
+__device__ __forceinline__ int attn_len(const DecodeParams& p, int b) {
+  return p.positions ? p.positions[b] + 1 : (p.seq_lens ? p.seq_lens[b] : p.seq_len);
+}
 
 // Cross-workgroup exchange of the split partials.  The partials are small, so
 // they are written and read with relaxed agent-scope atomic stores/loads
@@ -88,11 +108,15 @@ __device__ __forceinline__ bool arrive_last(unsigned int* slot, int S) {
 
 // Workgroup epilogue shared by both kernels.  sm_m[w][h], sm_l[w][h] and
 // sm_o[w][h][D] hold the 4 waves' states for the hc heads of this chunk.
-// `lds_w` is unused scratch kept for the call signature.
-template <int D>
+// `after` runs once the workgroup's partial is registered (or its output
+// written): work whose stores must not delay the arrival.
+struct NoTail {
+  __device__ void operator()() const {}
+};
+template <int D, typename Tail = NoTail>
 __device__ void finish_workgroup(const DecodeParams& p, const float* sm_m, const float* sm_l,
                                  const float* sm_o, int hc, int b, int kvh, int chunk, int hq0,
-                                 int split, int hstride, float* lds_w) {
+                                 int split, int hstride, Tail after = Tail()) {
   const int tid = threadIdx.x;
   const int S = p.num_splits;
   for (int idx = tid; idx < hc * D; idx += 256) {
@@ -121,14 +145,18 @@ __device__ void finish_workgroup(const DecodeParams& p, const float* sm_m, const
       }
     }
   }
-  if (S == 1) return;
+  if (S == 1) {
+    after();
+    return;
+  }
   unsigned int* slot = p.slots + ((long long)b * p.n_head_kv + kvh) * p.n_chunks + chunk;
-  if (!arrive_last(slot, S)) return;
+  const bool last = arrive_last(slot, S);
+  after();
+  if (!last) return;
 
   // Fold all splits, 8 at a time: each chunk's m, l and o loads are issued
   // together (one memory round trip per 8 splits), then merged into a
   // running (max, sum, accumulator) per output element.
-  (void)lds_w;
   for (int idx = tid; idx < hc * D; idx += 256) {
     const int h = idx / D, d = idx % D;
     const long long row = (long long)b * p.n_head + hq0 + h;
@@ -183,13 +211,14 @@ __global__ __launch_bounds__(256) void decode_f32_kernel(DecodeParams p) {
   __shared__ float sp[4][HC][64];
   __shared__ __attribute__((aligned(16))) float sm[SM_FLOATS];
 
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar branches
   const int b = blockIdx.z;
   const int kvh = blockIdx.y / p.n_chunks, chunk = blockIdx.y % p.n_chunks;
   const int hq0 = kvh * p.group + chunk * p.head_chunk;
   const int hc = min(p.head_chunk, p.group - chunk * p.head_chunk);
   const int split = blockIdx.x;
-  const int L = p.seq_lens ? p.seq_lens[b] : p.seq_len;
+  const int L = attn_len(p, b);
   const int s0 = split * p.split_len;
   const int s1 = split == p.num_splits - 1 ? L : min(L, s0 + p.split_len);  // last split takes the rest
 
@@ -293,7 +322,7 @@ __global__ __launch_bounds__(256) void decode_f32_kernel(DecodeParams p) {
     }
   }
   __syncthreads();
-  finish_workgroup<D>(p, sm_m, sm_l, sm_o, hc, b, kvh, chunk, hq0, split, HC, sm);
+  finish_workgroup<D>(p, sm_m, sm_l, sm_o, hc, b, kvh, chunk, hq0, split, HC);
 }
 
 // ---------------------------------------------------------------------------
@@ -364,13 +393,14 @@ __device__ __forceinline__ u16x8 load_row8(const uint16_t* row, int col, int lim
   }
   return r;
 }
-__device__ __forceinline__ u16x8 mask_row8(u16x8 r, int col, int lim) {
+// Columns >= lim read as zero; column `newcol` (if any) takes `nv`.
+__device__ __forceinline__ u16x8 mask_row8(u16x8 r, int col, int lim, int newcol = -1, uint16_t nv = 0) {
 #pragma unroll
-  for (int e = 0; e < 8; ++e) r[e] = (col + e < lim) ? r[e] : (uint16_t)0;
+  for (int e = 0; e < 8; ++e) r[e] = (col + e == newcol) ? nv : ((col + e < lim) ? r[e] : (uint16_t)0);
   return r;
 }
 
-template <int D, int DT, bool VEC, bool PIPE>
+template <int D, int DT, bool VEC, bool PIPE, bool STEP>
 __global__ __launch_bounds__(256, PIPE ? (D == 64 ? 2 : 1) : 4) void decode_mfma_kernel(DecodeParams p) {
   typedef typename MfmaT<DT>::vec vec;
   constexpr int KS = D / 32;      // k-steps of the QK^T product
@@ -383,16 +413,19 @@ __global__ __launch_bounds__(256, PIPE ? (D == 64 ? 2 : 1) : 4) void decode_mfma
   constexpr int FUSE_BYTES = (16 * kMaxFusedSplits + 16) * 4;
   constexpr int LDS_A = KT_BYTES > MERGE_BYTES ? KT_BYTES : MERGE_BYTES;
   constexpr int LDS_BYTES = LDS_A > FUSE_BYTES ? LDS_A : FUSE_BYTES;
+  static_assert(18 * D * 4 <= LDS_BYTES, "step prologue buffers alias the K tiles");
   __shared__ __attribute__((aligned(16))) unsigned char lds_raw[LDS_BYTES];
+  __shared__ uint16_t snew[STEP ? 2 * D : 1];  // new column's k, v in storage bits
 
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar branches
   const int g = lane >> 4, c = lane & 15;
   const int b = blockIdx.z;
   const int kvh = blockIdx.y / p.n_chunks, chunk = blockIdx.y % p.n_chunks;
   const int hq0 = kvh * p.group + chunk * p.head_chunk;
   const int hc = min(p.head_chunk, p.group - chunk * p.head_chunk);
   const int split = blockIdx.x;
-  const int L = p.seq_lens ? p.seq_lens[b] : p.seq_len;
+  const int L = attn_len(p, b);
   const int s0 = split * p.split_len;
   const int s1 = split == p.num_splits - 1 ? L : min(L, s0 + p.split_len);  // last split takes the rest
 
@@ -403,7 +436,11 @@ __global__ __launch_bounds__(256, PIPE ? (D == 64 ? 2 : 1) : 4) void decode_mfma
 
   // K tile: row = lane/4 + 16*r, 8 columns at 8*(lane&3); V operand: row
   // 16*nb + c, columns t0+8g .. +7.
+  // The scheduling barriers keep each tile's loads together and in program
+  // order, so a compute waits only for its own tile, never for loads issued
+  // after it.
   auto load_tile = [&](int t0, u16x8* kr, u16x8* vr) {
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int r = 0; r < KR; ++r) {
       const int row = (lane >> 2) + 16 * r;
@@ -412,23 +449,116 @@ __global__ __launch_bounds__(256, PIPE ? (D == 64 ? 2 : 1) : 4) void decode_mfma
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb)
       vr[nb] = load_row8<VEC>(V + (long long)(16 * nb + c) * p.max_len, t0 + 8 * g, s1, p.max_len);
+    __builtin_amdgcn_sched_barrier(0);
   };
 
-  // Issue the first tile's loads before anything else.
+  // Fused step: the new token's head vectors this workgroup needs are
+  // vector j < hc: q head hq0 + j; j == hc: k; j == hc + 1: v (the last two
+  // only in the split that holds the new column).  Wave w takes j = w, w+4, ...
+  // Every global read of the prologue (the vectors, norm weights, the lane's
+  // RoPE frequency) is issued unconditionally before the first tile's loads,
+  // so waiting for them never waits for the tile.
+  constexpr int DPL = D / 64;  // elements d = lane + 64e of a head vector per lane
+  constexpr int VPW = 5;       // vectors per wave: (16 heads + k + v) / 4, rounded up
+  const int newc = L - 1;
+  const bool has_new = STEP && s0 <= newc && newc < s1;
+  const int nvec = hc + (has_new ? 2 : 0);
+  float act[STEP ? VPW : 1][DPL], wq[DPL], wk[DPL];
+  float theta_lane = 0.f;
+  if constexpr (STEP) {
+    const float* qb = p.q + ((long long)b * p.n_head + hq0) * D;
+    const float* kb_ = p.k_act + ((long long)b * p.n_head_kv + kvh) * D;
+    const float* vb_ = p.v_act + ((long long)b * p.n_head_kv + kvh) * D;
+#pragma unroll
+    for (int u = 0; u < VPW; ++u) {
+      const int j = min(wave + 4 * u, nvec - 1);
+      const float* src = j < hc ? qb + j * D : (j == hc ? kb_ : vb_);
+#pragma unroll
+      for (int e = 0; e < DPL; ++e) act[u][e] = src[lane + 64 * e];
+    }
+    const float* nq = p.q_norm_w ? p.q_norm_w : qb;  // stand-ins keep the loads unconditional
+    const float* nk = p.k_norm_w ? p.k_norm_w : qb;
+#pragma unroll
+    for (int e = 0; e < DPL; ++e) {
+      wq[e] = nq[lane + 64 * e];
+      wk[e] = nk[lane + 64 * e];
+    }
+    theta_lane = p.theta.t[lane];
+  }
+
+  // Plain kernel: this lane's q values, also loaded ahead of the tiles.
+  const bool live = c < hc;
+  f32x4 qraw[STEP ? 1 : 2 * KS];
+  if constexpr (!STEP) {
+    const float* qrow = p.q + ((long long)b * p.n_head + hq0 + (live ? c : 0)) * D;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      qraw[2 * ks] = *(const f32x4*)(qrow + 32 * ks + 8 * g);
+      qraw[2 * ks + 1] = *(const f32x4*)(qrow + 32 * ks + 8 * g + 4);
+    }
+  }
+
+  // Issue the first tile (and, prefetching, the second) unconditionally: a
+  // wave with fewer tiles re-reads one it already asked for (a cache hit), so
+  // every wait below can count loads exactly.
   int t0 = s0 + wave * 32;
   u16x8 ka[KR], va[NB], kb[KR], vb[NB];
-  if (t0 < s1) load_tile(t0, ka, va);
+  const int ta = t0 < s1 ? t0 : s0;
+  load_tile(ta, ka, va);
+  if constexpr (PIPE) load_tile(t0 + 128 < s1 ? t0 + 128 : ta, kb, vb);
+
+  // Fused step prologue: qkNorm + RoPE of this chunk's q heads into LDS, and
+  // in the split that holds the new column, of k (and v as is).  That split
+  // substitutes the new column into its tile registers (it need not see the
+  // cache write), and its chunk-0 workgroup writes the column to the cache.
+  // Same arithmetic as the stand-alone per-head kernel (shared helpers).
+  float* sq = (float*)lds_raw;  // [16][D] roped q, then [2][D] new k, v
+  if constexpr (STEP) {
+    float* skv = sq + 16 * D;
+    const int half = p.rope_dim / 2;  // <= D/2 <= 64: one pair per lane
+    // Evaluated on every lane (lanes >= half discard it), so that the
+    // frequency load stays ahead of the tile loads.
+    const float angle = (float)newc * theta_lane;
+    const float cs = cosf(angle), sn = sinf(angle);
+#pragma unroll
+    for (int u = 0; u < VPW; ++u) {
+      const int j = wave + 4 * u;
+      if (j < nvec) {
+        const bool isq = j < hc, isk = j == hc;
+        float x[DPL];
+#pragma unroll
+        for (int e = 0; e < DPL; ++e) x[e] = act[u][e];
+        if ((isq && p.q_norm_w) || (isk && p.k_norm_w)) {
+          float ss = 0.f;
+#pragma unroll
+          for (int e = 0; e < DPL; ++e) ss = sq_acc(ss, x[e]);
+          const float inv = rms_inv(ss, D, p.eps);
+#pragma unroll
+          for (int e = 0; e < DPL; ++e) x[e] = norm_apply(x[e], inv, isq ? wq[e] : wk[e]);
+        }
+        float* dst = isq ? sq + j * D : skv + (j - hc) * D;
+#pragma unroll
+        for (int e = 0; e < DPL; ++e) dst[lane + 64 * e] = x[e];
+        if (isq || isk) {
+          wave_lds_sync();
+          if (lane < half) rope_rotate(dst, lane, half, p.rope_style, cs, sn);
+        }
+      }
+    }
+    __syncthreads();
+    if (has_new)
+      for (int i = tid; i < 2 * D; i += 256) snew[i] = to_bits<DT>(skv[i]);
+  }
 
   // Q^T operand: lane (g, c) holds q[head c][32*ks + 8g + e], scaled, hi/lo.
   vec qh[KS], ql[KS];
   {
-    const bool live = c < hc;
-    const float* qrow = p.q + ((long long)b * p.n_head + hq0 + (live ? c : 0)) * D;
+    const float* qrow = sq + (live ? c : 0) * D;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       float x[8];
-      const f32x4 a = *(const f32x4*)(qrow + 32 * ks + 8 * g);
-      const f32x4 bb = *(const f32x4*)(qrow + 32 * ks + 8 * g + 4);
+      const f32x4 a = STEP ? *(const f32x4*)(qrow + 32 * ks + 8 * g) : qraw[STEP ? 0 : 2 * ks];
+      const f32x4 bb = STEP ? *(const f32x4*)(qrow + 32 * ks + 8 * g + 4) : qraw[STEP ? 0 : 2 * ks + 1];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         x[e] = live ? a[e] * p.scale_log2 : 0.f;
@@ -437,6 +567,7 @@ __global__ __launch_bounds__(256, PIPE ? (D == 64 ? 2 : 1) : 4) void decode_mfma
       split_hi_lo<DT>(x, qh[ks], ql[ks]);
     }
   }
+  if constexpr (STEP) __syncthreads();  // sq is dead; the K tiles reuse its LDS
 
   f32x4 o[NB];
 #pragma unroll
@@ -445,11 +576,18 @@ __global__ __launch_bounds__(256, PIPE ? (D == 64 ? 2 : 1) : 4) void decode_mfma
 
   // One 32-column tile whose K/V registers have been loaded.
   auto compute = [&](int t0, u16x8* kr, u16x8* vr) {
-    if (VEC && t0 + 32 > s1) {  // boundary tile (wave-uniform): zero columns >= s1
+    // Boundary tile (wave-uniform): columns >= s1 read as zero.  In a fused
+    // step the new column is s1 - 1 of the split that holds it (has_new), so
+    // it is in this tile too, and takes the new k / v bits instead of the
+    // cache's.
+    if (has_new ? t0 + 32 >= s1 : (VEC && t0 + 32 > s1)) {
+      const int newcol = has_new ? s1 - 1 : -1;
 #pragma unroll
-      for (int r = 0; r < KR; ++r) kr[r] = mask_row8(kr[r], t0 + 8 * (lane & 3), s1);
+      for (int r = 0; r < KR; ++r)
+        kr[r] = mask_row8(kr[r], t0 + 8 * (lane & 3), s1, newcol, STEP ? snew[(lane >> 2) + 16 * r] : 0);
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb) vr[nb] = mask_row8(vr[nb], t0 + 8 * g, s1);
+      for (int nb = 0; nb < NB; ++nb)
+        vr[nb] = mask_row8(vr[nb], t0 + 8 * g, s1, newcol, STEP ? snew[D + 16 * nb + c] : 0);
     }
 #pragma unroll
     for (int r = 0; r < KR; ++r) {
@@ -520,11 +658,15 @@ __global__ __launch_bounds__(256, PIPE ? (D == 64 ? 2 : 1) : 4) void decode_mfma
     }
   };
 
-  // PIPE: two-stage pipeline over this wave's tiles (t0, t0+128, ...):
-  // buffers a and b alternate, and each branch below is uniform across the
-  // wave, so the loads of the next tile stay in flight while the current one
-  // computes.  !PIPE (about one tile per wave): no second buffer, fewer
-  // registers, more resident waves.
+  // PIPE: two buffers, a and b, hold this wave's tiles t0 and t0 + 128
+  // (t0, t0+128, ... step 128).  While one computes, the next tile's loads
+  // into the other are in flight.  The loop covers the pairs that are
+  // followed by a whole pair, so its loads are unconditional and every path
+  // into a compute has the same loads outstanding (the compiler's waits then
+  // count exactly: a compute waits for its own tile only); the last 2 or 3
+  // tiles are finished after it without further speculative loads.
+  // !PIPE (about one tile per wave): no second buffer, fewer registers,
+  // more resident waves.
   if (!PIPE) {
     if (t0 < s1) {
       compute(t0, ka, va);
@@ -533,24 +675,27 @@ __global__ __launch_bounds__(256, PIPE ? (D == 64 ? 2 : 1) : 4) void decode_mfma
         compute(t0, ka, va);
       }
     }
-  } else if (t0 < s1) {
-    while (true) {
-      if (t0 + 128 < s1) {
-        load_tile(t0 + 128, kb, vb);
+  } else {
+    const int n_tiles = t0 < s1 ? (s1 - t0 + 127) / 128 : 0;  // wave-uniform
+    if (n_tiles >= 2) {
+      int i = 0;
+      for (; i + 4 <= n_tiles; i += 2, t0 += 256) {
         compute(t0, ka, va);
-        t0 += 128;
+        load_tile(t0 + 256, ka, va);
+        compute(t0 + 128, kb, vb);
+        load_tile(t0 + 384, kb, vb);
+      }
+      if (n_tiles - i == 3) {
+        compute(t0, ka, va);
+        load_tile(t0 + 256, ka, va);
+        compute(t0 + 128, kb, vb);
+        compute(t0 + 256, ka, va);
       } else {
         compute(t0, ka, va);
-        break;
+        compute(t0 + 128, kb, vb);
       }
-      if (t0 + 128 < s1) {
-        load_tile(t0 + 128, ka, va);
-        compute(t0, kb, vb);
-        t0 += 128;
-      } else {
-        compute(t0, kb, vb);
-        break;
-      }
+    } else if (n_tiles == 1) {
+      compute(t0, ka, va);
     }
   }
 
@@ -570,7 +715,20 @@ __global__ __launch_bounds__(256, PIPE ? (D == 64 ? 2 : 1) : 4) void decode_mfma
 #pragma unroll
     for (int i = 0; i < 4; ++i) sm_o[(wave * HS + 4 * g + i) * D + 16 * nb + c] = o[nb][i];
   __syncthreads();
-  finish_workgroup<D>(p, sm_m, sm_l, sm_o, hc, b, kvh, chunk, hq0, split, HS, (float*)lds_raw);
+  if constexpr (STEP) {
+    // The new column goes to the cache after this workgroup's arrival, so its
+    // stores neither count against the tile waits nor delay the merge.
+    finish_workgroup<D>(p, sm_m, sm_l, sm_o, hc, b, kvh, chunk, hq0, split, HS, [&]() {
+      if (has_new && chunk == 0) {
+        for (int i = tid; i < 2 * D; i += 256) {
+          uint16_t* cache = (uint16_t*)(i < D ? p.k : p.v);
+          cache[base + (long long)(i < D ? i : i - D) * p.max_len + newc] = snew[i];
+        }
+      }
+    });
+  } else {
+    finish_workgroup<D>(p, sm_m, sm_l, sm_o, hc, b, kvh, chunk, hq0, split, HS);
+  }
 }
 
 // Zero-fills a workspace (a kernel rather than a memset node, so that it can
@@ -599,16 +757,24 @@ namespace {
 
 typedef void (*KernelFn)(DecodeParams);
 
-template <int D, int DT>
+// The prefetching kernel exists for the 16-byte path only (the element-wise
+// loads of unaligned caches would not fit its registers).
+template <int D, int DT, bool STEP>
 KernelFn pick_mfma(bool vec, bool pipe) {
-  if (vec) return pipe ? decode_mfma_kernel<D, DT, true, true> : decode_mfma_kernel<D, DT, true, false>;
-  return pipe ? decode_mfma_kernel<D, DT, false, true> : decode_mfma_kernel<D, DT, false, false>;
+  if (vec) return pipe ? decode_mfma_kernel<D, DT, true, true, STEP> : decode_mfma_kernel<D, DT, true, false, STEP>;
+  return decode_mfma_kernel<D, DT, false, false, STEP>;
 }
 
-KernelFn pick_kernel(int kv_dtype, int D, bool vec, bool pipe) {
+template <int D, int DT>
+KernelFn pick_mfma(bool vec, bool pipe, bool step) {
+  return step ? pick_mfma<D, DT, true>(vec, pipe) : pick_mfma<D, DT, false>(vec, pipe);
+}
+
+KernelFn pick_kernel(int kv_dtype, int D, bool vec, bool pipe, bool step) {
   if (kv_dtype == HL_F32) return D == 64 ? decode_f32_kernel<64> : decode_f32_kernel<128>;
-  if (kv_dtype == HL_F16) return D == 64 ? pick_mfma<64, HL_F16>(vec, pipe) : pick_mfma<128, HL_F16>(vec, pipe);
-  return D == 64 ? pick_mfma<64, HL_BF16>(vec, pipe) : pick_mfma<128, HL_BF16>(vec, pipe);
+  if (kv_dtype == HL_F16)
+    return D == 64 ? pick_mfma<64, HL_F16>(vec, pipe, step) : pick_mfma<128, HL_F16>(vec, pipe, step);
+  return D == 64 ? pick_mfma<64, HL_BF16>(vec, pipe, step) : pick_mfma<128, HL_BF16>(vec, pipe, step);
 }
 
 // Resident workgroups of a kernel on the whole device (cached).
@@ -632,6 +798,23 @@ int capacity(KernelFn fn) {
   return per_cu * cus;
 }
 
+int cu_count() {
+  static std::mutex mu;
+  static std::map<int, int> cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 256;
+  std::lock_guard<std::mutex> lk(mu);
+  auto it = cache.find(dev);
+  if (it != cache.end()) return it->second;
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) {
+    (void)hipGetLastError();
+    return 256;
+  }
+  cache[dev] = cus;
+  return cus;
+}
+
 bool vec_path(const hl_decode_args* a) {
   const long long stride = a->cache_batch_stride ? a->cache_batch_stride
                                                  : (long long)a->n_head_kv * a->head_dim * a->max_len;
@@ -641,28 +824,34 @@ bool vec_path(const hl_decode_args* a) {
 
 }  // namespace
 
-void decode_plan(const hl_decode_args* a, DecodePlan* plan) {
+void decode_plan(const hl_decode_args* a, DecodePlan* plan, bool step) {
   const int G = a->n_head / a->n_head_kv;
   plan->head_chunk = G < 16 ? G : 16;
   plan->n_chunks = (G + plan->head_chunk - 1) / plan->head_chunk;
   plan->vec = vec_path(a);
+  plan->step = step && a->kv_dtype != HL_F32;
   const bool mfma = a->kv_dtype != HL_F32;
   const int tile = mfma ? 32 : 64;
   const int tiles = (a->seq_len + tile - 1) / tile;
   const long long units = (long long)a->batch * a->n_head_kv * plan->n_chunks;
-  // Splits fill one round of resident workgroups.  When that leaves about one
-  // tile per wave, the register-light kernel (no prefetch buffer, more
-  // resident waves) is used.
-  auto splits_for = [&](bool pipe) {
-    if (a->num_splits > 0) return a->num_splits;
-    const int cap = capacity(pick_kernel(a->kv_dtype, a->head_dim, plan->vec, pipe));
-    int S = (int)(cap / units);
-    return S < 1 ? 1 : S;
-  };
-  int S = splits_for(false);
-  plan->pipe = !mfma ? false : (tiles / (S < tiles ? S : tiles) > 5);
-  if (plan->pipe) S = splits_for(true);
-  if (S > tiles) S = tiles;
+  // The prefetching kernel streams best with one workgroup per CU (its own
+  // loads in flight hide the latency; more splits only add partials to
+  // merge), and is used when that gives each wave at least two tiles (8 per
+  // split).  Otherwise the register-light kernel fills one round of resident
+  // workgroups.
+  auto clamp_splits = [&](long long S) { return (int)(S < 1 ? 1 : (S > tiles ? tiles : S)); };
+  const int s_pipe = clamp_splits(cu_count() / units);
+  int S;
+  if (a->num_splits > 0) {
+    S = a->num_splits < tiles ? a->num_splits : tiles;
+    plan->pipe = mfma && plan->vec && tiles / S >= 8;
+  } else if (mfma && plan->vec && tiles / s_pipe >= 8) {
+    plan->pipe = true;
+    S = s_pipe;
+  } else {
+    plan->pipe = false;
+    S = clamp_splits(capacity(pick_kernel(a->kv_dtype, a->head_dim, plan->vec, false, plan->step)) / units);
+  }
   if (S > kMaxFusedSplits) S = kMaxFusedSplits;
   const int tiles_per_split = tiles / S;  // the last split also takes the remainder
   plan->split_len = tiles_per_split * tile;
@@ -681,8 +870,21 @@ void decode_plan(const hl_decode_args* a, DecodePlan* plan) {
 }
 
 hipError_t decode_launch(const hl_decode_args* a, const DecodePlan* plan, void* ws,
-                         hipStream_t stream) {
+                         hipStream_t stream, const DecodeStep* step) {
   DecodeParams p;
+  memset(&p, 0, sizeof(p));
+  if (step) {
+    p.k_act = step->k;
+    p.v_act = step->v;
+    p.q_norm_w = step->q_norm_w;
+    p.k_norm_w = step->k_norm_w;
+    p.eps = step->eps;
+    p.rope_dim = step->rope_dim;
+    p.rope_style = step->rope_style;
+    p.pos = step->pos;
+    p.positions = step->positions;
+    p.theta = step->theta;
+  }
   const int D = a->head_dim;
   p.q = a->q;
   p.k = a->k_cache;
@@ -708,7 +910,7 @@ hipError_t decode_launch(const hl_decode_args* a, const DecodePlan* plan, void* 
   p.scale_log2 = scale * kLog2e;
 
   dim3 grid(plan->num_splits, a->n_head_kv * plan->n_chunks, a->batch);
-  KernelFn fn = pick_kernel(a->kv_dtype, D, plan->vec, plan->pipe);
+  KernelFn fn = pick_kernel(a->kv_dtype, D, plan->vec, plan->pipe, plan->step);
   hipLaunchKernelGGL(fn, grid, dim3(256), 0, stream, p);
   return hipGetLastError();
 }

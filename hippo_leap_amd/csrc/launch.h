@@ -14,12 +14,26 @@ struct DecodePlan {
   int head_chunk, n_chunks, num_splits, split_len;
   bool vec;             // 16-byte cache loads (fp16/bf16, aligned rows)
   bool pipe;            // prefetching kernel (several tiles per wave)
+  bool step;            // fused decode step (qkNorm + RoPE + cache write inside)
   size_t counters_bytes;  // arrival counters at the workspace start, partials after
   size_t ws_bytes;
 };
-void decode_plan(const hl_decode_args* a, DecodePlan* plan);
+// The new token's inputs of a fused decode step (fp16/bf16 KV): a->q is then
+// the raw q activation, and the kernel ropes q and k, writes k and v into
+// cache column pos (positions[b] if given) and attends over pos + 1 columns.
+struct DecodeStep {
+  const float* k;
+  const float* v;
+  const float* q_norm_w;
+  const float* k_norm_w;
+  float eps;
+  int rope_dim, rope_style, pos;
+  const int* positions;
+  ThetaTable theta;
+};
+void decode_plan(const hl_decode_args* a, DecodePlan* plan, bool step = false);
 hipError_t decode_launch(const hl_decode_args* a, const DecodePlan* plan, void* ws,
-                         hipStream_t stream);
+                         hipStream_t stream, const DecodeStep* step = nullptr);
 hipError_t zero_fill_launch(void* ws, size_t bytes, hipStream_t stream);
 
 // ---- per-token head-vector ops (rope_store.hip) ---------------------------

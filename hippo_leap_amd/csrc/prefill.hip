@@ -99,7 +99,8 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma_kernel(MfmaPrefillParams 
   constexpr int VI = VT / 8 / 64 / 4;  // (V)
   __shared__ __attribute__((aligned(1024))) uint16_t lds[2 * STAGE];
 
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar branches
   const int hh = lane >> 5, ln = lane & 31;
 
   // Work item: heaviest (last) query blocks first; within a query block the

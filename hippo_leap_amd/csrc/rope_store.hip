@@ -21,19 +21,10 @@
 //   theta[i]  powf(1/base, 2i/rope_dim) on the host (:3850-3861), passed to
 //             the kernel by value.
 #include "common.h"
+#include "headvec.h"
 #include "launch.h"
 
 namespace hl {
-
-__device__ __forceinline__ void rope_pair_index(int i, int half, int style, int& i0, int& i1) {
-  if (style == HL_ROPE_HALF_SPLIT) {
-    i0 = i;
-    i1 = i + half;
-  } else {
-    i0 = 2 * i;
-    i1 = 2 * i + 1;
-  }
-}
 
 // ---------------------------------------------------------------------------
 // Decode side: one wave per head vector of the new token.
@@ -81,40 +72,13 @@ __global__ __launch_bounds__(64) void headvec_kernel(HeadVecOp op) {
   }
 
   for (int d = lane; d < D; d += 64) sx[d] = xin[d];
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-
-  if (nw) {
-    float ss = 0.f;
-    for (int d = lane; d < D; d += 64) ss += sx[d] * sx[d];
-    ss = wave_sum(ss);
-    const float inv = 1.0f / sqrtf(ss / (float)D + op.eps);
-    for (int d = lane; d < D; d += 64) sx[d] = sx[d] * inv * nw[d];
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  }
-  if (rope && op.do_rope) {
-    const int pos = op.positions ? op.positions[b] : op.pos;
-    const int half = op.rope_dim / 2;
-    for (int i = lane; i < half; i += 64) {
-      int i0, i1;
-      rope_pair_index(i, half, op.rope_style, i0, i1);
-      const float angle = (float)pos * op.theta.t[i];
-      const float c = cosf(angle), s = sinf(angle);
-      const float v0 = sx[i0], v1 = sx[i1];
-      sx[i0] = v0 * c - v1 * s;
-      sx[i1] = v0 * s + v1 * c;
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  }
+  wave_lds_sync();
+  const int pos = op.positions ? op.positions[b] : op.pos;
+  headvec_norm_rope(sx, D, lane, nw, op.eps, (rope && op.do_rope) ? op.rope_dim : 0, op.rope_style,
+                    op.theta, pos);
   if (x && (nw || (rope && op.do_rope)))
     for (int d = lane; d < D; d += 64) x[d] = sx[d];
   if (cache) {
-    const int pos = op.positions ? op.positions[b] : op.pos;
     const long long base = (long long)b * op.batch_stride + (long long)hv * D * op.max_len + pos;
     for (int d = lane; d < D; d += 64) store_elem<KDT>(cache, base + (long long)d * op.max_len, sx[d]);
   }

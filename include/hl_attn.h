@@ -244,6 +244,24 @@ typedef struct hl_rope_store_args {
  * for the host `pos`; device positions are not inspected).               */
 int hl_rope_store_decode(const hl_rope_store_args* a, void* stream);
 
+/* One decode step for the new token of B sequences: the result of
+ * hl_rope_store_decode(rs) followed by hl_attn_decode(at) on the same
+ * stream (identical cache contents and output), in one launch for fp16/bf16
+ * KV (two for fp32).  It replaces the reference's per-layer sequence
+ * gpuQkNorm + gpuFusedRopeStoreKV + gpuAttentionDecode (naive.nim:4697-4700,
+ * 3149-3223, 3369-3383).  rs and at must describe the same tensors
+ * (at->q == rs->q, same caches, shapes, dtype and stride); at->seq_lens must
+ * be null: sequence b attends over positions[b] + 1 columns (rs->pos + 1
+ * when rs->positions is null, and then at->seq_len must equal rs->pos + 1;
+ * with positions, at->seq_len is the longest such length, used only to plan
+ * the splits).  Unlike hl_rope_store_decode, q and k are read only when the
+ * step runs as one launch; with fp32 KV they are rotated in place, so treat
+ * their contents as unspecified afterwards.  The workspace follows the rules
+ * of hl_attn_decode's, sized by hl_decode_step_workspace_bytes.          */
+size_t hl_decode_step_workspace_bytes(const hl_rope_store_args* rs, const hl_decode_args* at);
+int hl_decode_step(const hl_rope_store_args* rs, const hl_decode_args* at, void* workspace,
+                   size_t ws_bytes, void* stream);
+
 typedef struct hl_prefill_args {
   int n_head, n_head_kv, head_dim, seq_len;
   int io_dtype;                 /* dtype of q/k/v/out: HL_F32|HL_F16|HL_BF16     */

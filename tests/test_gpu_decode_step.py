@@ -1,0 +1,146 @@
+"""GPU parity: the fused decode step (hl_decode_step) against the two-call
+sequence it replaces (hl_rope_store_decode then hl_attn_decode, bit for bit
+at the same split count) and against the CPU oracle (qkNorm -> RoPE -> cache
+store -> attention, naive.nim:4697-4700, 3149-3223, 3369-3383).
+
+Bars: cache columns and outputs identical to the two-call path; outputs
+within 1e-4 (fp32 KV) / 2e-3 (fp16/bf16 KV) relative of the oracle."""
+import numpy as np
+import pytest
+import torch
+
+from util import TOL_F32, TOL_LOWP, rel_err
+from test_gpu_decode import TDT, dev_bits, make_case
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(x):
+    return torch.from_numpy(np.ascontiguousarray(x, np.float32)).cuda()
+
+
+def cache_bits(t, dt):
+    return t.cpu().numpy() if dt == 0 else t.view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def run_both(orc, B, hq, hkv, d, max_len, dt, positions, rope_dim, style, norm, splits, seed):
+    """Returns (step out, step caches, two-call out, two-call caches, inputs)."""
+    from hippo_leap_amd import attention as A
+    q, kb, vb = make_case(orc, B, hq, hkv, d, max_len, max_len, dt, seed)
+    qa = orc.normal(B * hq * d, seed + 3)
+    ka = orc.normal(B * hkv * d, seed + 4)
+    va = orc.normal(B * hkv * d, seed + 5)
+    wq = orc.uniform(d, seed + 6, 0.5, 1.5) if norm else None
+    wk = orc.uniform(d, seed + 7, 0.5, 1.5) if norm else None
+    pos_t = torch.tensor(positions, dtype=torch.int32, device="cuda") if len(positions) > 1 else None
+    pos0 = positions[0]
+    L = max(positions) + 1
+    base = 5e5
+    outs = []
+    for fused in (True, False):
+        qd, kd, vd = dev(qa), dev(ka), dev(va)
+        kc, vc = dev_bits(kb, dt), dev_bits(vb, dt)
+        out = torch.full((B * hq * d,), float("nan"), device="cuda")
+        rs = A.rope_store_args(qd, kd, vd, kc, vc, hq, hkv, d, max_len, pos0, base,
+                               rope_dim=rope_dim, rope_style=style, positions=pos_t,
+                               q_norm_w=dev(wq) if norm else None,
+                               k_norm_w=dev(wk) if norm else None, eps=1e-6)
+        if fused:
+            at = A.decode_args(qd, kc, vc, out, hq, hkv, d, max_len, L, num_splits=splits)
+            A.decode_step(rs, at, A.decode_step_workspace(rs, at))
+        else:
+            lens = (pos_t + 1) if pos_t is not None else None
+            at = A.decode_args(qd, kc, vc, out, hq, hkv, d, max_len, L, seq_lens=lens,
+                               num_splits=splits)
+            A.rope_store_decode(qd, kd, vd, kc, vc, hq, hkv, d, max_len, pos0, base,
+                                rope_dim=rope_dim, rope_style=style, positions=pos_t,
+                                q_norm_w=dev(wq) if norm else None,
+                                k_norm_w=dev(wk) if norm else None, eps=1e-6)
+            A.attn_decode(at, A.decode_workspace(at))
+        torch.cuda.synchronize()
+        outs.append((out.cpu().numpy(), cache_bits(kc, dt), cache_bits(vc, dt)))
+    return outs, (q, kb, vb, qa, ka, va, wq, wk, base)
+
+
+def oracle_step(orc, B, hq, hkv, d, max_len, dt, positions, rope_dim, style, inputs):
+    _, kb, vb, qa, ka, va, wq, wk, base = inputs
+    rd = rope_dim or d
+    th = orc.theta_table(rd, base)
+    per = hkv * d * max_len
+    out = np.empty(B * hq * d, np.float32)
+    for b in range(B):
+        p = positions[b] if len(positions) > 1 else positions[0]
+        qb = qa[b * hq * d:(b + 1) * hq * d]
+        kbv = ka[b * hkv * d:(b + 1) * hkv * d]
+        if wq is not None:
+            qb = orc.qk_norm(qb, wq, hq, d, 1e-6)
+            kbv = orc.qk_norm(kbv, wk, hkv, d, 1e-6)
+        qb = orc.rope_heads(qb, hq, d, rd, th, p, style)
+        kbv = orc.rope_heads(kbv, hkv, d, rd, th, p, style)
+        kc = orc.upcast(kb[b * per:(b + 1) * per], dt).reshape(hkv * d, max_len).copy()
+        vc = orc.upcast(vb[b * per:(b + 1) * per], dt).reshape(hkv * d, max_len).copy()
+        kc[:, p] = orc.upcast(orc.to_storage(kbv, dt), dt)
+        vc[:, p] = orc.upcast(orc.to_storage(va[b * hkv * d:(b + 1) * hkv * d], dt), dt)
+        out[b * hq * d:(b + 1) * hq * d] = orc.attention_decode(qb, kc.reshape(-1), vc.reshape(-1),
+                                                                hq, hkv, d, p + 1, max_len)
+    return out
+
+
+CASES = [
+    # B, hq, hkv, d, max_len, positions, rope_dim, style, norm, splits
+    (8, 32, 8, 64, 2112, [2048], 0, 0, False, 8),          # the c3 step shape
+    (3, 32, 4, 128, 960, [0, 500, 959], 0, 0, True, 4),    # ragged, qkNorm, first/last column
+    (2, 40, 2, 64, 512, [31, 32], 32, 1, False, 0),        # G=20: two head chunks, partial interleaved rope
+    (1, 16, 16, 128, 4096, [4095], 64, 0, True, 0),        # G=1, long, partial half-split rope
+    (2, 8, 2, 64, 256, [63, 64], 0, 0, True, 3),           # new column on a tile edge
+]
+
+
+@pytest.mark.parametrize("dt", [0, 1, 2])
+@pytest.mark.parametrize("case", range(len(CASES)))
+def test_decode_step_matches_two_calls_and_oracle(hl, orc, dt, case):
+    B, hq, hkv, d, max_len, positions, rope_dim, style, norm, splits = CASES[case]
+    print(f"decode_step case {case} dt {dt}", flush=True)
+    outs, inputs = run_both(orc, B, hq, hkv, d, max_len, dt, positions, rope_dim, style, norm,
+                            splits, 1300 + 10 * case)
+    (fo, fk, fv), (so, sk, sv) = outs
+    assert np.array_equal(fk, sk) and np.array_equal(fv, sv)
+    if splits:
+        assert np.array_equal(fo, so)
+    else:  # planner may pick different split counts for the two kernels
+        assert rel_err(fo, so) < 1e-5
+    ref = oracle_step(orc, B, hq, hkv, d, max_len, dt, positions, rope_dim, style, inputs)
+    assert rel_err(fo, ref) < (TOL_F32 if dt == 0 else TOL_LOWP)
+
+
+def test_decode_step_graph_replay(hl, orc):
+    """The step in a HIP graph: replays with eager work in between give the
+    eager result every time (the cache column is rewritten with the same bits)."""
+    from hippo_leap_amd import attention as A
+    B, hq, hkv, d, M, dt = 4, 32, 8, 64, 1024, 1
+    q, kb, vb = make_case(orc, B, hq, hkv, d, M, M, dt, 1400)
+    qd = dev(orc.normal(B * hq * d, 1401))
+    kd, vd = dev(orc.normal(B * hkv * d, 1402)), dev(orc.normal(B * hkv * d, 1403))
+    kc, vc = dev_bits(kb, dt), dev_bits(vb, dt)
+    out = torch.empty(B * hq * d, device="cuda")
+    rs = A.rope_store_args(qd, kd, vd, kc, vc, hq, hkv, d, M, 700, 5e5)
+    at = A.decode_args(qd, kc, vc, out, hq, hkv, d, M, 701)
+    ws = A.decode_step_workspace(rs, at)
+    A.decode_step(rs, at, ws)
+    torch.cuda.synchronize()
+    eager = out.cpu().numpy().copy()
+    g = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        A.decode_step(rs, at, ws)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g):
+        A.decode_step(rs, at, ws)
+    for _ in range(4):
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(out.cpu().numpy(), eager)
