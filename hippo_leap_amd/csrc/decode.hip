@@ -393,10 +393,9 @@ __device__ __forceinline__ u16x8 load_row8(const uint16_t* row, int col, int lim
   }
   return r;
 }
-// Columns >= lim read as zero; column `newcol` (if any) takes `nv`.
-__device__ __forceinline__ u16x8 mask_row8(u16x8 r, int col, int lim, int newcol = -1, uint16_t nv = 0) {
+__device__ __forceinline__ u16x8 mask_row8(u16x8 r, int col, int lim) {
 #pragma unroll
-  for (int e = 0; e < 8; ++e) r[e] = (col + e == newcol) ? nv : ((col + e < lim) ? r[e] : (uint16_t)0);
+  for (int e = 0; e < 8; ++e) r[e] = (col + e < lim) ? r[e] : (uint16_t)0;
   return r;
 }
 
@@ -427,7 +426,13 @@ __global__ __launch_bounds__(256, PIPE ? (D == 64 ? 2 : 1) : 4) void decode_mfma
   const int split = blockIdx.x;
   const int L = attn_len(p, b);
   const int s0 = split * p.split_len;
-  const int s1 = split == p.num_splits - 1 ? L : min(L, s0 + p.split_len);  // last split takes the rest
+  const int s_end = split == p.num_splits - 1 ? L : min(L, s0 + p.split_len);  // last split takes the rest
+  // Fused step: the new column L - 1 belongs to exactly one split (has_new).
+  // Its k / v are computed in this kernel, so that split seeds its softmax
+  // state with the column directly and its tiles stop before it.
+  const int newc = L - 1;
+  const bool has_new = STEP && s0 <= newc && newc < s_end;
+  const int s1 = has_new ? newc : s_end;  // end of the columns read from the cache
 
   const long long base = (long long)b * p.batch_stride + (long long)kvh * D * p.max_len;
   const uint16_t* K = (const uint16_t*)p.k + base;
@@ -460,8 +465,6 @@ __global__ __launch_bounds__(256, PIPE ? (D == 64 ? 2 : 1) : 4) void decode_mfma
   // so waiting for them never waits for the tile.
   constexpr int DPL = D / 64;  // elements d = lane + 64e of a head vector per lane
   constexpr int VPW = 5;       // vectors per wave: (16 heads + k + v) / 4, rounded up
-  const int newc = L - 1;
-  const bool has_new = STEP && s0 <= newc && newc < s1;
   const int nvec = hc + (has_new ? 2 : 0);
   float act[STEP ? VPW : 1][DPL], wq[DPL], wk[DPL];
   float theta_lane = 0.f;
@@ -567,27 +570,41 @@ __global__ __launch_bounds__(256, PIPE ? (D == 64 ? 2 : 1) : 4) void decode_mfma
       split_hi_lo<DT>(x, qh[ks], ql[ks]);
     }
   }
-  if constexpr (STEP) __syncthreads();  // sq is dead; the K tiles reuse its LDS
-
   f32x4 o[NB];
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) o[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m_run = -INFINITY, l_run = 0.f;
+  if constexpr (STEP) {
+    // Wave 0 of the split holding the new column starts from that column:
+    // m = its score, l = 1 (counted once, in lane group 0), o = its v for
+    // every head.  The score uses the stored (rounded) k, as a read of the
+    // cache would.
+    if (has_new && wave == 0) {
+      const float* qrow = sq + (live ? c : 0) * D;
+      constexpr int DG = D / 4;  // dims per lane group
+      float dot = 0.f;
+#pragma unroll
+      for (int d = 0; d < DG; ++d) dot += qrow[DG * g + d] * from_bits<DT>(snew[DG * g + d]);
+      dot += __shfl_xor(dot, 16, 64);
+      dot += __shfl_xor(dot, 32, 64);
+      m_run = live ? dot * p.scale_log2 : 0.f;
+      l_run = g == 0 ? 1.f : 0.f;
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        const float vn = from_bits<DT>(snew[D + 16 * nb + c]);
+        o[nb] = f32x4{vn, vn, vn, vn};
+      }
+    }
+    __syncthreads();  // sq is dead; the K tiles reuse its LDS
+  }
 
   // One 32-column tile whose K/V registers have been loaded.
   auto compute = [&](int t0, u16x8* kr, u16x8* vr) {
-    // Boundary tile (wave-uniform): columns >= s1 read as zero.  In a fused
-    // step the new column is s1 - 1 of the split that holds it (has_new), so
-    // it is in this tile too, and takes the new k / v bits instead of the
-    // cache's.
-    if (has_new ? t0 + 32 >= s1 : (VEC && t0 + 32 > s1)) {
-      const int newcol = has_new ? s1 - 1 : -1;
+    if (VEC && t0 + 32 > s1) {  // boundary tile (wave-uniform): zero columns >= s1
 #pragma unroll
-      for (int r = 0; r < KR; ++r)
-        kr[r] = mask_row8(kr[r], t0 + 8 * (lane & 3), s1, newcol, STEP ? snew[(lane >> 2) + 16 * r] : 0);
+      for (int r = 0; r < KR; ++r) kr[r] = mask_row8(kr[r], t0 + 8 * (lane & 3), s1);
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb)
-        vr[nb] = mask_row8(vr[nb], t0 + 8 * g, s1, newcol, STEP ? snew[D + 16 * nb + c] : 0);
+      for (int nb = 0; nb < NB; ++nb) vr[nb] = mask_row8(vr[nb], t0 + 8 * g, s1);
     }
 #pragma unroll
     for (int r = 0; r < KR; ++r) {

@@ -1,10 +1,14 @@
 """GPU parity: the fused decode step (hl_decode_step) against the two-call
-sequence it replaces (hl_rope_store_decode then hl_attn_decode, bit for bit
-at the same split count) and against the CPU oracle (qkNorm -> RoPE -> cache
-store -> attention, naive.nim:4697-4700, 3149-3223, 3369-3383).
+sequence it replaces (hl_rope_store_decode then hl_attn_decode) and against
+the CPU oracle (qkNorm -> RoPE -> cache store -> attention,
+naive.nim:4697-4700, 3149-3223, 3369-3383).
 
-Bars: cache columns and outputs identical to the two-call path; outputs
-within 1e-4 (fp32 KV) / 2e-3 (fp16/bf16 KV) relative of the oracle."""
+Bars: cache columns identical to the two-call path, bit for bit; outputs
+within 1e-5 relative of it (the fused kernel scores the new column with an
+fp32 dot product, the attention kernel with the split hi/lo MFMA, which
+carries about 16 significant bits of q for bf16 KV; with fp32 KV the step
+runs the same two kernels and matches exactly);
+outputs within 1e-4 (fp32 KV) / 2e-3 (fp16/bf16 KV) relative of the oracle."""
 import numpy as np
 import pytest
 import torch
@@ -105,9 +109,9 @@ def test_decode_step_matches_two_calls_and_oracle(hl, orc, dt, case):
                             splits, 1300 + 10 * case)
     (fo, fk, fv), (so, sk, sv) = outs
     assert np.array_equal(fk, sk) and np.array_equal(fv, sv)
-    if splits:
+    if dt == 0 and splits:
         assert np.array_equal(fo, so)
-    else:  # planner may pick different split counts for the two kernels
+    else:
         assert rel_err(fo, so) < 1e-5
     ref = oracle_step(orc, B, hq, hkv, d, max_len, dt, positions, rope_dim, style, inputs)
     assert rel_err(fo, ref) < (TOL_F32 if dt == 0 else TOL_LOWP)
