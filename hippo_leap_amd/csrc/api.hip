@@ -562,6 +562,7 @@ int hl_decode_step(const hl_rope_store_args* rs, const hl_decode_args* at, void*
 // ---------------------------------------------------------------------------
 struct PrefillPlan {
   bool mfma;
+  bool q_in_kernel;  // MFMA kernel builds Q from the raw activations (no qt)
   int t_pad;
   size_t off_q, off_k, off_v, off_tab, bytes;
 };
@@ -593,18 +594,19 @@ static int validate_prefill(const hl_prefill_args* a, PrefillPlan* pl) {
     return fail(HL_EUNSUPPORTED, "prefill: write_back_qk needs fp32 activations");
   const size_t D = a->head_dim, T = a->seq_len;
   pl->mfma = a->io_dtype != HL_F32;
+  const int rd = a->rope_dim ? a->rope_dim : a->head_dim;
+  // The MFMA kernel applies RoPE to Q itself when every rotation pair lies in
+  // one lane's registers: interleaved pairs, or half-split over all dims.
+  pl->q_in_kernel = pl->mfma && (!a->apply_rope || a->rope_style == HL_ROPE_INTERLEAVED || rd == a->head_dim);
   if (pl->mfma) {
     pl->t_pad = prefill_mfma_tpad(a->seq_len);
     const size_t tp = pl->t_pad;
     pl->off_q = 0;
-    pl->off_k = pl->off_q + (size_t)a->n_head * tp * D * 2;
+    pl->off_k = pl->off_q + (pl->q_in_kernel ? 0 : (size_t)a->n_head * tp * D * 2);
     pl->off_v = pl->off_k + (size_t)a->n_head_kv * tp * D * 2;
     pl->off_tab = pl->off_v + (size_t)a->n_head_kv * tp * D * 2;
     pl->bytes = pl->off_tab;
-    if (a->apply_rope) {  // (cos, sin) table [T][rope_dim/2]
-      const int rd = a->rope_dim ? a->rope_dim : a->head_dim;
-      pl->bytes += (size_t)T * (rd / 2) * 8;
-    }
+    if (a->apply_rope) pl->bytes += (size_t)T * (rd / 2) * 8;  // (cos, sin) table [rope_dim/2][T]
   } else {
     pl->t_pad = a->seq_len;
     const bool pre = a->apply_rope || a->q_norm_w || a->k_norm_w;
@@ -670,11 +672,15 @@ int hl_attn_prefill(const hl_prefill_args* a, void* workspace, size_t ws_bytes, 
   pf.t_pad = pl.t_pad;
   hipError_t e;
   if (pl.mfma) {
-    op.qt = (uint16_t*)(ws + pl.off_q);
+    op.qt = pl.q_in_kernel ? nullptr : (uint16_t*)(ws + pl.off_q);
     op.kt = (uint16_t*)(ws + pl.off_k);
     op.vt = (uint16_t*)(ws + pl.off_v);
     op.qt_scale = scale * kLog2e;
-    if (a->apply_rope && rope_dim / 2 <= 64) {
+    if (pl.q_in_kernel) {  // the prologue handles the k and v heads only
+      op.q = nullptr;
+      op.hv_first = a->n_head;
+    }
+    if (a->apply_rope) {
       float2* tab = (float2*)(ws + pl.off_tab);
       if ((e = rope_table_launch(tab, op.theta, a->start_pos, a->seq_len, rope_dim / 2, st)) != hipSuccess)
         return hip_fail(e, "rope table launch");
@@ -684,6 +690,15 @@ int hl_attn_prefill(const hl_prefill_args* a, void* workspace, size_t ws_bytes, 
     pf.qt = op.qt;
     pf.kt = op.kt;
     pf.vt = op.vt;
+    pf.q_in = a->q;
+    pf.io_dtype = a->io_dtype;
+    pf.q_norm_w = a->q_norm_w;
+    pf.eps = a->eps;
+    pf.scale_log2 = scale * kLog2e;
+    pf.do_rope = a->apply_rope;
+    pf.rope_dim = rope_dim;
+    pf.rope_style = a->rope_style;
+    pf.rope_tab = op.rope_tab;
     e = prefill_mfma_launch(pf, st);
     return e == hipSuccess ? HL_OK : hip_fail(e, "prefill launch");
   }

@@ -85,13 +85,15 @@ struct PrologueOp {
   float eps;
   float qt_scale;     // multiplier folded into qt
   int t_pad;          // row count of qt/kt/vt (seq_len rounded up); pad rows zeroed
+  int hv_first;       // first head vector processed (n_head: k and v heads only)
+  int hpg;            // head vectors per workgroup (set by prologue_launch)
   ThetaTable theta;
-  const float2* rope_tab;  // optional [seq_len][rope_dim/2] (cos, sin) of positions start_pos + t
+  const float2* rope_tab;  // optional [rope_dim/2][seq_len] (cos, sin) of positions start_pos + t
 };
 hipError_t prologue_launch(const PrologueOp& op, hipStream_t stream);
 
 // (cos, sin) of angle = float(start_pos + t) * theta[i] for t < T, i < half,
-// written as tab[t * half + i]; one evaluation per (position, pair) shared by
+// written as tab[i * T + t]; one evaluation per (position, pair) shared by
 // every head of a prefill.
 hipError_t rope_table_launch(float2* tab, const ThetaTable& theta, int start_pos, int T, int half,
                              hipStream_t stream);
@@ -112,13 +114,21 @@ struct PrefillLaunch {
   const float* k;
   const float* v;
   // MFMA path: qt [Hq][Tp][D], kt [Hkv][Tp][D], vt [Hkv][D][Tp] (fp16 bits)
-  const uint16_t* qt;
+  const uint16_t* qt;  // null: the MFMA kernel builds Q from q_in itself
   const uint16_t* kt;
   const uint16_t* vt;
   void* out;
   int out_dtype;
   int n_head, n_head_kv, head_dim, seq_len, t_pad;
-  float scale_log2;   // fp32 path only (MFMA path has it folded into qt)
+  float scale_log2;   // fp32 path; MFMA path: folded into qt, or applied to q_in
+  // MFMA path with qt == null: raw col-major q [Hq*D, T] in io_dtype, with
+  // optional qkNorm and RoPE (full-dimension half-split, or interleaved)
+  const void* q_in;
+  int io_dtype;
+  const float* q_norm_w;
+  float eps;
+  int do_rope, rope_dim, rope_style;
+  const float2* rope_tab;  // [rope_dim/2][seq_len]
 };
 hipError_t prefill_f32_launch(const PrefillLaunch& p, hipStream_t stream);
 hipError_t prefill_mfma_launch(const PrefillLaunch& p, hipStream_t stream);

@@ -41,10 +41,16 @@ struct MfmaPrefillParams {
   const uint16_t* vt;
   void* out;
   int n_head, n_head_kv, group, T, Tp;
-  int nh;          // heads per workgroup (waves split nh x (4/nh) row blocks)
+  int nh;          // heads per workgroup (8 waves split nh x (8/nh) row blocks)
   int rows_wg;     // query rows per workgroup = 32 * (4/nh)
   int n_qblk;      // query row blocks of rows_wg
   int n_hgrp;      // head groups of nh per kv head
+  // Q built in the kernel (QIN != 0): raw col-major q [Hq*D, T]
+  const uint16_t* q_in;
+  const float* q_norm_w;
+  float eps, qscale;  // qscale = scale * log2 e
+  int do_rope, rope_dim, rope_style;
+  const float2* rope_tab;  // [rope_dim/2][T] (cos, sin)
 };
 
 __device__ __forceinline__ f32x16 mma32(f16x8 a, f16x8 b, f32x16 c) {
@@ -86,21 +92,110 @@ __device__ __forceinline__ int sigma_row(int m) {
 // tile i+2 is requested right after the one barrier that ends tile i.
 // LDS rows are stored with their 16-byte chunks XOR-swizzled by the row so
 // that the fragment reads (32 rows, one chunk each) hit distinct banks.
-template <int D, int ODT>
-__global__ __launch_bounds__(256, 2) void prefill_mfma_kernel(MfmaPrefillParams p) {
+// Q^T operand of one wave built from the raw activations: lane (ln, hh) holds
+// q[t = r0 + ln][16k + 8hh + e] after optional qkNorm (RMSNorm over the head
+// dimension: the lane's 64 values plus the other half via one xor-32
+// exchange) and RoPE, times scale * log2 e, rounded to fp16.  RoPE partners
+// are in the same lane: half-split over the full head dimension pairs dims
+// d and d + D/2 (k-steps k and k + KSTEPS/2), interleaved pairs e and e + 1.
+// Same formulas as the stand-alone prologue: x * (1/sqrtf(ss/D + eps)) * w[d],
+// (v0, v1) -> (v0*c - v1*s, v0*s + v1*c).
+template <int D, int QDT>
+__device__ __forceinline__ void build_q(const MfmaPrefillParams& p, int hq, int r0, int ln, int hh,
+                                        f16x8* qf) {
+  constexpr int KSTEPS = D / 16;
+  const int t = r0 + ln;
+  const bool tv = t < p.T;
+  const int tc = tv ? t : p.T - 1;
+  const uint16_t* qcol = p.q_in + (long long)hq * D * p.T + tc;
+  float x[KSTEPS][8];
+#pragma unroll
+  for (int k = 0; k < KSTEPS; ++k)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[k][e] = from_bits<QDT>(qcol[(long long)(16 * k + 8 * hh + e) * p.T]);
+  if (p.q_norm_w) {
+    float ss = 0.f;
+#pragma unroll
+    for (int k = 0; k < KSTEPS; ++k)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss += x[k][e] * x[k][e];
+    ss += __shfl_xor(ss, 32, 64);
+    const float inv = 1.0f / sqrtf(ss / (float)D + p.eps);
+#pragma unroll
+    for (int k = 0; k < KSTEPS; ++k)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[k][e] = x[k][e] * inv * p.q_norm_w[16 * k + 8 * hh + e];
+  }
+  if (p.do_rope) {
+    const float2* tab = p.rope_tab + tc;
+    if (p.rope_style == HL_ROPE_HALF_SPLIT) {  // rope_dim == D
+#pragma unroll
+      for (int k = 0; k < KSTEPS / 2; ++k)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float2 cs = tab[(long long)(16 * k + 8 * hh + e) * p.T];
+          const float v0 = x[k][e], v1 = x[k + KSTEPS / 2][e];
+          x[k][e] = v0 * cs.x - v1 * cs.y;
+          x[k + KSTEPS / 2][e] = v0 * cs.y + v1 * cs.x;
+        }
+    } else {
+#pragma unroll
+      for (int k = 0; k < KSTEPS; ++k)
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+          const int d = 16 * k + 8 * hh + e;
+          if (d < p.rope_dim) {
+            const float2 cs = tab[(long long)(d / 2) * p.T];
+            const float v0 = x[k][e], v1 = x[k][e + 1];
+            x[k][e] = v0 * cs.x - v1 * cs.y;
+            x[k][e + 1] = v0 * cs.y + v1 * cs.x;
+          }
+        }
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < KSTEPS; ++k)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) qf[k][e] = (_Float16)(tv ? x[k][e] * p.qscale : 0.f);
+}
+
+// Ping-pong flash kernel.  A workgroup has 8 waves, two per SIMD (waves w
+// and w + 4 share SIMD w % 4).  A SIMD overlaps matrix-core work with vector
+// ALU work only across waves, so the waves run in two groups one phase apart
+// (barrier between phases): while group 0 issues MFMAs (the previous tile's
+// P.V and this tile's S^T = K Q^T), group 1 runs a softmax on the vector
+// ALUs, and the next phase swaps the roles.
+//
+// Wave w owns 32 query rows of one head: head w % nh of the workgroup's nh
+// heads (one GQA group shares the K/V tiles), row block w / nh.  Per wave:
+//   S^T[j][t] = K[j][:] . Q^T[:][t]     (v_mfma_f32_32x32x16_f16, K from LDS,
+//                                        Q^T in registers; the accumulators
+//                                        start at -m_run: scores arrive
+//                                        relative to the row's reference max)
+//   softmax over j for each row t (row t = lane % 32: in-lane plus one xor-32
+//                                        exchange)
+//   O^T[d][t] += V^T[d][j] . P^T[j][t]  (V from LDS, P^T straight from the
+//                                        S^T registers as fp16)
+// The O^T formulation keeps each row's rescale factor a per-lane scalar.
+// K and V tiles go global -> LDS with direct (VGPR-free) copies into two K
+// and two V stages, requested two phases before their first use.  LDS rows
+// are stored with their 16-byte chunks XOR-swizzled by the row so that the
+// fragment reads (32 rows, one chunk each) hit distinct banks.
+template <int D, int ODT, int QIN>
+__global__ __launch_bounds__(512) void prefill_mfma_kernel(MfmaPrefillParams p) {
   constexpr int KSTEPS = D / 16;    // QK^T k-steps
   constexpr int DB = D / 32;        // 32-dim blocks of O^T
   constexpr int KCPR = D / 8;       // 16-byte chunks per K row (key j: D dims)
   constexpr int VCPR = BN / 8;      // 16-byte chunks per V row (dim d: BN keys)
   constexpr int KT = BN * D;        // K stage elements
   constexpr int VT = D * BN;        // V stage elements
-  constexpr int STAGE = KT + VT;
-  constexpr int KI = KT / 8 / 64 / 4;  // direct copies per wave per tile (K)
-  constexpr int VI = VT / 8 / 64 / 4;  // (V)
-  __shared__ __attribute__((aligned(1024))) uint16_t lds[2 * STAGE];
+  constexpr int KI = KT / 8 / 64 / 8;  // direct copies per wave per tile (K)
+  constexpr int VI = VT / 8 / 64 / 8;  // (V)
+  __shared__ __attribute__((aligned(1024))) uint16_t lds[2 * KT + 2 * VT];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar branches
+  const int grp = wave >> 2;                                  // 0 leads, 1 lags one phase
   const int hh = lane >> 5, ln = lane & 31;
 
   // Work item: heaviest (last) query blocks first; within a query block the
@@ -121,33 +216,42 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma_kernel(MfmaPrefillParams 
 
   const uint16_t* kbase = p.kt + (long long)kvh * p.Tp * D;
   const uint16_t* vbase = p.vt + (long long)kvh * D * p.Tp;
+  uint16_t* const kst0 = lds;
+  uint16_t* const vst0 = lds + 2 * KT;
 
-  // Tile j0 -> stage: every wave copies KI + VI KB of the 2*BN*D*2-byte tile.
-  auto request_tile = [&](int j0, uint16_t* st) {
+  // Tile j -> its stage: every wave copies KI (K) or VI (V) 1 KB blocks.
+  auto request_k = [&](int j) {
+    uint16_t* st = kst0 + (j & 1) * KT;
 #pragma unroll
     for (int r = 0; r < KI; ++r) {
       const int blk = wave * KI + r;            // 1 KB block of the K stage
-      const int j = blk * (64 / KCPR) + lane / KCPR;
+      const int row = blk * (64 / KCPR) + lane / KCPR;
       const int slot = lane % KCPR;
-      const int c = slot ^ (j % KCPR);
-      copy16_to_lds(kbase + (long long)(j0 + j) * D + 8 * c, st + blk * 512);
+      const int c = slot ^ (row % KCPR);
+      copy16_to_lds(kbase + (long long)(j * BN + row) * D + 8 * c, st + blk * 512);
     }
+  };
+  auto request_v = [&](int j) {
+    uint16_t* st = vst0 + (j & 1) * VT;
 #pragma unroll
     for (int r = 0; r < VI; ++r) {
       const int blk = wave * VI + r;            // 1 KB block of the V stage
       const int d = blk * (64 / VCPR) + lane / VCPR;
       const int slot = lane % VCPR;
       const int c = slot ^ (d % VCPR);
-      copy16_to_lds(vbase + (long long)d * p.Tp + j0 + 8 * c, st + KT + blk * 512);
+      copy16_to_lds(vbase + (long long)d * p.Tp + j * BN + 8 * c, st + blk * 512);
     }
   };
 
-  request_tile(0, lds);
-  if (n_tiles > 1) request_tile(BN, lds + STAGE);
+  request_k(0);
+  if (n_tiles > 1) request_k(1);
+  request_v(0);
 
   // Q^T operand: lane holds q[t = r0 + ln][16*k + 8*hh .. +7]
   f16x8 qf[KSTEPS];
-  {
+  if constexpr (QIN != 0) {
+    build_q<D, QIN>(p, hq, r0, ln, hh, qf);
+  } else {
     const int t = min(r0 + ln, p.Tp - 1);
     const uint16_t* qrow = p.qt + ((long long)hq * p.Tp + t) * D;
 #pragma unroll
@@ -159,118 +263,164 @@ __global__ __launch_bounds__(256, 2) void prefill_mfma_kernel(MfmaPrefillParams 
   for (int db = 0; db < DB; ++db)
 #pragma unroll
     for (int i = 0; i < 16; ++i) o[db][i] = 0.f;
-  float m_run = -INFINITY, l_run = 0.f;
+  // Scores are kept relative to a per-row reference max m_run (log2 units):
+  // the S^T accumulators start at -m_run (negm), so the exponentials take
+  // the MFMA output as it is.  m_run starts at the first tile's max and only
+  // moves when a tile's max exceeds it by more than kRescale.
+  float m_run = 0.f, l_run = 0.f;
+  f32x16 negm;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) negm[i] = 0.f;
   const f16x2 ones = {(_Float16)1.0f, (_Float16)1.0f};
   const int t_abs = r0 + ln;
 
   // Per-lane LDS offsets (elements) of the fragments this lane reads.
   int koff[2], voff[DB];
 #pragma unroll
-  for (int mb = 0; mb < 2; ++mb) {
-    const int j = 32 * mb + sigma_row(ln);
-    koff[mb] = j * D;  // chunk (2k + hh) ^ (j % KCPR) added per k-step
-  }
+  for (int mb = 0; mb < 2; ++mb) koff[mb] = (32 * mb + sigma_row(ln)) * D;
 #pragma unroll
-  for (int db = 0; db < DB; ++db) voff[db] = KT + (32 * db + ln) * BN;
+  for (int db = 0; db < DB; ++db) voff[db] = (32 * db + ln) * BN;
   const int kswz[2] = {(32 * 0 + sigma_row(ln)) % KCPR, (32 * 1 + sigma_row(ln)) % KCPR};
   const int vswz = ln % VCPR;  // (32*db + ln) % 8 == ln % 8
 
-  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): tile 0 (and 1) landed for this wave
+  f32x16 s[2];   // S^T of the tile between its QK^T and its softmax
+  f16x8 pf[4];   // P^T of the tile between its softmax and its P.V:
+                 // k-step 2*mb + u holds keys 16(2mb+u) + 8hh + 0..7
+
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): K tiles 0, 1 and V tile 0 landed for this wave
   __syncthreads();
 
-  for (int tile = 0; tile < n_tiles; ++tile) {
-    const int j0 = tile * BN;
-    const uint16_t* st = lds + (tile & 1) * STAGE;
-
-    if (tile < wave_tiles) {
-      // All K fragments first, then the two key-block MFMA chains interleaved.
-      f32x16 s[2];
-      f16x8 kf[2][KSTEPS];
+  // Matrix step m: P.V of tile m - 1, then S^T of tile m.
+  auto matrix_step = [&](const int j) {
+    // Fragments
+    // are read one k-step ahead of their MFMAs and the steps are fenced,
+    // so only two steps' fragments are live (the other wave of the SIMD
+    // covers the LDS latency with its softmax).
+    const bool do_pv = j >= 1 && j - 1 < wave_tiles, do_qk = j < wave_tiles;
+    const uint16_t* vst = vst0 + ((j - 1) & 1) * VT;
+    const uint16_t* kst = kst0 + (j & 1) * KT;
+    if (do_pv) {
+      f16x8 va[2][DB];
 #pragma unroll
-      for (int mb = 0; mb < 2; ++mb)
+      for (int db = 0; db < DB; ++db) va[0][db] = *(const f16x8*)(vst + voff[db] + 8 * (hh ^ vswz));
 #pragma unroll
-        for (int k = 0; k < KSTEPS; ++k)
-          kf[mb][k] = *(const f16x8*)(st + koff[mb] + 8 * ((2 * k + hh) ^ kswz[mb]));
+      for (int u = 0; u < 4; ++u) {
+        if (u + 1 < 4) {
 #pragma unroll
-      for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) s[mb][i] = 0.f;
-#pragma unroll
-      for (int k = 0; k < KSTEPS; ++k)
-#pragma unroll
-        for (int mb = 0; mb < 2; ++mb) s[mb] = mma32(kf[mb][k], qf[k], s[mb]);
-      __builtin_amdgcn_sched_group_barrier(0x100, 2 * KSTEPS, 0);  // LDS reads first
-      __builtin_amdgcn_sched_group_barrier(0x008, 2 * KSTEPS, 0);  // then the MFMAs
-
-      // causal mask on the diagonal tile only: key j > row t -> -inf
-      if (j0 + BN - 1 > r0) {
-#pragma unroll
-        for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            const int a = i >> 2;
-            const int j = j0 + 32 * mb + 16 * (a >> 1) + 8 * hh + 4 * (a & 1) + (i & 3);
-            s[mb][i] = j > t_abs ? -INFINITY : s[mb][i];
-          }
-      }
-
-      float mt = -INFINITY;
-#pragma unroll
-      for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) mt = fmaxf(mt, s[mb][i]);
-      mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
-      // Every row t < T has an unmasked key j0 <= t in each tile it visits;
-      // rows >= T (padding) score their zero-padded q, so mt is finite.
-      const bool grew = mt > m_run + kRescale;
-      const float mn = grew ? mt : m_run;
-      f16x8 pf[4];  // P^T operands: k-step 2*mb + u holds keys 16(2mb+u) + 8hh + 0..7
-      float ps = 0.f;
-#pragma unroll
-      for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-#pragma unroll
-          for (int e = 0; e < 8; ++e)
-            pf[2 * mb + u][e] = (_Float16)fast_exp2(s[mb][8 * u + e] - mn);
-          // row sum from the same fp16 values the MFMA consumes
-#pragma unroll
-          for (int e = 0; e < 8; e += 2) {
-            const f16x2 pr = {pf[2 * mb + u][e], pf[2 * mb + u][e + 1]};
-            ps = __builtin_amdgcn_fdot2(pr, ones, ps, false);
-          }
+          for (int db = 0; db < DB; ++db)
+            va[(u + 1) & 1][db] = *(const f16x8*)(vst + voff[db] + 8 * ((2 * (u + 1) + hh) ^ vswz));
         }
-      // rescale only when some row's reference max moved (uniform test
-      // across the wave); on the first tile o and l are still zero
-      if (tile > 0 && __builtin_amdgcn_ballot_w64(grew) != 0) {
-        const float alpha = fast_exp2(m_run - mn);
+#pragma unroll
+        for (int db = 0; db < DB; ++db) o[db] = mma32(va[u & 1][db], pf[u], o[db]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    if (do_qk) {
+      f16x8 kf[2][2];
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb) kf[0][mb] = *(const f16x8*)(kst + koff[mb] + 8 * (hh ^ kswz[mb]));
+#pragma unroll
+      for (int k = 0; k < KSTEPS; ++k) {
+        if (k + 1 < KSTEPS) {
+#pragma unroll
+          for (int mb = 0; mb < 2; ++mb)
+            kf[(k + 1) & 1][mb] = *(const f16x8*)(kst + koff[mb] + 8 * ((2 * (k + 1) + hh) ^ kswz[mb]));
+        }
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb) s[mb] = mma32(kf[k & 1][mb], qf[k], k == 0 ? negm : s[mb]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  };
+  // Vector step: softmax of tile j.
+  auto vector_step = [&](const int j) {
+    if (j < 0 || j >= wave_tiles) return;
+    const int j0 = j * BN;
+    if (j0 + BN - 1 > r0) {  // causal mask: key j > row t -> -inf
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int a = i >> 2;
+          const int key = j0 + 32 * mb + 16 * (a >> 1) + 8 * hh + 4 * (a & 1) + (i & 3);
+          s[mb][i] = key > t_abs ? -INFINITY : s[mb][i];
+        }
+    }
+    float mt = -INFINITY;
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) mt = fmaxf(mt, s[mb][i]);
+    mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+    // Every row t < T has an unmasked key j0 <= t in each tile it visits;
+    // rows >= T (padding) score their zero-padded q, so mt is finite.
+    // The first tile sets the reference; later ones move it only when
+    // their max exceeds it by more than kRescale (then o and l rescale).
+    const bool grew = j == 0 || mt > kRescale;
+    if (__builtin_amdgcn_ballot_w64(grew) != 0) {  // uniform, rare after the first tile
+      const float dm = grew ? mt : 0.f;
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) s[mb][i] -= dm;
+      if (j > 0) {
+        const float alpha = fast_exp2(-dm);
         l_run *= alpha;
 #pragma unroll
         for (int db = 0; db < DB; ++db)
 #pragma unroll
           for (int i = 0; i < 16; ++i) o[db][i] *= alpha;
       }
-      m_run = mn;
-      l_run += ps;
-
-      // All V fragments, then DB independent MFMA chains interleaved.
-      f16x8 va[DB][4];
+      m_run += dm;
 #pragma unroll
-      for (int db = 0; db < DB; ++db)
-#pragma unroll
-        for (int u = 0; u < 4; ++u)
-          va[db][u] = *(const f16x8*)(st + voff[db] + 8 * ((2 * u + hh) ^ vswz));
-#pragma unroll
-      for (int u = 0; u < 4; ++u)
-#pragma unroll
-        for (int db = 0; db < DB; ++db) o[db] = mma32(va[db][u], pf[u], o[db]);
+      for (int i = 0; i < 16; ++i) negm[i] = -m_run;
     }
-
-    // End of tile: every wave is done with this stage and its copies of the
-    // next tile have landed; then the stage is refilled with tile + 2.
-    __builtin_amdgcn_s_waitcnt(0x0F70);
-    __syncthreads();
-    if (tile + 2 < n_tiles) request_tile(j0 + 2 * BN, lds + (tile & 1) * STAGE);
+    float ps = 0.f;
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) pf[2 * mb + u][e] = (_Float16)fast_exp2(s[mb][8 * u + e]);
+        // row sum from the same fp16 values the MFMA consumes
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+          const f16x2 pr = {pf[2 * mb + u][e], pf[2 * mb + u][e + 1]};
+          ps = __builtin_amdgcn_fdot2(pr, ones, ps, false);
+        }
+      }
+    l_run += ps;
+  };
+  // Phase 2m: the stages of K(m-1) and V(m-2) are no longer read, so they
+  // take K(m+1) and V(m); both are first read at phase 2m+2.  After each odd
+  // phase every wave's copies have landed; the barrier publishes them.
+  auto copies = [&](const int m) {
+    if (m >= 1) {
+      if (m + 1 < n_tiles) request_k(m + 1);
+      if (m < n_tiles) request_v(m);
+    }
+  };
+  // Group 0 runs matrix step m in phase 2m and vector step m in phase 2m+1;
+  // group 1 runs vector step m-1 in phase 2m and matrix step m in 2m+1.
+  // Both loops pass the same barriers.
+  if (grp == 0) {
+    for (int m = 0; m <= n_tiles; ++m) {
+      copies(m);
+      matrix_step(m);
+      __syncthreads();
+      vector_step(m);
+      __builtin_amdgcn_s_waitcnt(0x0F70);
+      __syncthreads();
+    }
+  } else {
+    for (int m = 0; m <= n_tiles; ++m) {
+      copies(m);
+      vector_step(m - 1);
+      __syncthreads();
+      matrix_step(m);
+      __builtin_amdgcn_s_waitcnt(0x0F70);
+      __syncthreads();
+    }
   }
 
   if (!live) return;
@@ -299,22 +449,38 @@ hipError_t prefill_mfma_launch(const PrefillLaunch& a, hipStream_t stream) {
   p.T = a.seq_len;
   p.Tp = a.t_pad;
   p.nh = (p.group % 4 == 0) ? 4 : ((p.group % 2 == 0) ? 2 : 1);
-  p.rows_wg = QR * (4 / p.nh);
+  p.rows_wg = QR * (8 / p.nh);
   p.n_qblk = (p.T + p.rows_wg - 1) / p.rows_wg;
   p.n_hgrp = p.group / p.nh;
+  p.q_in = (const uint16_t*)a.q_in;
+  p.q_norm_w = a.q_norm_w;
+  p.eps = a.eps;
+  p.qscale = a.scale_log2;
+  p.do_rope = a.do_rope;
+  p.rope_dim = a.rope_dim;
+  p.rope_style = a.rope_style;
+  p.rope_tab = a.rope_tab;
+  const int qin = a.qt ? 0 : a.io_dtype;
   dim3 grid(a.n_head_kv * p.n_hgrp * p.n_qblk);
-#define HL_PF(DD, OD) hipLaunchKernelGGL((prefill_mfma_kernel<DD, OD>), grid, dim3(256), 0, stream, p)
+#define HL_PF(DD, OD, QI) hipLaunchKernelGGL((prefill_mfma_kernel<DD, OD, QI>), grid, dim3(512), 0, stream, p)
+#define HL_PF_Q(DD, OD)                          \
+  switch (qin) {                                 \
+    case HL_F16: HL_PF(DD, OD, HL_F16); break;   \
+    case HL_BF16: HL_PF(DD, OD, HL_BF16); break; \
+    default: HL_PF(DD, OD, 0); break;            \
+  }
   if (a.head_dim == 64) {
-    if (a.out_dtype == HL_F16) HL_PF(64, HL_F16);
-    else if (a.out_dtype == HL_BF16) HL_PF(64, HL_BF16);
-    else HL_PF(64, HL_F32);
+    if (a.out_dtype == HL_F16) HL_PF_Q(64, HL_F16)
+    else if (a.out_dtype == HL_BF16) HL_PF_Q(64, HL_BF16)
+    else HL_PF_Q(64, HL_F32)
   } else if (a.head_dim == 128) {
-    if (a.out_dtype == HL_F16) HL_PF(128, HL_F16);
-    else if (a.out_dtype == HL_BF16) HL_PF(128, HL_BF16);
-    else HL_PF(128, HL_F32);
+    if (a.out_dtype == HL_F16) HL_PF_Q(128, HL_F16)
+    else if (a.out_dtype == HL_BF16) HL_PF_Q(128, HL_BF16)
+    else HL_PF_Q(128, HL_F32)
   } else {
     return hipErrorInvalidValue;
   }
+#undef HL_PF_Q
 #undef HL_PF
   return hipGetLastError();
 }

@@ -103,7 +103,7 @@ hipError_t headvec_launch(const HeadVecOp& op, hipStream_t stream) {
 // head, and with angles up to ~T rad it is the costly part of this kernel.
 // ---------------------------------------------------------------------------
 constexpr int kPT = 32;   // tokens per tile
-constexpr int kHPG = 8;   // head vectors per workgroup
+constexpr int kHPG = 8;   // most head vectors per workgroup
 constexpr int kTabHalf = 64;  // largest rope_dim/2 served from the LDS table
 
 // 8 consecutive elements [t, t+8) of one activation row as fp32; t >= lim -> 0.
@@ -153,9 +153,9 @@ __device__ __forceinline__ void store_row8(void* base, long long off, int t, int
   }
 }
 
-template <int IODT, int KDT>
+template <int IODT, int KDT, int DMAX>
 __global__ __launch_bounds__(256) void prologue_kernel(PrologueOp op) {
-  __shared__ float sx[HL_MAX_HEAD_DIM][kPT + 1];
+  __shared__ float sx[DMAX][kPT + 1];  // DMAX >= head_dim: the tile, sized to its class
   __shared__ float scos[kTabHalf][kPT], ssin[kTabHalf][kPT];
   __shared__ float sred[8][kPT];
   __shared__ float sinv[kPT];
@@ -163,8 +163,8 @@ __global__ __launch_bounds__(256) void prologue_kernel(PrologueOp op) {
   const int T = op.seq_len, D = op.head_dim;
   const int t0 = blockIdx.x * kPT;
   const int n_vec = op.n_head + 2 * op.n_head_kv;
-  const int hv0 = blockIdx.y * kHPG;
-  const int hv1 = min(n_vec, hv0 + kHPG);
+  const int hv0 = op.hv_first + blockIdx.y * op.hpg;
+  const int hv1 = min(n_vec, hv0 + op.hpg);
   const int tc = tid & (kPT - 1), part = tid / kPT;  // 8 parts of 32 lanes
   const int t = t0 + tc;
   const int half = op.rope_dim / 2;
@@ -173,7 +173,7 @@ __global__ __launch_bounds__(256) void prologue_kernel(PrologueOp op) {
   if (tab) {
     if (op.rope_tab) {  // precomputed by rope_table_kernel
       for (int i = part; i < half; i += 8) {
-        const float2 cs = t < T ? op.rope_tab[(long long)t * half + i] : make_float2(1.f, 0.f);
+        const float2 cs = t < T ? op.rope_tab[(long long)i * T + t] : make_float2(1.f, 0.f);
         scos[i][tc] = cs.x;
         ssin[i][tc] = cs.y;
       }
@@ -203,7 +203,7 @@ __global__ __launch_bounds__(256) void prologue_kernel(PrologueOp op) {
   auto src_of = [&](int kind) { return kind == 0 ? op.q : (kind == 1 ? op.k : op.v); };
   // Loads head hv's [D, 32] tile into registers: thread -> (row, 8-token
   // chunk), 64 rows per pass, D <= 256 -> at most 4 passes.
-  constexpr int kPass = HL_MAX_HEAD_DIM / 64;
+  constexpr int kPass = DMAX / 64;
   const int c8 = (tid & 3) * 8;
   auto load_regs = [&](int hv, float (*x)[8]) {
     int kind, h;
@@ -334,9 +334,18 @@ __global__ __launch_bounds__(256) void prologue_kernel(PrologueOp op) {
 
 hipError_t prologue_launch(const PrologueOp& op, hipStream_t stream) {
   const int cols = op.t_pad > op.seq_len ? op.t_pad : op.seq_len;
-  const int n_vec = op.n_head + 2 * op.n_head_kv;
-  dim3 grid((cols + kPT - 1) / kPT, (n_vec + kHPG - 1) / kHPG);
-#define HL_PRO(IO, KD) hipLaunchKernelGGL((prologue_kernel<IO, KD>), grid, dim3(256), 0, stream, op)
+  const int n_vec = op.n_head + 2 * op.n_head_kv - op.hv_first;
+  const int tiles = (cols + kPT - 1) / kPT;
+  // Head vectors per workgroup: enough workgroups (~2048) to keep every CU
+  // busy through the load latency of a tile, and up to kHPG so that small
+  // prefills share one cos/sin table fill across heads.
+  PrologueOp o2 = op;
+  o2.hpg = kHPG;
+  while (o2.hpg > 1 && (long long)tiles * ((n_vec + o2.hpg - 1) / o2.hpg) < 2048) o2.hpg >>= 1;
+  dim3 grid(tiles, (n_vec + o2.hpg - 1) / o2.hpg);
+#define HL_PRO(IO, KD)                                                                          \
+  if (op.head_dim <= 128) hipLaunchKernelGGL((prologue_kernel<IO, KD, 128>), grid, dim3(256), 0, stream, o2); \
+  else hipLaunchKernelGGL((prologue_kernel<IO, KD, HL_MAX_HEAD_DIM>), grid, dim3(256), 0, stream, o2)
 #define HL_PRO_IO(IO)                      \
   switch (op.kv_dtype) {                   \
     case HL_F32: HL_PRO(IO, HL_F32); break; \
@@ -357,7 +366,7 @@ __global__ __launch_bounds__(256) void rope_table_kernel(float2* tab, ThetaTable
                                                          int T, int half) {
   const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
   if (idx >= (long long)T * half) return;
-  const int t = (int)(idx / half), i = (int)(idx % half);
+  const int i = (int)(idx / T), t = (int)(idx % T);  // layout [pair][token]
   const float angle = (float)(start_pos + t) * theta.t[i];
   tab[idx] = make_float2(cosf(angle), sinf(angle));
 }

@@ -116,23 +116,51 @@ def test_prefill_mfma_shapes(hl, orc, dt, T, hq, hkv, d):
 
 
 @pytest.mark.parametrize("dt", [1, 2])
-def test_prefill_mfma_qknorm_interleaved_partial_rope_cache(hl, orc, dt):
-    hq, hkv, d, T, max_len, rd = 16, 4, 128, 150, 160, 64
+@pytest.mark.parametrize("style,rd", [(1, 64), (0, 128), (0, 64)])
+def test_prefill_mfma_qknorm_rope_cache(hl, orc, dt, style, rd):
+    """qkNorm + RoPE + cache write.  Interleaved (any rope_dim) and full-width
+    half-split RoPE are applied to Q inside the MFMA kernel; half-split over
+    part of the head goes through the prepared-Q layout."""
+    hq, hkv, d, T, max_len = 16, 4, 128, 150, 160
     q, k, v = (orc.upcast(orc.to_storage(orc.normal(h * d * T, 50 + i), dt), dt).reshape(-1, T)
                for i, h in enumerate((hq, hkv, hkv)))
     wq, wk = orc.uniform(d, 53, 0.5, 1.5), orc.uniform(d, 54, 0.5, 1.5)
-    ref, _, kr = oracle_prefill(orc, q, k, v, hq, hkv, d, T, base=1e6, style=1, wq=wq, wk=wk,
+    ref, _, kr = oracle_prefill(orc, q, k, v, hq, hkv, d, T, base=1e6, style=style, wq=wq, wk=wk,
                                 rope_dim=rd)
     kc = torch.zeros(hkv * d, max_len, dtype=TDT[dt], device="cuda")
     vc = torch.zeros(hkv * d, max_len, dtype=TDT[dt], device="cuda")
     out = run_prefill(to_dev(q, dt), to_dev(k, dt), to_dev(v, dt), hq, hkv, d, T,
-                      apply_rope=True, rope_base=1e6, rope_style=1, rope_dim=rd,
+                      apply_rope=True, rope_base=1e6, rope_style=style, rope_dim=rd,
                       q_norm_w=torch.from_numpy(wq).cuda(), k_norm_w=torch.from_numpy(wk).cuda(),
                       k_cache=kc, v_cache=vc, max_len=max_len)
     assert rel_err(from_dev(out), ref) < TOL_LOWP
     # cache: V bit-exact conversion; K within one storage ulp of the oracle's roped K
     assert np.array_equal(from_dev(vc)[:, :T], v)
     assert rel_err(from_dev(kc)[:, :T], kr) < 2 ** -7
+
+
+@pytest.mark.parametrize("style", [0, 1])
+def test_prefill_mfma_start_pos(hl, orc, style):
+    """A chunk that continues a sequence: RoPE at positions start_pos + t and
+    the cache written from column start_pos; earlier columns untouched."""
+    hq, hkv, d, T, start, max_len, dt = 8, 2, 64, 70, 37, 128, 2
+    q, k, v = (orc.upcast(orc.to_storage(orc.normal(h * d * T, 80 + i), dt), dt).reshape(-1, T)
+               for i, h in enumerate((hq, hkv, hkv)))
+    th = orc.theta_table(d, 5e5)
+    qr = orc.rope_cols(q, hq, d, T, d, th, start, style)
+    kr = orc.rope_cols(k, hkv, d, T, d, th, start, style)
+    ref = orc.attention_prefill(qr, kr, v, hq, hkv, d, T)
+    kc = torch.full((hkv * d, max_len), 7.0, dtype=TDT[dt], device="cuda")
+    vc = torch.full((hkv * d, max_len), 7.0, dtype=TDT[dt], device="cuda")
+    out = run_prefill(to_dev(q, dt), to_dev(k, dt), to_dev(v, dt), hq, hkv, d, T,
+                      apply_rope=True, rope_base=5e5, rope_style=style, k_cache=kc, v_cache=vc,
+                      max_len=max_len, start_pos=start)
+    assert rel_err(from_dev(out), ref) < TOL_LOWP
+    kch, vch = from_dev(kc), from_dev(vc)
+    assert np.array_equal(vch[:, start:start + T], v)
+    assert rel_err(kch[:, start:start + T], kr) < 2 ** -7
+    assert np.all(kch[:, :start] == 7.0) and np.all(kch[:, start + T:] == 7.0)
+    assert np.all(vch[:, :start] == 7.0) and np.all(vch[:, start + T:] == 7.0)
 
 
 def test_prefill_c4_full_size_sampled(hl, orc):
