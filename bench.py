@@ -58,6 +58,13 @@ def event_time_ms(torch, fn, iters):
     return e0.elapsed_time(e1) / iters
 
 
+# HBM bytes per launch of the fused c3 step kernel, measured with rocprofv3
+# FETCH_SIZE / WRITE_SIZE and scaled by a copy kernel of known size (the
+# summary with the commands is profiles/decode_step_c3_traffic.md); to be
+# re-measured whenever the decode kernel changes.
+C3_STEP_TRAFFIC_BYTES = 35_161_600
+
+
 def capture(torch, fn, n, first=0):
     """Captures n calls fn(first), fn(first+1), ... into one HIP graph."""
     side = torch.cuda.Stream()
@@ -229,6 +236,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", choices=["all", "decode", "prefill", "c5"], default="all")
+    ap.add_argument("--calib", action="store_true",
+                    help="also run a 256 MiB -> 256 MiB elementwise copy (3x): the known-size "
+                         "kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
@@ -240,6 +250,14 @@ def main():
     torch.cuda.init()
     info = A.device_info()
     log(f"device: {info['arch']} CUs={info['cu_count']} clk={info['clock_khz']} kHz")
+
+    if args.calib:  # an elementwise kernel that reads and writes 256 MiB each
+        src = torch.ones(64 << 20, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            torch.mul(src, 1.0, out=dst)
+        torch.cuda.synchronize()
+        del src, dst
 
     result = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
               "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
@@ -267,7 +285,10 @@ def main():
             "roofline": {"bound": "hbm", "kernel": "decode_mfma_kernel (fused step)",
                          "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(achieved / HBM_PEAK_GBS, 4),
-                         "traffic": None, "algorithmic_bytes": wl.kv_bytes,
+                         "traffic": C3_STEP_TRAFFIC_BYTES,
+                         "traffic_source": "profiles/decode_step_c3_traffic.md: rocprofv3 "
+                                           "FETCH_SIZE x 1.99981 + WRITE_SIZE x 1.0 per launch",
+                         "algorithmic_bytes": wl.kv_bytes,
                          "avg_us": round(t["kernel"] * 1e3, 3)},
             "attention_only_us": round(t["attn"] * 1e3, 3),
             "rope_store_only_us": round(t["rope_store"] * 1e3, 3),
