@@ -680,12 +680,7 @@ int hl_attn_prefill(const hl_prefill_args* a, void* workspace, size_t ws_bytes, 
       op.q = nullptr;
       op.hv_first = a->n_head;
     }
-    if (a->apply_rope) {
-      float2* tab = (float2*)(ws + pl.off_tab);
-      if ((e = rope_table_launch(tab, op.theta, a->start_pos, a->seq_len, rope_dim / 2, st)) != hipSuccess)
-        return hip_fail(e, "rope table launch");
-      op.rope_tab = tab;
-    }
+    if (a->apply_rope) op.rope_tab_out = (float2*)(ws + pl.off_tab);  // written by the prologue
     if ((e = prologue_launch(op, st)) != hipSuccess) return hip_fail(e, "prefill prologue launch");
     pf.qt = op.qt;
     pf.kt = op.kt;
@@ -698,7 +693,7 @@ int hl_attn_prefill(const hl_prefill_args* a, void* workspace, size_t ws_bytes, 
     pf.do_rope = a->apply_rope;
     pf.rope_dim = rope_dim;
     pf.rope_style = a->rope_style;
-    pf.rope_tab = op.rope_tab;
+    pf.rope_tab = op.rope_tab_out;
     e = prefill_mfma_launch(pf, st);
     return e == hipSuccess ? HL_OK : hip_fail(e, "prefill launch");
   }

@@ -88,15 +88,10 @@ struct PrologueOp {
   int hv_first;       // first head vector processed (n_head: k and v heads only)
   int hpg;            // head vectors per workgroup (set by prologue_launch)
   ThetaTable theta;
-  const float2* rope_tab;  // optional [rope_dim/2][seq_len] (cos, sin) of positions start_pos + t
+  float2* rope_tab_out;  // optional: receives the (cos, sin) table [rope_dim/2][seq_len] of
+                         // positions start_pos + t (rope_dim/2 <= 64)
 };
 hipError_t prologue_launch(const PrologueOp& op, hipStream_t stream);
-
-// (cos, sin) of angle = float(start_pos + t) * theta[i] for t < T, i < half,
-// written as tab[i * T + t]; one evaluation per (position, pair) shared by
-// every head of a prefill.
-hipError_t rope_table_launch(float2* tab, const ThetaTable& theta, int start_pos, int T, int half,
-                             hipStream_t stream);
 
 // Plain column copy with dtype conversion: cache[r*cache_cols + start + c] =
 // src[r*src_cols + c] (two tensors when src2 != null).

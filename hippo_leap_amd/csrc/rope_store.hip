@@ -171,19 +171,16 @@ __global__ __launch_bounds__(256) void prologue_kernel(PrologueOp op) {
   const bool tab = op.do_rope && half <= kTabHalf && hv0 < op.n_head + op.n_head_kv;
 
   if (tab) {
-    if (op.rope_tab) {  // precomputed by rope_table_kernel
-      for (int i = part; i < half; i += 8) {
-        const float2 cs = t < T ? op.rope_tab[(long long)i * T + t] : make_float2(1.f, 0.f);
-        scos[i][tc] = cs.x;
-        ssin[i][tc] = cs.y;
-      }
-    } else {
-      const float pos = (float)(op.start_pos + t);
-      for (int i = part; i < half; i += 8) {
-        const float angle = pos * op.theta.t[i];
-        scos[i][tc] = cosf(angle);
-        ssin[i][tc] = sinf(angle);
-      }
+    // The first head group's workgroup of each tile also publishes its slice
+    // as tab_out[i][t] for the flash kernel's Q.
+    const bool publish = op.rope_tab_out && blockIdx.y == 0;
+    const float pos = (float)(op.start_pos + t);
+    for (int i = part; i < half; i += 8) {
+      const float angle = pos * op.theta.t[i];
+      const float c = cosf(angle), sn = sinf(angle);
+      scos[i][tc] = c;
+      ssin[i][tc] = sn;
+      if (publish && t < T) op.rope_tab_out[(long long)i * T + t] = make_float2(c, sn);
     }
   }
 
@@ -359,23 +356,6 @@ hipError_t prologue_launch(const PrologueOp& op, hipStream_t stream) {
   }
 #undef HL_PRO_IO
 #undef HL_PRO
-  return hipGetLastError();
-}
-
-__global__ __launch_bounds__(256) void rope_table_kernel(float2* tab, ThetaTable theta, int start_pos,
-                                                         int T, int half) {
-  const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
-  if (idx >= (long long)T * half) return;
-  const int i = (int)(idx / T), t = (int)(idx % T);  // layout [pair][token]
-  const float angle = (float)(start_pos + t) * theta.t[i];
-  tab[idx] = make_float2(cosf(angle), sinf(angle));
-}
-
-hipError_t rope_table_launch(float2* tab, const ThetaTable& theta, int start_pos, int T, int half,
-                             hipStream_t stream) {
-  const long long n = (long long)T * half;
-  hipLaunchKernelGGL(rope_table_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, tab,
-                     theta, start_pos, T, half);
   return hipGetLastError();
 }
 
