@@ -329,8 +329,159 @@ __global__ __launch_bounds__(256) void prologue_kernel(PrologueOp op) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// K/V prologue of an MFMA prefill whose Q the flash kernel builds itself.
+// One workgroup per (32-token tile, kv head) handles that head's K and V with
+// no fp32 staging: thread (r = tid / 4, c8 = 8 * (tid % 4)) holds rows r and
+// r + 64 (D = 128) of 8 tokens.  Half-split RoPE over
+// the whole head pairs rows r and r + D/2, which are in one thread;
+// interleaved RoPE pairs rows 2i and 2i + 1, one lane-shuffle apart.  V goes
+// from registers to the cache and to vt; only kt (token-major) is transposed,
+// through a 32 x D fp16 LDS tile.  Formulas as the general prologue's:
+// x * (1/sqrtf(ss/D + eps)) * w[d], (v0c - v1s, v0s + v1c), angle =
+// float(start_pos + t) * theta[i].
+// ---------------------------------------------------------------------------
+template <int IODT, int KDT, int D>
+__global__ __launch_bounds__(256) void kv_prologue_kernel(PrologueOp op) {
+  static_assert(D == 128, "two rows per thread: r and r + 64");
+  constexpr int NP = D / 64;  // row passes: rows r + 64 * ps
+  __shared__ __attribute__((aligned(16))) uint16_t skt[kPT][D + 8];  // kt tile (fp16 bits), padded rows
+  __shared__ float sred[4][kPT];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int T = op.seq_len;
+  const int t0 = blockIdx.x * kPT;
+  const int h = blockIdx.y;
+  const int r = tid >> 2, c8 = (tid & 3) * 8;
+  const int t = t0 + c8;  // this thread's first token
+  const long long hbase = (long long)h * D * T;
+
+  float k[NP][8], v[NP][8];
+#pragma unroll
+  for (int ps = 0; ps < NP; ++ps) {
+    load_row8_f32<IODT>(op.k, hbase + (long long)(r + 64 * ps) * T + t, t, T, k[ps]);
+    load_row8_f32<IODT>(op.v, hbase + (long long)(r + 64 * ps) * T + t, t, T, v[ps]);
+  }
+
+  // V: cache column block and vt, straight from registers.
+#pragma unroll
+  for (int ps = 0; ps < NP; ++ps) {
+    const int row = r + 64 * ps;
+    if (op.v_cache)
+      store_row8<KDT>(op.v_cache, ((long long)h * D + row) * op.max_len + op.start_pos + t, t, T, v[ps]);
+    if (t < op.t_pad) {
+      float x[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = t + e < T ? v[ps][e] : 0.f;
+      store_row8<HL_F16>(op.vt, ((long long)h * D + row) * op.t_pad + t, t, op.t_pad, x);
+    }
+  }
+
+  // K: RMSNorm over the head dimension per token.
+  if (op.k_norm_w) {
+    float ss[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float a = 0.f;
+#pragma unroll
+      for (int ps = 0; ps < NP; ++ps) a += k[ps][e] * k[ps][e];
+      // lanes with the same c8 (tid % 4) hold the other rows of this wave
+#pragma unroll
+      for (int m = 4; m < 64; m <<= 1) a += __shfl_xor(a, m, 64);
+      ss[e] = a;
+    }
+    if (lane < 4) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sred[wave][c8 + e] = ss[e];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float tot = sred[0][c8 + e] + sred[1][c8 + e] + sred[2][c8 + e] + sred[3][c8 + e];
+      const float inv = 1.0f / sqrtf(tot / (float)D + op.eps);
+#pragma unroll
+      for (int ps = 0; ps < NP; ++ps) k[ps][e] = k[ps][e] * inv * op.k_norm_w[r + 64 * ps];
+    }
+  }
+
+  // K: RoPE at positions start_pos + t.  The kv head 0 workgroup of each tile
+  // publishes the (cos, sin) of its tokens for the flash kernel's Q.
+  if (op.do_rope) {
+    const bool publish = op.rope_tab_out && h == 0;
+    const int half = op.rope_dim / 2;
+    if (op.rope_style == HL_ROPE_HALF_SPLIT) {  // rope_dim == D: pair (r, r + 64)
+      const int i = r;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float angle = (float)(op.start_pos + t + e) * op.theta.t[i];
+        const float c = cosf(angle), sn = sinf(angle);
+        const float v0 = k[0][e], v1 = k[1][e];
+        k[0][e] = v0 * c - v1 * sn;
+        k[1][e] = v0 * sn + v1 * c;
+        if (publish && t + e < T) op.rope_tab_out[(long long)i * T + t + e] = make_float2(c, sn);
+      }
+    } else {  // interleaved: rows 2i and 2i + 1 are lanes 4 apart
+      const bool even = (r & 1) == 0;
+#pragma unroll
+      for (int ps = 0; ps < NP; ++ps) {
+        const int row = r + 64 * ps;
+        const int i = row >> 1;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float other = __shfl_xor(k[ps][e], 4, 64);
+          if (row < op.rope_dim) {
+            const float angle = (float)(op.start_pos + t + e) * op.theta.t[i];
+            const float c = cosf(angle), sn = sinf(angle);
+            const float v0 = even ? k[ps][e] : other, v1 = even ? other : k[ps][e];
+            k[ps][e] = even ? v0 * c - v1 * sn : v0 * sn + v1 * c;
+            if (publish && even && t + e < T) op.rope_tab_out[(long long)i * T + t + e] = make_float2(c, sn);
+          }
+        }
+      }
+    }
+  }
+
+  // K: cache column block, and kt through LDS (token-major fp16).
+#pragma unroll
+  for (int ps = 0; ps < NP; ++ps) {
+    const int row = r + 64 * ps;
+    if (op.k_cache)
+      store_row8<KDT>(op.k_cache, ((long long)h * D + row) * op.max_len + op.start_pos + t, t, T, k[ps]);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) skt[c8 + e][row] = t + e < T ? f32_to_f16_bits(k[ps][e]) : (uint16_t)0;
+  }
+  __syncthreads();
+  constexpr int CH = D / 8;  // 16-byte chunks per token row
+  for (int idx = tid; idx < kPT * CH; idx += 256) {
+    const int tt = idx / CH, ch = idx % CH;
+    const int tg = t0 + tt;
+    if (tg < op.t_pad) *(u16x8*)(op.kt + ((long long)h * op.t_pad + tg) * D + 8 * ch) = *(const u16x8*)&skt[tt][8 * ch];
+  }
+}
+
+// True when kv_prologue_kernel covers the op: K/V only, MFMA layouts, and a
+// RoPE whose pairs it holds in-thread or one shuffle apart.
+static bool kv_prologue_fits(const PrologueOp& op) {
+  if (op.q || op.q_inplace || op.k_inplace || !op.kt || !op.vt) return false;
+  if (op.hv_first != op.n_head) return false;
+  if (op.head_dim != 128) return false;
+  if (op.do_rope && op.rope_style == HL_ROPE_HALF_SPLIT && op.rope_dim != op.head_dim) return false;
+  return true;
+}
+
 hipError_t prologue_launch(const PrologueOp& op, hipStream_t stream) {
   const int cols = op.t_pad > op.seq_len ? op.t_pad : op.seq_len;
+  if (kv_prologue_fits(op)) {
+    dim3 grid((cols + kPT - 1) / kPT, op.n_head_kv);
+#define HL_KVP(IO, KD) hipLaunchKernelGGL((kv_prologue_kernel<IO, KD, 128>), grid, dim3(256), 0, stream, op)
+    const int kd = op.k_cache ? op.kv_dtype : HL_BF16;
+    if (op.io_dtype == HL_F16) {
+      if (kd == HL_F32) HL_KVP(HL_F16, HL_F32); else if (kd == HL_F16) HL_KVP(HL_F16, HL_F16); else HL_KVP(HL_F16, HL_BF16);
+    } else {
+      if (kd == HL_F32) HL_KVP(HL_BF16, HL_F32); else if (kd == HL_F16) HL_KVP(HL_BF16, HL_F16); else HL_KVP(HL_BF16, HL_BF16);
+    }
+#undef HL_KVP
+    return hipGetLastError();
+  }
   const int n_vec = op.n_head + 2 * op.n_head_kv - op.hv_first;
   const int tiles = (cols + kPT - 1) / kPT;
   // Head vectors per workgroup: enough workgroups (~2048) to keep every CU

@@ -163,6 +163,25 @@ def test_prefill_mfma_start_pos(hl, orc, style):
     assert np.all(vch[:, :start] == 7.0) and np.all(vch[:, start + T:] == 7.0)
 
 
+@pytest.mark.parametrize("dt", [1, 2])
+def test_prefill_mfma_no_rope_cache_start_pos(hl, orc, dt):
+    """D=128 without RoPE or qkNorm (K/V prologue only converts and stores),
+    cache written from start_pos, T not a multiple of the tile."""
+    hq, hkv, d, T, start, max_len = 8, 2, 128, 77, 19, 128
+    q, k, v = (orc.upcast(orc.to_storage(orc.normal(h * d * T, 90 + i), dt), dt).reshape(-1, T)
+               for i, h in enumerate((hq, hkv, hkv)))
+    ref = orc.attention_prefill(q, k, v, hq, hkv, d, T)
+    kc = torch.full((hkv * d, max_len), 5.0, dtype=TDT[dt], device="cuda")
+    vc = torch.full((hkv * d, max_len), 5.0, dtype=TDT[dt], device="cuda")
+    out = run_prefill(to_dev(q, dt), to_dev(k, dt), to_dev(v, dt), hq, hkv, d, T, k_cache=kc,
+                      v_cache=vc, max_len=max_len, start_pos=start)
+    assert rel_err(from_dev(out), ref) < TOL_LOWP
+    kch, vch = from_dev(kc), from_dev(vc)
+    assert np.array_equal(kch[:, start:start + T], k) and np.array_equal(vch[:, start:start + T], v)
+    assert np.all(kch[:, :start] == 5.0) and np.all(kch[:, start + T:] == 5.0)
+    assert np.all(vch[:, :start] == 5.0) and np.all(vch[:, start + T:] == 5.0)
+
+
 def test_prefill_c4_full_size_sampled(hl, orc):
     """Config 4 at full size (T=4096, Hq32/Hkv8, D128, bf16, RoPE 5e5, cache
     write); the oracle checks 4 heads x 48 sampled rows incl. first/last."""
