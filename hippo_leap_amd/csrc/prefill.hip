@@ -316,18 +316,21 @@ __global__ __launch_bounds__(512) void prefill_mfma_kernel(MfmaPrefillParams p) 
       }
     }
     if (do_qk) {
-      f16x8 kf[2][2];
+      // Two k-steps of K fragments in flight ahead of the MFMAs.
+      f16x8 kf[3][2];
 #pragma unroll
-      for (int mb = 0; mb < 2; ++mb) kf[0][mb] = *(const f16x8*)(kst + koff[mb] + 8 * (hh ^ kswz[mb]));
+      for (int k = 0; k < 2; ++k)
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb) kf[k][mb] = *(const f16x8*)(kst + koff[mb] + 8 * ((2 * k + hh) ^ kswz[mb]));
 #pragma unroll
       for (int k = 0; k < KSTEPS; ++k) {
-        if (k + 1 < KSTEPS) {
+        if (k + 2 < KSTEPS) {
 #pragma unroll
           for (int mb = 0; mb < 2; ++mb)
-            kf[(k + 1) & 1][mb] = *(const f16x8*)(kst + koff[mb] + 8 * ((2 * (k + 1) + hh) ^ kswz[mb]));
+            kf[(k + 2) % 3][mb] = *(const f16x8*)(kst + koff[mb] + 8 * ((2 * (k + 2) + hh) ^ kswz[mb]));
         }
 #pragma unroll
-        for (int mb = 0; mb < 2; ++mb) s[mb] = mma32(kf[k & 1][mb], qf[k], k == 0 ? negm : s[mb]);
+        for (int mb = 0; mb < 2; ++mb) s[mb] = mma32(kf[k % 3][mb], qf[k], k == 0 ? negm : s[mb]);
         __builtin_amdgcn_sched_barrier(0);
       }
     }

@@ -97,6 +97,8 @@ CASES = [
     (2, 40, 2, 64, 512, [31, 32], 32, 1, False, 0),        # G=20: two head chunks, partial interleaved rope
     (1, 16, 16, 128, 4096, [4095], 64, 0, True, 0),        # G=1, long, partial half-split rope
     (2, 8, 2, 64, 256, [63, 64], 0, 0, True, 3),           # new column on a tile edge
+    (3, 16, 4, 64, 257, [5, 200, 256], 0, 0, True, 0),     # odd max_len: element-wise loads
+    (2, 24, 3, 128, 131, [130, 64], 0, 1, False, 2),       # odd max_len, D128, interleaved
 ]
 
 
