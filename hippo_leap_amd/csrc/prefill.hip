@@ -58,6 +58,7 @@ __device__ __forceinline__ f32x16 mma32(f16x8 a, f16x8 b, f32x16 c) {
 }
 
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2v __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) void lds_void_t;
 typedef __attribute__((address_space(1))) const void global_cvoid_t;
 
@@ -108,11 +109,35 @@ __device__ __forceinline__ void build_q(const MfmaPrefillParams& p, int hq, int 
   const bool tv = t < p.T;
   const int tc = tv ? t : p.T - 1;
   const uint16_t* qcol = p.q_in + (long long)hq * D * p.T + tc;
+  // All loads (q, then the lane's 32 cos/sin pairs) are issued before any
+  // of them is used: one memory round trip.  Interleaved pairs beyond
+  // rope_dim read a clamped (valid) table entry and are not applied.
+  uint16_t xb[KSTEPS][8];
+#pragma unroll
+  for (int k = 0; k < KSTEPS; ++k)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) xb[k][e] = qcol[(long long)(16 * k + 8 * hh + e) * p.T];
+  const bool half_split = p.rope_style == HL_ROPE_HALF_SPLIT;  // then rope_dim == D
+  float2 cs[KSTEPS / 2][8];
+  if (p.do_rope) {
+    const float2* tab = p.rope_tab + tc;
+    const int last_pair = p.rope_dim / 2 - 1;
+#pragma unroll
+    for (int k = 0; k < KSTEPS / 2; ++k)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        // half-split: pair 16k+8hh+e (k < KSTEPS/2); interleaved: pair
+        // (16kk+8hh+ee)/2 for kk = 2k + e/4 (the lane's even dims, in order)
+        const int kk = 2 * k + (e >> 2), ee = 2 * (e & 3);
+        const int i = half_split ? 16 * k + 8 * hh + e : min((16 * kk + 8 * hh + ee) / 2, last_pair);
+        cs[k][e] = tab[(long long)i * p.T];
+      }
+  }
   float x[KSTEPS][8];
 #pragma unroll
   for (int k = 0; k < KSTEPS; ++k)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) x[k][e] = from_bits<QDT>(qcol[(long long)(16 * k + 8 * hh + e) * p.T]);
+    for (int e = 0; e < 8; ++e) x[k][e] = from_bits<QDT>(xb[k][e]);
   if (p.q_norm_w) {
     float ss = 0.f;
 #pragma unroll
@@ -127,16 +152,15 @@ __device__ __forceinline__ void build_q(const MfmaPrefillParams& p, int hq, int 
       for (int e = 0; e < 8; ++e) x[k][e] = x[k][e] * inv * p.q_norm_w[16 * k + 8 * hh + e];
   }
   if (p.do_rope) {
-    const float2* tab = p.rope_tab + tc;
-    if (p.rope_style == HL_ROPE_HALF_SPLIT) {  // rope_dim == D
+    if (half_split) {
 #pragma unroll
       for (int k = 0; k < KSTEPS / 2; ++k)
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          const float2 cs = tab[(long long)(16 * k + 8 * hh + e) * p.T];
+          const float2 c = cs[k][e];
           const float v0 = x[k][e], v1 = x[k + KSTEPS / 2][e];
-          x[k][e] = v0 * cs.x - v1 * cs.y;
-          x[k + KSTEPS / 2][e] = v0 * cs.y + v1 * cs.x;
+          x[k][e] = v0 * c.x - v1 * c.y;
+          x[k + KSTEPS / 2][e] = v0 * c.y + v1 * c.x;
         }
     } else {
 #pragma unroll
@@ -145,10 +169,10 @@ __device__ __forceinline__ void build_q(const MfmaPrefillParams& p, int hq, int 
         for (int e = 0; e < 8; e += 2) {
           const int d = 16 * k + 8 * hh + e;
           if (d < p.rope_dim) {
-            const float2 cs = tab[(long long)(d / 2) * p.T];
+            const float2 c = cs[k >> 1][4 * (k & 1) + e / 2];
             const float v0 = x[k][e], v1 = x[k][e + 1];
-            x[k][e] = v0 * cs.x - v1 * cs.y;
-            x[k][e + 1] = v0 * cs.y + v1 * cs.x;
+            x[k][e] = v0 * c.x - v1 * c.y;
+            x[k][e + 1] = v0 * c.y + v1 * c.x;
           }
         }
     }
@@ -271,7 +295,6 @@ __global__ __launch_bounds__(512) void prefill_mfma_kernel(MfmaPrefillParams p) 
   f32x16 negm;
 #pragma unroll
   for (int i = 0; i < 16; ++i) negm[i] = 0.f;
-  const f16x2 ones = {(_Float16)1.0f, (_Float16)1.0f};
   const int t_abs = r0 + ln;
 
   // Per-lane LDS offsets (elements) of the fragments this lane reads.
@@ -378,21 +401,25 @@ __global__ __launch_bounds__(512) void prefill_mfma_kernel(MfmaPrefillParams p) 
 #pragma unroll
       for (int i = 0; i < 16; ++i) negm[i] = -m_run;
     }
-    float ps = 0.f;
+    // Row sum of the tile in fp32 from the unrounded exponentials, four
+    // independent chains; P itself is rounded to fp16 once (RNE, packed)
+    // for the P.V MFMA.  (fp16 dot products against (1, 1) would sum the
+    // rounded values in fewer instructions, but their results wait on the
+    // matrix pipeline while the other group's MFMAs run.)
+    float ps[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-      for (int u = 0; u < 2; ++u) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) pf[2 * mb + u][e] = (_Float16)fast_exp2(s[mb][8 * u + e]);
-        // row sum from the same fp16 values the MFMA consumes
+      for (int u = 0; u < 2; ++u)
 #pragma unroll
         for (int e = 0; e < 8; e += 2) {
-          const f16x2 pr = {pf[2 * mb + u][e], pf[2 * mb + u][e + 1]};
-          ps = __builtin_amdgcn_fdot2(pr, ones, ps, false);
+          const f32x2v ev = {fast_exp2(s[mb][8 * u + e]), fast_exp2(s[mb][8 * u + e + 1])};
+          const f16x2 pr = __builtin_convertvector(ev, f16x2);
+          pf[2 * mb + u][e] = pr[0];
+          pf[2 * mb + u][e + 1] = pr[1];
+          ps[(e / 2) & 3] += ev.x + ev.y;
         }
-      }
-    l_run += ps;
+    l_run += (ps[0] + ps[1]) + (ps[2] + ps[3]);
   };
   // Phase 2m: the stages of K(m-1) and V(m-2) are no longer read, so they
   // take K(m+1) and V(m); both are first read at phase 2m+2.  After each odd
@@ -409,7 +436,9 @@ __global__ __launch_bounds__(512) void prefill_mfma_kernel(MfmaPrefillParams p) 
   if (grp == 0) {
     for (int m = 0; m <= n_tiles; ++m) {
       copies(m);
+      __builtin_amdgcn_s_setprio(1);  // MFMAs issue ahead of the other group's VALU work
       matrix_step(m);
+      __builtin_amdgcn_s_setprio(0);
       __syncthreads();
       vector_step(m);
       __builtin_amdgcn_s_waitcnt(0x0F70);
@@ -420,7 +449,9 @@ __global__ __launch_bounds__(512) void prefill_mfma_kernel(MfmaPrefillParams p) 
       copies(m);
       vector_step(m - 1);
       __syncthreads();
+      __builtin_amdgcn_s_setprio(1);  // MFMAs issue ahead of the other group's VALU work
       matrix_step(m);
+      __builtin_amdgcn_s_setprio(0);
       __builtin_amdgcn_s_waitcnt(0x0F70);
       __syncthreads();
     }
