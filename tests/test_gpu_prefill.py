@@ -102,7 +102,7 @@ def test_prefill_fp32_lengths(hl, orc, T):
 
 
 @pytest.mark.parametrize("dt", [1, 2])
-@pytest.mark.parametrize("T", [1, 17, 32, 64, 65, 100, 257])
+@pytest.mark.parametrize("T", [1, 17, 32, 64, 65, 100, 136, 257])
 @pytest.mark.parametrize("hq,hkv,d", [(8, 2, 128), (4, 4, 64), (16, 2, 64), (6, 3, 128)])
 def test_prefill_mfma_shapes(hl, orc, dt, T, hq, hkv, d):
     qs = orc.to_storage(orc.normal(hq * d * T, 40 + T), dt)
@@ -117,11 +117,13 @@ def test_prefill_mfma_shapes(hl, orc, dt, T, hq, hkv, d):
 
 @pytest.mark.parametrize("dt", [1, 2])
 @pytest.mark.parametrize("style,rd", [(1, 64), (0, 128), (0, 64)])
-def test_prefill_mfma_qknorm_rope_cache(hl, orc, dt, style, rd):
+@pytest.mark.parametrize("T", [150, 152])
+def test_prefill_mfma_qknorm_rope_cache(hl, orc, dt, style, rd, T):
     """qkNorm + RoPE + cache write.  Interleaved (any rope_dim) and full-width
     half-split RoPE are applied to Q inside the MFMA kernel; half-split over
-    part of the head goes through the prepared-Q layout."""
-    hq, hkv, d, T, max_len = 16, 4, 128, 150, 160
+    part of the head goes through the prepared-Q layout.  T = 152 (a multiple
+    of 8) fetches q through the LDS staging copies, T = 150 element-wise."""
+    hq, hkv, d, max_len = 16, 4, 128, 160
     q, k, v = (orc.upcast(orc.to_storage(orc.normal(h * d * T, 50 + i), dt), dt).reshape(-1, T)
                for i, h in enumerate((hq, hkv, hkv)))
     wq, wk = orc.uniform(d, 53, 0.5, 1.5), orc.uniform(d, 54, 0.5, 1.5)
