@@ -4,11 +4,11 @@ Headline workload ("decode attn GB/s at 2K ctx"):
   Llama-3.2-1B-shape batched decode step, fp16 KV cache: B=8 sequences with
   2048 cached positions each, one new token per sequence (L = 2049),
   Hq=32 / Hkv=8, D=64, RoPE theta 5e5, K/V ~ N(0, 0.5) (sigma 0.5).
-  One step = hl_rope_store_decode (RoPE of the new q/k, K/V write at column
-  2048) + hl_attn_decode (split-K attention + merge); the W warmup and K timed
-  steps each run as one captured HIP graph.  16 cache sets are
+  One step = hl_decode_step: RoPE of the new q/k, the K/V write at column
+  2048 and split-K attention with its merge, in one launch; the W warmup and
+  K timed steps each run as one captured HIP graph.  16 cache sets are
   rotated (16 x 33.6 MB > the 256 MB Infinity Cache) so every step streams
-  its K/V from HBM.
+  its K/V from HBM.  The caches use the reference's column-major layout.
   value = algorithmic K+V bytes of one step / step time (GB/s).
 
 Extra objects on the same JSON line:
@@ -17,8 +17,11 @@ Extra objects on the same JSON line:
     4*Hq*D*T(T+1)/2 (prologue + flash kernel).
   decode_c5: configs[4], Qwen3-30B-A3B-shape decode, bf16 KV, B=16, L=32769,
     Hq32/Hkv4, D128, qkNorm + RoPE 1e6.
-  roofline: the decode attention call (split-K kernel + merge) timed with HIP
-    events on the stream it runs on.
+  decode_c5_tiled, decode_c3_tiled: the same steps with the caches in the
+    opt-in tiled layout (HL_KV_TILED32: per kv head, 32-column tiles of
+    [D][32]), same values.
+  roofline: the fused step kernel (qkNorm/RoPE + KV write + split-K
+    attention + merge) timed with HIP events on the stream it runs on.
   cpu_baseline: the C oracle (single-threaded scalar fp32 restatement of the
     reference's tensor.nim math) timed on this host on a bounded sample.
 """
@@ -101,7 +104,8 @@ def graph_time_ms(torch, fn, n_inner=64, replays=8):
 # Decode (c3 headline, c5 extra)
 # ---------------------------------------------------------------------------
 class DecodeWorkload:
-    def __init__(self, torch, A, B, hq, hkv, d, prev, kv_dtype, sigma, base, n_sets, qknorm, seed):
+    def __init__(self, torch, A, B, hq, hkv, d, prev, kv_dtype, sigma, base, n_sets, qknorm, seed,
+                 kv_layout=0):
         self.t, self.A = torch, A
         self.B, self.hq, self.hkv, self.d, self.prev = B, hq, hkv, d, prev
         self.L = prev + 1
@@ -112,6 +116,10 @@ class DecodeWorkload:
                    for _ in range(n_sets)]
         self.vc = [(torch.randn(n, generator=g, device="cuda") * sigma).to(kv_dtype)
                    for _ in range(n_sets)]
+        if kv_layout:  # same values, stored as 32-column tiles
+            self.kc = [A.kv_to_tiled(c, hkv, d, self.max_len) for c in self.kc]
+            self.vc = [A.kv_to_tiled(c, hkv, d, self.max_len) for c in self.vc]
+        self.kv_layout = kv_layout
         self.q = torch.randn(B * hq * d, generator=g, device="cuda") * sigma
         self.k = torch.randn(B * hkv * d, generator=g, device="cuda") * sigma
         self.v = torch.randn(B * hkv * d, generator=g, device="cuda") * sigma
@@ -121,11 +129,13 @@ class DecodeWorkload:
             self.wk = torch.rand(d, generator=g, device="cuda") + 0.5
         self.base = base
         self.out = torch.empty(B * hq * d, device="cuda")
-        self.args = [A.decode_args(self.q, kc, vc, self.out, hq, hkv, d, self.max_len, self.L)
+        self.args = [A.decode_args(self.q, kc, vc, self.out, hq, hkv, d, self.max_len, self.L,
+                                   kv_layout=kv_layout)
                      for kc, vc in zip(self.kc, self.vc)]
         self.ws = A.decode_workspace(self.args[0])
         self.rs = [A.rope_store_args(self.q, self.k, self.v, kc, vc, hq, hkv, d, self.max_len, prev,
-                                     base, q_norm_w=self.wq, k_norm_w=self.wk, eps=1e-6)
+                                     base, q_norm_w=self.wq, k_norm_w=self.wk, eps=1e-6,
+                                     kv_layout=kv_layout)
                    for kc, vc in zip(self.kc, self.vc)]
         self.step_ws = A.decode_step_workspace(self.rs[0], self.args[0])
         self.kv_bytes = 2 * B * hkv * d * self.L * self.kc[0].element_size()  # columns < L
@@ -135,7 +145,7 @@ class DecodeWorkload:
         s = i % len(self.kc)
         self.A.rope_store_decode(self.q, self.k, self.v, self.kc[s], self.vc[s], self.hq, self.hkv,
                                  self.d, self.max_len, self.prev, self.base, q_norm_w=self.wq,
-                                 k_norm_w=self.wk, eps=1e-6)
+                                 k_norm_w=self.wk, eps=1e-6, kv_layout=self.kv_layout)
 
     def attend(self, i):
         self.A.attn_decode(self.args[i % len(self.args)], self.ws)
@@ -229,6 +239,23 @@ def cpu_baseline(budget_s=12.0):
     }
 
 
+def decode_extra(wl, t, workload):
+    """Extra decode object: host-clock step rate, step-kernel roofline."""
+    ach = wl.kv_bytes / (t["kernel"] * 1e-3) / 1e9
+    return {
+        "workload": workload,
+        "kv_layout": "tiled32" if wl.kv_layout else "colmajor (reference)",
+        "value": round(wl.kv_bytes / (t["step"] * 1e-3) / 1e9, 2), "unit": "GB/s",
+        "ms_per_step": round(t["step"], 5),
+        "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),
+                     "algorithmic_bytes": wl.kv_bytes, "avg_us": round(t["kernel"] * 1e3, 3)},
+        "attention_only_us": round(t["attn"] * 1e3, 3),
+        "attention_only_frac": round(wl.kv_bytes / (t["attn"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "two_call_step_us": round(t["two_calls"] * 1e3, 3),
+    }
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -307,6 +334,15 @@ def main():
             f"{t['rope_store']*1e3:.2f} us, two calls {t['two_calls']*1e3:.2f} us")
         del wl
         torch.cuda.empty_cache()
+        log("decode_c3_tiled ...")
+        wl = DecodeWorkload(torch, A, B=8, hq=32, hkv=8, d=64, prev=2048,
+                            kv_dtype=torch.float16, sigma=0.5, base=5e5, n_sets=16,
+                            qknorm=False, seed=3, kv_layout=1)
+        t = bench_decode(torch, A, wl, args.steps, args.warmup)
+        result["decode_c3_tiled"] = decode_extra(wl, t, "c3 step, caches in the tiled layout")
+        log(f"decode_c3_tiled: step {t['step']*1e3:.2f} us, step kernel {t['kernel']*1e3:.2f} us")
+        del wl
+        torch.cuda.empty_cache()
 
     if args.only in ("all", "prefill"):
         log("prefill c4 ...")
@@ -331,28 +367,19 @@ def main():
         torch.cuda.empty_cache()
 
     if args.only in ("all", "c5"):
-        log("decode c5 ...")
-        wl = DecodeWorkload(torch, A, B=16, hq=32, hkv=4, d=128, prev=32768,
-                            kv_dtype=torch.bfloat16, sigma=1.0, base=1e6, n_sets=1,
-                            qknorm=True, seed=5)
-        t = bench_decode(torch, A, wl, max(10, args.steps // 4), 3)
-        step_ms = t["step"]
-        ach = wl.kv_bytes / (t["kernel"] * 1e-3) / 1e9
-        result["decode_c5"] = {
-            "workload": "c5: Qwen3-30B-A3B-shape decode, bf16 KV, B=16, L=32769, Hq32/Hkv4, "
-                        "D128, qkNorm + RoPE 1e6",
-            "value": round(wl.kv_bytes / (step_ms * 1e-3) / 1e9, 2), "unit": "GB/s",
-            "ms_per_step": round(step_ms, 5),
-            "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS,
-                         "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),
-                         "algorithmic_bytes": wl.kv_bytes, "avg_us": round(t["kernel"] * 1e3, 3)},
-            "attention_only_us": round(t["attn"] * 1e3, 3),
-            "two_call_step_us": round(t["two_calls"] * 1e3, 3),
-        }
-        log(f"decode c5: step {step_ms*1e3:.1f} us, step kernel {t['kernel']*1e3:.1f} us "
-            f"({ach:.0f} GB/s), attention alone {t['attn']*1e3:.1f} us")
-        del wl
-        torch.cuda.empty_cache()
+        for layout, key in ((0, "decode_c5"), (1, "decode_c5_tiled")):
+            log(f"{key} ...")
+            wl = DecodeWorkload(torch, A, B=16, hq=32, hkv=4, d=128, prev=32768,
+                                kv_dtype=torch.bfloat16, sigma=1.0, base=1e6, n_sets=1,
+                                qknorm=True, seed=5, kv_layout=layout)
+            t = bench_decode(torch, A, wl, max(10, args.steps // 4), 3)
+            result[key] = decode_extra(wl, t, "c5: Qwen3-30B-A3B-shape decode, bf16 KV, B=16, "
+                                       "L=32769, Hq32/Hkv4, D128, qkNorm + RoPE 1e6")
+            log(f"{key}: step {t['step']*1e3:.1f} us, step kernel {t['kernel']*1e3:.1f} us "
+                f"({result[key]['roofline']['achieved']:.0f} GB/s), attention alone "
+                f"{t['attn']*1e3:.1f} us")
+            del wl
+            torch.cuda.empty_cache()
 
     if not args.no_cpu:
         log("cpu baseline ...")

@@ -25,8 +25,8 @@ import ctypes
 import torch
 
 from . import _lib
-from ._lib import (HL_BF16, HL_F16, HL_F32, HL_ROPE_HALF_SPLIT, DecodeArgs, PrefillArgs,
-                   RopeStoreArgs, check)
+from ._lib import (HL_BF16, HL_F16, HL_F32, HL_KV_COLMAJOR, HL_KV_TILED32, HL_ROPE_HALF_SPLIT,
+                   DecodeArgs, PrefillArgs, RopeStoreArgs, check)
 
 _DT = {torch.float32: HL_F32, torch.float16: HL_F16, torch.bfloat16: HL_BF16}
 
@@ -138,7 +138,8 @@ def device_info() -> dict:
 # Batched / typed API
 # ---------------------------------------------------------------------------
 def decode_args(q, k_cache, v_cache, out, n_head, n_head_kv, head_dim, max_len, seq_len,
-                seq_lens=None, cache_batch_stride=0, scale=0.0, num_splits=0) -> DecodeArgs:
+                seq_lens=None, cache_batch_stride=0, scale=0.0, num_splits=0,
+                kv_layout=HL_KV_COLMAJOR) -> DecodeArgs:
     a = DecodeArgs()
     a.batch = q.numel() // (n_head * head_dim)
     a.n_head, a.n_head_kv, a.head_dim = n_head, n_head_kv, head_dim
@@ -148,8 +149,24 @@ def decode_args(q, k_cache, v_cache, out, n_head, n_head_kv, head_dim, max_len, 
     a.cache_batch_stride = cache_batch_stride
     a.q, a.k_cache, a.v_cache, a.out = q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), out.data_ptr()
     a.scale, a.num_splits = scale, num_splits
+    a.kv_layout = kv_layout
     a._tensors = (q, k_cache, v_cache, out, seq_lens)  # the struct holds raw pointers into these
     return a
+
+
+def kv_to_tiled(cache, n_head_kv, head_dim, max_len):
+    """Column-major cache [..., Hkv*D, max_len] -> the HL_KV_TILED32 layout
+    (per kv head, max_len/32 tiles of [D][32]); same numel, new tensor."""
+    lead = cache.numel() // (n_head_kv * head_dim * max_len)
+    t = cache.reshape(lead, n_head_kv, head_dim, max_len // 32, 32)
+    return t.permute(0, 1, 3, 2, 4).contiguous().reshape(cache.shape)
+
+
+def kv_from_tiled(cache, n_head_kv, head_dim, max_len):
+    """Inverse of kv_to_tiled."""
+    lead = cache.numel() // (n_head_kv * head_dim * max_len)
+    t = cache.reshape(lead, n_head_kv, max_len // 32, head_dim, 32)
+    return t.permute(0, 1, 3, 2, 4).contiguous().reshape(cache.shape)
 
 
 def decode_workspace_bytes(args: DecodeArgs) -> int:
@@ -176,7 +193,7 @@ def attn_decode(args: DecodeArgs, workspace=None, stream=None) -> None:
 def rope_store_args(q, k, v, k_cache, v_cache, n_head_q, n_head_kv, head_dim, max_len, pos,
                     rope_base, rope_dim=0, rope_style=HL_ROPE_HALF_SPLIT, positions=None,
                     q_norm_w=None, k_norm_w=None, eps=1e-6, cache_batch_stride=0,
-                    use_installed_theta=False) -> RopeStoreArgs:
+                    use_installed_theta=False, kv_layout=HL_KV_COLMAJOR) -> RopeStoreArgs:
     a = RopeStoreArgs()
     a.batch = q.numel() // (n_head_q * head_dim)
     a.n_head_q, a.n_head_kv, a.head_dim = n_head_q, n_head_kv, head_dim
@@ -190,6 +207,7 @@ def rope_store_args(q, k, v, k_cache, v_cache, n_head_q, n_head_kv, head_dim, ma
     a.q_norm_w = q_norm_w.data_ptr() if q_norm_w is not None else None
     a.k_norm_w = k_norm_w.data_ptr() if k_norm_w is not None else None
     a.eps = eps
+    a.kv_layout = kv_layout
     a._tensors = (q, k, v, k_cache, v_cache, positions, q_norm_w, k_norm_w)
     return a
 
@@ -222,7 +240,8 @@ def decode_step(rs: RopeStoreArgs, at: DecodeArgs, workspace=None, stream=None) 
 def prefill_args(q, k, v, out, n_head, n_head_kv, head_dim, seq_len, rope_base=0.0,
                  apply_rope=False, rope_dim=0, rope_style=HL_ROPE_HALF_SPLIT, q_norm_w=None,
                  k_norm_w=None, eps=1e-6, k_cache=None, v_cache=None, max_len=0, start_pos=0,
-                 scale=0.0, write_back_qk=False, use_installed_theta=False) -> PrefillArgs:
+                 scale=0.0, write_back_qk=False, use_installed_theta=False,
+                 kv_layout=HL_KV_COLMAJOR) -> PrefillArgs:
     """Arguments of hl_attn_prefill; the output dtype is taken from `out`."""
     a = PrefillArgs()
     a.n_head, a.n_head_kv, a.head_dim, a.seq_len = n_head, n_head_kv, head_dim, seq_len
@@ -239,6 +258,7 @@ def prefill_args(q, k, v, out, n_head, n_head_kv, head_dim, seq_len, rope_base=0
     a.max_len, a.start_pos, a.scale = max_len, start_pos, scale
     a.write_back_qk = int(write_back_qk)
     a.out_dtype = dtype_code(out)
+    a.kv_layout = kv_layout
     a._tensors = (q, k, v, out, q_norm_w, k_norm_w, k_cache, v_cache)
     return a
 

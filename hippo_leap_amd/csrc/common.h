@@ -66,6 +66,14 @@ __device__ __forceinline__ float from_bits(uint16_t b) {
   else return bf16_bits_to_f32(b);
 }
 
+// Offset of element (row d, column t) inside one kv head's cache block
+// (the block starts at h * D * max_len in either layout): column-major rows
+// of max_len, or max_len/32 tiles of [D][32].
+__host__ __device__ __forceinline__ int64_t kv_off(int layout, int d, int t, int D, int max_len) {
+  return layout == HL_KV_TILED32 ? ((int64_t)(t >> 5) * D + d) * 32 + (t & 31)
+                                 : (int64_t)d * max_len + t;
+}
+
 // ---------------------------------------------------------------------------
 // Wave64 reductions (xor butterflies over ds_swizzle / DPP via __shfl_xor).
 // ---------------------------------------------------------------------------

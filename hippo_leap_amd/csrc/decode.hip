@@ -48,6 +48,7 @@ struct DecodeParams {
   long long batch_stride;
   int n_head, n_head_kv, head_dim, group, head_chunk, n_chunks;
   int max_len, seq_len, split_len, num_splits;
+  int kv_layout;  // HL_KV_COLMAJOR | HL_KV_TILED32 (VEC kernels only)
   float scale_log2;
   // Fused decode step (STEP kernels only): q above is the raw new-token
   // activation; k_act / v_act are the new token's k and v.  The kernel applies
@@ -444,16 +445,34 @@ __global__ __launch_bounds__(256, PIPE ? (D == 64 ? 2 : 1) : 4) void decode_mfma
   // The scheduling barriers keep each tile's loads together and in program
   // order, so a compute waits only for its own tile, never for loads issued
   // after it.
+  // Tiled caches (VEC only): tile t0 / 32 of the head is [D][32] at
+  // (t0 / 32) * D * 32, rows 32 elements apart; the address form is selected
+  // without a branch so that both layouts issue the same loads.
+  const bool tiled = VEC && p.kv_layout == HL_KV_TILED32;
+  const int rstride = tiled ? 32 : p.max_len;
   auto load_tile = [&](int t0, u16x8* kr, u16x8* vr) {
     __builtin_amdgcn_sched_barrier(0);
+    if constexpr (VEC) {
+      const long long tb = tiled ? (long long)(t0 >> 5) * (D * 32) : 0;
+      const int ck = tiled ? 8 * (lane & 3) : min(t0 + 8 * (lane & 3), p.max_len - 8);
+      const int cv = tiled ? 8 * g : min(t0 + 8 * g, p.max_len - 8);
 #pragma unroll
-    for (int r = 0; r < KR; ++r) {
-      const int row = (lane >> 2) + 16 * r;
-      kr[r] = load_row8<VEC>(K + (long long)row * p.max_len, t0 + 8 * (lane & 3), s1, p.max_len);
+      for (int r = 0; r < KR; ++r) {
+        const int row = (lane >> 2) + 16 * r;
+        kr[r] = *(const u16x8*)(K + tb + (long long)row * rstride + ck);
+      }
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) vr[nb] = *(const u16x8*)(V + tb + (long long)(16 * nb + c) * rstride + cv);
+    } else {
+#pragma unroll
+      for (int r = 0; r < KR; ++r) {
+        const int row = (lane >> 2) + 16 * r;
+        kr[r] = load_row8<false>(K + (long long)row * p.max_len, t0 + 8 * (lane & 3), s1, p.max_len);
+      }
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+        vr[nb] = load_row8<false>(V + (long long)(16 * nb + c) * p.max_len, t0 + 8 * g, s1, p.max_len);
     }
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb)
-      vr[nb] = load_row8<VEC>(V + (long long)(16 * nb + c) * p.max_len, t0 + 8 * g, s1, p.max_len);
     __builtin_amdgcn_sched_barrier(0);
   };
 
@@ -739,7 +758,7 @@ __global__ __launch_bounds__(256, PIPE ? (D == 64 ? 2 : 1) : 4) void decode_mfma
       if (has_new && chunk == 0) {
         for (int i = tid; i < 2 * D; i += 256) {
           uint16_t* cache = (uint16_t*)(i < D ? p.k : p.v);
-          cache[base + (long long)(i < D ? i : i - D) * p.max_len + newc] = snew[i];
+          cache[base + kv_off(p.kv_layout, i < D ? i : i - D, newc, D, p.max_len)] = snew[i];
         }
       }
     });
@@ -920,6 +939,7 @@ hipError_t decode_launch(const hl_decode_args* a, const DecodePlan* plan, void* 
   p.head_chunk = plan->head_chunk;
   p.n_chunks = plan->n_chunks;
   p.max_len = a->max_len;
+  p.kv_layout = a->kv_layout;
   p.seq_len = a->seq_len;
   p.split_len = plan->split_len;
   p.num_splits = plan->num_splits;

@@ -49,6 +49,7 @@ struct HeadVecOp {
   const int* positions;
   int pos;
   int batch, n_head_q, n_head_kv, head_dim, rope_dim, rope_style, do_rope, kv_dtype, max_len;
+  int kv_layout;       // HL_KV_COLMAJOR | HL_KV_TILED32
   long long batch_stride;
   const float* q_norm_w;
   const float* k_norm_w;
@@ -78,6 +79,7 @@ struct PrologueOp {
   void* k_cache;
   void* v_cache;
   int kv_dtype, max_len, start_pos;
+  int kv_layout;      // of the caches: HL_KV_COLMAJOR | HL_KV_TILED32
   int n_head, n_head_kv, head_dim, seq_len;
   int do_rope, rope_dim, rope_style;
   const float* q_norm_w;

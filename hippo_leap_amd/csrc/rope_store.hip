@@ -79,8 +79,8 @@ __global__ __launch_bounds__(64) void headvec_kernel(HeadVecOp op) {
   if (x && (nw || (rope && op.do_rope)))
     for (int d = lane; d < D; d += 64) x[d] = sx[d];
   if (cache) {
-    const long long base = (long long)b * op.batch_stride + (long long)hv * D * op.max_len + pos;
-    for (int d = lane; d < D; d += 64) store_elem<KDT>(cache, base + (long long)d * op.max_len, sx[d]);
+    const long long base = (long long)b * op.batch_stride + (long long)hv * D * op.max_len;
+    for (int d = lane; d < D; d += 64) store_elem<KDT>(cache, base + kv_off(op.kv_layout, d, pos, D, op.max_len), sx[d]);
   }
 }
 
@@ -150,6 +150,22 @@ __device__ __forceinline__ void store_row8(void* base, long long off, int t, int
 #pragma unroll
     for (int e = 0; e < 8; ++e)
       if (t + e < lim) store_elem<DT>(base, off + e, x[e]);
+  }
+}
+
+// Cache columns pos .. pos+7 of row d of one kv head's block (hbase), the
+// values of tokens t .. t+7 (t + e < lim stored): 16-byte store when the 8
+// columns are contiguous and aligned in the layout (a tiled cache's 8 columns
+// are when they stay inside one 32-column tile), else element by element.
+template <int DT>
+__device__ __forceinline__ void store_cache8(void* cache, long long hbase, int layout, int d, int pos, int D,
+                                             int max_len, int t, int lim, const float* x) {
+  if (layout == HL_KV_TILED32 && (pos & 31) > 24) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      if (t + e < lim) store_elem<DT>(cache, hbase + kv_off(layout, d, pos + e, D, max_len), x[e]);
+  } else {
+    store_row8<DT>(cache, hbase + kv_off(layout, d, pos, D, max_len), t, lim, x);
   }
 }
 
@@ -295,8 +311,8 @@ __global__ __launch_bounds__(256) void prologue_kernel(PrologueOp op) {
         for (int e = 0; e < 8; ++e) x[e] = sx[r][c8 + e];
         if (inplace) store_row8<HL_F32>(inplace, hbase + (long long)r * T + t0 + c8, t0 + c8, T, x);
         if (cache)
-          store_row8<KDT>(cache, ((long long)h * D + r) * op.max_len + op.start_pos + t0 + c8,
-                          t0 + c8, T, x);
+          store_cache8<KDT>(cache, (long long)h * D * op.max_len, op.kv_layout, r, op.start_pos + t0 + c8, D,
+                            op.max_len, t0 + c8, T, x);
       }
     }
 
@@ -367,7 +383,8 @@ __global__ __launch_bounds__(256) void kv_prologue_kernel(PrologueOp op) {
   for (int ps = 0; ps < NP; ++ps) {
     const int row = r + 64 * ps;
     if (op.v_cache)
-      store_row8<KDT>(op.v_cache, ((long long)h * D + row) * op.max_len + op.start_pos + t, t, T, v[ps]);
+      store_cache8<KDT>(op.v_cache, (long long)h * D * op.max_len, op.kv_layout, row, op.start_pos + t, D,
+                        op.max_len, t, T, v[ps]);
     if (t < op.t_pad) {
       float x[8];
 #pragma unroll
@@ -445,7 +462,8 @@ __global__ __launch_bounds__(256) void kv_prologue_kernel(PrologueOp op) {
   for (int ps = 0; ps < NP; ++ps) {
     const int row = r + 64 * ps;
     if (op.k_cache)
-      store_row8<KDT>(op.k_cache, ((long long)h * D + row) * op.max_len + op.start_pos + t, t, T, k[ps]);
+      store_cache8<KDT>(op.k_cache, (long long)h * D * op.max_len, op.kv_layout, row, op.start_pos + t, D,
+                        op.max_len, t, T, k[ps]);
 #pragma unroll
     for (int e = 0; e < 8; ++e) skt[c8 + e][row] = t + e < T ? f32_to_f16_bits(k[ps][e]) : (uint16_t)0;
   }

@@ -170,6 +170,21 @@ int hl_gpu_attention_prefill(float* dst, const float* q, const float* k,
 /* Batched / typed API (extends the reference: B sequences, fp16/bf16 KV)   */
 /* ------------------------------------------------------------------------ */
 
+/* KV-cache layouts (the kv_layout fields below; 0 when a caller leaves the
+ * field zero).  HL_KV_COLMAJOR is the reference's cache: per sequence,
+ * [Hkv*D, max_len] column-major, element (row h*D + d, column t) at
+ * (h*D + d)*max_len + t (naive.nim:3565-3567, 3239).  HL_KV_TILED32 keeps
+ * each kv head's block the same size and at the same place, h*D*max_len,
+ * but stores it as max_len/32 tiles of [D][32]: element (d, t) of head h at
+ * h*D*max_len + ((t/32)*D + d)*32 + t%32, so 32 columns of a head are one
+ * contiguous run (8 KB at D = 128 in fp16/bf16) instead of D runs of 64
+ * bytes max_len apart.  Tiled caches: fp16/bf16 only, max_len % 32 == 0,
+ * 16-byte aligned, batch stride a multiple of 8 elements.  No counterpart
+ * in the reference (docs/future.md:38-43 lists cache layouts as future
+ * work); a layout for callers that own their cache format.                */
+#define HL_KV_COLMAJOR 0
+#define HL_KV_TILED32 1
+
 typedef struct hl_decode_args {
   int batch;                    /* B >= 1                                        */
   int n_head;                   /* Hq                                            */
@@ -187,6 +202,7 @@ typedef struct hl_decode_args {
   float* out;                   /* device [B][Hq*D] fp32                         */
   float scale;                  /* 0 -> 1/sqrtf(D) (naive.nim:3374)              */
   int num_splits;               /* 0 -> chosen to fill the GPU                   */
+  int kv_layout;                /* HL_KV_COLMAJOR (0) | HL_KV_TILED32            */
 } hl_decode_args;
 
 /* Workspace bytes hl_attn_decode needs for these args: one 4-byte arrival
@@ -233,6 +249,7 @@ typedef struct hl_rope_store_args {
   const float* q_norm_w;        /* optional device [D]: qkNorm before RoPE       */
   const float* k_norm_w;        /* optional device [D]                           */
   float eps;
+  int kv_layout;                /* HL_KV_COLMAJOR (0) | HL_KV_TILED32            */
 } hl_rope_store_args;
 
 /* One launch for the new token of B sequences: optional qkNorm of q and k
@@ -290,6 +307,8 @@ typedef struct hl_prefill_args {
   int out_dtype;                /* dtype of `out`: HL_F32 (default, the
                                    reference's fp32 act1) or, for fp16/bf16
                                    io, HL_F16 / HL_BF16 (RNE of the fp32 value) */
+  int kv_layout;                /* of k_cache/v_cache: HL_KV_COLMAJOR (0) |
+                                   HL_KV_TILED32                                */
 } hl_prefill_args;
 
 size_t hl_attn_prefill_workspace_bytes(const hl_prefill_args* a);

@@ -29,7 +29,7 @@ def test_exports_match_header(hl):
 
 
 def test_abi_version(hl):
-    assert hl.hl_abi_version() == 1
+    assert hl.hl_abi_version() == 2
 
 
 def _err(hl):
@@ -162,3 +162,59 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setattr(_lib, "LIB_PATH", str(tmp_path / "libhl_attn.so"))
     with pytest.raises(RuntimeError, match="no CPU fallback"):
         _lib.load()
+
+
+def test_kv_layout_validation(hl):
+    """Tiled caches: fp16/bf16, max_len % 32 == 0, aligned; unknown layouts
+    are rejected (decode, rope/store and prefill alike)."""
+    T = _lib.HL_KV_TILED32
+    a = _decode_args(kv_layout=T)  # max_len 2049
+    assert hl.hl_attn_decode(ctypes.byref(a), None, 0, None) == _lib.HL_EINVAL
+    assert "max_len % 32" in _err(hl)
+    a = _decode_args(kv_layout=T, max_len=2080, kv_dtype=_lib.HL_F32)
+    assert hl.hl_attn_decode(ctypes.byref(a), None, 0, None) == _lib.HL_EUNSUPPORTED
+    a = _decode_args(kv_layout=T, max_len=2080, k_cache=FAKE + 8)
+    assert hl.hl_attn_decode(ctypes.byref(a), None, 0, None) == _lib.HL_EINVAL
+    assert "aligned" in _err(hl)
+    a = _decode_args(kv_layout=7)
+    assert hl.hl_attn_decode(ctypes.byref(a), None, 0, None) == _lib.HL_EINVAL
+    assert "kv_layout" in _err(hl)
+    a = _decode_args(kv_layout=T, max_len=2080)
+    assert hl.hl_attn_decode_workspace_bytes(ctypes.byref(a)) > 0  # valid: plans normally
+
+    r = _lib.RopeStoreArgs()
+    r.batch, r.n_head_q, r.n_head_kv, r.head_dim = 1, 32, 4, 128
+    r.rope_base, r.kv_dtype, r.max_len, r.pos = 1e6, _lib.HL_BF16, 100, 10
+    r.q = r.k = r.v = r.k_cache = r.v_cache = FAKE
+    r.kv_layout = T
+    assert hl.hl_rope_store_decode(ctypes.byref(r), None) == _lib.HL_EINVAL
+    assert "max_len % 32" in _err(hl)
+
+    p = _prefill_args(k_cache=FAKE, v_cache=FAKE, kv_dtype=_lib.HL_F32, max_len=4096,
+                      kv_layout=T)
+    assert hl.hl_attn_prefill(ctypes.byref(p), None, 0, None) == _lib.HL_EUNSUPPORTED
+    p = _prefill_args(kv_layout=3)
+    assert hl.hl_attn_prefill(ctypes.byref(p), None, 0, None) == _lib.HL_EINVAL
+
+
+def test_struct_sizes_match_header(tmp_path):
+    """ctypes mirrors of the argument structs have the C compiler's size and
+    kv_layout offset (the field the ABI version 2 added)."""
+    import shutil
+    import subprocess
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if cc is None:
+        pytest.skip("no C compiler")
+    src = tmp_path / "sz.c"
+    src.write_text('#include <stddef.h>\n#include <stdio.h>\n#include "hl_attn.h"\n'
+                   'int main(void) { printf("%zu %zu %zu %zu %zu %zu\\n",'
+                   ' sizeof(hl_decode_args), offsetof(hl_decode_args, kv_layout),'
+                   ' sizeof(hl_rope_store_args), offsetof(hl_rope_store_args, kv_layout),'
+                   ' sizeof(hl_prefill_args), offsetof(hl_prefill_args, kv_layout)); return 0; }\n')
+    exe = tmp_path / "sz"
+    subprocess.check_call([cc, "-I", os.path.dirname(HEADER), str(src), "-o", str(exe)])
+    got = [int(x) for x in subprocess.check_output([str(exe)], text=True).split()]
+    want = []
+    for cls in (_lib.DecodeArgs, _lib.RopeStoreArgs, _lib.PrefillArgs):
+        want += [ctypes.sizeof(cls), cls.kv_layout.offset]
+    assert got == want
