@@ -40,6 +40,7 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16/fp16 MFMA
+FP32_PEAK_TFLOPS = 157.3       # MI355X fp32 (vector / matrix)
 METRIC = "decode attn GB/s (%HBM peak) at 2K ctx; prefill attn TFLOP/s (%MFMA peak)"
 
 
@@ -262,7 +263,7 @@ def main():
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--only", choices=["all", "decode", "prefill", "c5"], default="all")
+    ap.add_argument("--only", choices=["all", "decode", "prefill", "c5", "fp32"], default="all")
     ap.add_argument("--calib", action="store_true",
                     help="also run a 256 MiB -> 256 MiB elementwise copy (3x): the known-size "
                          "kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes")
@@ -342,6 +343,53 @@ def main():
         result["decode_c3_tiled"] = decode_extra(wl, t, "c3 step, caches in the tiled layout")
         log(f"decode_c3_tiled: step {t['step']*1e3:.2f} us, step kernel {t['kernel']*1e3:.2f} us")
         del wl
+        torch.cuda.empty_cache()
+
+    if args.only in ("all", "fp32"):
+        # The reference-contract fp32 path (configs[0] decode, configs[1] prefill):
+        # the entry points a Nim caller of gpuAttentionDecode / gpuAttentionPrefill hits.
+        log("decode c1 / prefill c2 (fp32) ...")
+        g = torch.Generator(device="cuda").manual_seed(11)
+        n1 = 4 * 64 * 512
+        sets = [(torch.rand(n1, generator=g, device="cuda") * 2 - 1,
+                 torch.rand(n1, generator=g, device="cuda") * 2 - 1) for _ in range(256)]
+        q1 = torch.rand(32 * 64, generator=g, device="cuda") * 2 - 1
+        o1 = torch.empty_like(q1)
+        lib = A._lib.load()
+        st = lambda: torch.cuda.current_stream().cuda_stream
+        c1 = lambda i: A.check(lib.hl_gpu_attention_decode(
+            o1.data_ptr(), q1.data_ptr(), sets[i % 256][0].data_ptr(), sets[i % 256][1].data_ptr(),
+            32, 4, 64, 512, 512, st()))
+        ms1 = graph_time_ms(torch, c1, 256, 4)
+        b1 = 2 * n1 * 4
+        result["decode_c1"] = {
+            "workload": "c1: TinyLlama-shape decode, fp32 KV, B=1, Hq32/Hkv4, D64, L=512 "
+                        "(hl_gpu_attention_decode, the reference's call contract; 256 rotating "
+                        "cache sets = 268 MB)",
+            "us": round(ms1 * 1e3, 3), "unit": "GB/s", "value": round(b1 / (ms1 * 1e-3) / 1e9, 1),
+            "frac_hbm": round(b1 / (ms1 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "note": "1 MB per call: launch- and latency-bound"}
+        T2 = 512
+        q2 = torch.randn(32 * 64, T2, generator=g, device="cuda")
+        k2 = torch.randn(4 * 64, T2, generator=g, device="cuda")
+        v2 = torch.randn(4 * 64, T2, generator=g, device="cuda")
+        kc2 = torch.empty(4 * 64, T2, device="cuda")
+        vc2 = torch.empty(4 * 64, T2, device="cuda")
+        o2 = torch.empty(32 * 64, T2, device="cuda")
+        a2 = A.prefill_args(q2, k2, v2, o2, 32, 4, 64, T2, rope_base=1e4, apply_rope=True,
+                            k_cache=kc2, v_cache=vc2, max_len=T2)
+        ws2 = A.workspace(A.prefill_workspace_bytes(a2))
+        ms2 = graph_time_ms(torch, lambda i: A.attn_prefill(a2, ws2), 32, 4)
+        f2 = 4 * 32 * 64 * T2 * (T2 + 1) // 2
+        result["prefill_c2"] = {
+            "workload": "c2: TinyLlama-shape causal prefill, fp32, T=512, Hq32/Hkv4, D64, RoPE 1e4, "
+                        "KV cache written (fp32 vector-ALU path)",
+            "us": round(ms2 * 1e3, 3), "unit": "TFLOP/s",
+            "value": round(f2 / (ms2 * 1e-3) / 1e12, 3),
+            "frac_fp32_peak": round(f2 / (ms2 * 1e-3) / 1e12 / FP32_PEAK_TFLOPS, 4)}
+        log(f"decode c1: {ms1*1e3:.2f} us; prefill c2: {ms2*1e3:.1f} us "
+            f"({f2 / (ms2 * 1e-3) / 1e12:.2f} TFLOP/s)")
+        del sets
         torch.cuda.empty_cache()
 
     if args.only in ("all", "prefill"):

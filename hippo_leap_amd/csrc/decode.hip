@@ -201,7 +201,7 @@ __device__ void finish_workgroup(const DecodeParams& p, const float* sm_m, const
 // lane j scores column t0+j for every head of the chunk, then lanes switch to
 // owning output dims for the P.V product.
 // ---------------------------------------------------------------------------
-template <int D>
+template <int D, bool V4>
 __global__ __launch_bounds__(256) void decode_f32_kernel(DecodeParams p) {
   constexpr int HC = 16;  // max heads per chunk
   constexpr int DPL = (D + 63) / 64;  // output dims per lane
@@ -209,7 +209,7 @@ __global__ __launch_bounds__(256) void decode_f32_kernel(DecodeParams p) {
   constexpr int FUSE_FLOATS = 16 * kMaxFusedSplits + 16;
   constexpr int SM_FLOATS = MERGE_FLOATS > FUSE_FLOATS ? MERGE_FLOATS : FUSE_FLOATS;
   __shared__ __attribute__((aligned(16))) float sq[HC * D];
-  __shared__ float sp[4][HC][64];
+  __shared__ __attribute__((aligned(16))) float sp[4][HC][64];
   __shared__ __attribute__((aligned(16))) float sm[SM_FLOATS];
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -223,16 +223,46 @@ __global__ __launch_bounds__(256) void decode_f32_kernel(DecodeParams p) {
   const int s0 = split * p.split_len;
   const int s1 = split == p.num_splits - 1 ? L : min(L, s0 + p.split_len);  // last split takes the rest
 
+  const long long base = (long long)b * p.batch_stride + (long long)kvh * D * p.max_len;
+  const float* K = (const float*)p.k + base;
+  const float* V = (const float*)p.v + base;
+
+  // A wave owns 64 consecutive columns per tile: lane j scores column t0+j
+  // for every head, then lanes switch to owning output dims d = lane + 64i
+  // for the P.V product.  Every global load of a tile (the first K column
+  // batch, coalesced across lanes, and the lane's V rows) is issued before
+  // any is used: one memory round trip per tile, not one per element.  The
+  // first tile's loads go out before q is staged, so they overlap it.
+  float kv[64], vv[DPL][64];
+  auto load_tile = [&](int t0) {
+    const int colc = min(t0 + lane, s1 - 1);  // in bounds; scores of lanes past s1 are dropped
+#pragma unroll
+    for (int u = 0; u < 64; ++u) kv[u] = K[(long long)u * p.max_len + colc];
+#pragma unroll
+    for (int i = 0; i < DPL; ++i) {
+      const float* vrow = V + (long long)(lane + 64 * i) * p.max_len;
+      if constexpr (V4) {
+#pragma unroll
+        for (int c4 = 0; c4 < 16; ++c4) {
+          const f32x4 x = *(const f32x4*)(vrow + min(t0 + 4 * c4, p.max_len - 4));
+#pragma unroll
+          for (int e = 0; e < 4; ++e) vv[i][4 * c4 + e] = x[e];
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 64; ++j) vv[i][j] = vrow[min(t0 + j, s1 - 1)];
+      }
+    }
+  };
+  int t0 = s0 + wave * 64;
+  if (t0 < s1) load_tile(t0);
+
   const float* qb = p.q + ((long long)b * p.n_head + hq0) * D;
   for (int i = tid; i < HC * D; i += 256) {
     const int h = i / D;
     sq[i] = h < hc ? qb[i] : 0.f;
   }
   __syncthreads();
-
-  const long long base = (long long)b * p.batch_stride + (long long)kvh * D * p.max_len;
-  const float* K = (const float*)p.k + base;
-  const float* V = (const float*)p.v + base;
 
   float m_run[HC], l_run[HC], acc[HC][DPL];
 #pragma unroll
@@ -243,33 +273,38 @@ __global__ __launch_bounds__(256) void decode_f32_kernel(DecodeParams p) {
     for (int i = 0; i < DPL; ++i) acc[h][i] = 0.f;
   }
 
-  for (int t0 = s0 + wave * 64; t0 < s1; t0 += 256) {
+  for (bool first = true; t0 < s1; t0 += 256, first = false) {
+    if (!first) load_tile(t0);
     const int col = t0 + lane;
     const bool valid = col < s1;
+    const int colc = valid ? col : s1 - 1;
     float s[HC];
 #pragma unroll
     for (int h = 0; h < HC; ++h) s[h] = 0.f;
-    if (valid) {
-      for (int d = 0; d < D; d += 4) {
-        float kv[4];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) kv[u] = K[(long long)(d + u) * p.max_len + col];
+    for (int db = 0; db < D / 64; ++db) {
+      if (db > 0) {
 #pragma unroll
-        for (int h = 0; h < HC; ++h) {
-          const f32x4 qv = *(const f32x4*)&sq[h * D + d];
+        for (int u = 0; u < 64; ++u) kv[u] = K[(long long)(64 * db + u) * p.max_len + colc];
+      }
 #pragma unroll
-          for (int u = 0; u < 4; ++u) s[h] = fmaf(qv[u], kv[u], s[h]);
+      for (int h = 0; h < HC; ++h) {
+        if (h < hc) {  // uniform
+#pragma unroll
+          for (int u = 0; u < 64; u += 4) {
+            const f32x4 qv = *(const f32x4*)&sq[h * D + 64 * db + u];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) s[h] = fmaf(qv[e], kv[u + e], s[h]);
+          }
         }
       }
     }
     // score = dot * scale (naive.nim:3328), here in log2 units
-#pragma unroll
-    for (int h = 0; h < HC; ++h) s[h] *= p.scale_log2;
     float alpha[HC];
 #pragma unroll
     for (int h = 0; h < HC; ++h) {
       if (h < hc) {
-        const float sv = valid ? s[h] : -INFINITY;
+        const float sv = valid ? s[h] * p.scale_log2 : -INFINITY;
         const float mt = wave_max(sv);
         const float mn = fmaxf(m_run[h], mt);
         alpha[h] = fast_exp2(m_run[h] - mn);
@@ -286,18 +321,21 @@ __global__ __launch_bounds__(256) void decode_f32_kernel(DecodeParams p) {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     const int nj = min(64, s1 - t0);
 #pragma unroll
-    for (int h = 0; h < HC; ++h)
+    for (int i = 0; i < DPL; ++i)
 #pragma unroll
-      for (int i = 0; i < DPL; ++i) acc[h][i] *= alpha[h];
+      for (int j = 0; j < 64; ++j) vv[i][j] = j < nj ? vv[i][j] : 0.f;
 #pragma unroll
-    for (int i = 0; i < DPL; ++i) {
-      const int d = lane + 64 * i;
-      if (d < D) {
-        const float* vrow = V + (long long)d * p.max_len + t0;
-        for (int j = 0; j < nj; ++j) {
-          const float vv = vrow[j];
+    for (int h = 0; h < HC; ++h) {
+      if (h < hc) {
 #pragma unroll
-          for (int h = 0; h < HC; ++h) acc[h][i] = fmaf(sp[wave][h][j], vv, acc[h][i]);
+        for (int i = 0; i < DPL; ++i) acc[h][i] *= alpha[h];
+#pragma unroll
+        for (int j = 0; j < 64; j += 4) {
+          const f32x4 pw = *(const f32x4*)&sp[wave][h][j];
+#pragma unroll
+          for (int i = 0; i < DPL; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[h][i] = fmaf(pw[e], vv[i][j + e], acc[h][i]);
         }
       }
     }
@@ -807,7 +845,10 @@ KernelFn pick_mfma(bool vec, bool pipe, bool step) {
 }
 
 KernelFn pick_kernel(int kv_dtype, int D, bool vec, bool pipe, bool step) {
-  if (kv_dtype == HL_F32) return D == 64 ? decode_f32_kernel<64> : decode_f32_kernel<128>;
+  if (kv_dtype == HL_F32) {
+    if (vec) return D == 64 ? decode_f32_kernel<64, true> : decode_f32_kernel<128, true>;
+    return D == 64 ? decode_f32_kernel<64, false> : decode_f32_kernel<128, false>;
+  }
   if (kv_dtype == HL_F16)
     return D == 64 ? pick_mfma<64, HL_F16>(vec, pipe, step) : pick_mfma<128, HL_F16>(vec, pipe, step);
   return D == 64 ? pick_mfma<64, HL_BF16>(vec, pipe, step) : pick_mfma<128, HL_BF16>(vec, pipe, step);
@@ -854,7 +895,9 @@ int cu_count() {
 bool vec_path(const hl_decode_args* a) {
   const long long stride = a->cache_batch_stride ? a->cache_batch_stride
                                                  : (long long)a->n_head_kv * a->head_dim * a->max_len;
-  return a->kv_dtype != HL_F32 && (a->max_len % 8 == 0) && (stride % 8 == 0) &&
+  // 16-byte loads of cache rows: 8 elements (fp16/bf16) or 4 (fp32)
+  const int per16 = a->kv_dtype == HL_F32 ? 4 : 8;
+  return (a->max_len % per16 == 0) && (stride % per16 == 0) &&
          ((uintptr_t)a->k_cache & 15) == 0 && ((uintptr_t)a->v_cache & 15) == 0;
 }
 
