@@ -262,7 +262,7 @@ __global__ __launch_bounds__(512) void prefill_mfma_kernel(MfmaPrefillParams p) 
       const int blk = wave * VI + r;            // 1 KB block of the V stage
       const int d = blk * (64 / VCPR) + lane / VCPR;
       const int slot = lane % VCPR;
-      const int c = slot ^ (d % VCPR);
+      const int c = slot ^ ((d >> 1) % VCPR);
       copy16_to_lds(vbase + (long long)d * p.Tp + j * BN + 8 * c, st + blk * 512);
     }
   };
@@ -304,7 +304,10 @@ __global__ __launch_bounds__(512) void prefill_mfma_kernel(MfmaPrefillParams p) 
 #pragma unroll
   for (int db = 0; db < DB; ++db) voff[db] = (32 * db + ln) * BN;
   const int kswz[2] = {(32 * 0 + sigma_row(ln)) % KCPR, (32 * 1 + sigma_row(ln)) % KCPR};
-  const int vswz = ln % VCPR;  // (32*db + ln) % 8 == ln % 8
+  // V rows are 128 bytes (32 banks) apart, so a fragment read's bank group
+  // is (row parity, chunk): swizzling the chunk by (row >> 1) makes the 16
+  // lanes served together (rows ln .. ln+15) hit 16 distinct groups.
+  const int vswz = (ln >> 1) % VCPR;  // ((32*db + ln) >> 1) % 8 == (ln >> 1) % 8
 
   f32x16 s[2];   // S^T of the tile between its QK^T and its softmax
   f16x8 pf[4];   // P^T of the tile between its softmax and its P.V:

@@ -357,6 +357,12 @@ __global__ __launch_bounds__(256) void prologue_kernel(PrologueOp op) {
 // x * (1/sqrtf(ss/D + eps)) * w[d], (v0c - v1s, v0s + v1c), angle =
 // float(start_pos + t) * theta[i].
 // ---------------------------------------------------------------------------
+// Column swizzle of the kt transposition tile: token rows t and t + 16 of
+// the 272-byte-pitch tile start in the same bank, so the second half of the
+// tokens stores its head dims XOR 16 (a whole 16-byte chunk pair, so the
+// token-major readout still reads contiguous 16-byte chunks).
+__device__ __forceinline__ int kt_swz(int tok) { return (tok & 16); }
+
 template <int IODT, int KDT, int D>
 __global__ __launch_bounds__(256) void kv_prologue_kernel(PrologueOp op) {
   static_assert(D == 128, "two rows per thread: r and r + 64");
@@ -465,14 +471,14 @@ __global__ __launch_bounds__(256) void kv_prologue_kernel(PrologueOp op) {
       store_cache8<KDT>(op.k_cache, (long long)h * D * op.max_len, op.kv_layout, row, op.start_pos + t, D,
                         op.max_len, t, T, k[ps]);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) skt[c8 + e][row] = t + e < T ? f32_to_f16_bits(k[ps][e]) : (uint16_t)0;
+    for (int e = 0; e < 8; ++e) skt[c8 + e][row ^ kt_swz(c8 + e)] = t + e < T ? f32_to_f16_bits(k[ps][e]) : (uint16_t)0;
   }
   __syncthreads();
   constexpr int CH = D / 8;  // 16-byte chunks per token row
   for (int idx = tid; idx < kPT * CH; idx += 256) {
     const int tt = idx / CH, ch = idx % CH;
     const int tg = t0 + tt;
-    if (tg < op.t_pad) *(u16x8*)(op.kt + ((long long)h * op.t_pad + tg) * D + 8 * ch) = *(const u16x8*)&skt[tt][8 * ch];
+    if (tg < op.t_pad) *(u16x8*)(op.kt + ((long long)h * op.t_pad + tg) * D + 8 * ch) = *(const u16x8*)&skt[tt][(8 * ch) ^ kt_swz(tt)];
   }
 }
 
