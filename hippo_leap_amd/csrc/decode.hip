@@ -444,7 +444,10 @@ __global__ __launch_bounds__(256, PIPE ? (D == 64 ? 2 : 1) : 4) void decode_mfma
   constexpr int KS = D / 32;      // k-steps of the QK^T product
   constexpr int NB = D / 16;      // 16-dim output blocks
   constexpr int KR = D / 16;      // 16-byte K loads per lane per tile
-  constexpr int PITCH = 40;       // LDS row pitch (elements) of a 32-column K tile
+  // LDS row pitch (elements) of a 32-column K tile: 72 bytes, so that the
+  // gathers of one MFMA operand (rows 8 apart) fall in distinct banks; rows
+  // are 8-byte aligned and written as two 8-byte halves per 16-byte chunk.
+  constexpr int PITCH = 36;
   constexpr int HS = 16;          // head slots of the merge buffers
   constexpr int KT_BYTES = 4 * D * PITCH * 2;                   // 4 wave tiles (uint16)
   constexpr int MERGE_BYTES = 4 * HS * (D + 2) * 4;
@@ -666,7 +669,10 @@ __global__ __launch_bounds__(256, PIPE ? (D == 64 ? 2 : 1) : 4) void decode_mfma
 #pragma unroll
     for (int r = 0; r < KR; ++r) {
       const int row = (lane >> 2) + 16 * r;
-      *(u16x8*)(kt + row * PITCH + 8 * (lane & 3)) = kr[r];
+      typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
+      uint16_t* dst = kt + row * PITCH + 8 * (lane & 3);
+      *(u16x4*)dst = u16x4{kr[r][0], kr[r][1], kr[r][2], kr[r][3]};
+      *(u16x4*)(dst + 4) = u16x4{kr[r][4], kr[r][5], kr[r][6], kr[r][7]};
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
