@@ -530,10 +530,10 @@ hipError_t prefill_mfma_launch(const PrefillLaunch& a, hipStream_t stream) {
 template <int D>
 __global__ __launch_bounds__(256) void prefill_f32_kernel(PrefillLaunch p) {
   constexpr int BM = 32, BNF = 64, DU = D / 64;
+  constexpr int NL = D * BNF / 256;  // K (and V) tile elements per thread
   __shared__ __attribute__((aligned(16))) float sq[D][BM];        // Q tile, [d][row]
-  // K tile as [d][col] (D x (BNF+4)), then V tile as [col][d] (BNF x (D+4))
-  constexpr int KV_FLOATS = D * (BNF + 4) > BNF * (D + 4) ? D * (BNF + 4) : BNF * (D + 4);
-  __shared__ __attribute__((aligned(16))) float skv[KV_FLOATS];
+  __shared__ __attribute__((aligned(16))) float sk[D * (BNF + 4)];  // K tile, [d][col]
+  __shared__ __attribute__((aligned(16))) float sv[BNF * (D + 4)];  // V tile, [col][d]
   __shared__ __attribute__((aligned(16))) float sp[BM][BNF + 4];
 
   const int tid = threadIdx.x;
@@ -547,6 +547,24 @@ __global__ __launch_bounds__(256) void prefill_f32_kernel(PrefillLaunch p) {
   const float* Q = p.q + (long long)h * D * T;
   const float* K = p.k + (long long)kvh * D * T;
   const float* V = p.v + (long long)kvh * D * T;
+  const int last_row = min(T - 1, i0 + BM - 1);
+  const int n_tiles = last_row / BNF + 1;
+
+  // Thread tid moves column lc = tid % 64 of rows d = tid/64 + 4k of each
+  // K / V tile (coalesced).  The next tile's loads are issued before the
+  // current one is computed, so each tile's memory latency hides behind the
+  // previous tile's work; columns >= T read a valid column and become 0.
+  const int lc = tid & (BNF - 1), ld0 = tid / BNF;
+  float kr[NL], vr[NL];
+  auto load_kv = [&](int j0) {
+    const int col = min(j0 + lc, T - 1);
+#pragma unroll
+    for (int k = 0; k < NL; ++k) {
+      kr[k] = K[(long long)(ld0 + 4 * k) * T + col];
+      vr[k] = V[(long long)(ld0 + 4 * k) * T + col];
+    }
+  };
+  load_kv(0);
 
   for (int idx = tid; idx < D * BM; idx += 256) {
     const int d = idx / BM, r = idx % BM;
@@ -559,26 +577,30 @@ __global__ __launch_bounds__(256) void prefill_f32_kernel(PrefillLaunch p) {
 #pragma unroll
     for (int b = 0; b < 4 * DU; ++b) o[a][b] = 0.f;
   float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};
-  const int last_row = min(T - 1, i0 + BM - 1);
-  const int n_tiles = last_row / BNF + 1;
 
   for (int tile = 0; tile < n_tiles; ++tile) {
     const int j0 = tile * BNF;
-    __syncthreads();
-    // K tile as [d][col] (pitch BNF+4)
-    for (int idx = tid; idx < D * BNF; idx += 256) {
-      const int d = idx / BNF, c = idx % BNF;
-      skv[d * (BNF + 4) + c] = (j0 + c < T) ? K[(long long)d * T + j0 + c] : 0.f;
+    __syncthreads();  // the previous tile's sk / sv / sp reads are done
+    {
+      const bool in = j0 + lc < T;
+#pragma unroll
+      for (int k = 0; k < NL; ++k) {
+        const int d = ld0 + 4 * k;
+        sk[d * (BNF + 4) + lc] = in ? kr[k] : 0.f;
+        sv[lc * (D + 4) + d] = in ? vr[k] : 0.f;
+      }
     }
+    if (tile + 1 < n_tiles) load_kv(j0 + BNF);
     __syncthreads();
     float s[2][4];
 #pragma unroll
     for (int a = 0; a < 2; ++a)
 #pragma unroll
       for (int b = 0; b < 4; ++b) s[a][b] = 0.f;
+#pragma unroll 8
     for (int d = 0; d < D; ++d) {
       const float q0 = sq[d][2 * rg], q1 = sq[d][2 * rg + 1];
-      const f32x4 kv = *(const f32x4*)&skv[d * (BNF + 4) + 4 * cg];
+      const f32x4 kv = *(const f32x4*)&sk[d * (BNF + 4) + 4 * cg];
 #pragma unroll
       for (int b = 0; b < 4; ++b) {
         s[0][b] = fmaf(q0, kv[b], s[0][b]);
@@ -618,22 +640,17 @@ __global__ __launch_bounds__(256) void prefill_f32_kernel(PrefillLaunch p) {
       l_run[a] = l_run[a] * alpha[a] + ps;
     }
     __syncthreads();
-    // V tile as [col][d] (pitch D+4)
-    for (int idx = tid; idx < D * BNF; idx += 256) {
-      const int d = idx / BNF, c = idx % BNF;
-      skv[c * (D + 4) + d] = (j0 + c < T) ? V[(long long)d * T + j0 + c] : 0.f;
-    }
-    __syncthreads();
 #pragma unroll
     for (int a = 0; a < 2; ++a)
 #pragma unroll
       for (int b = 0; b < 4 * DU; ++b) o[a][b] *= alpha[a];
     const int ncols = min(BNF, T - j0);
+#pragma unroll 4
     for (int c = 0; c < ncols; ++c) {
       const float p0 = sp[2 * rg][c], p1 = sp[2 * rg + 1][c];
 #pragma unroll
       for (int u = 0; u < DU; ++u) {
-        const f32x4 vv = *(const f32x4*)&skv[c * (D + 4) + 4 * cg + 64 * u];
+        const f32x4 vv = *(const f32x4*)&sv[c * (D + 4) + 4 * cg + 64 * u];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           o[0][4 * u + e] = fmaf(p0, vv[e], o[0][4 * u + e]);
