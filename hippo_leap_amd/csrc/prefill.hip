@@ -81,18 +81,6 @@ __device__ __forceinline__ int sigma_row(int m) {
   return 16 * (a >> 1) + 8 * h + 4 * (a & 1) + e;
 }
 
-// Each wave owns 32 query rows of one head.  Per 64-key tile:
-//   S^T[j][t] = K[j][:] . Q^T[:][t]     (v_mfma_f32_32x32x16_f16, K from LDS,
-//                                        Q^T in registers)
-//   online softmax over j for each row t (row t = lane % 32: in-lane plus one
-//                                        xor-32 exchange)
-//   O^T[d][t] += V^T[d][j] . P^T[j][t]  (V from LDS, P^T straight from the
-//                                        S^T registers as fp16)
-// The O^T formulation keeps each row's rescale factor a per-lane scalar.
-// K/V tiles go global -> LDS with direct (VGPR-free) copies into two stages;
-// tile i+2 is requested right after the one barrier that ends tile i.
-// LDS rows are stored with their 16-byte chunks XOR-swizzled by the row so
-// that the fragment reads (32 rows, one chunk each) hit distinct banks.
 // Q^T operand of one wave built from the raw activations: lane (ln, hh) holds
 // q[t = r0 + ln][16k + 8hh + e] after optional qkNorm (RMSNorm over the head
 // dimension: the lane's 64 values plus the other half via one xor-32
@@ -184,11 +172,11 @@ __device__ __forceinline__ void build_q(const MfmaPrefillParams& p, int hq, int 
 }
 
 // Ping-pong flash kernel.  A workgroup has 8 waves, two per SIMD (waves w
-// and w + 4 share SIMD w % 4).  A SIMD overlaps matrix-core work with vector
-// ALU work only across waves, so the waves run in two groups one phase apart
+// and w + 4 share SIMD w % 4).  The waves run in two groups one phase apart
 // (barrier between phases): while group 0 issues MFMAs (the previous tile's
 // P.V and this tile's S^T = K Q^T), group 1 runs a softmax on the vector
-// ALUs, and the next phase swaps the roles.
+// ALUs, and the next phase swaps the roles, so each SIMD keeps its matrix
+// core and its vector ALU busy with the two waves' independent work.
 //
 // Wave w owns 32 query rows of one head: head w % nh of the workgroup's nh
 // heads (one GQA group shares the K/V tiles), row block w / nh.  Per wave:
@@ -203,8 +191,8 @@ __device__ __forceinline__ void build_q(const MfmaPrefillParams& p, int hq, int 
 // The O^T formulation keeps each row's rescale factor a per-lane scalar.
 // K and V tiles go global -> LDS with direct (VGPR-free) copies into two K
 // and two V stages, requested two phases before their first use.  LDS rows
-// are stored with their 16-byte chunks XOR-swizzled by the row so that the
-// fragment reads (32 rows, one chunk each) hit distinct banks.
+// are stored with their 16-byte chunks XOR-swizzled (K by the row, V by the
+// row / 2) so that each fragment read's 16-lane groups hit distinct banks.
 template <int D, int ODT, int QIN>
 __global__ __launch_bounds__(512) void prefill_mfma_kernel(MfmaPrefillParams p) {
   constexpr int KSTEPS = D / 16;    // QK^T k-steps
