@@ -33,6 +33,7 @@ constexpr int QR = 32;          // query rows per wave
 constexpr float kRescale = 8.0f;
 }  // namespace
 
+
 int prefill_mfma_tpad(int seq_len) { return (seq_len + BN - 1) / BN * BN; }
 
 struct MfmaPrefillParams {
@@ -189,8 +190,8 @@ __device__ __forceinline__ void build_q(const MfmaPrefillParams& p, int hq, int 
 //   O^T[d][t] += V^T[d][j] . P^T[j][t]  (V from LDS, P^T straight from the
 //                                        S^T registers as fp16)
 // The O^T formulation keeps each row's rescale factor a per-lane scalar.
-// K and V tiles go global -> LDS with direct (VGPR-free) copies into two K
-// and two V stages, requested two phases before their first use.  LDS rows
+// K and V tiles go global -> LDS with direct (VGPR-free) copies into three
+// K and three V stages, requested three phases before their matrix steps.  LDS rows
 // are stored with their 16-byte chunks XOR-swizzled (K by the row, V by the
 // row / 2) so that each fragment read's 16-lane groups hit distinct banks.
 template <int D, int ODT, int QIN>
@@ -203,7 +204,13 @@ __global__ __launch_bounds__(512) void prefill_mfma_kernel(MfmaPrefillParams p) 
   constexpr int VT = D * BN;        // V stage elements
   constexpr int KI = KT / 8 / 64 / 8;  // direct copies per wave per tile (K)
   constexpr int VI = VT / 8 / 64 / 8;  // (V)
-  __shared__ __attribute__((aligned(1024))) uint16_t lds[2 * KT + 2 * VT];
+  // Three K and three V stages, each tile copied one phase before the
+  // softmax step that precedes its first matrix step: that softmax step
+  // reads the first K fragments of the next matrix step, which then starts
+  // with operands in registers instead of waiting on LDS.  (Prefetching the
+  // first V fragments as well needs 16 more VGPRs than the kernel has.)
+  constexpr int NS = 3;
+  __shared__ __attribute__((aligned(1024))) uint16_t lds[NS * KT + NS * VT];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar branches
@@ -229,11 +236,11 @@ __global__ __launch_bounds__(512) void prefill_mfma_kernel(MfmaPrefillParams p) 
   const uint16_t* kbase = p.kt + (long long)kvh * p.Tp * D;
   const uint16_t* vbase = p.vt + (long long)kvh * D * p.Tp;
   uint16_t* const kst0 = lds;
-  uint16_t* const vst0 = lds + 2 * KT;
+  uint16_t* const vst0 = lds + NS * KT;
 
   // Tile j -> its stage: every wave copies KI (K) or VI (V) 1 KB blocks.
   auto request_k = [&](int j) {
-    uint16_t* st = kst0 + (j & 1) * KT;
+    uint16_t* st = kst0 + (j % NS) * KT;
 #pragma unroll
     for (int r = 0; r < KI; ++r) {
       const int blk = wave * KI + r;            // 1 KB block of the K stage
@@ -244,7 +251,7 @@ __global__ __launch_bounds__(512) void prefill_mfma_kernel(MfmaPrefillParams p) 
     }
   };
   auto request_v = [&](int j) {
-    uint16_t* st = vst0 + (j & 1) * VT;
+    uint16_t* st = vst0 + (j % NS) * VT;
 #pragma unroll
     for (int r = 0; r < VI; ++r) {
       const int blk = wave * VI + r;            // 1 KB block of the V stage
@@ -304,6 +311,7 @@ __global__ __launch_bounds__(512) void prefill_mfma_kernel(MfmaPrefillParams p) 
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): K tiles 0, 1 and V tile 0 landed for this wave
   __syncthreads();
 
+  f16x8 kpre[2][2];  // first K fragments of the next matrix step
   // Matrix step m: P.V of tile m - 1, then S^T of tile m.
   auto matrix_step = [&](const int j) {
     // Fragments
@@ -311,8 +319,9 @@ __global__ __launch_bounds__(512) void prefill_mfma_kernel(MfmaPrefillParams p) 
     // so only two steps' fragments are live (the other wave of the SIMD
     // covers the LDS latency with its softmax).
     const bool do_pv = j >= 1 && j - 1 < wave_tiles, do_qk = j < wave_tiles;
-    const uint16_t* vst = vst0 + ((j - 1) & 1) * VT;
-    const uint16_t* kst = kst0 + (j & 1) * KT;
+    const uint16_t* vst = vst0 + ((j + NS - 1) % NS) * VT;
+    const uint16_t* kst = kst0 + (j % NS) * KT;
+    const bool pre_k = j >= 1;  // first K fragments prefetched by vector_step(j - 1)
     if (do_pv) {
       f16x8 va[2][DB];
 #pragma unroll
@@ -335,7 +344,8 @@ __global__ __launch_bounds__(512) void prefill_mfma_kernel(MfmaPrefillParams p) 
 #pragma unroll
       for (int k = 0; k < 2; ++k)
 #pragma unroll
-        for (int mb = 0; mb < 2; ++mb) kf[k][mb] = *(const f16x8*)(kst + koff[mb] + 8 * ((2 * k + hh) ^ kswz[mb]));
+        for (int mb = 0; mb < 2; ++mb)
+          kf[k][mb] = pre_k ? kpre[k][mb] : *(const f16x8*)(kst + koff[mb] + 8 * ((2 * k + hh) ^ kswz[mb]));
 #pragma unroll
       for (int k = 0; k < KSTEPS; ++k) {
         if (k + 2 < KSTEPS) {
@@ -411,15 +421,24 @@ __global__ __launch_bounds__(512) void prefill_mfma_kernel(MfmaPrefillParams p) 
           ps[(e / 2) & 3] += ev.x + ev.y;
         }
     l_run += (ps[0] + ps[1]) + (ps[2] + ps[3]);
-  };
-  // Phase 2m: the stages of K(m-1) and V(m-2) are no longer read, so they
-  // take K(m+1) and V(m); both are first read at phase 2m+2.  After each odd
-  // phase every wave's copies have landed; the barrier publishes them.
-  auto copies = [&](const int m) {
-    if (m >= 1) {
-      if (m + 1 < n_tiles) request_k(m + 1);
-      if (m < n_tiles) request_v(m);
+    // First K fragments of matrix step j + 1 (K(j+1), k-steps 0 and 1; the
+    // tile is visible since the previous barrier).
+    if (j + 1 < wave_tiles) {
+      const uint16_t* kst = kst0 + ((j + 1) % NS) * KT;
+#pragma unroll
+      for (int k = 0; k < 2; ++k)
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb) kpre[k][mb] = *(const f16x8*)(kst + koff[mb] + 8 * ((2 * k + hh) ^ kswz[mb]));
     }
+  };
+  // Phase 2m takes K(m+2) into the stage of K(m-1) and V(m+1) into that of
+  // V(m-2), whose last reads were in phase 2m-1.  After each odd phase every
+  // wave's copies have landed and the barrier publishes them: K(m+2) and
+  // V(m+1) are visible from phase 2m+2, a phase before the matrix steps
+  // that use them, when the preceding softmax step prefetches from K.
+  auto copies = [&](const int m) {
+    if (m + 2 < n_tiles) request_k(m + 2);
+    if (m + 1 < n_tiles) request_v(m + 1);
   };
   // Group 0 runs matrix step m in phase 2m and vector step m in phase 2m+1;
   // group 1 runs vector step m-1 in phase 2m and matrix step m in 2m+1.
