@@ -218,3 +218,19 @@ def test_struct_sizes_match_header(tmp_path):
     for cls in (_lib.DecodeArgs, _lib.RopeStoreArgs, _lib.PrefillArgs):
         want += [ctypes.sizeof(cls), cls.kv_layout.offset]
     assert got == want
+
+
+def test_kv_layout_helpers_match_header_formula():
+    """kv_to_tiled / kv_from_tiled (host side of HL_KV_TILED32) place element
+    (sequence b, kv head h, row d, column t) at
+    b*Hkv*D*M + h*D*M + ((t/32)*D + d)*32 + t%32, as the header states."""
+    import torch
+    from hippo_leap_amd import attention as A
+    B, H, D, M = 2, 3, 8, 96
+    x = torch.arange(B * H * D * M, dtype=torch.int32).reshape(B, H * D, M)
+    t = A.kv_to_tiled(x, H, D, M).reshape(-1)
+    rng = np.random.default_rng(5)
+    for _ in range(200):
+        b, h, d, c = (int(rng.integers(n)) for n in (B, H, D, M))
+        assert t[b * H * D * M + h * D * M + ((c // 32) * D + d) * 32 + c % 32] == x[b, h * D + d, c]
+    assert torch.equal(A.kv_from_tiled(A.kv_to_tiled(x, H, D, M), H, D, M), x)
