@@ -264,6 +264,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", choices=["all", "decode", "prefill", "c5", "fp32"], default="all")
+    ap.add_argument("--layouts", choices=["both", "colmajor", "tiled"], default="both",
+                    help="KV-cache layouts of the decode runs (the headline c3 line is column-major; "
+                         "one layout per run keeps a profiler's per-kernel averages to one layout)")
     ap.add_argument("--calib", action="store_true",
                     help="also run a 256 MiB -> 256 MiB elementwise copy (3x): the known-size "
                          "kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes")
@@ -292,7 +295,7 @@ def main():
               "data": "synthetic (seeded torch.randn on the GPU, random values of the "
                       "configs' shapes/distributions)"}
 
-    if args.only in ("all", "decode"):
+    if args.only in ("all", "decode") and args.layouts != "tiled":
         log("decode c3 ...")
         wl = DecodeWorkload(torch, A, B=8, hq=32, hkv=8, d=64, prev=2048,
                             kv_dtype=torch.float16, sigma=0.5, base=5e5, n_sets=16,
@@ -335,6 +338,7 @@ def main():
             f"{t['rope_store']*1e3:.2f} us, two calls {t['two_calls']*1e3:.2f} us")
         del wl
         torch.cuda.empty_cache()
+    if args.only in ("all", "decode") and args.layouts != "colmajor":
         log("decode_c3_tiled ...")
         wl = DecodeWorkload(torch, A, B=8, hq=32, hkv=8, d=64, prev=2048,
                             kv_dtype=torch.float16, sigma=0.5, base=5e5, n_sets=16,
@@ -416,6 +420,8 @@ def main():
 
     if args.only in ("all", "c5"):
         for layout, key in ((0, "decode_c5"), (1, "decode_c5_tiled")):
+            if args.layouts == ("tiled" if layout == 0 else "colmajor"):
+                continue
             log(f"{key} ...")
             wl = DecodeWorkload(torch, A, B=16, hq=32, hkv=4, d=128, prev=32768,
                                 kv_dtype=torch.bfloat16, sigma=1.0, base=1e6, n_sets=1,
