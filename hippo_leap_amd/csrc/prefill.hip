@@ -9,13 +9,14 @@
 // group it holds, with no length cap.
 //
 // Two kernels:
-//  * prefill_mfma_kernel: fp16 MFMA (v_mfma_f32_32x32x16_f16) on operands
-//    prepared by prologue_kernel: qt[Hq][Tp][D] (q pre-scaled by
-//    scale*log2 e), kt[Hkv][Tp][D], vt[Hkv][D][Tp].  fp16 operands keep 11
-//    significant bits (bf16 has 8), which keeps the result within 2e-3 of the
-//    fp32 reference; P is rounded to fp16, accumulation is fp32.
-//  * prefill_f32_kernel: fp32 vector-ALU flash kernel on the reference's
-//    col-major fp32 tensors (the 1e-4 path).
+//  * prefill_mfma_kernel: fp16 MFMA (v_mfma_f32_32x32x16_f16) for bf16/fp16
+//    activations, on K/V operands prepared by the prologue (kt[Hkv][Tp][D],
+//    vt[Hkv][D][Tp]) and Q built in the kernel (or qt[Hq][Tp][D]).  fp16
+//    operands keep 11 significant bits (bf16 has 8), which keeps the result
+//    within 2e-3 of the fp32 reference; P is rounded to fp16, accumulation
+//    is fp32.
+//  * prefill_f32mfma_kernel: fp32 MFMA (v_mfma_f32_32x32x2_f32) on the
+//    reference's col-major fp32 tensors (the 1e-4 path).
 #include "common.h"
 #include "launch.h"
 
@@ -530,165 +531,196 @@ hipError_t prefill_mfma_launch(const PrefillLaunch& a, hipStream_t stream) {
 }
 
 // ===========================================================================
-// fp32 path: 32 query rows x 64 key columns per step, 256 threads.
-// Thread (rg = tid/16, cg = tid%16) owns score rows {2rg, 2rg+1} x columns
-// {4cg..4cg+3} and output rows {2rg, 2rg+1} x dims {4cg + 64u + 0..3}.
+// fp32 path on the matrix cores: v_mfma_f32_32x32x2_f32 (fp32 products and
+// accumulation), 4 waves; wave w owns 32 query rows of one head of the
+// workgroup's nh heads (one GQA group shares the K/V tiles), row block
+// w / nh.  Per 64-key tile:
+//   S^T[j][t] = K[j][:] . Q^T[:][t]   (A = K from LDS, B = q in registers,
+//                                      pre-scaled by scale * log2 e)
+//   online softmax over j for row t = lane % 32 (in-lane + one xor-32)
+//   O^T[d][t] += V^T[d][j] . P^T[j][t] (A = V from LDS, B = P in registers)
+// MFMA k-step ks pairs element 2ks + h with lane half h.  S^T output row
+// m = 8a + 4h + e of key block mb is key 32mb + 8a + 2e + h, so output
+// register 4a + e of lane half h is exactly the P^T operand of P.V k-step
+// 16mb + 4a + e: P never leaves registers.  K rows are staged in LDS as
+// [h][key][ks], V rows as [h][d][ks] (ks = the pair index), 16-byte chunks
+// XOR-swizzled by the row: one 16-byte read gives four k-steps' operands.
 // ===========================================================================
-template <int D>
-__global__ __launch_bounds__(256) void prefill_f32_kernel(PrefillLaunch p) {
-  constexpr int BM = 32, BNF = 64, DU = D / 64;
-  constexpr int NL = D * BNF / 256;  // K (and V) tile elements per thread
-  __shared__ __attribute__((aligned(16))) float sq[D][BM];        // Q tile, [d][row]
-  __shared__ __attribute__((aligned(16))) float sk[D * (BNF + 4)];  // K tile, [d][col]
-  __shared__ __attribute__((aligned(16))) float sv[BNF * (D + 4)];  // V tile, [col][d]
-  __shared__ __attribute__((aligned(16))) float sp[BM][BNF + 4];
+namespace {
+__device__ __forceinline__ f32x16 mma32f(float a, float b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+}  // namespace
 
-  const int tid = threadIdx.x;
-  const int rg = tid >> 4, cg = tid & 15;
+template <int D>
+__global__ __launch_bounds__(256) void prefill_f32mfma_kernel(PrefillLaunch p, int nh) {
+  constexpr int NW = 4;             // waves
+  constexpr int KS = D / 2;         // S^T k-steps (pairs of head dims)
+  constexpr int KC = KS / 4;        // 16-byte chunks per staged K row
+  constexpr int DB = D / 32;        // 32-dim blocks of O^T
+  constexpr int BN = 64;            // keys per tile
+  constexpr int NL = D * BN / (64 * NW);  // K (and V) tile elements per thread
+  __shared__ __attribute__((aligned(16))) float sk[2 * BN * KS];  // [h][key][ks]
+  __shared__ __attribute__((aligned(16))) float sv[2 * D * 32];   // [h][d][ks]
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int ln = lane & 31, hh = lane >> 5;
   const int T = p.seq_len;
-  const int nq = (T + BM - 1) / BM;
-  const int h = blockIdx.y;
-  const int qb = nq - 1 - blockIdx.x;  // heavy blocks first
-  const int i0 = qb * BM;
-  const int kvh = h / (p.n_head / p.n_head_kv);
-  const float* Q = p.q + (long long)h * D * T;
+  const int group = p.n_head / p.n_head_kv;
+  const int rows_wg = 32 * (NW / nh);
+  const int n_qblk = (T + rows_wg - 1) / rows_wg;
+  const int n_hgrp = group / nh;
+  const int per_q = p.n_head_kv * n_hgrp;
+  const int item = blockIdx.x;
+  const int qblk = n_qblk - 1 - item / per_q;  // heaviest query blocks first
+  const int kvh = (item % per_q) / n_hgrp;
+  const int hgrp = (item % per_q) % n_hgrp;
+  const int hq = kvh * group + hgrp * nh + wave % nh;
+  const int r0 = qblk * rows_wg + (wave / nh) * 32;
+  const int wg_last_row = min(T - 1, qblk * rows_wg + rows_wg - 1);
+  const int n_tiles = wg_last_row / BN + 1;
+  const int t_abs = r0 + ln;
+  const bool live = r0 < T;
+
   const float* K = p.k + (long long)kvh * D * T;
   const float* V = p.v + (long long)kvh * D * T;
-  const int last_row = min(T - 1, i0 + BM - 1);
-  const int n_tiles = last_row / BNF + 1;
 
-  // Thread tid moves column lc = tid % 64 of rows d = tid/64 + 4k of each
-  // K / V tile (coalesced).  The next tile's loads are issued before the
-  // current one is computed, so each tile's memory latency hides behind the
-  // previous tile's work; columns >= T read a valid column and become 0.
-  const int lc = tid & (BNF - 1), ld0 = tid / BNF;
+  // K/V tiles: thread moves column lc (key j0 + lc) of rows d = ld0 + 4k;
+  // the next tile's values are loaded while the current one is computed.
+  const int lc = tid & 63, ld0 = tid >> 6;
   float kr[NL], vr[NL];
   auto load_kv = [&](int j0) {
     const int col = min(j0 + lc, T - 1);
 #pragma unroll
     for (int k = 0; k < NL; ++k) {
-      kr[k] = K[(long long)(ld0 + 4 * k) * T + col];
-      vr[k] = V[(long long)(ld0 + 4 * k) * T + col];
+      kr[k] = K[(long long)(ld0 + NW * k) * T + col];
+      vr[k] = V[(long long)(ld0 + NW * k) * T + col];
     }
   };
   load_kv(0);
 
-  for (int idx = tid; idx < D * BM; idx += 256) {
-    const int d = idx / BM, r = idx % BM;
-    sq[d][r] = (i0 + r < T) ? Q[(long long)d * T + i0 + r] : 0.f;
+  // q operand: lane (ln, hh) holds q[t][2ks + hh] * scale * log2 e
+  float qv[KS];
+  {
+    const float* Q = p.q + (long long)hq * D * T;
+    const int t = min(t_abs, T - 1);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) qv[ks] = Q[(long long)(2 * ks + hh) * T + t] * p.scale_log2;
   }
+  // Swizzled 16-byte chunk of a staged row (rows 2D or 128 bytes long).
+  auto kswz = [](int key) { return D == 64 ? (key >> 1) & 7 : key & 15; };
+  auto vswz = [](int d) { return (d >> 1) & 7; };
 
-  float o[2][4 * DU];
+  f32x16 o[DB];
 #pragma unroll
-  for (int a = 0; a < 2; ++a)
+  for (int db = 0; db < DB; ++db)
 #pragma unroll
-    for (int b = 0; b < 4 * DU; ++b) o[a][b] = 0.f;
-  float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};
+    for (int i = 0; i < 16; ++i) o[db][i] = 0.f;
+  float m_run = -INFINITY, l_run = 0.f;
 
   for (int tile = 0; tile < n_tiles; ++tile) {
-    const int j0 = tile * BNF;
-    __syncthreads();  // the previous tile's sk / sv / sp reads are done
+    const int j0 = tile * BN;
+    __syncthreads();  // the previous tile's sk / sv reads are done
     {
       const bool in = j0 + lc < T;
 #pragma unroll
       for (int k = 0; k < NL; ++k) {
-        const int d = ld0 + 4 * k;
-        sk[d * (BNF + 4) + lc] = in ? kr[k] : 0.f;
-        sv[lc * (D + 4) + d] = in ? vr[k] : 0.f;
+        const int d = ld0 + NW * k;
+        const float kx = in ? kr[k] : 0.f, vx = in ? vr[k] : 0.f;
+        // K: (h = d & 1, key = lc, ks = d >> 1); V: (h = lc & 1, d, ks = lc >> 1)
+        const int ksk = d >> 1, ksv = lc >> 1;
+        sk[((d & 1) * BN + lc) * KS + (((ksk >> 2) ^ kswz(lc)) << 2) + (ksk & 3)] = kx;
+        sv[((lc & 1) * D + d) * 32 + (((ksv >> 2) ^ vswz(d)) << 2) + (ksv & 3)] = vx;
       }
     }
-    if (tile + 1 < n_tiles) load_kv(j0 + BNF);
+    if (tile + 1 < n_tiles) load_kv(j0 + BN);
     __syncthreads();
-    float s[2][4];
+    if (!live || j0 > r0 + 31) continue;  // wave-uniform: no key of this tile is visible
+
+    f32x16 s[2];
 #pragma unroll
-    for (int a = 0; a < 2; ++a)
+    for (int mb = 0; mb < 2; ++mb) {
+      const int m = ln;  // A operand row = key 32mb + 8a + 2e + h for m = 8a + 4h + e
+      const int key = 32 * mb + 8 * (m >> 3) + 2 * (m & 3) + ((m >> 2) & 1);
+      const float* row = sk + (hh * BN + key) * KS;
 #pragma unroll
-      for (int b = 0; b < 4; ++b) s[a][b] = 0.f;
-#pragma unroll 8
-    for (int d = 0; d < D; ++d) {
-      const float q0 = sq[d][2 * rg], q1 = sq[d][2 * rg + 1];
-      const f32x4 kv = *(const f32x4*)&sk[d * (BNF + 4) + 4 * cg];
+      for (int i = 0; i < 16; ++i) s[mb][i] = 0.f;
 #pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        s[0][b] = fmaf(q0, kv[b], s[0][b]);
-        s[1][b] = fmaf(q1, kv[b], s[1][b]);
+      for (int c = 0; c < KC; ++c) {
+        const f32x4 kf = *(const f32x4*)(row + ((c ^ kswz(key)) << 2));
+#pragma unroll
+        for (int e = 0; e < 4; ++e) s[mb] = mma32f(kf[e], qv[4 * c + e], s[mb]);
       }
     }
-    // scale (naive.nim:3415), causal mask, online softmax per row
-    float alpha[2];
+    // Causal mask and keys beyond T: output register i = 4a + e of lane half
+    // hh in block mb is key j0 + 32mb + 8a + 2e + hh.
+    float mt = -INFINITY;
 #pragma unroll
-    for (int a = 0; a < 2; ++a) {
-      const int i = i0 + 2 * rg + a;
-      float mt = -INFINITY;
+    for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        const int j = j0 + 4 * cg + b;
-        s[a][b] = (j <= i && j < T) ? s[a][b] * p.scale_log2 : -INFINITY;
-        mt = fmaxf(mt, s[a][b]);
+      for (int i = 0; i < 16; ++i) {
+        const int key = j0 + 32 * mb + 8 * (i >> 2) + 2 * (i & 3) + hh;
+        s[mb][i] = (key <= t_abs && key < T) ? s[mb][i] : -INFINITY;
+        mt = fmaxf(mt, s[mb][i]);
       }
+    mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+    const float mn = fmaxf(m_run, mt);  // finite: key j0 <= t_abs for every live row
+    const float alpha = fast_exp2(m_run - mn);
+    m_run = mn;
+    float ps = 0.f;
 #pragma unroll
-      for (int off = 8; off > 0; off >>= 1) mt = fmaxf(mt, __shfl_xor(mt, off, 16));
-      const float mn = fmaxf(m_run[a], mt);
-      if (mn == -INFINITY) {  // row entirely masked in this tile and before
-        alpha[a] = 1.f;
+    for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-        for (int b = 0; b < 4; ++b) sp[2 * rg + a][4 * cg + b] = 0.f;
-        continue;
+      for (int i = 0; i < 16; ++i) {
+        s[mb][i] = fast_exp2(s[mb][i] - mn);
+        ps += s[mb][i];
       }
-      alpha[a] = fast_exp2(m_run[a] - mn);
-      m_run[a] = mn;
-      float ps = 0.f;
+    l_run = l_run * alpha + ps;
 #pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        const float pv = fast_exp2(s[a][b] - mn);
-        ps += pv;
-        sp[2 * rg + a][4 * cg + b] = pv;
-      }
-      l_run[a] = l_run[a] * alpha[a] + ps;
-    }
-    __syncthreads();
+    for (int db = 0; db < DB; ++db)
 #pragma unroll
-    for (int a = 0; a < 2; ++a)
+      for (int i = 0; i < 16; ++i) o[db][i] *= alpha;
+    // O^T += V^T P^T: k-step ks = 16mb + i pairs keys 2ks + h.
 #pragma unroll
-      for (int b = 0; b < 4 * DU; ++b) o[a][b] *= alpha[a];
-    const int ncols = min(BNF, T - j0);
-#pragma unroll 4
-    for (int c = 0; c < ncols; ++c) {
-      const float p0 = sp[2 * rg][c], p1 = sp[2 * rg + 1][c];
+    for (int db = 0; db < DB; ++db) {
+      const int d = 32 * db + ln;
+      const float* row = sv + (hh * D + d) * 32;
 #pragma unroll
-      for (int u = 0; u < DU; ++u) {
-        const f32x4 vv = *(const f32x4*)&sv[c * (D + 4) + 4 * cg + 64 * u];
+      for (int c = 0; c < 8; ++c) {
+        const f32x4 vf = *(const f32x4*)(row + ((c ^ vswz(d)) << 2));
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          o[0][4 * u + e] = fmaf(p0, vv[e], o[0][4 * u + e]);
-          o[1][4 * u + e] = fmaf(p1, vv[e], o[1][4 * u + e]);
+          const int ks = 4 * c + e;
+          o[db] = mma32f(vf[e], s[ks >> 4][ks & 15], o[db]);
         }
       }
     }
   }
 
-  float* O = (float*)p.out + (long long)h * D * T;
+  if (!live) return;
+  const float l = l_run + __shfl_xor(l_run, 32, 64);
+  const float inv = 1.0f / l;
+  if (t_abs < T) {
+    float* O = (float*)p.out + (long long)hq * D * T;
 #pragma unroll
-  for (int a = 0; a < 2; ++a) {
-    float l = l_run[a];
+    for (int db = 0; db < DB; ++db)
 #pragma unroll
-    for (int off = 8; off > 0; off >>= 1) l += __shfl_xor(l, off, 16);
-    const int i = i0 + 2 * rg + a;
-    if (i < T) {
-      const float inv = 1.0f / l;
-#pragma unroll
-      for (int u = 0; u < DU; ++u)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) O[(long long)(4 * cg + 64 * u + e) * T + i] = o[a][4 * u + e] * inv;
-    }
+      for (int i = 0; i < 16; ++i) {
+        const int d = 32 * db + 8 * (i >> 2) + 4 * hh + (i & 3);
+        O[(long long)d * T + t_abs] = o[db][i] * inv;
+      }
   }
 }
 
 hipError_t prefill_f32_launch(const PrefillLaunch& p, hipStream_t stream) {
-  dim3 grid((p.seq_len + 31) / 32, p.n_head);
+  const int group = p.n_head / p.n_head_kv;
+  const int nh = (group % 4 == 0) ? 4 : ((group % 2 == 0) ? 2 : 1);  // heads per workgroup
+  const int rows_wg = 32 * (4 / nh);
+  dim3 grid(p.n_head_kv * (group / nh) * ((p.seq_len + rows_wg - 1) / rows_wg));
   switch (p.head_dim) {
-    case 64: hipLaunchKernelGGL(prefill_f32_kernel<64>, grid, dim3(256), 0, stream, p); break;
-    case 128: hipLaunchKernelGGL(prefill_f32_kernel<128>, grid, dim3(256), 0, stream, p); break;
+    case 64: hipLaunchKernelGGL(prefill_f32mfma_kernel<64>, grid, dim3(256), 0, stream, p, nh); break;
+    case 128: hipLaunchKernelGGL(prefill_f32mfma_kernel<128>, grid, dim3(256), 0, stream, p, nh); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
