@@ -20,6 +20,10 @@ Extra objects on the same JSON line:
   decode_c5_tiled, decode_c3_tiled: the same steps with the caches in the
     opt-in tiled layout (HL_KV_TILED32: per kv head, 32-column tiles of
     [D][32]), same values.
+  decode_c1, prefill_c2: configs[0] and configs[1], the reference's fp32
+    call contract (hl_gpu_attention_decode; fp32 prefill with RoPE 1e4 and
+    the cache write), timed for reference: they are parity cases, not the
+    metric.
   roofline: the fused step kernel (qkNorm/RoPE + KV write + split-K
     attention + merge) timed with HIP events on the stream it runs on.
   cpu_baseline: the C oracle (single-threaded scalar fp32 restatement of the
