@@ -26,6 +26,9 @@ Extra objects on the same JSON line:
     metric.
   roofline: the fused step kernel (qkNorm/RoPE + KV write + split-K
     attention + merge) timed with HIP events on the stream it runs on.
+  linear: hl_gpu_linear_col (the gpuLinearCol drop-in, fp32) at the
+    projection shapes around attention: decode GEMV GB/s (weights from HBM)
+    and prefill GEMM TFLOP/s against the fp32 peak.
   cpu_baseline: the C oracle (single-threaded scalar fp32 restatement of the
     reference's tensor.nim math) timed on this host on a bounded sample.
 """
@@ -261,13 +264,57 @@ def decode_extra(wl, t, workload):
     }
 
 
+# ---------------------------------------------------------------------------
+# fp32 linear layer (gpuLinearCol drop-in): the projections around attention
+# ---------------------------------------------------------------------------
+def bench_linear(torch, A):
+    """hl_gpu_linear_col at the projection shapes of the configs' models.
+    Decode (seq_len 1): GB/s over the weight bytes (+ x, y), weights rotated
+    over > 512 MB of copies so every call reads them from HBM.  Prefill:
+    TFLOP/s on 2*M*K*T against the fp32 peak."""
+    out = {}
+    g = torch.Generator(device="cuda").manual_seed(13)
+    for name, M, K in (("decode_tinyllama_q", 2048, 2048), ("decode_llama8b_q", 4096, 4096),
+                       ("decode_llama8b_kv", 1024, 4096), ("decode_llama8b_ffn_up", 14336, 4096)):
+        wbytes = M * K * 4
+        n = max(2, -(-(600 << 20) // wbytes))
+        ws = [torch.rand(M, K, generator=g, device="cuda") for _ in range(n)]
+        x = torch.randn(K, generator=g, device="cuda")
+        y = torch.empty(M, device="cuda")
+        fn = lambda i: A.gpu_linear_col(y, x, ws[i % n], K, M, 1)
+        ms = graph_time_ms(torch, fn, n_inner=max(n, 16), replays=4)
+        nbytes = wbytes + (K + M) * 4
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out[name] = {"shape": f"W {M}x{K} fp32, T=1", "us": round(ms * 1e3, 3), "unit": "GB/s",
+                     "value": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
+                     "weight_copies": n}
+        log(f"linear {name}: {ms*1e3:.2f} us, {gbs:.0f} GB/s")
+        del ws
+    for name, M, K, T in (("prefill_tinyllama_q_c2", 2048, 2048, 512),
+                          ("prefill_llama8b_q_c4", 4096, 4096, 4096)):
+        w = torch.rand(M, K, generator=g, device="cuda")
+        x = torch.randn(K, T, generator=g, device="cuda")
+        y = torch.empty(M, T, device="cuda")
+        fn = lambda i: A.gpu_linear_col(y, x, w, K, M, T)
+        ms = graph_time_ms(torch, fn, n_inner=8, replays=4)
+        tf = 2.0 * M * K * T / (ms * 1e-3) / 1e12
+        out[name] = {"shape": f"W {M}x{K} x X {K}x{T} fp32", "us": round(ms * 1e3, 2),
+                     "unit": "TFLOP/s", "value": round(tf, 2),
+                     "frac_fp32_peak": round(tf / FP32_PEAK_TFLOPS, 4)}
+        log(f"linear {name}: {ms*1e3:.1f} us, {tf:.1f} TFLOP/s")
+        del w, x, y
+    torch.cuda.empty_cache()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--only", choices=["all", "decode", "prefill", "c5", "fp32"], default="all")
+    ap.add_argument("--only", choices=["all", "decode", "prefill", "c5", "fp32", "linear"],
+                    default="all")
     ap.add_argument("--layouts", choices=["both", "colmajor", "tiled"], default="both",
                     help="KV-cache layouts of the decode runs (the headline c3 line is column-major; "
                          "one layout per run keeps a profiler's per-kernel averages to one layout)")
@@ -391,7 +438,7 @@ def main():
         f2 = 4 * 32 * 64 * T2 * (T2 + 1) // 2
         result["prefill_c2"] = {
             "workload": "c2: TinyLlama-shape causal prefill, fp32, T=512, Hq32/Hkv4, D64, RoPE 1e4, "
-                        "KV cache written (fp32 vector-ALU path)",
+                        "KV cache written (prologue + fp32-MFMA flash kernel)",
             "us": round(ms2 * 1e3, 3), "unit": "TFLOP/s",
             "value": round(f2 / (ms2 * 1e-3) / 1e12, 3),
             "frac_fp32_peak": round(f2 / (ms2 * 1e-3) / 1e12 / FP32_PEAK_TFLOPS, 4)}
@@ -438,6 +485,9 @@ def main():
                 f"{t['attn']*1e3:.1f} us")
             del wl
             torch.cuda.empty_cache()
+
+    if args.only in ("all", "linear"):
+        result["linear"] = bench_linear(torch, A)
 
     if not args.no_cpu:
         log("cpu baseline ...")

@@ -109,6 +109,12 @@ def gpu_attention_prefill(dst, q, k, v, n_head, n_head_kv, head_dim, seq_len, st
                                                head_dim, seq_len, _stream(stream)))
 
 
+def gpu_linear_col(dst, x, w, w_cols, w_rows, seq_len, stream=None):
+    """gpuLinearCol (naive.nim:3519-3547): dst[w_rows, seq_len] = w . x, fp32."""
+    check(_lib.load().hl_gpu_linear_col(_p(dst), _p(x), _p(w), w_cols, w_rows, seq_len,
+                                        _stream(stream)))
+
+
 def set_rope_theta(rope_dim: int, rope_base: float) -> None:
     """Installs the theta table (naive.nim:3850-3861) used by the *_theta procs."""
     check(_lib.load().hl_set_rope_theta(rope_dim, rope_base))

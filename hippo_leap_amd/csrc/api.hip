@@ -766,6 +766,24 @@ int hl_gpu_attention_prefill(float* dst, const float* q, const float* k, const f
   return hl_attn_prefill(&a, nullptr, 0, stream);
 }
 
+static bool overlaps(const void* a, size_t abytes, const void* b, size_t bbytes) {
+  const uintptr_t a0 = (uintptr_t)a, b0 = (uintptr_t)b;
+  return a0 < b0 + bbytes && b0 < a0 + abytes;
+}
+
+int hl_gpu_linear_col(float* dst, const float* x, const float* w, int w_cols, int w_rows,
+                      int seq_len, void* stream) {
+  if (!dst || !x || !w) return fail(HL_EINVAL, "linear_col: null pointer");
+  if (w_cols <= 0 || w_rows <= 0 || seq_len <= 0)
+    return fail(HL_EINVAL, "linear_col: bad shape (w_cols=%d, w_rows=%d, seq_len=%d)", w_cols,
+                w_rows, seq_len);
+  const size_t ybytes = (size_t)w_rows * seq_len * 4, xbytes = (size_t)w_cols * seq_len * 4;
+  if (overlaps(dst, ybytes, x, xbytes) || overlaps(dst, ybytes, w, (size_t)w_rows * w_cols * 4))
+    return fail(HL_EINVAL, "linear_col: dst overlaps x or w");
+  hipError_t e = linear_col_launch(dst, x, w, w_cols, w_rows, seq_len, as_stream(stream));
+  return e == hipSuccess ? HL_OK : hip_fail(e, "linear_col launch");
+}
+
 int hl_kv_cache_to_f32(float* dst, const void* cache, int kv_dtype, int rows, int max_len, int col0,
                        int ncols, void* stream) {
   if (!dst || !cache) return fail(HL_EINVAL, "cache_to_f32: null pointer");

@@ -131,4 +131,17 @@ hipError_t prefill_f32_launch(const PrefillLaunch& p, hipStream_t stream);
 hipError_t prefill_mfma_launch(const PrefillLaunch& p, hipStream_t stream);
 int prefill_mfma_tpad(int seq_len);
 
+// ---- fp32 linear layer (linear.hip) ----------------------------------------
+// Y[M, T] = W[M, K] . X[K, T]: GEMV for T == 1, fp32-MFMA GEMM otherwise.
+struct LinearPlan {
+  bool gemv;
+  bool vec;      // 16-byte loads (K % 4 == 0, T % 4 == 0 for the GEMM, aligned w, x)
+  int wpr;       // GEMV: waves per row (1, or 4 when M is small)
+  int tile;      // GEMM: output tile edge (64 or 128)
+  int grid_x, grid_y;
+};
+LinearPlan linear_plan(int M, int K, int T, const float* w, const float* x);
+hipError_t linear_col_launch(float* y, const float* x, const float* w, int K, int M, int T,
+                             hipStream_t stream);
+
 }  // namespace hl

@@ -166,6 +166,16 @@ int hl_gpu_attention_prefill(float* dst, const float* q, const float* k,
                              const float* v, int n_head, int n_head_kv,
                              int head_dim, int seq_len, void* stream);
 
+/* gpuLinearCol (naive.nim:3519-3547), the Q/K/V and O projections around
+ * attention: dst[wRows, seqLen] = w[wRows, wCols] . x[wCols, seqLen], all
+ * fp32; w row-major (wCols fastest), x and dst with seqLen fastest.
+ * seq_len == 1 is the decode GEMV, seq_len > 1 the prefill GEMM.  dst must
+ * not overlap x or w (HL_EINVAL: the outputs would race with the reads).
+ * Unlike the reference's decode kernel there is no width cap
+ * (HippoMaxDecodeCols = 18432, naive.nim:20, 3530-3533).                 */
+int hl_gpu_linear_col(float* dst, const float* x, const float* w, int w_cols,
+                      int w_rows, int seq_len, void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* Batched / typed API (extends the reference: B sequences, fp16/bf16 KV)   */
 /* ------------------------------------------------------------------------ */

@@ -234,3 +234,16 @@ def test_kv_layout_helpers_match_header_formula():
         b, h, d, c = (int(rng.integers(n)) for n in (B, H, D, M))
         assert t[b * H * D * M + h * D * M + ((c // 32) * D + d) * 32 + c % 32] == x[b, h * D + d, c]
     assert torch.equal(A.kv_from_tiled(A.kv_to_tiled(x, H, D, M), H, D, M), x)
+
+
+def test_linear_col_validation(hl):
+    """gpuLinearCol's arguments: shapes must be positive, dst may not alias
+    the input it reads (the reference's in-place call, naive.nim:4115, races)."""
+    F = FAKE
+    assert hl.hl_gpu_linear_col(None, F, F, 64, 64, 1, None) == _lib.HL_EINVAL
+    assert hl.hl_gpu_linear_col(F, F + (1 << 24), F + (1 << 25), 0, 64, 1, None) == _lib.HL_EINVAL
+    assert hl.hl_gpu_linear_col(F, F + (1 << 24), F + (1 << 25), 64, 64, 0, None) == _lib.HL_EINVAL
+    # dst [64, 8] overlaps x [64, 8] by one float; then dst inside w
+    assert hl.hl_gpu_linear_col(F, F + 64 * 8 * 4 - 4, F + (1 << 25), 64, 64, 8, None) == _lib.HL_EINVAL
+    assert hl.hl_gpu_linear_col(F + 4096, F + (1 << 24), F, 64, 64, 1, None) == _lib.HL_EINVAL
+    assert b"overlaps" in hl.hl_last_error()
