@@ -8,14 +8,18 @@
 // W is row-major with K fastest (the GGUF weight as loaded, naive.nim:4091);
 // X and Y keep the token index fastest (ggml column-major [dim, T]).
 //
-// * T == 1 (decode): linear_gemv_kernel reads W once from HBM with 16-byte
-//   loads, eight in flight per lane; the bound is HBM bandwidth over
-//   M*K*4 bytes.  One wave per row (four per row when M is small, so the
-//   grid still covers the chip), one cross-lane reduction per row.
+// * T == 1 (decode): linear_gemv_kernel reads W once from HBM with
+//   non-temporal 16-byte loads, eight in flight per lane; the bound is HBM
+//   bandwidth over M*K*4 bytes.  One wave per row (four per row when M is
+//   small, so the grid still covers the chip), one cross-lane reduction per
+//   row.  x is re-read from L2 by every wave (staging it in LDS measured
+//   slower).
 // * T > 1 (prefill): linear_mfma_kernel on fp32 MFMA
 //   (v_mfma_f32_32x32x2_f32); the bound is the fp32 matrix peak over
-//   2*M*K*T FLOPs.  Workgroup tiles of 64x64 or 128x128 outputs, K staged
-//   through LDS 32 at a time, double-buffered, one barrier per chunk.
+//   2*M*K*T FLOPs.  Workgroup tiles of 128x128 outputs (4 waves, 2x2 blocks
+//   of 32x32 each) when there are enough of them to fill the chip, else
+//   64x64 (8 waves in two K halves); K staged through double-buffered LDS
+//   with two chunks in flight in registers, one barrier per chunk.
 //
 // Accumulation is fp32 as in the reference; only the summation order
 // differs (the reference's decode kernel reduces 256 strided partial sums,
@@ -65,7 +69,8 @@ __global__ __launch_bounds__(256) void linear_gemv_kernel(const float* __restric
       for (; k + (U - 1) * STEP < K4; k += U * STEP) {
         f32x4 wv[U], xv[U];
 #pragma unroll
-        for (int u = 0; u < U; ++u) wv[u] = w4[k + u * STEP];
+        for (int u = 0; u < U; ++u)
+          wv[u] = __builtin_nontemporal_load(&w4[k + u * STEP]);  // W is read once
 #pragma unroll
         for (int u = 0; u < U; ++u) xv[u] = x4[k + u * STEP];
 #pragma unroll
@@ -77,7 +82,7 @@ __global__ __launch_bounds__(256) void linear_gemv_kernel(const float* __restric
         }
       }
       for (; k < K4; k += STEP) {
-        const f32x4 wv = w4[k], xv = x4[k];
+        const f32x4 wv = __builtin_nontemporal_load(&w4[k]), xv = x4[k];
         s[0] += wv.x * xv.x;
         s[1] += wv.y * xv.y;
         s[2] += wv.z * xv.z;
@@ -113,89 +118,96 @@ __global__ __launch_bounds__(256) void linear_gemv_kernel(const float* __restric
 // group are one contiguous 16-byte LDS read.
 //
 // The 2x2 waves of a workgroup each own a (32*WM) x (32*WN) block of the
-// (64*WM) x (64*WN) output tile.
-template <int WM, int WN, bool VEC>
-__global__ __launch_bounds__(256) void linear_mfma_kernel(const float* __restrict__ w,
+// (64*WM) x (64*WN) output tile.  KW = 2 doubles the workgroup to 8 waves:
+// waves 4..7 take the upper half of every K chunk for the same blocks (two
+// waves per SIMD to cover each other's LDS and barrier waits), and their
+// sums are added through LDS at the end.
+template <int WM, int WN, int BK, int KW, bool VEC, int PF = 2>
+__global__ __launch_bounds__(256 * KW) void linear_mfma_kernel(const float* __restrict__ w,
                                                           const float* __restrict__ x,
                                                           float* __restrict__ y, int M, int K,
                                                           int T) {
-  constexpr int BM = 64 * WM, BN = 64 * WN, BK = 32;
+  constexpr int BM = 64 * WM, BN = 64 * WN;
   // Row pitches in floats.  SA = 36: the 16 lanes served together by one
   // ds_read_b128 (rows m..m+15, same k) start on distinct 4-bank groups.
   // SB = BN + 8: rows k and k + 4 (the two lane halves of a b32 read) sit
   // 32 banks apart, so the 64 lanes hit 64 distinct banks.
   constexpr int SA = BK + 4, SB = BN + 8;
-  constexpr int NA = BM * BK / 4 / 256;  // 16-byte A chunks per thread
-  constexpr int NB = BK * BN / 4 / 256;  // 16-byte B chunks per thread
+  constexpr int NTH = 256 * KW;
+  constexpr int NA = BM * BK / 4 / NTH;  // 16-byte A chunks per thread
+  constexpr int NB = BK * BN / 4 / NTH;  // 16-byte B chunks per thread
+  static_assert(NA * NTH * 4 == BM * BK && NB * NTH * 4 == BK * BN, "tile / thread mismatch");
   __shared__ __attribute__((aligned(16))) float sA[2][BM * SA];
   __shared__ __attribute__((aligned(16))) float sB[2][BK * SB];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = tid >> 6;
   const int ln = lane & 31, hh = lane >> 5;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int kg = wave >> 2;  // K half of each chunk (KW = 2)
+  const int wm = (wave >> 1) & 1, wn = wave & 1;
   const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
 
-  f32x4 ra[NA], rb[NB];
-  auto load = [&](int c) {
+  f32x4 ra[PF][NA], rb[PF][NB];  // PF chunks in flight, one register set each
+  auto load = [&](int c, int st) {
     const int k0 = c * BK;
 #pragma unroll
     for (int j = 0; j < NA; ++j) {
-      const int idx = tid + 256 * j, r = idx >> 3, kk = k0 + 4 * (idx & 7);
+      const int idx = tid + NTH * j, r = idx / (BK / 4), kk = k0 + 4 * (idx % (BK / 4));
       const int m = m0 + r;
       if (VEC) {
-        ra[j] = (m < M && kk < K) ? *(const f32x4*)(w + (size_t)m * K + kk) : f32x4{0.f, 0.f, 0.f, 0.f};
+        ra[st][j] = (m < M && kk < K) ? *(const f32x4*)(w + (size_t)m * K + kk) : f32x4{0.f, 0.f, 0.f, 0.f};
       } else {
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          ra[j][e] = (m < M && kk + e < K) ? w[(size_t)m * K + kk + e] : 0.f;
+          ra[st][j][e] = (m < M && kk + e < K) ? w[(size_t)m * K + kk + e] : 0.f;
       }
     }
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
-      const int idx = tid + 256 * j, r = idx / (BN / 4), n = n0 + 4 * (idx % (BN / 4));
+      const int idx = tid + NTH * j, r = idx / (BN / 4), n = n0 + 4 * (idx % (BN / 4));
       const int k = k0 + r;
       if (VEC) {
-        rb[j] = (k < K && n < T) ? *(const f32x4*)(x + (size_t)k * T + n) : f32x4{0.f, 0.f, 0.f, 0.f};
+        rb[st][j] = (k < K && n < T) ? *(const f32x4*)(x + (size_t)k * T + n) : f32x4{0.f, 0.f, 0.f, 0.f};
       } else {
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          rb[j][e] = (k < K && n + e < T) ? x[(size_t)k * T + n + e] : 0.f;
+          rb[st][j][e] = (k < K && n + e < T) ? x[(size_t)k * T + n + e] : 0.f;
       }
     }
   };
-  auto store = [&](int buf) {
+  auto store = [&](int buf, int st) {
 #pragma unroll
     for (int j = 0; j < NA; ++j) {
-      const int idx = tid + 256 * j;
-      *(f32x4*)&sA[buf][(idx >> 3) * SA + 4 * (idx & 7)] = ra[j];
+      const int idx = tid + NTH * j;
+      *(f32x4*)&sA[buf][(idx / (BK / 4)) * SA + 4 * (idx % (BK / 4))] = ra[st][j];
     }
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
-      const int idx = tid + 256 * j;
-      *(f32x4*)&sB[buf][(idx / (BN / 4)) * SB + 4 * (idx % (BN / 4))] = rb[j];
+      const int idx = tid + NTH * j;
+      *(f32x4*)&sB[buf][(idx / (BN / 4)) * SB + 4 * (idx % (BN / 4))] = rb[st][j];
     }
   };
 
-  f32x16 acc[WM][WN];
+  // Independent accumulation chains per output block: back-to-back MFMAs
+  // into one accumulator wait for each other, so with a single 32x32 block
+  // per wave the k-steps rotate over CH accumulators (summed at the end).
+  constexpr int CH = (WM * WN >= 2) ? 1 : 2;
+  f32x16 acc[WM][WN][CH];
 #pragma unroll
   for (int a = 0; a < WM; ++a)
 #pragma unroll
     for (int b = 0; b < WN; ++b)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) acc[a][b][e] = 0.f;
+      for (int h = 0; h < CH; ++h)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[a][b][h][e] = 0.f;
 
-  const int nk = (K + BK - 1) / BK;
-  load(0);
-  store(0);
-  __syncthreads();
-  for (int c = 0; c < nk; ++c) {
-    const int buf = c & 1;
-    if (c + 1 < nk) load(c + 1);
+  auto compute = [&](int buf) {
     const float* pa = &sA[buf][(wm * 32 * WM + ln) * SA + 4 * hh];
     const float* pb = &sB[buf][(4 * hh) * SB + wn * 32 * WN + ln];
+    constexpr int GPW = BK / 8 / KW;  // groups of 8 k per wave and chunk
 #pragma unroll
-    for (int g = 0; g < BK / 8; ++g) {
+    for (int g = kg * GPW; g < (kg + 1) * GPW; ++g) {
       f32x4 af[WM];
       float bf[WN][4];
 #pragma unroll
@@ -210,22 +222,64 @@ __global__ __launch_bounds__(256) void linear_mfma_kernel(const float* __restric
         for (int a = 0; a < WM; ++a)
 #pragma unroll
           for (int b = 0; b < WN; ++b)
-            acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[a][i], bf[b][i], acc[a][b], 0, 0, 0);
+            acc[a][b][i % CH] =
+                __builtin_amdgcn_mfma_f32_32x32x2f32(af[a][i], bf[b][i], acc[a][b][i % CH], 0, 0, 0);
     }
-    if (c + 1 < nk) store(buf ^ 1);
-    __syncthreads();
+  };
+
+  // Chunk j travels in register set j % PF: chunks 0..PF-1 are requested up
+  // front, and each iteration refills the set it has just written to LDS
+  // with the chunk PF further on.
+  const int nk = (K + BK - 1) / BK;
+#pragma unroll
+  for (int st = 0; st < PF; ++st)
+    if (st < nk) load(st, st);
+  store(0, 0);
+  if (PF < nk) load(PF, 0);
+  __syncthreads();
+  for (int c0 = 0; c0 < nk; c0 += PF) {
+#pragma unroll
+    for (int q = 0; q < PF; ++q) {
+      const int c = c0 + q;
+      if (c < nk) {
+        compute(c & 1);
+        const int st = (q + 1) % PF;
+        if (c + 1 < nk) store((c + 1) & 1, st);
+        if (c + 1 + PF < nk) load(c + 1 + PF, st);
+        __syncthreads();
+      }
+    }
   }
 
+  float* red = sA[0];  // KW = 2: the upper waves' sums, [wave][a][b][e][lane]
+  if (KW == 2 && kg == 1) {
+#pragma unroll
+    for (int a = 0; a < WM; ++a)
+#pragma unroll
+      for (int b = 0; b < WN; ++b)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          float v = acc[a][b][0][e];
+#pragma unroll
+          for (int h = 1; h < CH; ++h) v += acc[a][b][h][e];
+          red[((((wave & 3) * WM + a) * WN + b) * 16 + e) * 64 + lane] = v;
+        }
+  }
+  if (KW == 2) __syncthreads();
+  if (kg == 1) return;
 #pragma unroll
   for (int a = 0; a < WM; ++a)
 #pragma unroll
     for (int b = 0; b < WN; ++b) {
       const int n = n0 + wn * 32 * WN + b * 32 + ln;
-      if (n >= T) continue;
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const int m = m0 + wm * 32 * WM + a * 32 + 8 * (e >> 2) + 4 * hh + (e & 3);
-        if (m < M) y[(size_t)m * T + n] = acc[a][b][e];
+        float v = acc[a][b][0][e];
+#pragma unroll
+        for (int h = 1; h < CH; ++h) v += acc[a][b][h][e];
+        if (KW == 2) v += red[(((wave * WM + a) * WN + b) * 16 + e) * 64 + lane];
+        if (m < M && n < T) y[(size_t)m * T + n] = v;
       }
     }
 }
@@ -266,11 +320,11 @@ hipError_t linear_col_launch(float* y, const float* x, const float* w, int K, in
       else hipLaunchKernelGGL((linear_gemv_kernel<4, false>), grid, block, 0, stream, w, x, y, M, K);
     }
   } else if (p.tile == 128) {
-    if (p.vec) hipLaunchKernelGGL((linear_mfma_kernel<2, 2, true>), grid, block, 0, stream, w, x, y, M, K, T);
-    else hipLaunchKernelGGL((linear_mfma_kernel<2, 2, false>), grid, block, 0, stream, w, x, y, M, K, T);
+    if (p.vec) hipLaunchKernelGGL((linear_mfma_kernel<2, 2, 32, 1, true>), grid, block, 0, stream, w, x, y, M, K, T);
+    else hipLaunchKernelGGL((linear_mfma_kernel<2, 2, 32, 1, false>), grid, block, 0, stream, w, x, y, M, K, T);
   } else {
-    if (p.vec) hipLaunchKernelGGL((linear_mfma_kernel<1, 1, true>), grid, block, 0, stream, w, x, y, M, K, T);
-    else hipLaunchKernelGGL((linear_mfma_kernel<1, 1, false>), grid, block, 0, stream, w, x, y, M, K, T);
+    if (p.vec) hipLaunchKernelGGL((linear_mfma_kernel<1, 1, 64, 2, true>), grid, dim3(512), 0, stream, w, x, y, M, K, T);
+    else hipLaunchKernelGGL((linear_mfma_kernel<1, 1, 64, 2, false>), grid, dim3(512), 0, stream, w, x, y, M, K, T);
   }
   return hipGetLastError();
 }
