@@ -29,6 +29,8 @@ Extra objects on the same JSON line:
   linear: hl_gpu_linear_col (the gpuLinearCol drop-in, fp32) at the
     projection shapes around attention: decode GEMV GB/s (weights from HBM)
     and prefill GEMM TFLOP/s against the fp32 peak.
+  decode_ends: greedy argmax over the logits (hl_argmax_async / hl_gpu_argmax)
+    and the token embedding (hl_gpu_embedding), the ends of a decode step.
   cpu_baseline: the C oracle (single-threaded scalar fp32 restatement of the
     reference's tensor.nim math) timed on this host on a bounded sample.
 """
@@ -307,6 +309,45 @@ def bench_linear(torch, A):
     return out
 
 
+def bench_ends(torch, A):
+    """The decode step's ends: greedy argmax over a vocabulary of logits
+    (hl_argmax_async, result left on the device as in a captured decode loop;
+    hl_gpu_argmax adds a device-to-host copy and a stream wait) and the token
+    embedding lookup (one token; a 4096-token prefill)."""
+    out = {}
+    g = torch.Generator(device="cuda").manual_seed(17)
+    res = torch.empty(1, dtype=torch.int32, device="cuda")
+    for name, n in (("argmax_llama3_vocab", 128256), ("argmax_qwen3_vocab", 151936)):
+        xs = [torch.randn(n, generator=g, device="cuda") for _ in range(64)]
+        A.argmax_async(xs[0], n, res)
+        ms = graph_time_ms(torch, lambda i: A.argmax_async(xs[i % 64], n, res), 64, 4)
+        t0 = time.perf_counter()
+        for i in range(50):
+            A.gpu_argmax(xs[i % 64], n)
+        host_ms = (time.perf_counter() - t0) / 50 * 1e3
+        out[name] = {"n": n, "us": round(ms * 1e3, 3), "unit": "GB/s",
+                     "value": round(n * 4 / (ms * 1e-3) / 1e9, 1),
+                     "with_host_result_us": round(host_ms * 1e3, 1)}
+        log(f"{name}: {ms*1e3:.2f} us in a graph, {host_ms*1e3:.1f} us with the host result")
+        del xs
+    for name, n_emb, n_tok in (("embedding_decode_llama8b", 4096, 1),
+                               ("embedding_prefill_llama8b_t4096", 4096, 4096)):
+        n_vocab = 128256
+        w = torch.randn(n_vocab, n_emb, generator=g, device="cuda")
+        toks = [torch.randint(0, n_vocab, (n_tok,), generator=g, device="cuda",
+                              dtype=torch.int32) for _ in range(16)]
+        o = torch.empty(n_emb, n_tok, device="cuda")
+        ms = graph_time_ms(torch, lambda i: A.gpu_embedding(o, w, toks[i % 16], n_emb, n_tok,
+                                                            n_vocab), 16, 4)
+        nbytes = 2 * n_emb * n_tok * 4
+        out[name] = {"n_emb": n_emb, "n_tokens": n_tok, "us": round(ms * 1e3, 3), "unit": "GB/s",
+                     "value": round(nbytes / (ms * 1e-3) / 1e9, 1)}
+        log(f"{name}: {ms*1e3:.2f} us")
+        del w
+    torch.cuda.empty_cache()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -488,6 +529,7 @@ def main():
 
     if args.only in ("all", "linear"):
         result["linear"] = bench_linear(torch, A)
+        result["decode_ends"] = bench_ends(torch, A)
 
     if not args.no_cpu:
         log("cpu baseline ...")

@@ -115,6 +115,24 @@ def gpu_linear_col(dst, x, w, w_cols, w_rows, seq_len, stream=None):
                                         _stream(stream)))
 
 
+def gpu_argmax(logits, n_vocab, stream=None) -> int:
+    """gpuArgmax (naive.nim:2105-2127): greedy token index (waits for the stream)."""
+    out = ctypes.c_int32(0)
+    check(_lib.load().hl_gpu_argmax(_p(logits), n_vocab, ctypes.byref(out), _stream(stream)))
+    return out.value
+
+
+def argmax_async(logits, n_vocab, result, stream=None) -> None:
+    """Greedy token index into result (an int32 device tensor), no host wait."""
+    check(_lib.load().hl_argmax_async(_p(logits), n_vocab, _p(result), _stream(stream)))
+
+
+def gpu_embedding(dst, weight, token_ids, n_emb, n_tokens, n_vocab, stream=None):
+    """gpuEmbedding (naive.nim:2975-3001): dst[nEmb, nTokens] = weight rows of the tokens."""
+    check(_lib.load().hl_gpu_embedding(_p(dst), _p(weight), _p(token_ids), n_emb, n_tokens,
+                                       n_vocab, _stream(stream)))
+
+
 def set_rope_theta(rope_dim: int, rope_base: float) -> None:
     """Installs the theta table (naive.nim:3850-3861) used by the *_theta procs."""
     check(_lib.load().hl_set_rope_theta(rope_dim, rope_base))

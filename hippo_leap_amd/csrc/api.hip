@@ -51,6 +51,7 @@ struct DevWs {
   size_t zero_prefix = 0;  // leading bytes known to hold zero arrival counters
 };
 std::vector<DevWs> g_ws;
+std::vector<void*> g_argmax_ws;  // per device, kArgmaxScratchBytes, counter zero between calls
 
 void build_theta(ThetaTable& t, int rope_dim, float base) {
   memset(&t, 0, sizeof(t));
@@ -782,6 +783,61 @@ int hl_gpu_linear_col(float* dst, const float* x, const float* w, int w_cols, in
     return fail(HL_EINVAL, "linear_col: dst overlaps x or w");
   hipError_t e = linear_col_launch(dst, x, w, w_cols, w_rows, seq_len, as_stream(stream));
   return e == hipSuccess ? HL_OK : hip_fail(e, "linear_col launch");
+}
+
+// Library-owned argmax scratch of the current device (allocated and zeroed
+// on the first call on that device).
+static int argmax_scratch(unsigned int** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  std::lock_guard<std::mutex> lk(g_mu);
+  if ((int)g_argmax_ws.size() <= dev) g_argmax_ws.resize(dev + 1, nullptr);
+  if (!g_argmax_ws[dev]) {
+    void* p = nullptr;
+    e = hipMalloc(&p, kArgmaxScratchBytes);
+    if (e != hipSuccess) return hip_fail(e, "hipMalloc(argmax scratch)");
+    e = hipMemset(p, 0, kArgmaxScratchBytes);
+    if (e != hipSuccess) return hip_fail(e, "hipMemset(argmax scratch)");
+    g_argmax_ws[dev] = p;
+  }
+  *out = (unsigned int*)g_argmax_ws[dev];
+  return HL_OK;
+}
+
+int hl_argmax_async(const float* logits, int n_vocab, int32_t* result_dev, void* stream) {
+  if (!logits || !result_dev) return fail(HL_EINVAL, "argmax: null pointer");
+  if (n_vocab < 0) return fail(HL_EINVAL, "argmax: n_vocab %d < 0", n_vocab);
+  unsigned int* scratch = nullptr;
+  int rc = argmax_scratch(&scratch);
+  if (rc) return rc;
+  hipError_t e = argmax_launch(logits, n_vocab, scratch, result_dev, as_stream(stream));
+  return e == hipSuccess ? HL_OK : hip_fail(e, "argmax launch");
+}
+
+int hl_gpu_argmax(const float* logits, int n_vocab, int32_t* result, void* stream) {
+  if (!logits || !result) return fail(HL_EINVAL, "argmax: null pointer");
+  if (n_vocab < 0) return fail(HL_EINVAL, "argmax: n_vocab %d < 0", n_vocab);
+  unsigned int* scratch = nullptr;
+  int rc = argmax_scratch(&scratch);
+  if (rc) return rc;
+  int* slot = (int*)((char*)scratch + kArgmaxScratchBytes - 8);
+  hipError_t e = argmax_launch(logits, n_vocab, scratch, slot, as_stream(stream));
+  if (e != hipSuccess) return hip_fail(e, "argmax launch");
+  e = hipMemcpyAsync(result, slot, sizeof(int32_t), hipMemcpyDeviceToHost, as_stream(stream));
+  if (e != hipSuccess) return hip_fail(e, "argmax copy");
+  e = hipStreamSynchronize(as_stream(stream));
+  return e == hipSuccess ? HL_OK : hip_fail(e, "argmax sync");
+}
+
+int hl_gpu_embedding(float* dst, const float* weight, const int32_t* token_ids, int n_emb,
+                     int n_tokens, int n_vocab, void* stream) {
+  if (!dst || !weight || !token_ids) return fail(HL_EINVAL, "embedding: null pointer");
+  if (n_emb <= 0 || n_tokens <= 0 || n_vocab <= 0)
+    return fail(HL_EINVAL, "embedding: bad shape (n_emb=%d, n_tokens=%d, n_vocab=%d)", n_emb,
+                n_tokens, n_vocab);
+  hipError_t e = embedding_launch(dst, weight, token_ids, n_emb, n_tokens, n_vocab, as_stream(stream));
+  return e == hipSuccess ? HL_OK : hip_fail(e, "embedding launch");
 }
 
 int hl_kv_cache_to_f32(float* dst, const void* cache, int kv_dtype, int rows, int max_len, int col0,

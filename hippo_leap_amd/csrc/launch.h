@@ -144,4 +144,15 @@ LinearPlan linear_plan(int M, int K, int T, const float* w, const float* x);
 hipError_t linear_col_launch(float* y, const float* x, const float* w, int K, int M, int T,
                              hipStream_t stream);
 
+// ---- decode-step ends: argmax and embedding (tokens.hip) -------------------
+constexpr int kArgmaxMaxGroups = 256;
+// Scratch: an 8-byte arrival counter (zero between calls), one 8-byte key
+// per workgroup, then the 4-byte result slot used by the host-result entry.
+constexpr size_t kArgmaxScratchBytes = 8 + 8 * kArgmaxMaxGroups + 8;
+int argmax_grid(int n);
+hipError_t argmax_launch(const float* x, int n, unsigned int* scratch, int* result,
+                         hipStream_t stream);
+hipError_t embedding_launch(float* out, const float* w, const int* tok, int n_emb, int n_tok,
+                            int n_vocab, hipStream_t stream);
+
 }  // namespace hl

@@ -176,6 +176,32 @@ int hl_gpu_attention_prefill(float* dst, const float* q, const float* k,
 int hl_gpu_linear_col(float* dst, const float* x, const float* w, int w_cols,
                       int w_rows, int seq_len, void* stream);
 
+/* gpuArgmax (naive.nim:2105-2127): index of the greedy token over
+ * logits[nVocab] (fp32, device), written to *result (host) after the stream
+ * has finished, as the reference returns it after gpuStreamSync.  Same
+ * result as the reference's two-pass kernel (naive.nim:1922-2103) on every
+ * input, ties included: among equal maxima at i = 65536r + 256b + t the
+ * smallest (bitrev8(b), bitrev8(t), r) wins, which is where the reference's
+ * 256x256-thread reduction tree puts them; NaN and values <= -3.4e38 are
+ * never chosen; -1 if nothing is.  Uses a
+ * small library-owned scratch per device: concurrent calls on one device
+ * must be serialised (the reference's module-global scratch, likewise).  */
+int hl_gpu_argmax(const float* logits, int n_vocab, int32_t* result,
+                  void* stream);
+
+/* As hl_gpu_argmax, but the index goes to result_dev (device memory) and
+ * nothing waits for the stream (for graph capture and pipelined decode).
+ * Extends the reference.                                                  */
+int hl_argmax_async(const float* logits, int n_vocab, int32_t* result_dev,
+                    void* stream);
+
+/* gpuEmbedding (naive.nim:2975-3001): dst[e*nTokens + t] =
+ * weight[tokenIds[t]*nEmb + e] for e < nEmb, t < nTokens (fp32; token ids
+ * in device memory).  A token id outside [0, nVocab) gives a NaN column
+ * (the reference reads out of bounds).                                    */
+int hl_gpu_embedding(float* dst, const float* weight, const int32_t* token_ids,
+                     int n_emb, int n_tokens, int n_vocab, void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* Batched / typed API (extends the reference: B sequences, fp16/bf16 KV)   */
 /* ------------------------------------------------------------------------ */

@@ -60,6 +60,8 @@ def lib() -> ctypes.CDLL:
             "orc_qk_norm_cols": (None, [_fp, _fp, _i, _i, _i, _f]),
             "orc_store_kv": (None, [ctypes.c_void_p, _i, _fp, _i, _i, _i, _i]),
             "orc_attention_decode": (None, [_fp, _fp, _fp, _fp, _i, _i, _i, _i, _i, _f, _fp]),
+            "orc_argmax": (_i, [_fp, _ll]),
+            "orc_embedding": (None, [_fp, ctypes.POINTER(_i), _fp, _i, _i]),
             "orc_attention_prefill": (None, [_fp, _fp, _fp, _fp, _i, _i, _i, _i, _f, _i, _i, _i,
                                              _i, _i, _fp]),
         }
@@ -228,4 +230,21 @@ def attention_prefill(q: np.ndarray, k: np.ndarray, v: np.ndarray, n_head: int, 
     r0, r1, rs = rows if rows is not None else (0, T, 1)
     lib().orc_attention_prefill(_ptr(q), _ptr(k), _ptr(v), _ptr(out), n_head, n_head_kv, head_dim,
                                 T, float(s), h0, h1, r0, r1, rs, _ptr(scores))
+    return out
+
+
+# ---- decode-step ends (naive.nim) ----------------------------------------------
+def argmax(x: np.ndarray) -> int:
+    """gpuArgmax's result (naive.nim:1922-2127), reduction tree and all."""
+    x = _f32(x).reshape(-1)
+    return lib().orc_argmax(_ptr(x), x.size)
+
+
+def embedding(w: np.ndarray, tokens, n_emb: int) -> np.ndarray:
+    """gpuEmbedding (naive.nim:2975-3001): col-major [n_emb, n_tokens]."""
+    w = _f32(w).reshape(-1)
+    tok = np.ascontiguousarray(tokens, dtype=np.int32)
+    out = np.empty((n_emb, tok.size), np.float32)
+    lib().orc_embedding(_ptr(w), tok.ctypes.data_as(ctypes.POINTER(_i)), _ptr(out), n_emb,
+                        tok.size)
     return out

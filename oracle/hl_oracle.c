@@ -23,6 +23,8 @@
  *   :3850-3861             theta table powf(1/base, 2i/ropeDim) in fp32
  *   :3565-3567, 3239       cache layout [kvDim, maxLen], column = position
  *   :4066-4074             qkNorm before RoPE
+ *   :1922-2127             argmax (two-pass reduction, its tie order)
+ *   :2975-3001             token embedding lookup
  *
  * Every routine is single-threaded scalar fp32 code (built -O2, no
  * fast-math), like the reference's CPU path.  fp16/bf16 inputs enter as
@@ -33,6 +35,9 @@
  *   attention decode/prefill: fp64 brute force + closed forms + torch
  *   scaled_dot_product_attention (fp64) through the golden fixtures.
  *   halfToFloat: the reference KAT tests/test_quant.nim:5-15.
+ *   argmax: numpy argmax on tie-free inputs, hand-derived tie winners of
+ *   the reduction tree, NaN / -inf / all-invalid cases.
+ *   embedding: numpy fancy indexing.
  *   f32->f16/bf16 RNE: numpy / torch conversions (exhaustive over a sweep).
  *   Device transcendental functions of the reference (hippo's expf, powf,
  *   cosf, sinf) are not pinned by any reference test: parity unpinned at
@@ -368,4 +373,69 @@ void orc_attention_prefill(const float* Q, const float* K, const float* V, float
       }
     }
   }
+}
+
+/* ---------------------------------------------------------------------- */
+/* Decode-step ends (backends/naive.nim)                                  */
+/* ---------------------------------------------------------------------- */
+
+/* One 256-thread block reduction of argmaxPass1Kernel / argmaxPass2Kernel
+ * (naive.nim:1942-1977, 2009-2044) on (val[256], idx[256]): the LDS steps
+ * 128 and 64, then wave64 shuffle-downs 32..1, each replacing only on a
+ * strictly greater value; lanes whose source is past lane 63 keep their own
+ * value (shuffle-down semantics).  Returns lane 0's (value, index). */
+static void orc_argmax_block(float* sv, int* si, float* out_v, int* out_i) {
+  for (int t = 0; t < 128; ++t)
+    if (sv[t + 128] > sv[t]) { sv[t] = sv[t + 128]; si[t] = si[t + 128]; }
+  for (int t = 0; t < 64; ++t)
+    if (sv[t + 64] > sv[t]) { sv[t] = sv[t + 64]; si[t] = si[t + 64]; }
+  for (int off = 32; off >= 1; off >>= 1) {
+    float nv[64];
+    int ni[64];
+    for (int l = 0; l < 64; ++l) {
+      float ov = l + off < 64 ? sv[l + off] : sv[l];
+      int oi = l + off < 64 ? si[l + off] : si[l];
+      nv[l] = sv[l];
+      ni[l] = si[l];
+      if (ov > nv[l]) { nv[l] = ov; ni[l] = oi; }
+    }
+    memcpy(sv, nv, sizeof(nv));
+    memcpy(si, ni, sizeof(ni));
+  }
+  *out_v = sv[0];
+  *out_i = si[0];
+}
+
+/* gpuArgmax (naive.nim:2105-2127) with the reference's geometry
+ * (ArgmaxGridBlocks = 256 blocks of 256 threads, naive.nim:2092):
+ * pass 1 (naive.nim:1922-1977): thread (b, t) scans i = b*256 + t, then
+ * i += 65536, keeping the first strictly greater value from -3.4e38 and
+ * index -1; each block reduces to (value, index).  Pass 2
+ * (naive.nim:1999-2044): one block reduces the 256 block results. */
+int orc_argmax(const float* x, int64_t n) {
+  static float bv[256], sv[256];
+  static int bi[256], si[256];
+  for (int b = 0; b < 256; ++b) {
+    for (int t = 0; t < 256; ++t) {
+      float v = -3.4e38f;
+      int idx = -1;
+      for (int64_t i = (int64_t)b * 256 + t; i < n; i += 65536)
+        if (x[i] > v) { v = x[i]; idx = (int)i; }
+      sv[t] = v;
+      si[t] = idx;
+    }
+    orc_argmax_block(sv, si, &bv[b], &bi[b]);
+  }
+  float v;
+  int idx;
+  orc_argmax_block(bv, bi, &v, &idx);
+  return idx;
+}
+
+/* gpuEmbedding (naive.nim:2975-3001): out[e*nTokens + t] =
+ * w[tok[t]*nEmb + e]; fp32 copy, token ids assumed in range. */
+void orc_embedding(const float* w, const int* tok, float* out, int n_emb, int n_tokens) {
+  for (int e = 0; e < n_emb; ++e)
+    for (int t = 0; t < n_tokens; ++t)
+      out[(int64_t)e * n_tokens + t] = w[(int64_t)tok[t] * n_emb + e];
 }

@@ -247,3 +247,12 @@ def test_linear_col_validation(hl):
     assert hl.hl_gpu_linear_col(F, F + 64 * 8 * 4 - 4, F + (1 << 25), 64, 64, 8, None) == _lib.HL_EINVAL
     assert hl.hl_gpu_linear_col(F + 4096, F + (1 << 24), F, 64, 64, 1, None) == _lib.HL_EINVAL
     assert b"overlaps" in hl.hl_last_error()
+
+
+def test_argmax_embedding_validation(hl):
+    out = ctypes.c_int32(0)
+    assert hl.hl_gpu_argmax(None, 10, ctypes.byref(out), None) == _lib.HL_EINVAL
+    assert hl.hl_gpu_argmax(FAKE, -1, ctypes.byref(out), None) == _lib.HL_EINVAL
+    assert hl.hl_argmax_async(FAKE, 10, None, None) == _lib.HL_EINVAL
+    assert hl.hl_gpu_embedding(FAKE, FAKE, FAKE, 0, 1, 10, None) == _lib.HL_EINVAL
+    assert hl.hl_gpu_embedding(FAKE, None, FAKE, 64, 1, 10, None) == _lib.HL_EINVAL

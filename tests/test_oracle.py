@@ -285,3 +285,66 @@ def test_decode_fp64_brute_force(orc):
             s = q.reshape(hq, d)[h].astype(np.float64) @ K[kv, :, :L] / np.sqrt(d)
             p = np.exp(s - s.max())
             assert rel_err(out[h], V[kv, :, :L] @ (p / p.sum())) < 1e-5
+
+
+# ---------------------------------------------------------------------------
+# decode-step ends: argmax (naive.nim:1922-2127), embedding (:2975-3001)
+# ---------------------------------------------------------------------------
+def _bitrev8(v):
+    return int(f"{v:08b}"[::-1], 2)
+
+
+def _argmax_closed_form(x):
+    """Winner implied by the reference's reduction tree: among the maxima of
+    the values > -3.4e38, the smallest (bitrev8(b), bitrev8(t), r) for
+    i = 65536 r + 256 b + t; -1 when no value qualifies."""
+    x = np.asarray(x, np.float32)
+    ok = x > np.float32(-3.4e38)
+    if not ok.any():
+        return -1
+    m = x[ok].max()
+    cand = np.nonzero(ok & (x == m))[0]
+    return int(min(cand, key=lambda i: (_bitrev8((i >> 8) & 255), _bitrev8(i & 255), i >> 16)))
+
+
+def test_argmax_tie_free_matches_numpy(orc):
+    for n, seed in ((1, 1), (7, 2), (300, 3), (65536, 4), (128256, 5), (152064, 6)):
+        x = orc.normal(n, 3400 + seed)
+        assert orc.argmax(x) == int(np.argmax(x))
+
+
+@pytest.mark.parametrize("n,levels,seed", [(200000, 3, 1), (70000, 2, 2), (131072, 1, 3),
+                                           (1000, 2, 4), (65537, 1, 5)])
+def test_argmax_ties_follow_the_reduction_tree(orc, n, levels, seed):
+    """Tie-heavy inputs (values drawn from `levels` integers): the literal
+    simulation of the two-pass kernel agrees with the tie order derived
+    from its merge structure."""
+    rng = np.random.default_rng(seed)
+    x = rng.integers(0, levels, n).astype(np.float32)
+    assert orc.argmax(x) == _argmax_closed_form(x)
+
+
+def test_argmax_hand_cases(orc):
+    x = np.zeros(300, np.float32)
+    # all equal: bitrev8 favours even thread indices; thread 0 of block 0 is index 0
+    assert orc.argmax(x) == 0
+    x = np.full(300, -1.0, np.float32)
+    x[[5, 260, 129]] = 2.0        # i=129: b=0, t=129 (bitrev 0b10000001); i=5: t=5 (0b10100000)
+    assert orc.argmax(x) == 129  # t=129 -> bitrev 129; t=5 -> bitrev 160; i=260: b=1 -> bitrev 128 > 0
+    x = np.full(70000, 0.0, np.float32)
+    x[0] = -1.0                  # index 0 loses; 65536 shares slot 0 (r = 1) and wins over slot 1
+    assert orc.argmax(x) == 65536
+    # NaN and values <= -3.4e38 are never chosen; all of them -> -1
+    assert orc.argmax(np.array([np.nan, -np.inf, -3.4e38, 1.0], np.float32)) == 3
+    assert orc.argmax(np.array([np.nan, -np.inf, -3.4e38], np.float32)) == -1
+    assert orc.argmax(np.zeros(0, np.float32)) == -1
+    # -0.0 and +0.0 are equal to the reference's >: the tree order decides
+    assert orc.argmax(np.array([-0.0, 0.0], np.float32)) == 0
+
+
+def test_embedding_matches_indexing(orc):
+    n_vocab, n_emb = 50, 24
+    w = orc.normal(n_vocab * n_emb, 3500).reshape(n_vocab, n_emb)
+    tok = np.array([3, 0, 49, 3, 17], np.int32)
+    out = orc.embedding(w, tok, n_emb)
+    assert np.array_equal(out, w[tok].T)
