@@ -99,6 +99,9 @@ SIGNATURES = {
     "hl_gpu_attention_prefill": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int,
                                          c_int, c_void_p]),
     "hl_gpu_linear_col": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_void_p]),
+    "hl_gpu_rmsnorm_cols": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_float, c_void_p]),
+    "hl_gpu_residual_rmsnorm": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_float,
+                                        c_void_p]),
     "hl_gpu_argmax": (c_int, [c_void_p, c_int, ctypes.POINTER(ctypes.c_int32), c_void_p]),
     "hl_argmax_async": (c_int, [c_void_p, c_int, c_void_p, c_void_p]),
     "hl_gpu_embedding": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_void_p]),

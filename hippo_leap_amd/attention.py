@@ -115,6 +115,18 @@ def gpu_linear_col(dst, x, w, w_cols, w_rows, seq_len, stream=None):
                                         _stream(stream)))
 
 
+def gpu_rmsnorm_cols(dst, x, weight, dim, seq_len, eps, stream=None):
+    """gpuRmsnormCols (naive.nim:2834-2843) on col-major [dim, seq_len] fp32."""
+    check(_lib.load().hl_gpu_rmsnorm_cols(_p(dst), _p(x), _p(weight), dim, seq_len, eps,
+                                          _stream(stream)))
+
+
+def gpu_residual_rmsnorm(norm_out, x, residual, weight, dim, eps, stream=None):
+    """gpuResidualRmsnorm (naive.nim:2874-2882): x += residual; norm_out = rmsnorm(x) * w."""
+    check(_lib.load().hl_gpu_residual_rmsnorm(_p(norm_out), _p(x), _p(residual), _p(weight), dim,
+                                              eps, _stream(stream)))
+
+
 def gpu_argmax(logits, n_vocab, stream=None) -> int:
     """gpuArgmax (naive.nim:2105-2127): greedy token index (waits for the stream)."""
     out = ctypes.c_int32(0)

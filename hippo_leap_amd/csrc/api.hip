@@ -785,6 +785,31 @@ int hl_gpu_linear_col(float* dst, const float* x, const float* w, int w_cols, in
   return e == hipSuccess ? HL_OK : hip_fail(e, "linear_col launch");
 }
 
+int hl_gpu_rmsnorm_cols(float* dst, const float* x, const float* weight, int dim, int seq_len,
+                        float eps, void* stream) {
+  if (!dst || !x || !weight) return fail(HL_EINVAL, "rmsnorm_cols: null pointer");
+  if (dim <= 0 || seq_len <= 0)
+    return fail(HL_EINVAL, "rmsnorm_cols: bad shape (dim=%d, seq_len=%d)", dim, seq_len);
+  if (!(eps >= 0.f)) return fail(HL_EINVAL, "rmsnorm_cols: eps must be >= 0");
+  const size_t bytes = (size_t)dim * seq_len * 4;
+  if (dst != x && overlaps(dst, bytes, x, bytes))
+    return fail(HL_EINVAL, "rmsnorm_cols: dst partially overlaps x");
+  hipError_t e = rmsnorm_cols_launch(dst, x, weight, dim, seq_len, eps, as_stream(stream));
+  return e == hipSuccess ? HL_OK : hip_fail(e, "rmsnorm_cols launch");
+}
+
+int hl_gpu_residual_rmsnorm(float* norm_out, float* x, const float* residual, const float* weight,
+                            int dim, float eps, void* stream) {
+  if (!norm_out || !x || !residual || !weight)
+    return fail(HL_EINVAL, "residual_rmsnorm: null pointer");
+  if (dim <= 0) return fail(HL_EINVAL, "residual_rmsnorm: bad dim %d", dim);
+  if (!(eps >= 0.f)) return fail(HL_EINVAL, "residual_rmsnorm: eps must be >= 0");
+  if (overlaps(norm_out, (size_t)dim * 4, x, (size_t)dim * 4))
+    return fail(HL_EINVAL, "residual_rmsnorm: norm_out overlaps x");
+  hipError_t e = residual_rmsnorm_launch(norm_out, x, residual, weight, dim, eps, as_stream(stream));
+  return e == hipSuccess ? HL_OK : hip_fail(e, "residual_rmsnorm launch");
+}
+
 // Library-owned argmax scratch of the current device (allocated and zeroed
 // on the first call on that device).
 static int argmax_scratch(unsigned int** out) {

@@ -144,6 +144,12 @@ LinearPlan linear_plan(int M, int K, int T, const float* w, const float* x);
 hipError_t linear_col_launch(float* y, const float* x, const float* w, int K, int M, int T,
                              hipStream_t stream);
 
+// ---- RMSNorm of the hidden state (norm.hip) --------------------------------
+hipError_t rmsnorm_cols_launch(float* out, const float* x, const float* w, int dim, int seq,
+                               float eps, hipStream_t stream);
+hipError_t residual_rmsnorm_launch(float* out, float* x, const float* res, const float* w, int dim,
+                                   float eps, hipStream_t stream);
+
 // ---- decode-step ends: argmax and embedding (tokens.hip) -------------------
 constexpr int kArgmaxMaxGroups = 256;
 // Scratch: an 8-byte arrival counter (zero between calls), one 8-byte key

@@ -176,6 +176,20 @@ int hl_gpu_attention_prefill(float* dst, const float* q, const float* k,
 int hl_gpu_linear_col(float* dst, const float* x, const float* w, int w_cols,
                       int w_rows, int seq_len, void* stream);
 
+/* gpuRmsnormCols (naive.nim:2834-2843): dst[r, t] = x[r, t] *
+ * (1/sqrtf(sum_r x[r, t]^2 / dim + eps)) * weight[r] over the col-major
+ * fp32 [dim, seqLen] (the norm in front of the Q/K/V projections and the
+ * final norm before the logits).  dst may equal x.                        */
+int hl_gpu_rmsnorm_cols(float* dst, const float* x, const float* weight,
+                        int dim, int seq_len, float eps, void* stream);
+
+/* gpuResidualRmsnorm (naive.nim:2874-2882): x[r] += residual[r] in place,
+ * then norm_out[r] = x[r] * (1/sqrtf(sum x^2 / dim + eps)) * weight[r]
+ * (one vector, the end of a decode layer).  norm_out must not overlap x.  */
+int hl_gpu_residual_rmsnorm(float* norm_out, float* x, const float* residual,
+                            const float* weight, int dim, float eps,
+                            void* stream);
+
 /* gpuArgmax (naive.nim:2105-2127): index of the greedy token over
  * logits[nVocab] (fp32, device), written to *result (host) after the stream
  * has finished, as the reference returns it after gpuStreamSync.  Same

@@ -256,3 +256,11 @@ def test_argmax_embedding_validation(hl):
     assert hl.hl_argmax_async(FAKE, 10, None, None) == _lib.HL_EINVAL
     assert hl.hl_gpu_embedding(FAKE, FAKE, FAKE, 0, 1, 10, None) == _lib.HL_EINVAL
     assert hl.hl_gpu_embedding(FAKE, None, FAKE, 64, 1, 10, None) == _lib.HL_EINVAL
+
+
+def test_rmsnorm_validation(hl):
+    assert hl.hl_gpu_rmsnorm_cols(FAKE, FAKE, None, 64, 1, 1e-5, None) == _lib.HL_EINVAL
+    assert hl.hl_gpu_rmsnorm_cols(FAKE, FAKE, FAKE, 0, 1, 1e-5, None) == _lib.HL_EINVAL
+    assert hl.hl_gpu_rmsnorm_cols(FAKE + 4, FAKE, FAKE + (1 << 24), 64, 2, 1e-5, None) == _lib.HL_EINVAL
+    assert hl.hl_gpu_residual_rmsnorm(FAKE, FAKE + 64, FAKE + 4096, FAKE + 8192, 64, 1e-6,
+                                      None) == _lib.HL_EINVAL
