@@ -25,10 +25,11 @@ import ctypes
 import torch
 
 from . import _lib
-from ._lib import (HL_BF16, HL_F16, HL_F32, HL_KV_COLMAJOR, HL_KV_TILED32, HL_ROPE_HALF_SPLIT,
+from ._lib import (HL_BF16, HL_F16, HL_F32, HL_FP8, HL_KV_COLMAJOR, HL_KV_TILED32, HL_ROPE_HALF_SPLIT,
                    DecodeArgs, PrefillArgs, RopeStoreArgs, check)
 
-_DT = {torch.float32: HL_F32, torch.float16: HL_F16, torch.bfloat16: HL_BF16}
+_DT = {torch.float32: HL_F32, torch.float16: HL_F16, torch.bfloat16: HL_BF16,
+       torch.float8_e4m3fn: HL_FP8, torch.uint8: HL_FP8}
 
 
 def dtype_code(t: torch.Tensor) -> int:

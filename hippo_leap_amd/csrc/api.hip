@@ -75,6 +75,11 @@ int check_dtype(int dt, const char* what) {
   return HL_OK;
 }
 
+// KV caches may also be fp8 (tiled layout only, checked with the layout).
+int check_kv_dtype(int dt, const char* what) {
+  return dt == HL_FP8 ? HL_OK : check_dtype(dt, what);
+}
+
 int check_rope(int head_dim, int rope_dim, int style) {
   if (rope_dim <= 0 || rope_dim > head_dim || (rope_dim & 1) || rope_dim > HL_MAX_ROPE_DIM)
     return fail(HL_EINVAL, "rope_dim %d must be even and in [2, head_dim=%d]", rope_dim, head_dim);
@@ -341,13 +346,17 @@ int hl_gpu_store_kv_pair(float* k_cache, const float* k_src, float* v_cache, con
 // ---------------------------------------------------------------------------
 // KV-cache layout
 // ---------------------------------------------------------------------------
-// Tiled caches are read with 16-byte loads of whole 32-column tile rows:
-// fp16/bf16, whole tiles (max_len % 32), aligned sequences and caches.
+// Tiled caches are read with vector loads of whole 32-column tile rows:
+// fp16/bf16/fp8, whole tiles (max_len % 32), aligned sequences and caches.
+// fp8 caches exist only in the tiled layout.
 static int check_layout(int layout, int kv_dtype, int max_len, long long stride, const void* kc,
                         const void* vc, const char* who) {
-  if (layout == HL_KV_COLMAJOR) return HL_OK;
+  if (layout == HL_KV_COLMAJOR) {
+    if (kv_dtype == HL_FP8) return fail(HL_EUNSUPPORTED, "%s: fp8 KV caches need the tiled layout", who);
+    return HL_OK;
+  }
   if (layout != HL_KV_TILED32) return fail(HL_EINVAL, "%s: unknown kv_layout %d", who, layout);
-  if (kv_dtype == HL_F32) return fail(HL_EUNSUPPORTED, "%s: tiled KV caches are fp16/bf16 only", who);
+  if (kv_dtype == HL_F32) return fail(HL_EUNSUPPORTED, "%s: tiled KV caches are fp16/bf16/fp8 only", who);
   if (max_len % 32) return fail(HL_EINVAL, "%s: tiled KV caches need max_len %% 32 == 0 (got %d)", who, max_len);
   if (stride % 8) return fail(HL_EINVAL, "%s: tiled KV caches need a batch stride multiple of 8", who);
   if (!aligned16(kc) || !aligned16(vc)) return fail(HL_EINVAL, "%s: tiled KV caches must be 16-byte aligned", who);
@@ -361,7 +370,7 @@ static int validate_decode(const hl_decode_args* a) {
   if (!a) return fail(HL_EINVAL, "decode: args is null");
   int rc = check_gqa(a->n_head, a->n_head_kv);
   if (rc) return rc;
-  if ((rc = check_dtype(a->kv_dtype, "decode kv_dtype"))) return rc;
+  if ((rc = check_kv_dtype(a->kv_dtype, "decode kv_dtype"))) return rc;
   if (a->batch <= 0) return fail(HL_EINVAL, "decode: batch must be >= 1");
   if (a->head_dim != 64 && a->head_dim != 128)
     return fail(HL_EUNSUPPORTED, "decode: head_dim %d not built (64, 128)", a->head_dim);
@@ -468,7 +477,7 @@ static int rope_store_op(const hl_rope_store_args* a, HeadVecOp& op) {
   if (!a) return fail(HL_EINVAL, "rope_store: args is null");
   int rc = check_gqa(a->n_head_q, a->n_head_kv);
   if (rc) return rc;
-  if ((rc = check_dtype(a->kv_dtype, "rope_store kv_dtype"))) return rc;
+  if ((rc = check_kv_dtype(a->kv_dtype, "rope_store kv_dtype"))) return rc;
   if (a->batch <= 0 || a->head_dim <= 0 || a->head_dim > HL_MAX_HEAD_DIM || (a->head_dim & 1))
     return fail(HL_EINVAL, "rope_store: bad shape");
   if (!a->q || !a->k || !a->v || !a->k_cache || !a->v_cache) return fail(HL_EINVAL, "rope_store: null pointer");
@@ -600,7 +609,7 @@ static int validate_prefill(const hl_prefill_args* a, PrefillPlan* pl) {
   if (!a->q || !a->k || !a->v || !a->out) return fail(HL_EINVAL, "prefill: null pointer");
   if (a->k_cache || a->v_cache) {
     if (!a->k_cache || !a->v_cache) return fail(HL_EINVAL, "prefill: give both caches or neither");
-    if ((rc = check_dtype(a->kv_dtype, "prefill kv_dtype"))) return rc;
+    if ((rc = check_kv_dtype(a->kv_dtype, "prefill kv_dtype"))) return rc;
     if (a->start_pos < 0) return fail(HL_EINVAL, "prefill: start_pos < 0");
     if ((long long)a->start_pos + a->seq_len > a->max_len)
       return fail(HL_ECAPACITY, "prefill exceeds KV cache capacity");
@@ -868,7 +877,7 @@ int hl_gpu_embedding(float* dst, const float* weight, const int32_t* token_ids, 
 int hl_kv_cache_to_f32(float* dst, const void* cache, int kv_dtype, int rows, int max_len, int col0,
                        int ncols, void* stream) {
   if (!dst || !cache) return fail(HL_EINVAL, "cache_to_f32: null pointer");
-  int rc = check_dtype(kv_dtype, "cache_to_f32");
+  int rc = check_kv_dtype(kv_dtype, "cache_to_f32");
   if (rc) return rc;
   if (rows <= 0 || ncols <= 0 || col0 < 0 || col0 + ncols > max_len)
     return fail(HL_EINVAL, "cache_to_f32: bad range");

@@ -39,10 +39,54 @@ __device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
   return __builtin_bit_cast(uint16_t, h);
 }
 
+// fp8 e4m3 (OCP "e4m3fn"): round to nearest even, saturating to +-448
+// (infinities included), NaN -> NaN; identical on host and device.
+__host__ __device__ __forceinline__ uint8_t f32_to_e4m3(float f) {
+  uint32_t u;
+  __builtin_memcpy(&u, &f, 4);
+  const uint32_t sign = (u >> 24) & 0x80u, a = u & 0x7FFFFFFFu;
+  if (a > 0x7F800000u) return (uint8_t)(sign | 0x7Fu);   // NaN
+  if (a >= 0x43E00000u) return (uint8_t)(sign | 0x7Eu);  // >= 448 (and inf): saturate
+  if (a >= 0x3C800000u) {                                // >= 2^-6: normal
+    const uint32_t r = a + 0x7FFFFu + ((a >> 20) & 1u);  // round off 20 mantissa bits
+    uint32_t v = (r >> 20) - (120u << 3);                // rebias 127 -> 7
+    if (v > 0x7Eu) v = 0x7Eu;
+    return (uint8_t)(sign | v);
+  }
+  // subnormal: m * 2^-9, m = round-to-even(|f| * 512) in 0..8 (8 = 2^-6)
+  float af;
+  __builtin_memcpy(&af, &a, 4);
+  const float s = af * 512.0f;  // exact: power-of-two scaling of a value < 8
+  uint32_t m = (uint32_t)s;
+  const float fr = s - (float)m;
+  if (fr > 0.5f || (fr == 0.5f && (m & 1u))) ++m;
+  return (uint8_t)(sign | m);
+}
+// Exact decode through the hardware conversion (v_cvt_scalef32_pk_f16_fp8
+// with scale 1 reproduces every e4m3fn code, NaN included).
+__device__ __forceinline__ uint16_t e4m3_to_f16_bits(uint8_t b) {
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  const h2 v = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8((uint32_t)b, 1.0f, false);
+  return __builtin_bit_cast(uint16_t, (_Float16)v[0]);
+}
+// Eight e4m3 values (bytes of lo, then hi) to eight fp16 bit patterns.
+__device__ __forceinline__ u16x8 e4m3x8_to_f16x8(uint32_t lo, uint32_t hi) {
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  const h2 a = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(lo, 1.0f, false);
+  const h2 b = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(lo, 1.0f, true);
+  const h2 c = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(hi, 1.0f, false);
+  const h2 d = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(hi, 1.0f, true);
+  typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+  const u32x4v w = {__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b),
+                    __builtin_bit_cast(uint32_t, c), __builtin_bit_cast(uint32_t, d)};
+  return __builtin_bit_cast(u16x8, w);
+}
+
 template <int DT>
 __device__ __forceinline__ float load_elem(const void* p, int64_t i) {
   if constexpr (DT == HL_F32) return ((const float*)p)[i];
   else if constexpr (DT == HL_F16) return f16_bits_to_f32(((const uint16_t*)p)[i]);
+  else if constexpr (DT == HL_FP8) return f16_bits_to_f32(e4m3_to_f16_bits(((const uint8_t*)p)[i]));
   else return bf16_bits_to_f32(((const uint16_t*)p)[i]);
 }
 template <int DT>
@@ -53,18 +97,26 @@ __device__ __forceinline__ void store_elem(void* p, int64_t i, float v) {
   if constexpr (DT != HL_F32) __asm__ volatile("" : "+v"(v));
   if constexpr (DT == HL_F32) ((float*)p)[i] = v;
   else if constexpr (DT == HL_F16) ((uint16_t*)p)[i] = f32_to_f16_bits(v);
+  else if constexpr (DT == HL_FP8) ((uint8_t*)p)[i] = f32_to_e4m3(v);
   else ((uint16_t*)p)[i] = f32_to_bf16_bits(v);
 }
+// 16-bit working form of a stored value: the storage bits for fp16/bf16; for
+// fp8 the fp16 bits of the e4m3-rounded value (exact), which is how fp8
+// caches enter the fp16 MFMAs.
 template <int DT>
 __device__ __forceinline__ uint16_t to_bits(float v) {
   if constexpr (DT == HL_F16) return f32_to_f16_bits(v);
+  else if constexpr (DT == HL_FP8) return e4m3_to_f16_bits(f32_to_e4m3(v));
   else return f32_to_bf16_bits(v);
 }
 template <int DT>
 __device__ __forceinline__ float from_bits(uint16_t b) {
-  if constexpr (DT == HL_F16) return f16_bits_to_f32(b);
+  if constexpr (DT == HL_F16 || DT == HL_FP8) return f16_bits_to_f32(b);
   else return bf16_bits_to_f32(b);
 }
+// Bytes per stored element.
+template <int DT>
+constexpr int elem_bytes() { return DT == HL_F32 ? 4 : (DT == HL_FP8 ? 1 : 2); }
 
 // Offset of element (row d, column t) inside one kv head's cache block
 // (the block starts at h * D * max_len in either layout): column-major rows

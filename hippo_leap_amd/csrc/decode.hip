@@ -22,6 +22,7 @@
 #include <cstring>
 #include <map>
 #include <mutex>
+#include <type_traits>
 
 #include "common.h"
 #include "headvec.h"
@@ -440,7 +441,12 @@ __device__ __forceinline__ u16x8 mask_row8(u16x8 r, int col, int lim) {
 
 template <int D, int DT, bool VEC, bool PIPE, bool STEP>
 __global__ __launch_bounds__(256, PIPE ? (D == 64 ? 2 : 1) : 4) void decode_mfma_kernel(DecodeParams p) {
-  typedef typename MfmaT<DT>::vec vec;
+  // MFMA operand type: the storage type, except fp8 caches, which are
+  // converted to fp16 (exactly) as their tiles arrive.
+  constexpr int MT = DT == HL_FP8 ? HL_F16 : DT;
+  static_assert(DT != HL_FP8 || VEC, "fp8 caches are read with vector loads only");
+  typedef typename MfmaT<MT>::vec vec;
+  typedef typename std::conditional<DT == HL_FP8, uint8_t, uint16_t>::type elem_t;
   constexpr int KS = D / 32;      // k-steps of the QK^T product
   constexpr int NB = D / 16;      // 16-dim output blocks
   constexpr int KR = D / 16;      // 16-byte K loads per lane per tile
@@ -477,8 +483,8 @@ __global__ __launch_bounds__(256, PIPE ? (D == 64 ? 2 : 1) : 4) void decode_mfma
   const int s1 = has_new ? newc : s_end;  // end of the columns read from the cache
 
   const long long base = (long long)b * p.batch_stride + (long long)kvh * D * p.max_len;
-  const uint16_t* K = (const uint16_t*)p.k + base;
-  const uint16_t* V = (const uint16_t*)p.v + base;
+  const elem_t* K = (const elem_t*)p.k + base;
+  const elem_t* V = (const elem_t*)p.v + base;
   uint16_t* kt = (uint16_t*)lds_raw + wave * D * PITCH;
 
   // K tile: row = lane/4 + 16*r, 8 columns at 8*(lane&3); V operand: row
@@ -497,14 +503,31 @@ __global__ __launch_bounds__(256, PIPE ? (D == 64 ? 2 : 1) : 4) void decode_mfma
       const long long tb = tiled ? (long long)(t0 >> 5) * (D * 32) : 0;
       const int ck = tiled ? 8 * (lane & 3) : min(t0 + 8 * (lane & 3), p.max_len - 8);
       const int cv = tiled ? 8 * g : min(t0 + 8 * g, p.max_len - 8);
+      if constexpr (DT == HL_FP8) {
+        // 8-byte loads of 8 e4m3 values, converted to fp16 at once.
+        typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
+        u32x2v kw[KR], vw[NB];
 #pragma unroll
-      for (int r = 0; r < KR; ++r) {
-        const int row = (lane >> 2) + 16 * r;
-        kr[r] = *(const u16x8*)(K + tb + (long long)row * rstride + ck);
+        for (int r = 0; r < KR; ++r) {
+          const int row = (lane >> 2) + 16 * r;
+          kw[r] = *(const u32x2v*)(K + tb + (long long)row * rstride + ck);
+        }
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) vw[nb] = *(const u32x2v*)(V + tb + (long long)(16 * nb + c) * rstride + cv);
+#pragma unroll
+        for (int r = 0; r < KR; ++r) kr[r] = e4m3x8_to_f16x8(kw[r][0], kw[r][1]);
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) vr[nb] = e4m3x8_to_f16x8(vw[nb][0], vw[nb][1]);
+      } else {
+#pragma unroll
+        for (int r = 0; r < KR; ++r) {
+          const int row = (lane >> 2) + 16 * r;
+          kr[r] = *(const u16x8*)(K + tb + (long long)row * rstride + ck);
+        }
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) vr[nb] = *(const u16x8*)(V + tb + (long long)(16 * nb + c) * rstride + cv);
       }
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb) vr[nb] = *(const u16x8*)(V + tb + (long long)(16 * nb + c) * rstride + cv);
-    } else {
+    } else if constexpr (DT != HL_FP8) {
 #pragma unroll
       for (int r = 0; r < KR; ++r) {
         const int row = (lane >> 2) + 16 * r;
@@ -627,7 +650,7 @@ __global__ __launch_bounds__(256, PIPE ? (D == 64 ? 2 : 1) : 4) void decode_mfma
         x[e] = live ? a[e] * p.scale_log2 : 0.f;
         x[e + 4] = live ? bb[e] * p.scale_log2 : 0.f;
       }
-      split_hi_lo<DT>(x, qh[ks], ql[ks]);
+      split_hi_lo<MT>(x, qh[ks], ql[ks]);
     }
   }
   f32x4 o[NB];
@@ -690,8 +713,8 @@ __global__ __launch_bounds__(256, PIPE ? (D == 64 ? 2 : 1) : 4) void decode_mfma
 #pragma unroll
         for (int e = 0; e < 8; ++e) a[e] = kt[(32 * ks + 8 * g + e) * PITCH + tc];
         const vec av = __builtin_bit_cast(vec, a);
-        s[mb] = MfmaT<DT>::mma(av, qh[ks], s[mb]);
-        s[mb] = MfmaT<DT>::mma(av, ql[ks], s[mb]);
+        s[mb] = MfmaT<MT>::mma(av, qh[ks], s[mb]);
+        s[mb] = MfmaT<MT>::mma(av, ql[ks], s[mb]);
       }
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -722,7 +745,7 @@ __global__ __launch_bounds__(256, PIPE ? (D == 64 ? 2 : 1) : 4) void decode_mfma
     }
     l_run = l_run * alpha + ps;
     vec ph, pl;
-    split_hi_lo<DT>(pe, ph, pl);
+    split_hi_lo<MT>(pe, ph, pl);
 
     // Output rows held by this lane are heads 4g+i: fetch their alphas.
     float ar[4];
@@ -733,8 +756,8 @@ __global__ __launch_bounds__(256, PIPE ? (D == 64 ? 2 : 1) : 4) void decode_mfma
 #pragma unroll
       for (int i = 0; i < 4; ++i) o[nb][i] *= ar[i];
       const vec bv = __builtin_bit_cast(vec, vr[nb]);
-      o[nb] = MfmaT<DT>::mma(ph, bv, o[nb]);
-      o[nb] = MfmaT<DT>::mma(pl, bv, o[nb]);
+      o[nb] = MfmaT<MT>::mma(ph, bv, o[nb]);
+      o[nb] = MfmaT<MT>::mma(pl, bv, o[nb]);
     }
   };
 
@@ -801,8 +824,11 @@ __global__ __launch_bounds__(256, PIPE ? (D == 64 ? 2 : 1) : 4) void decode_mfma
     finish_workgroup<D>(p, sm_m, sm_l, sm_o, hc, b, kvh, chunk, hq0, split, HS, [&]() {
       if (has_new && chunk == 0) {
         for (int i = tid; i < 2 * D; i += 256) {
-          uint16_t* cache = (uint16_t*)(i < D ? p.k : p.v);
-          cache[base + kv_off(p.kv_layout, i < D ? i : i - D, newc, D, p.max_len)] = snew[i];
+          const long long at = base + kv_off(p.kv_layout, i < D ? i : i - D, newc, D, p.max_len);
+          if constexpr (DT == HL_FP8)  // snew holds the fp16 form of an e4m3 value: exact
+            ((uint8_t*)(i < D ? p.k : p.v))[at] = f32_to_e4m3(from_bits<DT>(snew[i]));
+          else
+            ((uint16_t*)(i < D ? p.k : p.v))[at] = snew[i];
         }
       }
     });
@@ -841,8 +867,10 @@ typedef void (*KernelFn)(DecodeParams);
 // loads of unaligned caches would not fit its registers).
 template <int D, int DT, bool STEP>
 KernelFn pick_mfma(bool vec, bool pipe) {
-  if (vec) return pipe ? decode_mfma_kernel<D, DT, true, true, STEP> : decode_mfma_kernel<D, DT, true, false, STEP>;
-  return decode_mfma_kernel<D, DT, false, false, STEP>;
+  if (vec || DT == HL_FP8)  // fp8 caches are tiled: always vector loads
+    return pipe ? decode_mfma_kernel<D, DT, true, true, STEP> : decode_mfma_kernel<D, DT, true, false, STEP>;
+  if constexpr (DT != HL_FP8) return decode_mfma_kernel<D, DT, false, false, STEP>;
+  return nullptr;
 }
 
 template <int D, int DT>
@@ -857,6 +885,8 @@ KernelFn pick_kernel(int kv_dtype, int D, bool vec, bool pipe, bool step) {
   }
   if (kv_dtype == HL_F16)
     return D == 64 ? pick_mfma<64, HL_F16>(vec, pipe, step) : pick_mfma<128, HL_F16>(vec, pipe, step);
+  if (kv_dtype == HL_FP8)
+    return D == 64 ? pick_mfma<64, HL_FP8>(vec, pipe, step) : pick_mfma<128, HL_FP8>(vec, pipe, step);
   return D == 64 ? pick_mfma<64, HL_BF16>(vec, pipe, step) : pick_mfma<128, HL_BF16>(vec, pipe, step);
 }
 

@@ -89,6 +89,7 @@ hipError_t headvec_launch(const HeadVecOp& op, hipStream_t stream) {
   switch (op.kv_dtype) {
     case HL_F32: hipLaunchKernelGGL(headvec_kernel<HL_F32>, grid, dim3(64), 0, stream, op); break;
     case HL_F16: hipLaunchKernelGGL(headvec_kernel<HL_F16>, grid, dim3(64), 0, stream, op); break;
+    case HL_FP8: hipLaunchKernelGGL(headvec_kernel<HL_FP8>, grid, dim3(64), 0, stream, op); break;
     default: hipLaunchKernelGGL(headvec_kernel<HL_BF16>, grid, dim3(64), 0, stream, op); break;
   }
   return hipGetLastError();
@@ -110,6 +111,7 @@ constexpr int kTabHalf = 64;  // largest rope_dim/2 served from the LDS table
 template <int DT>
 __device__ __forceinline__ void load_row8_f32(const void* base, long long off, int t, int lim,
                                               float* x) {
+  static_assert(DT != HL_FP8, "activations are fp32/fp16/bf16");
   const int esz = DT == HL_F32 ? 4 : 2;
   if (t + 8 <= lim && (((uintptr_t)base + (uintptr_t)off * esz) & 15) == 0) {
     if constexpr (DT == HL_F32) {
@@ -132,14 +134,26 @@ __device__ __forceinline__ void load_row8_f32(const void* base, long long off, i
 }
 
 // Stores 8 consecutive elements [t, t+8) of one row; elements >= lim skipped.
+// Vector stores need 16-byte alignment (8 bytes for fp8).
 template <int DT>
 __device__ __forceinline__ void store_row8(void* base, long long off, int t, int lim,
                                            const float* x) {
-  const int esz = DT == HL_F32 ? 4 : 2;
-  if (t + 8 <= lim && (((uintptr_t)base + (uintptr_t)off * esz) & 15) == 0) {
+  constexpr int esz = elem_bytes<DT>();
+  constexpr uintptr_t amask = DT == HL_FP8 ? 7 : 15;
+  if (t + 8 <= lim && (((uintptr_t)base + (uintptr_t)off * esz) & amask) == 0) {
     if constexpr (DT == HL_F32) {
       *(f32x4*)((float*)base + off) = f32x4{x[0], x[1], x[2], x[3]};
       *(f32x4*)((float*)base + off + 4) = f32x4{x[4], x[5], x[6], x[7]};
+    } else if constexpr (DT == HL_FP8) {
+      uint32_t w[2] = {0u, 0u};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float v = x[e];
+        __asm__ volatile("" : "+v"(v));  // round the fp32 value, as store_elem does
+        w[e >> 2] |= (uint32_t)f32_to_e4m3(v) << (8 * (e & 3));
+      }
+      typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
+      *(u32x2v*)((uint8_t*)base + off) = u32x2v{w[0], w[1]};
     } else {
       u16x8 v;
 #pragma unroll
@@ -499,9 +513,11 @@ hipError_t prologue_launch(const PrologueOp& op, hipStream_t stream) {
 #define HL_KVP(IO, KD) hipLaunchKernelGGL((kv_prologue_kernel<IO, KD, 128>), grid, dim3(256), 0, stream, op)
     const int kd = op.k_cache ? op.kv_dtype : HL_BF16;
     if (op.io_dtype == HL_F16) {
-      if (kd == HL_F32) HL_KVP(HL_F16, HL_F32); else if (kd == HL_F16) HL_KVP(HL_F16, HL_F16); else HL_KVP(HL_F16, HL_BF16);
+      if (kd == HL_F32) HL_KVP(HL_F16, HL_F32); else if (kd == HL_F16) HL_KVP(HL_F16, HL_F16);
+      else if (kd == HL_FP8) HL_KVP(HL_F16, HL_FP8); else HL_KVP(HL_F16, HL_BF16);
     } else {
-      if (kd == HL_F32) HL_KVP(HL_BF16, HL_F32); else if (kd == HL_F16) HL_KVP(HL_BF16, HL_F16); else HL_KVP(HL_BF16, HL_BF16);
+      if (kd == HL_F32) HL_KVP(HL_BF16, HL_F32); else if (kd == HL_F16) HL_KVP(HL_BF16, HL_F16);
+      else if (kd == HL_FP8) HL_KVP(HL_BF16, HL_FP8); else HL_KVP(HL_BF16, HL_BF16);
     }
 #undef HL_KVP
     return hipGetLastError();
@@ -522,6 +538,7 @@ hipError_t prologue_launch(const PrologueOp& op, hipStream_t stream) {
   switch (op.kv_dtype) {                   \
     case HL_F32: HL_PRO(IO, HL_F32); break; \
     case HL_F16: HL_PRO(IO, HL_F16); break; \
+    case HL_FP8: HL_PRO(IO, HL_FP8); break; \
     default: HL_PRO(IO, HL_BF16); break;    \
   }
   switch (op.io_dtype) {
@@ -595,6 +612,10 @@ hipError_t cache_to_f32_launch(float* dst, const void* cache, int kv_dtype, int 
       break;
     case HL_F16:
       hipLaunchKernelGGL(cache_to_f32_kernel<HL_F16>, grid, dim3(256), 0, stream, dst, cache, rows,
+                         max_len, col0, ncols);
+      break;
+    case HL_FP8:
+      hipLaunchKernelGGL(cache_to_f32_kernel<HL_FP8>, grid, dim3(256), 0, stream, dst, cache, rows,
                          max_len, col0, ncols);
       break;
     default:

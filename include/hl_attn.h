@@ -45,7 +45,11 @@ enum {
 };
 
 /* ---- element types of activations and KV cache ------------------------- */
-enum { HL_F32 = 0, HL_F16 = 1, HL_BF16 = 2 };
+/* HL_FP8: OCP fp8 e4m3 ("e4m3fn": bias 7, no infinities, max 448), KV caches
+ * only and only in the HL_KV_TILED32 layout.  Writes round to nearest even
+ * and saturate to +-448 (infinities too; NaN stays NaN); reads are exact.
+ * Extends the reference, which keeps fp32 caches.                          */
+enum { HL_F32 = 0, HL_F16 = 1, HL_BF16 = 2, HL_FP8 = 3 };
 
 /* ---- RoPE pairing ------------------------------------------------------- */
 enum {

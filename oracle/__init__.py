@@ -19,7 +19,7 @@ import numpy as np
 
 ORACLE_DIR = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(ORACLE_DIR, "liboracle.so")
-F32, F16, BF16 = 0, 1, 2
+F32, F16, BF16, FP8 = 0, 1, 2, 3
 
 _lib = None
 _fp = ctypes.POINTER(ctypes.c_float)
@@ -101,7 +101,7 @@ def to_storage(x: np.ndarray, dtype: int) -> np.ndarray:
     x = _f32(x)
     if dtype == F32:
         return x.copy()
-    out = np.empty(x.shape, np.uint16)
+    out = np.empty(x.shape, np.uint8 if dtype == FP8 else np.uint16)
     lib().orc_convert_from_f32(dtype, _ptr(x), out.ctypes.data_as(ctypes.c_void_p), x.size)
     return out
 
@@ -109,7 +109,7 @@ def to_storage(x: np.ndarray, dtype: int) -> np.ndarray:
 def upcast(bits: np.ndarray, dtype: int) -> np.ndarray:
     if dtype == F32:
         return _f32(bits).copy()
-    bits = np.ascontiguousarray(bits, dtype=np.uint16)
+    bits = np.ascontiguousarray(bits, dtype=np.uint8 if dtype == FP8 else np.uint16)
     out = np.empty(bits.shape, np.float32)
     lib().orc_upcast_to_f32(dtype, bits.ctypes.data_as(ctypes.c_void_p), _ptr(out), bits.size)
     return out

@@ -51,6 +51,7 @@
 #define ORC_F32 0
 #define ORC_F16 1
 #define ORC_BF16 2
+#define ORC_FP8 3
 
 /* ---------------------------------------------------------------------- */
 /* Seeded input generator (shared by tests, fixtures and the CPU baseline) */
@@ -153,8 +154,47 @@ uint16_t orc_float_to_bf16_rne(float f) {
   return (uint16_t)(x >> 16);
 }
 
+/* OCP fp8 e4m3 ("e4m3fn": bias 7, no infinities, max 448), the library's
+ * fp8 KV storage (the reference has no fp8).  Encode: round to nearest even
+ * by the value's quantum, saturate at +-448 (infinities too), NaN -> 0x7F
+ * with the sign kept.  Written from the format's definition (frexp and a
+ * rounding of |x| / quantum), independently of the kernels' bit arithmetic. */
+uint8_t orc_float_to_e4m3(float f) {
+  const uint8_t sign = signbit(f) ? 0x80 : 0;
+  if (isnan(f)) return (uint8_t)(sign | 0x7F);
+  const double a = fabs((double)f);
+  if (a >= 448.0) return (uint8_t)(sign | 0x7E);
+  int e;
+  frexp(a, &e);                     /* a in [2^(e-1), 2^e) */
+  int ex = e - 1;
+  if (ex < -6) ex = -6;             /* below 2^-6 the quantum stays 2^-9 */
+  const double q = ldexp(1.0, ex - 3);
+  const double r = nearbyint(a / q) * q; /* ties to even (default mode) */
+  if (r == 0.0) return sign;
+  if (r >= 448.0) return (uint8_t)(sign | 0x7E);
+  int e2;
+  frexp(r, &e2);
+  const int E = e2 - 1;
+  if (E < -6) return (uint8_t)(sign | (uint8_t)(r / ldexp(1.0, -9)));
+  const int mant = (int)((r / ldexp(1.0, E) - 1.0) * 8.0);
+  return (uint8_t)(sign | (uint8_t)(((E + 7) << 3) | mant));
+}
+
+float orc_e4m3_to_float(uint8_t b) {
+  const int e = (b >> 3) & 15, m = b & 7;
+  float v;
+  if (e == 15 && m == 7) v = NAN;
+  else if (e == 0) v = ldexpf((float)m, -9);
+  else v = ldexpf(1.0f + (float)m / 8.0f, e - 7);
+  return (b & 0x80) ? -v : v;
+}
+
 void orc_convert_from_f32(int dtype, const float* src, void* dst, int64_t n) {
   if (dtype == ORC_F32) { memcpy(dst, src, (size_t)n * 4); return; }
+  if (dtype == ORC_FP8) {
+    for (int64_t i = 0; i < n; ++i) ((uint8_t*)dst)[i] = orc_float_to_e4m3(src[i]);
+    return;
+  }
   uint16_t* d = (uint16_t*)dst;
   for (int64_t i = 0; i < n; ++i)
     d[i] = dtype == ORC_F16 ? orc_float_to_half_rne(src[i]) : orc_float_to_bf16_rne(src[i]);
@@ -162,6 +202,10 @@ void orc_convert_from_f32(int dtype, const float* src, void* dst, int64_t n) {
 
 void orc_upcast_to_f32(int dtype, const void* src, float* dst, int64_t n) {
   if (dtype == ORC_F32) { memcpy(dst, src, (size_t)n * 4); return; }
+  if (dtype == ORC_FP8) {
+    for (int64_t i = 0; i < n; ++i) dst[i] = orc_e4m3_to_float(((const uint8_t*)src)[i]);
+    return;
+  }
   const uint16_t* s = (const uint16_t*)src;
   for (int64_t i = 0; i < n; ++i)
     dst[i] = dtype == ORC_F16 ? orc_half_to_float(s[i]) : orc_bf16_to_float(s[i]);

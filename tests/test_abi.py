@@ -264,3 +264,17 @@ def test_rmsnorm_validation(hl):
     assert hl.hl_gpu_rmsnorm_cols(FAKE + 4, FAKE, FAKE + (1 << 24), 64, 2, 1e-5, None) == _lib.HL_EINVAL
     assert hl.hl_gpu_residual_rmsnorm(FAKE, FAKE + 64, FAKE + 4096, FAKE + 8192, 64, 1e-6,
                                       None) == _lib.HL_EINVAL
+
+
+def test_fp8_kv_validation(hl):
+    """fp8 KV caches: accepted in the tiled layout only; never as activations."""
+    T = _lib.HL_KV_TILED32
+    a = _decode_args(kv_dtype=_lib.HL_FP8, max_len=2080)
+    assert hl.hl_attn_decode(ctypes.byref(a), None, 0, None) == _lib.HL_EUNSUPPORTED
+    assert "tiled" in _err(hl)
+    a = _decode_args(kv_dtype=_lib.HL_FP8, max_len=2080, kv_layout=T)
+    assert hl.hl_attn_decode_workspace_bytes(ctypes.byref(a)) > 0
+    p = _prefill_args(k_cache=FAKE, v_cache=FAKE, kv_dtype=_lib.HL_FP8, max_len=4096)
+    assert hl.hl_attn_prefill(ctypes.byref(p), None, 0, None) == _lib.HL_EUNSUPPORTED
+    p = _prefill_args(io_dtype=_lib.HL_FP8)
+    assert hl.hl_attn_prefill(ctypes.byref(p), None, 0, None) == _lib.HL_EINVAL

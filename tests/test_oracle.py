@@ -348,3 +348,35 @@ def test_embedding_matches_indexing(orc):
     tok = np.array([3, 0, 49, 3, 17], np.int32)
     out = orc.embedding(w, tok, n_emb)
     assert np.array_equal(out, w[tok].T)
+
+
+# ---------------------------------------------------------------------------
+# fp8 e4m3 KV storage (the library's extension; no reference counterpart)
+# ---------------------------------------------------------------------------
+def test_e4m3_decode_all_codes_match_torch(orc):
+    import torch
+    codes = np.arange(256, dtype=np.uint8)
+    got = orc.upcast(codes, orc.FP8)
+    ref = torch.from_numpy(codes).view(torch.float8_e4m3fn).float().numpy()
+    assert np.array_equal(np.isnan(got), np.isnan(ref))
+    ok = ~np.isnan(ref)
+    assert np.array_equal(got[ok], ref[ok]) and np.array_equal(np.signbit(got[ok]), np.signbit(ref[ok]))
+
+
+def test_e4m3_encode_matches_torch_below_overflow(orc):
+    """Round to nearest even, bit for bit with torch's float8_e4m3fn cast for
+    every |x| < 464 (where torch does not overflow), over a dense sweep that
+    includes every rounding midpoint; saturation at +-448 above it."""
+    import torch
+    rng = np.random.default_rng(0)
+    codes = torch.arange(0, 126, dtype=torch.uint8).view(torch.float8_e4m3fn).float().numpy()
+    mids = (codes[:-1] + codes[1:]) / 2                     # exact ties
+    x = np.concatenate([rng.uniform(-463.9, 463.9, 200000), rng.normal(0, 0.01, 100000),
+                        codes, -codes, mids, -mids, np.nextafter(mids, 0), np.nextafter(mids, 1e9),
+                        [0.0, -0.0, 448.0, -448.0, 463.99]]).astype(np.float32)
+    got = orc.to_storage(x, orc.FP8)
+    ref = torch.from_numpy(x).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert np.array_equal(got, ref)
+    big = np.array([464.0, 480.0, 1e30, np.inf, -np.inf, -1e9], np.float32)
+    assert orc.to_storage(big, orc.FP8).tolist() == [0x7E, 0x7E, 0x7E, 0x7E, 0xFE, 0xFE]
+    assert orc.to_storage(np.array([np.nan], np.float32), orc.FP8)[0] & 0x7F == 0x7F
