@@ -20,6 +20,8 @@ Extra objects on the same JSON line:
   decode_c5_tiled, decode_c3_tiled: the same steps with the caches in the
     opt-in tiled layout (HL_KV_TILED32: per kv head, 32-column tiles of
     [D][32]), same values.
+  decode_c5_fp8, decode_c3_fp8: the same steps with fp8 e4m3 caches (tiled),
+    GB/s of the fp8 bytes (half of the bf16/fp16 bytes per position).
   decode_c1, prefill_c2: configs[0] and configs[1], the reference's fp32
     call contract (hl_gpu_attention_decode; fp32 prefill with RoPE 1e4 and
     the cache write), timed for reference: they are parity cases, not the
@@ -122,10 +124,10 @@ class DecodeWorkload:
         self.max_len = (self.L + 63) // 64 * 64  # cache columns: allocation rounded to 64
         g = torch.Generator(device="cuda").manual_seed(seed)
         n = B * hkv * d * self.max_len
-        self.kc = [(torch.randn(n, generator=g, device="cuda") * sigma).to(kv_dtype)
-                   for _ in range(n_sets)]
-        self.vc = [(torch.randn(n, generator=g, device="cuda") * sigma).to(kv_dtype)
-                   for _ in range(n_sets)]
+        cast = (lambda x: x.to(kv_dtype).view(torch.uint8)) if kv_dtype == torch.float8_e4m3fn \
+            else (lambda x: x.to(kv_dtype))  # fp8: e4m3 bytes
+        self.kc = [cast(torch.randn(n, generator=g, device="cuda") * sigma) for _ in range(n_sets)]
+        self.vc = [cast(torch.randn(n, generator=g, device="cuda") * sigma) for _ in range(n_sets)]
         if kv_layout:  # same values, stored as 32-column tiles
             self.kc = [A.kv_to_tiled(c, hkv, d, self.max_len) for c in self.kc]
             self.vc = [A.kv_to_tiled(c, hkv, d, self.max_len) for c in self.vc]
@@ -255,6 +257,7 @@ def decode_extra(wl, t, workload):
     return {
         "workload": workload,
         "kv_layout": "tiled32" if wl.kv_layout else "colmajor (reference)",
+        "kv_dtype": {1: "fp8 e4m3", 2: "bf16/fp16"}.get(wl.kc[0].element_size(), "fp32"),
         "value": round(wl.kv_bytes / (t["step"] * 1e-3) / 1e9, 2), "unit": "GB/s",
         "ms_per_step": round(t["step"], 5),
         "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS,
@@ -440,6 +443,16 @@ def main():
         log(f"decode_c3_tiled: step {t['step']*1e3:.2f} us, step kernel {t['kernel']*1e3:.2f} us")
         del wl
         torch.cuda.empty_cache()
+        log("decode_c3_fp8 ...")
+        wl = DecodeWorkload(torch, A, B=8, hq=32, hkv=8, d=64, prev=2048,
+                            kv_dtype=torch.float8_e4m3fn, sigma=0.5, base=5e5, n_sets=16,
+                            qknorm=False, seed=3, kv_layout=1)
+        t = bench_decode(torch, A, wl, args.steps, args.warmup)
+        result["decode_c3_fp8"] = decode_extra(wl, t, "c3 step, fp8 e4m3 caches in the tiled "
+                                               "layout (half the bytes)")
+        log(f"decode_c3_fp8: step {t['step']*1e3:.2f} us, step kernel {t['kernel']*1e3:.2f} us")
+        del wl
+        torch.cuda.empty_cache()
 
     if args.only in ("all", "fp32"):
         # The reference-contract fp32 path (configs[0] decode, configs[1] prefill):
@@ -511,12 +524,14 @@ def main():
         torch.cuda.empty_cache()
 
     if args.only in ("all", "c5"):
-        for layout, key in ((0, "decode_c5"), (1, "decode_c5_tiled")):
+        for layout, key, kvdt in ((0, "decode_c5", torch.bfloat16),
+                                  (1, "decode_c5_tiled", torch.bfloat16),
+                                  (1, "decode_c5_fp8", torch.float8_e4m3fn)):
             if args.layouts == ("tiled" if layout == 0 else "colmajor"):
                 continue
             log(f"{key} ...")
             wl = DecodeWorkload(torch, A, B=16, hq=32, hkv=4, d=128, prev=32768,
-                                kv_dtype=torch.bfloat16, sigma=1.0, base=1e6, n_sets=1,
+                                kv_dtype=kvdt, sigma=1.0, base=1e6, n_sets=1 if kvdt == torch.bfloat16 else 2,
                                 qknorm=True, seed=5, kv_layout=layout)
             t = bench_decode(torch, A, wl, max(10, args.steps // 4), 3)
             result[key] = decode_extra(wl, t, "c5: Qwen3-30B-A3B-shape decode, bf16 KV, B=16, "
