@@ -447,6 +447,11 @@ __global__ __launch_bounds__(256, PIPE ? (D == 64 ? 2 : 1) : 4) void decode_mfma
   static_assert(DT != HL_FP8 || VEC, "fp8 caches are read with vector loads only");
   typedef typename MfmaT<MT>::vec vec;
   typedef typename std::conditional<DT == HL_FP8, uint8_t, uint16_t>::type elem_t;
+  // Tile registers hold what the loads return: 8 fp16/bf16 values per row
+  // chunk, or for fp8 the 8 raw bytes, converted when the tile is computed
+  // (converting at load time would wait for the loads there).
+  typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
+  typedef typename std::conditional<DT == HL_FP8, u32x2v, u16x8>::type raw_t;
   constexpr int KS = D / 32;      // k-steps of the QK^T product
   constexpr int NB = D / 16;      // 16-dim output blocks
   constexpr int KR = D / 16;      // 16-byte K loads per lane per tile
@@ -497,27 +502,20 @@ __global__ __launch_bounds__(256, PIPE ? (D == 64 ? 2 : 1) : 4) void decode_mfma
   // without a branch so that both layouts issue the same loads.
   const bool tiled = VEC && p.kv_layout == HL_KV_TILED32;
   const int rstride = tiled ? 32 : p.max_len;
-  auto load_tile = [&](int t0, u16x8* kr, u16x8* vr) {
+  auto load_tile = [&](int t0, raw_t* kr, raw_t* vr) {
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (VEC) {
       const long long tb = tiled ? (long long)(t0 >> 5) * (D * 32) : 0;
       const int ck = tiled ? 8 * (lane & 3) : min(t0 + 8 * (lane & 3), p.max_len - 8);
       const int cv = tiled ? 8 * g : min(t0 + 8 * g, p.max_len - 8);
-      if constexpr (DT == HL_FP8) {
-        // 8-byte loads of 8 e4m3 values, converted to fp16 at once.
-        typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
-        u32x2v kw[KR], vw[NB];
+      if constexpr (DT == HL_FP8) {  // 8-byte loads of 8 e4m3 values
 #pragma unroll
         for (int r = 0; r < KR; ++r) {
           const int row = (lane >> 2) + 16 * r;
-          kw[r] = *(const u32x2v*)(K + tb + (long long)row * rstride + ck);
+          kr[r] = *(const u32x2v*)(K + tb + (long long)row * rstride + ck);
         }
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb) vw[nb] = *(const u32x2v*)(V + tb + (long long)(16 * nb + c) * rstride + cv);
-#pragma unroll
-        for (int r = 0; r < KR; ++r) kr[r] = e4m3x8_to_f16x8(kw[r][0], kw[r][1]);
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb) vr[nb] = e4m3x8_to_f16x8(vw[nb][0], vw[nb][1]);
+        for (int nb = 0; nb < NB; ++nb) vr[nb] = *(const u32x2v*)(V + tb + (long long)(16 * nb + c) * rstride + cv);
       } else {
 #pragma unroll
         for (int r = 0; r < KR; ++r) {
@@ -588,7 +586,7 @@ __global__ __launch_bounds__(256, PIPE ? (D == 64 ? 2 : 1) : 4) void decode_mfma
   // wave with fewer tiles re-reads one it already asked for (a cache hit), so
   // every wait below can count loads exactly.
   int t0 = s0 + wave * 32;
-  u16x8 ka[KR], va[NB], kb[KR], vb[NB];
+  raw_t ka[KR], va[NB], kb[KR], vb[NB];
   const int ta = t0 < s1 ? t0 : s0;
   load_tile(ta, ka, va);
   if constexpr (PIPE) load_tile(t0 + 128 < s1 ? t0 + 128 : ta, kb, vb);
@@ -682,7 +680,7 @@ __global__ __launch_bounds__(256, PIPE ? (D == 64 ? 2 : 1) : 4) void decode_mfma
   }
 
   // One 32-column tile whose K/V registers have been loaded.
-  auto compute = [&](int t0, u16x8* kr, u16x8* vr) {
+  auto compute_tile = [&](int t0, u16x8* kr, u16x8* vr) {
     if (VEC && t0 + 32 > s1) {  // boundary tile (wave-uniform): zero columns >= s1
 #pragma unroll
       for (int r = 0; r < KR; ++r) kr[r] = mask_row8(kr[r], t0 + 8 * (lane & 3), s1);
@@ -758,6 +756,19 @@ __global__ __launch_bounds__(256, PIPE ? (D == 64 ? 2 : 1) : 4) void decode_mfma
       const vec bv = __builtin_bit_cast(vec, vr[nb]);
       o[nb] = MfmaT<MT>::mma(ph, bv, o[nb]);
       o[nb] = MfmaT<MT>::mma(pl, bv, o[nb]);
+    }
+  };
+
+  auto compute = [&](int t0, raw_t* kw, raw_t* vw) {
+    if constexpr (DT == HL_FP8) {
+      u16x8 kr[KR], vr[NB];
+#pragma unroll
+      for (int r = 0; r < KR; ++r) kr[r] = e4m3x8_to_f16x8(kw[r][0], kw[r][1]);
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) vr[nb] = e4m3x8_to_f16x8(vw[nb][0], vw[nb][1]);
+      compute_tile(t0, kr, vr);
+    } else {
+      compute_tile(t0, kw, vw);
     }
   };
 
