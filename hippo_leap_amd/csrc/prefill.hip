@@ -552,23 +552,29 @@ __device__ __forceinline__ f32x16 mma32f(float a, float b, f32x16 c) {
 }
 }  // namespace
 
-template <int D>
+template <int D, int KSPLIT>
 __global__ __launch_bounds__(256) void prefill_f32mfma_kernel(PrefillLaunch p, int nh) {
   constexpr int NW = 4;             // waves
   constexpr int KS = D / 2;         // S^T k-steps (pairs of head dims)
   constexpr int KC = KS / 4;        // 16-byte chunks per staged K row
   constexpr int DB = D / 32;        // 32-dim blocks of O^T
   constexpr int BN = 64;            // keys per tile
-  constexpr int NL = D * BN / (64 * NW);  // K (and V) tile elements per thread
-  __shared__ __attribute__((aligned(16))) float sk[2 * BN * KS];  // [h][key][ks]
-  __shared__ __attribute__((aligned(16))) float sv[2 * D * 32];   // [h][d][ks]
+  constexpr int NL = D * BN / (64 * NW);  // K (and V) tile elements per thread and tile
+  // KSPLIT key groups: wave w serves head w % nh and the key tiles
+  // kq, kq + KSPLIT, ... (kq = w / nh); each step stages KSPLIT tiles.
+  constexpr int SKN = 2 * BN * KS, SVN = 2 * D * 32;
+  __shared__ __attribute__((aligned(16))) float sk[KSPLIT * SKN];  // [tile][h][key][ks]
+  __shared__ __attribute__((aligned(16))) float sv[KSPLIT * SVN];  // [tile][h][d][ks]
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int ln = lane & 31, hh = lane >> 5;
   const int T = p.seq_len;
   const int group = p.n_head / p.n_head_kv;
-  const int rows_wg = 32 * (NW / nh);
+  // wave = (kq * RB + rb) * nh + head: key group kq, row block rb, head.
+  const int RB = NW / (nh * KSPLIT);             // 32-row blocks per workgroup (1 when split)
+  const int kq = wave / (nh * RB);
+  const int rows_wg = 32 * RB;
   const int n_qblk = (T + rows_wg - 1) / rows_wg;
   const int n_hgrp = group / nh;
   const int per_q = p.n_head_kv * n_hgrp;
@@ -577,9 +583,10 @@ __global__ __launch_bounds__(256) void prefill_f32mfma_kernel(PrefillLaunch p, i
   const int kvh = (item % per_q) / n_hgrp;
   const int hgrp = (item % per_q) % n_hgrp;
   const int hq = kvh * group + hgrp * nh + wave % nh;
-  const int r0 = qblk * rows_wg + (wave / nh) * 32;
+  const int r0 = qblk * rows_wg + ((wave / nh) % RB) * 32;
   const int wg_last_row = min(T - 1, qblk * rows_wg + rows_wg - 1);
   const int n_tiles = wg_last_row / BN + 1;
+  const int n_steps = (n_tiles + KSPLIT - 1) / KSPLIT;
   const int t_abs = r0 + ln;
   const bool live = r0 < T;
 
@@ -587,15 +594,18 @@ __global__ __launch_bounds__(256) void prefill_f32mfma_kernel(PrefillLaunch p, i
   const float* V = p.v + (long long)kvh * D * T;
 
   // K/V tiles: thread moves column lc (key j0 + lc) of rows d = ld0 + 4k;
-  // the next tile's values are loaded while the current one is computed.
+  // the next step's tiles are loaded while the current ones are computed.
   const int lc = tid & 63, ld0 = tid >> 6;
-  float kr[NL], vr[NL];
-  auto load_kv = [&](int j0) {
-    const int col = min(j0 + lc, T - 1);
+  float kr[KSPLIT][NL], vr[KSPLIT][NL];
+  auto load_kv = [&](int step) {
 #pragma unroll
-    for (int k = 0; k < NL; ++k) {
-      kr[k] = K[(long long)(ld0 + NW * k) * T + col];
-      vr[k] = V[(long long)(ld0 + NW * k) * T + col];
+    for (int u = 0; u < KSPLIT; ++u) {
+      const int col = min((step * KSPLIT + u) * BN + lc, T - 1);
+#pragma unroll
+      for (int k = 0; k < NL; ++k) {
+        kr[u][k] = K[(long long)(ld0 + NW * k) * T + col];
+        vr[u][k] = V[(long long)(ld0 + NW * k) * T + col];
+      }
     }
   };
   load_kv(0);
@@ -619,31 +629,34 @@ __global__ __launch_bounds__(256) void prefill_f32mfma_kernel(PrefillLaunch p, i
     for (int i = 0; i < 16; ++i) o[db][i] = 0.f;
   float m_run = -INFINITY, l_run = 0.f;
 
-  for (int tile = 0; tile < n_tiles; ++tile) {
-    const int j0 = tile * BN;
-    __syncthreads();  // the previous tile's sk / sv reads are done
-    {
-      const bool in = j0 + lc < T;
+  for (int step = 0; step < n_steps; ++step) {
+    __syncthreads();  // the previous step's sk / sv reads are done
+#pragma unroll
+    for (int u = 0; u < KSPLIT; ++u) {
+      const bool in = (step * KSPLIT + u) * BN + lc < T;
 #pragma unroll
       for (int k = 0; k < NL; ++k) {
         const int d = ld0 + NW * k;
-        const float kx = in ? kr[k] : 0.f, vx = in ? vr[k] : 0.f;
+        const float kx = in ? kr[u][k] : 0.f, vx = in ? vr[u][k] : 0.f;
         // K: (h = d & 1, key = lc, ks = d >> 1); V: (h = lc & 1, d, ks = lc >> 1)
         const int ksk = d >> 1, ksv = lc >> 1;
-        sk[((d & 1) * BN + lc) * KS + (((ksk >> 2) ^ kswz(lc)) << 2) + (ksk & 3)] = kx;
-        sv[((lc & 1) * D + d) * 32 + (((ksv >> 2) ^ vswz(d)) << 2) + (ksv & 3)] = vx;
+        sk[u * SKN + ((d & 1) * BN + lc) * KS + (((ksk >> 2) ^ kswz(lc)) << 2) + (ksk & 3)] = kx;
+        sv[u * SVN + ((lc & 1) * D + d) * 32 + (((ksv >> 2) ^ vswz(d)) << 2) + (ksv & 3)] = vx;
       }
     }
-    if (tile + 1 < n_tiles) load_kv(j0 + BN);
+    if (step + 1 < n_steps) load_kv(step + 1);
     __syncthreads();
+    const int j0 = (step * KSPLIT + kq) * BN;
     if (!live || j0 > r0 + 31) continue;  // wave-uniform: no key of this tile is visible
+    const float* tk = sk + kq * SKN;
+    const float* tv = sv + kq * SVN;
 
     f32x16 s[2];
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb) {
       const int m = ln;  // A operand row = key 32mb + 8a + 2e + h for m = 8a + 4h + e
       const int key = 32 * mb + 8 * (m >> 3) + 2 * (m & 3) + ((m >> 2) & 1);
-      const float* row = sk + (hh * BN + key) * KS;
+      const float* row = tk + (hh * BN + key) * KS;
 #pragma unroll
       for (int i = 0; i < 16; ++i) s[mb][i] = 0.f;
 #pragma unroll
@@ -665,7 +678,9 @@ __global__ __launch_bounds__(256) void prefill_f32mfma_kernel(PrefillLaunch p, i
         mt = fmaxf(mt, s[mb][i]);
       }
     mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
-    const float mn = fmaxf(m_run, mt);  // finite: key j0 <= t_abs for every live row
+    // Finite: a visible tile starts at or before the row block (tiles are 64
+    // keys, row blocks 32 rows, both aligned), so every row sees key j0.
+    const float mn = fmaxf(m_run, mt);
     const float alpha = fast_exp2(m_run - mn);
     m_run = mn;
     float ps = 0.f;
@@ -685,7 +700,7 @@ __global__ __launch_bounds__(256) void prefill_f32mfma_kernel(PrefillLaunch p, i
 #pragma unroll
     for (int db = 0; db < DB; ++db) {
       const int d = 32 * db + ln;
-      const float* row = sv + (hh * D + d) * 32;
+      const float* row = tv + (hh * D + d) * 32;
 #pragma unroll
       for (int c = 0; c < 8; ++c) {
         const f32x4 vf = *(const f32x4*)(row + ((c ^ vswz(d)) << 2));
@@ -698,8 +713,55 @@ __global__ __launch_bounds__(256) void prefill_f32mfma_kernel(PrefillLaunch p, i
     }
   }
 
+  float l = l_run + __shfl_xor(l_run, 32, 64);
+  if constexpr (KSPLIT > 1) {
+    // Key groups 1.. hand (m, l, o) to group 0 through LDS (the tiles are
+    // dead); a group that saw no tile has m = -inf and weight 0.
+    __syncthreads();
+    // Slots: the waves of key groups 1.., slot = wave - nh (the launch uses
+    // the split only with one row block per workgroup, RB = 1).
+    constexpr int NSLOT = NW - NW / KSPLIT;
+    float* xm = sk;                  // [slot][lane] m
+    float* xl = xm + NSLOT * 64;     // [slot][lane] l
+    float* xo = xl + NSLOT * 64;     // [slot][db*16 + i][lane] o
+    static_assert(NSLOT * 64 * (2 + 16 * DB) <= KSPLIT * SKN, "merge buffers fit the K tiles");
+    if (kq > 0) {
+      const int sl = wave - nh;
+      xm[sl * 64 + lane] = m_run;
+      xl[sl * 64 + lane] = l;
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) xo[(sl * 16 * DB + db * 16 + i) * 64 + lane] = o[db][i];
+    }
+    __syncthreads();
+    if (kq > 0) return;
+    // O^T layout: every element this lane holds belongs to its own query
+    // row t_abs, so the merge factors are per-lane scalars.
+    float mall = m_run;
+#pragma unroll
+    for (int q = 1; q < KSPLIT; ++q) mall = fmaxf(mall, xm[(wave + (q - 1) * nh) * 64 + lane]);
+    const float a0 = fast_exp2(m_run - mall);
+    float aq[KSPLIT];
+    l *= a0;
+#pragma unroll
+    for (int q = 1; q < KSPLIT; ++q) {
+      const int sl = wave + (q - 1) * nh;  // slot of this row block's key group q
+      aq[q] = fast_exp2(xm[sl * 64 + lane] - mall);  // 0 for a group with no tile
+      l += aq[q] * xl[sl * 64 + lane];
+    }
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        float v = o[db][i] * a0;
+#pragma unroll
+        for (int q = 1; q < KSPLIT; ++q)
+          v += aq[q] * xo[((wave + (q - 1) * nh) * 16 * DB + db * 16 + i) * 64 + lane];
+        o[db][i] = v;
+      }
+  }
   if (!live) return;
-  const float l = l_run + __shfl_xor(l_run, 32, 64);
   const float inv = 1.0f / l;
   if (t_abs < T) {
     float* O = (float*)p.out + (long long)hq * D * T;
@@ -715,12 +777,24 @@ __global__ __launch_bounds__(256) void prefill_f32mfma_kernel(PrefillLaunch p, i
 
 hipError_t prefill_f32_launch(const PrefillLaunch& p, hipStream_t stream) {
   const int group = p.n_head / p.n_head_kv;
-  const int nh = (group % 4 == 0) ? 4 : ((group % 2 == 0) ? 2 : 1);  // heads per workgroup
-  const int rows_wg = 32 * (4 / nh);
-  dim3 grid(p.n_head_kv * (group / nh) * ((p.seq_len + rows_wg - 1) / rows_wg));
+  int nh = (group % 4 == 0) ? 4 : ((group % 2 == 0) ? 2 : 1);  // heads per workgroup
+  auto grid_of = [&](int nh_, int ks) {
+    const int rows_wg = 32 * (4 / (nh_ * ks));
+    return p.n_head_kv * (group / nh_) * ((p.seq_len + rows_wg - 1) / rows_wg);
+  };
+  // Split each row block's keys over two wave groups (two heads per
+  // workgroup) when four-head workgroups would leave CUs idle: twice the
+  // workgroups, half the longest causal walk.
+  // (A four-way split, one head per workgroup, measured 9% slower at c2.)
+  const int ksp = (nh >= 2 && grid_of(nh, 1) < 256 && p.head_dim == 64) ? 2 : 1;
+  if (ksp > 1) nh = 2;
+  const dim3 grid(grid_of(nh, ksp));
   switch (p.head_dim) {
-    case 64: hipLaunchKernelGGL(prefill_f32mfma_kernel<64>, grid, dim3(256), 0, stream, p, nh); break;
-    case 128: hipLaunchKernelGGL(prefill_f32mfma_kernel<128>, grid, dim3(256), 0, stream, p, nh); break;
+    case 64:
+      if (ksp == 2) hipLaunchKernelGGL((prefill_f32mfma_kernel<64, 2>), grid, dim3(256), 0, stream, p, nh);
+      else hipLaunchKernelGGL((prefill_f32mfma_kernel<64, 1>), grid, dim3(256), 0, stream, p, nh);
+      break;
+    case 128: hipLaunchKernelGGL((prefill_f32mfma_kernel<128, 1>), grid, dim3(256), 0, stream, p, nh); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
