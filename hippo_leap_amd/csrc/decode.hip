@@ -202,9 +202,15 @@ __device__ void finish_workgroup(const DecodeParams& p, const float* sm_m, const
 // lane j scores column t0+j for every head of the chunk, then lanes switch to
 // owning output dims for the P.V product.
 // ---------------------------------------------------------------------------
-template <int D, bool V4>
+// HC: head slots per chunk (4, 8 or 16, at least the chunk's heads).  Slots
+// past the chunk's heads score a zero q row and are never written out; every
+// slot is computed without a branch, so the heads' dependency chains (dot
+// products, wave reductions) interleave instead of running one after another.
+template <int D, bool V4, int HC>
 __global__ __launch_bounds__(256) void decode_f32_kernel(DecodeParams p) {
-  constexpr int HC = 16;  // max heads per chunk
+  // D = 128 keeps one head at a time (uniform branches): interleaving every
+  // head's chains there needs more registers than the kernel has.
+  constexpr bool SEQ = D > 64;
   constexpr int DPL = (D + 63) / 64;  // output dims per lane
   constexpr int MERGE_FLOATS = 4 * HC * (D + 2);
   constexpr int FUSE_FLOATS = 16 * kMaxFusedSplits + 16;
@@ -290,32 +296,41 @@ __global__ __launch_bounds__(256) void decode_f32_kernel(DecodeParams p) {
       }
 #pragma unroll
       for (int h = 0; h < HC; ++h) {
-        if (h < hc) {  // uniform
+        if (SEQ && h >= hc) continue;  // uniform
 #pragma unroll
-          for (int u = 0; u < 64; u += 4) {
-            const f32x4 qv = *(const f32x4*)&sq[h * D + 64 * db + u];
+        for (int u = 0; u < 64; u += 4) {
+          const f32x4 qv = *(const f32x4*)&sq[h * D + 64 * db + u];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) s[h] = fmaf(qv[e], kv[u + e], s[h]);
-          }
+          for (int e = 0; e < 4; ++e) s[h] = fmaf(qv[e], kv[u + e], s[h]);
         }
       }
     }
     // score = dot * scale (naive.nim:3328), here in log2 units
-    float alpha[HC];
+    float alpha[HC], sv[HC], mt[HC];
+#pragma unroll
+    for (int h = 0; h < HC; ++h) mt[h] = sv[h] = valid ? s[h] * p.scale_log2 : -INFINITY;
+    if constexpr (SEQ) {
+#pragma unroll
+      for (int h = 0; h < HC; ++h)
+        if (h < hc) mt[h] = wave_max(mt[h]);
+    } else {  // wave max of every head, the butterflies of all heads interleaved
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1)
+#pragma unroll
+        for (int h = 0; h < HC; ++h) mt[h] = fmaxf(mt[h], __shfl_xor(mt[h], o, 64));
+    }
 #pragma unroll
     for (int h = 0; h < HC; ++h) {
-      if (h < hc) {
-        const float sv = valid ? s[h] * p.scale_log2 : -INFINITY;
-        const float mt = wave_max(sv);
-        const float mn = fmaxf(m_run[h], mt);
-        alpha[h] = fast_exp2(m_run[h] - mn);
-        const float pv = fast_exp2(sv - mn);
-        m_run[h] = mn;
-        l_run[h] = l_run[h] * alpha[h] + pv;  // per-lane partial, summed at the end
-        sp[wave][h][lane] = pv;
-      } else {
+      if (SEQ && h >= hc) {
         alpha[h] = 1.f;
+        continue;
       }
+      const float mn = fmaxf(m_run[h], mt[h]);
+      alpha[h] = fast_exp2(m_run[h] - mn);
+      const float pv = fast_exp2(sv[h] - mn);
+      m_run[h] = mn;
+      l_run[h] = l_run[h] * alpha[h] + pv;  // per-lane partial, summed at the end
+      sp[wave][h][lane] = pv;
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -327,17 +342,16 @@ __global__ __launch_bounds__(256) void decode_f32_kernel(DecodeParams p) {
       for (int j = 0; j < 64; ++j) vv[i][j] = j < nj ? vv[i][j] : 0.f;
 #pragma unroll
     for (int h = 0; h < HC; ++h) {
-      if (h < hc) {
+      if (SEQ && h >= hc) continue;
 #pragma unroll
-        for (int i = 0; i < DPL; ++i) acc[h][i] *= alpha[h];
+      for (int i = 0; i < DPL; ++i) acc[h][i] *= alpha[h];
 #pragma unroll
-        for (int j = 0; j < 64; j += 4) {
-          const f32x4 pw = *(const f32x4*)&sp[wave][h][j];
+      for (int j = 0; j < 64; j += 4) {
+        const f32x4 pw = *(const f32x4*)&sp[wave][h][j];
 #pragma unroll
-          for (int i = 0; i < DPL; ++i)
+        for (int i = 0; i < DPL; ++i)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) acc[h][i] = fmaf(pw[e], vv[i][j + e], acc[h][i]);
-        }
+          for (int e = 0; e < 4; ++e) acc[h][i] = fmaf(pw[e], vv[i][j + e], acc[h][i]);
       }
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -348,9 +362,22 @@ __global__ __launch_bounds__(256) void decode_f32_kernel(DecodeParams p) {
   float* sm_m = sm;
   float* sm_l = sm_m + 4 * HC;
   float* sm_o = sm_l + 4 * HC;
+  float lsum[HC];
+#pragma unroll
+  for (int h = 0; h < HC; ++h) lsum[h] = l_run[h];
+  if constexpr (SEQ) {
+#pragma unroll
+    for (int h = 0; h < HC; ++h)
+      if (h < hc) lsum[h] = wave_sum(lsum[h]);
+  } else {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1)
+#pragma unroll
+      for (int h = 0; h < HC; ++h) lsum[h] += __shfl_xor(lsum[h], o, 64);
+  }
 #pragma unroll
   for (int h = 0; h < HC; ++h) {
-    const float l = wave_sum(l_run[h]);
+    const float l = lsum[h];
     if (lane == 0 && h < hc) {
       sm_m[wave * HC + h] = m_run[h];
       sm_l[wave * HC + h] = l;
@@ -876,6 +903,15 @@ typedef void (*KernelFn)(DecodeParams);
 
 // The prefetching kernel exists for the 16-byte path only (the element-wise
 // loads of unaligned caches would not fit its registers).
+template <int D, bool V4>
+KernelFn pick_f32_hc(int hc) {
+  return hc <= 4 ? decode_f32_kernel<D, V4, 4> : (hc <= 8 ? decode_f32_kernel<D, V4, 8> : decode_f32_kernel<D, V4, 16>);
+}
+KernelFn pick_f32(int D, bool vec, int hc) {
+  if (vec) return D == 64 ? pick_f32_hc<64, true>(hc) : pick_f32_hc<128, true>(hc);
+  return D == 64 ? pick_f32_hc<64, false>(hc) : pick_f32_hc<128, false>(hc);
+}
+
 template <int D, int DT, bool STEP>
 KernelFn pick_mfma(bool vec, bool pipe) {
   if (vec || DT == HL_FP8)  // fp8 caches are tiled: always vector loads
@@ -889,11 +925,8 @@ KernelFn pick_mfma(bool vec, bool pipe, bool step) {
   return step ? pick_mfma<D, DT, true>(vec, pipe) : pick_mfma<D, DT, false>(vec, pipe);
 }
 
-KernelFn pick_kernel(int kv_dtype, int D, bool vec, bool pipe, bool step) {
-  if (kv_dtype == HL_F32) {
-    if (vec) return D == 64 ? decode_f32_kernel<64, true> : decode_f32_kernel<128, true>;
-    return D == 64 ? decode_f32_kernel<64, false> : decode_f32_kernel<128, false>;
-  }
+KernelFn pick_kernel(int kv_dtype, int D, bool vec, bool pipe, bool step, int hc) {
+  if (kv_dtype == HL_F32) return pick_f32(D, vec, hc);
   if (kv_dtype == HL_F16)
     return D == 64 ? pick_mfma<64, HL_F16>(vec, pipe, step) : pick_mfma<128, HL_F16>(vec, pipe, step);
   if (kv_dtype == HL_FP8)
@@ -976,7 +1009,7 @@ void decode_plan(const hl_decode_args* a, DecodePlan* plan, bool step) {
     S = s_pipe;
   } else {
     plan->pipe = false;
-    S = clamp_splits(capacity(pick_kernel(a->kv_dtype, a->head_dim, plan->vec, false, plan->step)) / units);
+    S = clamp_splits(capacity(pick_kernel(a->kv_dtype, a->head_dim, plan->vec, false, plan->step, plan->head_chunk)) / units);
   }
   if (S > kMaxFusedSplits) S = kMaxFusedSplits;
   const int tiles_per_split = tiles / S;  // the last split also takes the remainder
@@ -1037,7 +1070,7 @@ hipError_t decode_launch(const hl_decode_args* a, const DecodePlan* plan, void* 
   p.scale_log2 = scale * kLog2e;
 
   dim3 grid(plan->num_splits, a->n_head_kv * plan->n_chunks, a->batch);
-  KernelFn fn = pick_kernel(a->kv_dtype, D, plan->vec, plan->pipe, plan->step);
+  KernelFn fn = pick_kernel(a->kv_dtype, D, plan->vec, plan->pipe, plan->step, plan->head_chunk);
   hipLaunchKernelGGL(fn, grid, dim3(256), 0, stream, p);
   return hipGetLastError();
 }
