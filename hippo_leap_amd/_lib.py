@@ -14,7 +14,7 @@ LIB_PATH = os.path.join(PKG_DIR, "libhl_attn.so")
 HL_OK, HL_EINVAL, HL_ECAPACITY, HL_EUNSUPPORTED, HL_EHIP = 0, -1, -2, -3, -4
 HL_F32, HL_F16, HL_BF16, HL_FP8 = 0, 1, 2, 3
 HL_ROPE_HALF_SPLIT, HL_ROPE_INTERLEAVED = 0, 1
-HL_KV_COLMAJOR, HL_KV_TILED32 = 0, 1
+HL_KV_COLMAJOR, HL_KV_TILED32, HL_KV_PAGED32 = 0, 1, 2
 
 c_int, c_float, c_void_p, c_size_t, c_longlong = (
     ctypes.c_int, ctypes.c_float, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_longlong)
@@ -45,6 +45,7 @@ class DecodeArgs(ctypes.Structure):
         ("seq_lens", c_void_p), ("cache_batch_stride", c_longlong),
         ("q", c_void_p), ("k_cache", c_void_p), ("v_cache", c_void_p), ("out", c_void_p),
         ("scale", c_float), ("num_splits", c_int), ("kv_layout", c_int),
+        ("block_table", c_void_p), ("blocks_per_seq", c_int),
     ]
 
 
@@ -58,7 +59,7 @@ class RopeStoreArgs(ctypes.Structure):
         ("k_cache", c_void_p), ("v_cache", c_void_p),
         ("positions", c_void_p), ("pos", c_int),
         ("q_norm_w", c_void_p), ("k_norm_w", c_void_p), ("eps", c_float),
-        ("kv_layout", c_int),
+        ("kv_layout", c_int), ("block_table", c_void_p), ("blocks_per_seq", c_int),
     ]
 
 
@@ -73,6 +74,7 @@ class PrefillArgs(ctypes.Structure):
         ("k_cache", c_void_p), ("v_cache", c_void_p), ("kv_dtype", c_int),
         ("max_len", c_int), ("start_pos", c_int), ("scale", c_float),
         ("write_back_qk", c_int), ("out_dtype", c_int), ("kv_layout", c_int),
+        ("block_table", c_void_p),
     ]
 
 

@@ -25,8 +25,9 @@ import ctypes
 import torch
 
 from . import _lib
-from ._lib import (HL_BF16, HL_F16, HL_F32, HL_FP8, HL_KV_COLMAJOR, HL_KV_TILED32, HL_ROPE_HALF_SPLIT,
-                   DecodeArgs, PrefillArgs, RopeStoreArgs, check)
+from ._lib import (HL_BF16, HL_F16, HL_F32, HL_FP8, HL_KV_COLMAJOR, HL_KV_PAGED32,  # noqa: F401
+                   HL_KV_TILED32, HL_ROPE_HALF_SPLIT, DecodeArgs, PrefillArgs, RopeStoreArgs,
+                   check)
 
 _DT = {torch.float32: HL_F32, torch.float16: HL_F16, torch.bfloat16: HL_BF16,
        torch.float8_e4m3fn: HL_FP8, torch.uint8: HL_FP8}
@@ -176,7 +177,9 @@ def device_info() -> dict:
 # ---------------------------------------------------------------------------
 def decode_args(q, k_cache, v_cache, out, n_head, n_head_kv, head_dim, max_len, seq_len,
                 seq_lens=None, cache_batch_stride=0, scale=0.0, num_splits=0,
-                kv_layout=HL_KV_COLMAJOR) -> DecodeArgs:
+                kv_layout=HL_KV_COLMAJOR, block_table=None) -> DecodeArgs:
+    """Arguments of hl_attn_decode.  block_table (paged layout): int32
+    device tensor [B, blocks_per_seq] of page indices."""
     a = DecodeArgs()
     a.batch = q.numel() // (n_head * head_dim)
     a.n_head, a.n_head_kv, a.head_dim = n_head, n_head_kv, head_dim
@@ -187,8 +190,36 @@ def decode_args(q, k_cache, v_cache, out, n_head, n_head_kv, head_dim, max_len, 
     a.q, a.k_cache, a.v_cache, a.out = q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), out.data_ptr()
     a.scale, a.num_splits = scale, num_splits
     a.kv_layout = kv_layout
-    a._tensors = (q, k_cache, v_cache, out, seq_lens)  # the struct holds raw pointers into these
+    _set_table(a, block_table)
+    a._tensors = (q, k_cache, v_cache, out, seq_lens, block_table)  # the struct holds raw pointers
     return a
+
+
+def _set_table(a, block_table, per_seq=True):
+    if block_table is None:
+        return
+    a.block_table = block_table.data_ptr()
+    if per_seq:
+        a.blocks_per_seq = block_table.shape[-1]
+
+
+def kv_to_paged(cache, n_head_kv, head_dim, max_len, block_table, n_pages):
+    """Column-major caches [B][Hkv*D, max_len] -> an HL_KV_PAGED32 pool of
+    n_pages pages [Hkv][D][32]: tile j of sequence b goes to page
+    block_table[b, j] (pages no entry names stay zero)."""
+    B = cache.numel() // (n_head_kv * head_dim * max_len)
+    nt = max_len // 32
+    t = cache.reshape(B, n_head_kv, head_dim, nt, 32).permute(0, 3, 1, 2, 4)  # [B, nt, Hkv, D, 32]
+    pool = torch.zeros(n_pages, n_head_kv, head_dim, 32, dtype=cache.dtype, device=cache.device)
+    pool[block_table[:, :nt].reshape(-1).long()] = t.reshape(B * nt, n_head_kv, head_dim, 32)
+    return pool.reshape(-1)
+
+
+def kv_from_paged(pool, n_head_kv, head_dim, max_len, block_table):
+    """Inverse of kv_to_paged: the column-major caches [B][Hkv*D, max_len]."""
+    B, nt = block_table.shape[0], max_len // 32
+    pages = pool.reshape(-1, n_head_kv, head_dim, 32)[block_table[:, :nt].reshape(-1).long()]
+    return pages.reshape(B, nt, n_head_kv, head_dim, 32).permute(0, 2, 3, 1, 4).reshape(-1)
 
 
 def kv_to_tiled(cache, n_head_kv, head_dim, max_len):
@@ -230,7 +261,8 @@ def attn_decode(args: DecodeArgs, workspace=None, stream=None) -> None:
 def rope_store_args(q, k, v, k_cache, v_cache, n_head_q, n_head_kv, head_dim, max_len, pos,
                     rope_base, rope_dim=0, rope_style=HL_ROPE_HALF_SPLIT, positions=None,
                     q_norm_w=None, k_norm_w=None, eps=1e-6, cache_batch_stride=0,
-                    use_installed_theta=False, kv_layout=HL_KV_COLMAJOR) -> RopeStoreArgs:
+                    use_installed_theta=False, kv_layout=HL_KV_COLMAJOR,
+                    block_table=None) -> RopeStoreArgs:
     a = RopeStoreArgs()
     a.batch = q.numel() // (n_head_q * head_dim)
     a.n_head_q, a.n_head_kv, a.head_dim = n_head_q, n_head_kv, head_dim
@@ -245,7 +277,8 @@ def rope_store_args(q, k, v, k_cache, v_cache, n_head_q, n_head_kv, head_dim, ma
     a.k_norm_w = k_norm_w.data_ptr() if k_norm_w is not None else None
     a.eps = eps
     a.kv_layout = kv_layout
-    a._tensors = (q, k, v, k_cache, v_cache, positions, q_norm_w, k_norm_w)
+    _set_table(a, block_table)
+    a._tensors = (q, k, v, k_cache, v_cache, positions, q_norm_w, k_norm_w, block_table)
     return a
 
 
@@ -278,8 +311,9 @@ def prefill_args(q, k, v, out, n_head, n_head_kv, head_dim, seq_len, rope_base=0
                  apply_rope=False, rope_dim=0, rope_style=HL_ROPE_HALF_SPLIT, q_norm_w=None,
                  k_norm_w=None, eps=1e-6, k_cache=None, v_cache=None, max_len=0, start_pos=0,
                  scale=0.0, write_back_qk=False, use_installed_theta=False,
-                 kv_layout=HL_KV_COLMAJOR) -> PrefillArgs:
-    """Arguments of hl_attn_prefill; the output dtype is taken from `out`."""
+                 kv_layout=HL_KV_COLMAJOR, block_table=None) -> PrefillArgs:
+    """Arguments of hl_attn_prefill; the output dtype is taken from `out`.
+    block_table (paged layout): int32 device tensor of this sequence's pages."""
     a = PrefillArgs()
     a.n_head, a.n_head_kv, a.head_dim, a.seq_len = n_head, n_head_kv, head_dim, seq_len
     a.io_dtype = dtype_code(q)
@@ -296,7 +330,8 @@ def prefill_args(q, k, v, out, n_head, n_head_kv, head_dim, seq_len, rope_base=0
     a.write_back_qk = int(write_back_qk)
     a.out_dtype = dtype_code(out)
     a.kv_layout = kv_layout
-    a._tensors = (q, k, v, out, q_norm_w, k_norm_w, k_cache, v_cache)
+    _set_table(a, block_table, per_seq=False)
+    a._tensors = (q, k, v, out, q_norm_w, k_norm_w, k_cache, v_cache, block_table)
     return a
 
 

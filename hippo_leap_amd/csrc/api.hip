@@ -109,7 +109,7 @@ extern "C" {
 
 const char* hl_last_error(void) { return g_err; }
 
-int hl_abi_version(void) { return 2; }  // 2: kv_layout in the decode, rope/store and prefill args
+int hl_abi_version(void) { return 3; }  // 2: kv_layout in the args; 3: block_table (paged caches)
 
 int hl_device_info_get(hl_device_info* info) {
   if (!info) return fail(HL_EINVAL, "info is null");
@@ -346,20 +346,31 @@ int hl_gpu_store_kv_pair(float* k_cache, const float* k_src, float* v_cache, con
 // ---------------------------------------------------------------------------
 // KV-cache layout
 // ---------------------------------------------------------------------------
-// Tiled caches are read with vector loads of whole 32-column tile rows:
-// fp16/bf16/fp8, whole tiles (max_len % 32), aligned sequences and caches.
-// fp8 caches exist only in the tiled layout.
+// Tiled and paged caches are read with vector loads of whole 32-column tile
+// rows: fp16/bf16/fp8, whole tiles (max_len % 32), aligned sequences and
+// caches; paged caches also need a block table covering max_len columns.
+// fp8 caches exist only in those two layouts.
 static int check_layout(int layout, int kv_dtype, int max_len, long long stride, const void* kc,
-                        const void* vc, const char* who) {
+                        const void* vc, const void* table, int bps, const char* who) {
   if (layout == HL_KV_COLMAJOR) {
-    if (kv_dtype == HL_FP8) return fail(HL_EUNSUPPORTED, "%s: fp8 KV caches need the tiled layout", who);
+    if (kv_dtype == HL_FP8) return fail(HL_EUNSUPPORTED, "%s: fp8 KV caches need the tiled or paged layout", who);
     return HL_OK;
   }
-  if (layout != HL_KV_TILED32) return fail(HL_EINVAL, "%s: unknown kv_layout %d", who, layout);
-  if (kv_dtype == HL_F32) return fail(HL_EUNSUPPORTED, "%s: tiled KV caches are fp16/bf16/fp8 only", who);
-  if (max_len % 32) return fail(HL_EINVAL, "%s: tiled KV caches need max_len %% 32 == 0 (got %d)", who, max_len);
-  if (stride % 8) return fail(HL_EINVAL, "%s: tiled KV caches need a batch stride multiple of 8", who);
-  if (!aligned16(kc) || !aligned16(vc)) return fail(HL_EINVAL, "%s: tiled KV caches must be 16-byte aligned", who);
+  if (layout != HL_KV_TILED32 && layout != HL_KV_PAGED32)
+    return fail(HL_EINVAL, "%s: unknown kv_layout %d", who, layout);
+  if (kv_dtype == HL_F32)
+    return fail(HL_EUNSUPPORTED, "%s: tiled and paged KV caches are fp16/bf16/fp8 only", who);
+  if (max_len % 32)
+    return fail(HL_EINVAL, "%s: tiled and paged KV caches need max_len %% 32 == 0 (got %d)", who, max_len);
+  if (layout == HL_KV_TILED32 && stride % 8)
+    return fail(HL_EINVAL, "%s: tiled KV caches need a batch stride multiple of 8", who);
+  if (!aligned16(kc) || !aligned16(vc))
+    return fail(HL_EINVAL, "%s: tiled and paged KV caches must be 16-byte aligned", who);
+  if (layout == HL_KV_PAGED32) {
+    if (!table) return fail(HL_EINVAL, "%s: paged KV caches need a block table", who);
+    if (bps < max_len / 32)
+      return fail(HL_EINVAL, "%s: blocks_per_seq %d < max_len/32 = %d", who, bps, max_len / 32);
+  }
   return HL_OK;
 }
 
@@ -383,7 +394,7 @@ static int validate_decode(const hl_decode_args* a) {
   if (a->cache_batch_stride != 0 && a->cache_batch_stride < dense)
     return fail(HL_EINVAL, "decode: cache_batch_stride smaller than one sequence's cache");
   return check_layout(a->kv_layout, a->kv_dtype, a->max_len, a->cache_batch_stride ? a->cache_batch_stride : dense,
-                      a->k_cache, a->v_cache, "decode");
+                      a->k_cache, a->v_cache, a->block_table, a->blocks_per_seq, "decode");
 }
 
 size_t hl_attn_decode_workspace_bytes(const hl_decode_args* a) {
@@ -488,7 +499,7 @@ static int rope_store_op(const hl_rope_store_args* a, HeadVecOp& op) {
   if (a->cache_batch_stride != 0 && a->cache_batch_stride < dense)
     return fail(HL_EINVAL, "rope_store: cache_batch_stride smaller than one sequence's cache");
   if ((rc = check_layout(a->kv_layout, a->kv_dtype, a->max_len, a->cache_batch_stride ? a->cache_batch_stride : dense,
-                         a->k_cache, a->v_cache, "rope_store")))
+                         a->k_cache, a->v_cache, a->block_table, a->blocks_per_seq, "rope_store")))
     return rc;
   memset(&op, 0, sizeof(op));
   if ((rc = theta_for(a->use_installed_theta, rope_dim, a->rope_base, op.theta))) return rc;
@@ -512,6 +523,8 @@ static int rope_store_op(const hl_rope_store_args* a, HeadVecOp& op) {
   op.max_len = a->max_len;
   op.batch_stride = a->cache_batch_stride ? a->cache_batch_stride : dense;
   op.kv_layout = a->kv_layout;
+  op.block_table = a->block_table;
+  op.bps = a->blocks_per_seq;
   op.q_norm_w = a->q_norm_w;
   op.k_norm_w = a->k_norm_w;
   op.eps = a->eps;
@@ -536,7 +549,9 @@ static int validate_step(const hl_rope_store_args* rs, const hl_decode_args* at,
   if (rs->batch != at->batch || rs->n_head_q != at->n_head || rs->n_head_kv != at->n_head_kv ||
       rs->head_dim != at->head_dim || rs->kv_dtype != at->kv_dtype || rs->max_len != at->max_len ||
       rs->cache_batch_stride != at->cache_batch_stride || rs->q != at->q ||
-      rs->k_cache != at->k_cache || rs->v_cache != at->v_cache || rs->kv_layout != at->kv_layout)
+      rs->k_cache != at->k_cache || rs->v_cache != at->v_cache || rs->kv_layout != at->kv_layout ||
+      (at->kv_layout == HL_KV_PAGED32 &&
+       (rs->block_table != at->block_table || rs->blocks_per_seq != at->blocks_per_seq)))
     return fail(HL_EINVAL, "decode_step: rope_store and decode args describe different tensors");
   if (at->seq_lens) return fail(HL_EINVAL, "decode_step: lengths come from the positions (seq_lens must be null)");
   if (!rs->positions && at->seq_len != rs->pos + 1)
@@ -613,9 +628,11 @@ static int validate_prefill(const hl_prefill_args* a, PrefillPlan* pl) {
     if (a->start_pos < 0) return fail(HL_EINVAL, "prefill: start_pos < 0");
     if ((long long)a->start_pos + a->seq_len > a->max_len)
       return fail(HL_ECAPACITY, "prefill exceeds KV cache capacity");
-    if ((rc = check_layout(a->kv_layout, a->kv_dtype, a->max_len, 0, a->k_cache, a->v_cache, "prefill")))
+    if ((rc = check_layout(a->kv_layout, a->kv_dtype, a->max_len, 0, a->k_cache, a->v_cache,
+                           a->block_table, a->max_len / 32, "prefill")))
       return rc;
-  } else if (a->kv_layout != HL_KV_COLMAJOR && a->kv_layout != HL_KV_TILED32) {
+  } else if (a->kv_layout != HL_KV_COLMAJOR && a->kv_layout != HL_KV_TILED32 &&
+             a->kv_layout != HL_KV_PAGED32) {
     return fail(HL_EINVAL, "prefill: unknown kv_layout %d", a->kv_layout);
   }
   if (a->apply_rope) {
@@ -684,6 +701,7 @@ int hl_attn_prefill(const hl_prefill_args* a, void* workspace, size_t ws_bytes, 
   op.kv_dtype = a->kv_dtype;
   op.max_len = a->max_len;
   op.kv_layout = a->kv_layout;
+  op.block_table = a->block_table;
   op.start_pos = a->start_pos;
   op.n_head = a->n_head;
   op.n_head_kv = a->n_head_kv;

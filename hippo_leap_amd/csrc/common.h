@@ -126,6 +126,14 @@ __host__ __device__ __forceinline__ int64_t kv_off(int layout, int d, int t, int
                                  : (int64_t)d * max_len + t;
 }
 
+// Paged caches (HL_KV_PAGED32): offset of element (d, t) of kv head h of
+// sequence b in the pool, through that sequence's row of the block table.
+__device__ __forceinline__ int64_t kv_paged_off(const int* table, int bps, int b, int n_head_kv, int h,
+                                                int D, int d, int t) {
+  const int64_t page = table[(int64_t)b * bps + (t >> 5)];
+  return page * ((int64_t)n_head_kv * D * 32) + ((int64_t)h * D + d) * 32 + (t & 31);
+}
+
 // ---------------------------------------------------------------------------
 // Wave64 reductions (xor butterflies over ds_swizzle / DPP via __shfl_xor).
 // ---------------------------------------------------------------------------

@@ -49,7 +49,9 @@ struct DecodeParams {
   long long batch_stride;
   int n_head, n_head_kv, head_dim, group, head_chunk, n_chunks;
   int max_len, seq_len, split_len, num_splits;
-  int kv_layout;  // HL_KV_COLMAJOR | HL_KV_TILED32 (VEC kernels only)
+  int kv_layout;  // HL_KV_COLMAJOR | HL_KV_TILED32 | HL_KV_PAGED32 (the last two: VEC kernels only)
+  const int* block_table;  // HL_KV_PAGED32: [B][bps] page of each 32-column tile
+  int bps;
   float scale_log2;
   // Fused decode step (STEP kernels only): q above is the raw new-token
   // activation; k_act / v_act are the new token's k and v.  The kernel applies
@@ -66,6 +68,7 @@ struct DecodeParams {
 };
 
 constexpr int kMaxFusedSplits = 256;
+constexpr long long kPagedMaxSplit = 32768;  // columns per split of a paged cache
 
 // Attention length of sequence b: the new token's column + 1 in a decode
 // step with per-sequence positions, else seq_lens[b] or seq_len.
@@ -514,7 +517,11 @@ __global__ __launch_bounds__(256, PIPE ? (D == 64 ? 2 : 1) : 4) void decode_mfma
   const bool has_new = STEP && s0 <= newc && newc < s_end;
   const int s1 = has_new ? newc : s_end;  // end of the columns read from the cache
 
-  const long long base = (long long)b * p.batch_stride + (long long)kvh * D * p.max_len;
+  // Paged caches: this head's [D][32] block inside every page; the page of
+  // each tile comes from the block table (see page_of below).
+  const bool paged = VEC && p.kv_layout == HL_KV_PAGED32;
+  const long long base = paged ? (long long)kvh * D * 32
+                               : (long long)b * p.batch_stride + (long long)kvh * D * p.max_len;
   const elem_t* K = (const elem_t*)p.k + base;
   const elem_t* V = (const elem_t*)p.v + base;
   uint16_t* kt = (uint16_t*)lds_raw + wave * D * PITCH;
@@ -527,12 +534,34 @@ __global__ __launch_bounds__(256, PIPE ? (D == 64 ? 2 : 1) : 4) void decode_mfma
   // Tiled caches (VEC only): tile t0 / 32 of the head is [D][32] at
   // (t0 / 32) * D * 32, rows 32 elements apart; the address form is selected
   // without a branch so that both layouts issue the same loads.
-  const bool tiled = VEC && p.kv_layout == HL_KV_TILED32;
+  // Paged: lane i of register q holds the page of this wave's tile
+  // 64q + i (columns s0 + 32*wave + 128*(64q + i)), read with readlane; up
+  // to 256 tiles per wave (the plan keeps splits within 32768 columns).
+  // Pages past the sequence's last column are never touched (clamped).
+  const bool tiled = VEC && (p.kv_layout == HL_KV_TILED32 || paged);
   const int rstride = tiled ? 32 : p.max_len;
+  int pg[4] = {0, 0, 0, 0}, pg_first = 0;
+  if (paged) {
+    const int* row = p.block_table + (long long)b * p.bps;
+    const int first = s0 >> 5, lastp = min((L - 1) >> 5, p.max_len / 32 - 1);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) pg[q] = row[min(first + wave + 4 * (lane + 64 * q), lastp)];
+    pg_first = row[min(first, lastp)];
+  }
+  const long long page_elems = (long long)p.n_head_kv * D * 32;
+  // Element offset of tile t0's [D][32] block (t0 is this wave's own tile,
+  // or s0 for a wave that has none: wave-uniform either way).
+  auto page_of = [&](int t0) -> long long {
+    const int rel = (t0 >> 5) - (s0 >> 5);
+    if ((rel & 3) != wave) return (long long)pg_first * page_elems;
+    const int i = rel >> 2, q = i >> 6;
+    const int v = q == 0 ? pg[0] : (q == 1 ? pg[1] : (q == 2 ? pg[2] : pg[3]));
+    return (long long)__builtin_amdgcn_readlane(v, i & 63) * page_elems;
+  };
   auto load_tile = [&](int t0, raw_t* kr, raw_t* vr) {
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (VEC) {
-      const long long tb = tiled ? (long long)(t0 >> 5) * (D * 32) : 0;
+      const long long tb = paged ? page_of(t0) : (tiled ? (long long)(t0 >> 5) * (D * 32) : 0);
       const int ck = tiled ? 8 * (lane & 3) : min(t0 + 8 * (lane & 3), p.max_len - 8);
       const int cv = tiled ? 8 * g : min(t0 + 8 * g, p.max_len - 8);
       if constexpr (DT == HL_FP8) {  // 8-byte loads of 8 e4m3 values
@@ -862,7 +891,9 @@ __global__ __launch_bounds__(256, PIPE ? (D == 64 ? 2 : 1) : 4) void decode_mfma
     finish_workgroup<D>(p, sm_m, sm_l, sm_o, hc, b, kvh, chunk, hq0, split, HS, [&]() {
       if (has_new && chunk == 0) {
         for (int i = tid; i < 2 * D; i += 256) {
-          const long long at = base + kv_off(p.kv_layout, i < D ? i : i - D, newc, D, p.max_len);
+          const int dd = i < D ? i : i - D;
+          const long long at = paged ? kv_paged_off(p.block_table, p.bps, b, p.n_head_kv, kvh, D, dd, newc)
+                                     : base + kv_off(p.kv_layout, dd, newc, D, p.max_len);
           if constexpr (DT == HL_FP8)  // snew holds the fp16 form of an e4m3 value: exact
             ((uint8_t*)(i < D ? p.k : p.v))[at] = f32_to_e4m3(from_bits<DT>(snew[i]));
           else
@@ -1012,6 +1043,12 @@ void decode_plan(const hl_decode_args* a, DecodePlan* plan, bool step) {
     S = clamp_splits(capacity(pick_kernel(a->kv_dtype, a->head_dim, plan->vec, false, plan->step, plan->head_chunk)) / units);
   }
   if (S > kMaxFusedSplits) S = kMaxFusedSplits;
+  // Paged caches: a wave keeps the pages of at most 256 tiles, so no split
+  // (the last one takes the remainder) may exceed 32768 columns.
+  if (a->kv_layout == HL_KV_PAGED32)
+    while (S < tiles && S < kMaxFusedSplits &&
+           (long long)a->seq_len - (long long)(S - 1) * (tiles / S) * tile > kPagedMaxSplit)
+      ++S;
   const int tiles_per_split = tiles / S;  // the last split also takes the remainder
   plan->split_len = tiles_per_split * tile;
   plan->num_splits = S;
@@ -1063,6 +1100,8 @@ hipError_t decode_launch(const hl_decode_args* a, const DecodePlan* plan, void* 
   p.n_chunks = plan->n_chunks;
   p.max_len = a->max_len;
   p.kv_layout = a->kv_layout;
+  p.block_table = a->block_table;
+  p.bps = a->blocks_per_seq;
   p.seq_len = a->seq_len;
   p.split_len = plan->split_len;
   p.num_splits = plan->num_splits;

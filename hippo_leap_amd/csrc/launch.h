@@ -49,7 +49,9 @@ struct HeadVecOp {
   const int* positions;
   int pos;
   int batch, n_head_q, n_head_kv, head_dim, rope_dim, rope_style, do_rope, kv_dtype, max_len;
-  int kv_layout;       // HL_KV_COLMAJOR | HL_KV_TILED32
+  int kv_layout;       // HL_KV_COLMAJOR | HL_KV_TILED32 | HL_KV_PAGED32
+  const int* block_table;  // paged: [B][bps]
+  int bps;
   long long batch_stride;
   const float* q_norm_w;
   const float* k_norm_w;
@@ -79,7 +81,8 @@ struct PrologueOp {
   void* k_cache;
   void* v_cache;
   int kv_dtype, max_len, start_pos;
-  int kv_layout;      // of the caches: HL_KV_COLMAJOR | HL_KV_TILED32
+  int kv_layout;      // of the caches: HL_KV_COLMAJOR | HL_KV_TILED32 | HL_KV_PAGED32
+  const int* block_table;  // paged: this sequence's pages
   int n_head, n_head_kv, head_dim, seq_len;
   int do_rope, rope_dim, rope_style;
   const float* q_norm_w;

@@ -80,7 +80,12 @@ __global__ __launch_bounds__(64) void headvec_kernel(HeadVecOp op) {
     for (int d = lane; d < D; d += 64) x[d] = sx[d];
   if (cache) {
     const long long base = (long long)b * op.batch_stride + (long long)hv * D * op.max_len;
-    for (int d = lane; d < D; d += 64) store_elem<KDT>(cache, base + kv_off(op.kv_layout, d, pos, D, op.max_len), sx[d]);
+    for (int d = lane; d < D; d += 64) {
+      const long long at = op.kv_layout == HL_KV_PAGED32
+                               ? kv_paged_off(op.block_table, op.bps, b, op.n_head_kv, hv, D, d, pos)
+                               : base + kv_off(op.kv_layout, d, pos, D, op.max_len);
+      store_elem<KDT>(cache, at, sx[d]);
+    }
   }
 }
 
@@ -167,19 +172,29 @@ __device__ __forceinline__ void store_row8(void* base, long long off, int t, int
   }
 }
 
-// Cache columns pos .. pos+7 of row d of one kv head's block (hbase), the
-// values of tokens t .. t+7 (t + e < lim stored): 16-byte store when the 8
-// columns are contiguous and aligned in the layout (a tiled cache's 8 columns
-// are when they stay inside one 32-column tile), else element by element.
+// Where a prefill's cache columns go: one sequence, kv head h, row d.
+struct CacheMap {
+  int layout, D, max_len, n_head_kv;
+  const int* table;  // paged: the sequence's pages
+};
+__device__ __forceinline__ long long cache_off(const CacheMap& m, int h, int d, int t) {
+  if (m.layout == HL_KV_PAGED32) return kv_paged_off(m.table, 0, 0, m.n_head_kv, h, m.D, d, t);
+  return (long long)h * m.D * m.max_len + kv_off(m.layout, d, t, m.D, m.max_len);
+}
+
+// Cache columns pos .. pos+7 of row d of kv head h, the values of tokens
+// t .. t+7 (t + e < lim stored): one vector store when the 8 columns are
+// contiguous and aligned in the layout (tiled and paged caches: when they
+// stay inside one 32-column tile), else element by element.
 template <int DT>
-__device__ __forceinline__ void store_cache8(void* cache, long long hbase, int layout, int d, int pos, int D,
-                                             int max_len, int t, int lim, const float* x) {
-  if (layout == HL_KV_TILED32 && (pos & 31) > 24) {
+__device__ __forceinline__ void store_cache8(void* cache, const CacheMap& m, int h, int d, int pos,
+                                             int t, int lim, const float* x) {
+  if (m.layout != HL_KV_COLMAJOR && (pos & 31) > 24) {
 #pragma unroll
     for (int e = 0; e < 8; ++e)
-      if (t + e < lim) store_elem<DT>(cache, hbase + kv_off(layout, d, pos + e, D, max_len), x[e]);
+      if (t + e < lim) store_elem<DT>(cache, cache_off(m, h, d, pos + e), x[e]);
   } else {
-    store_row8<DT>(cache, hbase + kv_off(layout, d, pos, D, max_len), t, lim, x);
+    store_row8<DT>(cache, cache_off(m, h, d, pos), t, lim, x);
   }
 }
 
@@ -325,8 +340,8 @@ __global__ __launch_bounds__(256) void prologue_kernel(PrologueOp op) {
         for (int e = 0; e < 8; ++e) x[e] = sx[r][c8 + e];
         if (inplace) store_row8<HL_F32>(inplace, hbase + (long long)r * T + t0 + c8, t0 + c8, T, x);
         if (cache)
-          store_cache8<KDT>(cache, (long long)h * D * op.max_len, op.kv_layout, r, op.start_pos + t0 + c8, D,
-                            op.max_len, t0 + c8, T, x);
+          store_cache8<KDT>(cache, CacheMap{op.kv_layout, D, op.max_len, op.n_head_kv, op.block_table}, h, r,
+                            op.start_pos + t0 + c8, t0 + c8, T, x);
       }
     }
 
@@ -403,8 +418,8 @@ __global__ __launch_bounds__(256) void kv_prologue_kernel(PrologueOp op) {
   for (int ps = 0; ps < NP; ++ps) {
     const int row = r + 64 * ps;
     if (op.v_cache)
-      store_cache8<KDT>(op.v_cache, (long long)h * D * op.max_len, op.kv_layout, row, op.start_pos + t, D,
-                        op.max_len, t, T, v[ps]);
+      store_cache8<KDT>(op.v_cache, CacheMap{op.kv_layout, D, op.max_len, op.n_head_kv, op.block_table}, h, row,
+                        op.start_pos + t, t, T, v[ps]);
     if (t < op.t_pad) {
       float x[8];
 #pragma unroll
@@ -482,8 +497,8 @@ __global__ __launch_bounds__(256) void kv_prologue_kernel(PrologueOp op) {
   for (int ps = 0; ps < NP; ++ps) {
     const int row = r + 64 * ps;
     if (op.k_cache)
-      store_cache8<KDT>(op.k_cache, (long long)h * D * op.max_len, op.kv_layout, row, op.start_pos + t, D,
-                        op.max_len, t, T, k[ps]);
+      store_cache8<KDT>(op.k_cache, CacheMap{op.kv_layout, D, op.max_len, op.n_head_kv, op.block_table}, h, row,
+                        op.start_pos + t, t, T, k[ps]);
 #pragma unroll
     for (int e = 0; e < 8; ++e) skt[c8 + e][row ^ kt_swz(c8 + e)] = t + e < T ? f32_to_f16_bits(k[ps][e]) : (uint16_t)0;
   }

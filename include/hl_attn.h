@@ -238,6 +238,17 @@ int hl_gpu_embedding(float* dst, const float* weight, const int32_t* token_ids,
  * work); a layout for callers that own their cache format.                */
 #define HL_KV_COLMAJOR 0
 #define HL_KV_TILED32 1
+/* HL_KV_PAGED32: the caches are pools of 32-position pages.  Page p holds
+ * positions 32j .. 32j+31 of one sequence for every kv head, as [Hkv][D][32]:
+ * element (d, t) of head h of sequence b is at
+ *   block_table[b * blocks_per_seq + t/32] * (Hkv*D*32) + (h*D + d)*32 + t%32
+ * (block_table: device int32).  Each head's 32 columns are the same [D][32]
+ * tile as in HL_KV_TILED32.  Same requirements as the tiled layout
+ * (fp16/bf16/fp8, max_len % 32 == 0 with max_len/32 <= blocks_per_seq,
+ * 16-byte aligned pools); cache_batch_stride is ignored.  A page is written
+ * by the steps and prefills of its sequence only; pages of positions at or
+ * past a sequence's length are never read.                                 */
+#define HL_KV_PAGED32 2
 
 typedef struct hl_decode_args {
   int batch;                    /* B >= 1                                        */
@@ -256,7 +267,9 @@ typedef struct hl_decode_args {
   float* out;                   /* device [B][Hq*D] fp32                         */
   float scale;                  /* 0 -> 1/sqrtf(D) (naive.nim:3374)              */
   int num_splits;               /* 0 -> chosen to fill the GPU                   */
-  int kv_layout;                /* HL_KV_COLMAJOR (0) | HL_KV_TILED32            */
+  int kv_layout;                /* HL_KV_COLMAJOR (0) | HL_KV_TILED32 | PAGED32  */
+  const int* block_table;       /* HL_KV_PAGED32: device int[B][blocks_per_seq]  */
+  int blocks_per_seq;
 } hl_decode_args;
 
 /* Workspace bytes hl_attn_decode needs for these args: one 4-byte arrival
@@ -303,7 +316,9 @@ typedef struct hl_rope_store_args {
   const float* q_norm_w;        /* optional device [D]: qkNorm before RoPE       */
   const float* k_norm_w;        /* optional device [D]                           */
   float eps;
-  int kv_layout;                /* HL_KV_COLMAJOR (0) | HL_KV_TILED32            */
+  int kv_layout;                /* HL_KV_COLMAJOR (0) | HL_KV_TILED32 | PAGED32  */
+  const int* block_table;       /* HL_KV_PAGED32: device int[B][blocks_per_seq]  */
+  int blocks_per_seq;
 } hl_rope_store_args;
 
 /* One launch for the new token of B sequences: optional qkNorm of q and k
@@ -362,7 +377,9 @@ typedef struct hl_prefill_args {
                                    reference's fp32 act1) or, for fp16/bf16
                                    io, HL_F16 / HL_BF16 (RNE of the fp32 value) */
   int kv_layout;                /* of k_cache/v_cache: HL_KV_COLMAJOR (0) |
-                                   HL_KV_TILED32                                */
+                                   HL_KV_TILED32 | HL_KV_PAGED32                */
+  const int* block_table;       /* HL_KV_PAGED32: device int[max_len/32], this
+                                   sequence's pages                             */
 } hl_prefill_args;
 
 size_t hl_attn_prefill_workspace_bytes(const hl_prefill_args* a);

@@ -29,7 +29,7 @@ def test_exports_match_header(hl):
 
 
 def test_abi_version(hl):
-    assert hl.hl_abi_version() == 2
+    assert hl.hl_abi_version() == 3
 
 
 def _err(hl):
@@ -277,4 +277,22 @@ def test_fp8_kv_validation(hl):
     p = _prefill_args(k_cache=FAKE, v_cache=FAKE, kv_dtype=_lib.HL_FP8, max_len=4096)
     assert hl.hl_attn_prefill(ctypes.byref(p), None, 0, None) == _lib.HL_EUNSUPPORTED
     p = _prefill_args(io_dtype=_lib.HL_FP8)
+    assert hl.hl_attn_prefill(ctypes.byref(p), None, 0, None) == _lib.HL_EINVAL
+
+
+def test_paged_kv_validation(hl):
+    """Paged caches: a block table is required and must cover max_len."""
+    P = _lib.HL_KV_PAGED32
+    a = _decode_args(kv_layout=P, max_len=2080)
+    assert hl.hl_attn_decode(ctypes.byref(a), None, 0, None) == _lib.HL_EINVAL
+    assert "block table" in _err(hl)
+    a = _decode_args(kv_layout=P, max_len=2080, block_table=FAKE, blocks_per_seq=64)
+    assert hl.hl_attn_decode(ctypes.byref(a), None, 0, None) == _lib.HL_EINVAL
+    assert "blocks_per_seq" in _err(hl)
+    a = _decode_args(kv_layout=P, max_len=2080, block_table=FAKE, blocks_per_seq=65)
+    assert hl.hl_attn_decode_workspace_bytes(ctypes.byref(a)) > 0
+    a = _decode_args(kv_layout=P, max_len=2080, block_table=FAKE, blocks_per_seq=65,
+                     kv_dtype=_lib.HL_F32)
+    assert hl.hl_attn_decode(ctypes.byref(a), None, 0, None) == _lib.HL_EUNSUPPORTED
+    p = _prefill_args(k_cache=FAKE, v_cache=FAKE, kv_dtype=_lib.HL_BF16, max_len=4096, kv_layout=P)
     assert hl.hl_attn_prefill(ctypes.byref(p), None, 0, None) == _lib.HL_EINVAL
