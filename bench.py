@@ -22,6 +22,8 @@ Extra objects on the same JSON line:
     [D][32]), same values.
   decode_c5_fp8, decode_c3_fp8: the same steps with fp8 e4m3 caches (tiled),
     GB/s of the fp8 bytes (half of the bf16/fp16 bytes per position).
+  decode_c5_paged: the c5 step with the caches in a page pool (HL_KV_PAGED32)
+    reached through a shuffled block table.
   decode_c1, prefill_c2: configs[0] and configs[1], the reference's fp32
     call contract (hl_gpu_attention_decode; fp32 prefill with RoPE 1e4 and
     the cache write), timed for reference: they are parity cases, not the
@@ -128,7 +130,14 @@ class DecodeWorkload:
             else (lambda x: x.to(kv_dtype))  # fp8: e4m3 bytes
         self.kc = [cast(torch.randn(n, generator=g, device="cuda") * sigma) for _ in range(n_sets)]
         self.vc = [cast(torch.randn(n, generator=g, device="cuda") * sigma) for _ in range(n_sets)]
-        if kv_layout:  # same values, stored as 32-column tiles
+        self.table = None
+        if kv_layout == 2:  # same values in a page pool, through a shuffled block table
+            nt = self.max_len // 32
+            perm = torch.randperm(B * nt, generator=torch.Generator().manual_seed(seed))
+            self.table = perm.reshape(B, nt).to(torch.int32).cuda()
+            self.kc = [A.kv_to_paged(c, hkv, d, self.max_len, self.table, B * nt) for c in self.kc]
+            self.vc = [A.kv_to_paged(c, hkv, d, self.max_len, self.table, B * nt) for c in self.vc]
+        elif kv_layout:  # same values, stored as 32-column tiles
             self.kc = [A.kv_to_tiled(c, hkv, d, self.max_len) for c in self.kc]
             self.vc = [A.kv_to_tiled(c, hkv, d, self.max_len) for c in self.vc]
         self.kv_layout = kv_layout
@@ -142,12 +151,12 @@ class DecodeWorkload:
         self.base = base
         self.out = torch.empty(B * hq * d, device="cuda")
         self.args = [A.decode_args(self.q, kc, vc, self.out, hq, hkv, d, self.max_len, self.L,
-                                   kv_layout=kv_layout)
+                                   kv_layout=kv_layout, block_table=self.table)
                      for kc, vc in zip(self.kc, self.vc)]
         self.ws = A.decode_workspace(self.args[0])
         self.rs = [A.rope_store_args(self.q, self.k, self.v, kc, vc, hq, hkv, d, self.max_len, prev,
                                      base, q_norm_w=self.wq, k_norm_w=self.wk, eps=1e-6,
-                                     kv_layout=kv_layout)
+                                     kv_layout=kv_layout, block_table=self.table)
                    for kc, vc in zip(self.kc, self.vc)]
         self.step_ws = A.decode_step_workspace(self.rs[0], self.args[0])
         self.kv_bytes = 2 * B * hkv * d * self.L * self.kc[0].element_size()  # columns < L
@@ -157,7 +166,8 @@ class DecodeWorkload:
         s = i % len(self.kc)
         self.A.rope_store_decode(self.q, self.k, self.v, self.kc[s], self.vc[s], self.hq, self.hkv,
                                  self.d, self.max_len, self.prev, self.base, q_norm_w=self.wq,
-                                 k_norm_w=self.wk, eps=1e-6, kv_layout=self.kv_layout)
+                                 k_norm_w=self.wk, eps=1e-6, kv_layout=self.kv_layout,
+                                 block_table=self.table)
 
     def attend(self, i):
         self.A.attn_decode(self.args[i % len(self.args)], self.ws)
@@ -256,7 +266,7 @@ def decode_extra(wl, t, workload):
     ach = wl.kv_bytes / (t["kernel"] * 1e-3) / 1e9
     return {
         "workload": workload,
-        "kv_layout": "tiled32" if wl.kv_layout else "colmajor (reference)",
+        "kv_layout": {0: "colmajor (reference)", 1: "tiled32", 2: "paged32"}[wl.kv_layout],
         "kv_dtype": {1: "fp8 e4m3", 2: "bf16/fp16"}.get(wl.kc[0].element_size(), "fp32"),
         "value": round(wl.kv_bytes / (t["step"] * 1e-3) / 1e9, 2), "unit": "GB/s",
         "ms_per_step": round(t["step"], 5),
@@ -526,7 +536,8 @@ def main():
     if args.only in ("all", "c5"):
         for layout, key, kvdt in ((0, "decode_c5", torch.bfloat16),
                                   (1, "decode_c5_tiled", torch.bfloat16),
-                                  (1, "decode_c5_fp8", torch.float8_e4m3fn)):
+                                  (1, "decode_c5_fp8", torch.float8_e4m3fn),
+                                  (2, "decode_c5_paged", torch.bfloat16)):
             if args.layouts == ("tiled" if layout == 0 else "colmajor"):
                 continue
             log(f"{key} ...")

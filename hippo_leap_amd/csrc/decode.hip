@@ -469,8 +469,11 @@ __device__ __forceinline__ u16x8 mask_row8(u16x8 r, int col, int lim) {
   return r;
 }
 
-template <int D, int DT, bool VEC, bool PIPE, bool STEP>
+// PG: paged caches (a compile-time variant, so the other layouts carry no
+// page lookups).
+template <int D, int DT, bool VEC, bool PIPE, bool STEP, bool PG = false>
 __global__ __launch_bounds__(256, PIPE ? (D == 64 ? 2 : 1) : 4) void decode_mfma_kernel(DecodeParams p) {
+  static_assert(!PG || VEC, "paged caches are read with vector loads only");
   // MFMA operand type: the storage type, except fp8 caches, which are
   // converted to fp16 (exactly) as their tiles arrive.
   constexpr int MT = DT == HL_FP8 ? HL_F16 : DT;
@@ -519,7 +522,7 @@ __global__ __launch_bounds__(256, PIPE ? (D == 64 ? 2 : 1) : 4) void decode_mfma
 
   // Paged caches: this head's [D][32] block inside every page; the page of
   // each tile comes from the block table (see page_of below).
-  const bool paged = VEC && p.kv_layout == HL_KV_PAGED32;
+  constexpr bool paged = PG;
   const long long base = paged ? (long long)kvh * D * 32
                                : (long long)b * p.batch_stride + (long long)kvh * D * p.max_len;
   const elem_t* K = (const elem_t*)p.k + base;
@@ -541,7 +544,7 @@ __global__ __launch_bounds__(256, PIPE ? (D == 64 ? 2 : 1) : 4) void decode_mfma
   const bool tiled = VEC && (p.kv_layout == HL_KV_TILED32 || paged);
   const int rstride = tiled ? 32 : p.max_len;
   int pg[4] = {0, 0, 0, 0}, pg_first = 0;
-  if (paged) {
+  if constexpr (paged) {
     const int* row = p.block_table + (long long)b * p.bps;
     const int first = s0 >> 5, lastp = min((L - 1) >> 5, p.max_len / 32 - 1);
 #pragma unroll
@@ -561,7 +564,9 @@ __global__ __launch_bounds__(256, PIPE ? (D == 64 ? 2 : 1) : 4) void decode_mfma
   auto load_tile = [&](int t0, raw_t* kr, raw_t* vr) {
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (VEC) {
-      const long long tb = paged ? page_of(t0) : (tiled ? (long long)(t0 >> 5) * (D * 32) : 0);
+      long long tb;
+      if constexpr (paged) tb = page_of(t0);
+      else tb = tiled ? (long long)(t0 >> 5) * (D * 32) : 0;
       const int ck = tiled ? 8 * (lane & 3) : min(t0 + 8 * (lane & 3), p.max_len - 8);
       const int cv = tiled ? 8 * g : min(t0 + 8 * g, p.max_len - 8);
       if constexpr (DT == HL_FP8) {  // 8-byte loads of 8 e4m3 values
@@ -892,8 +897,9 @@ __global__ __launch_bounds__(256, PIPE ? (D == 64 ? 2 : 1) : 4) void decode_mfma
       if (has_new && chunk == 0) {
         for (int i = tid; i < 2 * D; i += 256) {
           const int dd = i < D ? i : i - D;
-          const long long at = paged ? kv_paged_off(p.block_table, p.bps, b, p.n_head_kv, kvh, D, dd, newc)
-                                     : base + kv_off(p.kv_layout, dd, newc, D, p.max_len);
+          long long at;
+          if constexpr (paged) at = kv_paged_off(p.block_table, p.bps, b, p.n_head_kv, kvh, D, dd, newc);
+          else at = base + kv_off(p.kv_layout, dd, newc, D, p.max_len);
           if constexpr (DT == HL_FP8)  // snew holds the fp16 form of an e4m3 value: exact
             ((uint8_t*)(i < D ? p.k : p.v))[at] = f32_to_e4m3(from_bits<DT>(snew[i]));
           else
@@ -944,25 +950,27 @@ KernelFn pick_f32(int D, bool vec, int hc) {
 }
 
 template <int D, int DT, bool STEP>
-KernelFn pick_mfma(bool vec, bool pipe) {
-  if (vec || DT == HL_FP8)  // fp8 caches are tiled: always vector loads
+KernelFn pick_mfma(bool vec, bool pipe, bool paged) {
+  if (paged)
+    return pipe ? decode_mfma_kernel<D, DT, true, true, STEP, true> : decode_mfma_kernel<D, DT, true, false, STEP, true>;
+  if (vec || DT == HL_FP8)  // fp8 caches are tiled or paged: always vector loads
     return pipe ? decode_mfma_kernel<D, DT, true, true, STEP> : decode_mfma_kernel<D, DT, true, false, STEP>;
   if constexpr (DT != HL_FP8) return decode_mfma_kernel<D, DT, false, false, STEP>;
   return nullptr;
 }
 
 template <int D, int DT>
-KernelFn pick_mfma(bool vec, bool pipe, bool step) {
-  return step ? pick_mfma<D, DT, true>(vec, pipe) : pick_mfma<D, DT, false>(vec, pipe);
+KernelFn pick_mfma(bool vec, bool pipe, bool step, bool paged) {
+  return step ? pick_mfma<D, DT, true>(vec, pipe, paged) : pick_mfma<D, DT, false>(vec, pipe, paged);
 }
 
-KernelFn pick_kernel(int kv_dtype, int D, bool vec, bool pipe, bool step, int hc) {
+KernelFn pick_kernel(int kv_dtype, int D, bool vec, bool pipe, bool step, int hc, bool paged) {
   if (kv_dtype == HL_F32) return pick_f32(D, vec, hc);
   if (kv_dtype == HL_F16)
-    return D == 64 ? pick_mfma<64, HL_F16>(vec, pipe, step) : pick_mfma<128, HL_F16>(vec, pipe, step);
+    return D == 64 ? pick_mfma<64, HL_F16>(vec, pipe, step, paged) : pick_mfma<128, HL_F16>(vec, pipe, step, paged);
   if (kv_dtype == HL_FP8)
-    return D == 64 ? pick_mfma<64, HL_FP8>(vec, pipe, step) : pick_mfma<128, HL_FP8>(vec, pipe, step);
-  return D == 64 ? pick_mfma<64, HL_BF16>(vec, pipe, step) : pick_mfma<128, HL_BF16>(vec, pipe, step);
+    return D == 64 ? pick_mfma<64, HL_FP8>(vec, pipe, step, paged) : pick_mfma<128, HL_FP8>(vec, pipe, step, paged);
+  return D == 64 ? pick_mfma<64, HL_BF16>(vec, pipe, step, paged) : pick_mfma<128, HL_BF16>(vec, pipe, step, paged);
 }
 
 // Resident workgroups of a kernel on the whole device (cached).
@@ -1040,7 +1048,8 @@ void decode_plan(const hl_decode_args* a, DecodePlan* plan, bool step) {
     S = s_pipe;
   } else {
     plan->pipe = false;
-    S = clamp_splits(capacity(pick_kernel(a->kv_dtype, a->head_dim, plan->vec, false, plan->step, plan->head_chunk)) / units);
+    S = clamp_splits(capacity(pick_kernel(a->kv_dtype, a->head_dim, plan->vec, false, plan->step, plan->head_chunk,
+                                       a->kv_layout == HL_KV_PAGED32)) / units);
   }
   if (S > kMaxFusedSplits) S = kMaxFusedSplits;
   // Paged caches: a wave keeps the pages of at most 256 tiles, so no split
@@ -1109,7 +1118,8 @@ hipError_t decode_launch(const hl_decode_args* a, const DecodePlan* plan, void* 
   p.scale_log2 = scale * kLog2e;
 
   dim3 grid(plan->num_splits, a->n_head_kv * plan->n_chunks, a->batch);
-  KernelFn fn = pick_kernel(a->kv_dtype, D, plan->vec, plan->pipe, plan->step, plan->head_chunk);
+  KernelFn fn = pick_kernel(a->kv_dtype, D, plan->vec, plan->pipe, plan->step, plan->head_chunk,
+                            a->kv_layout == HL_KV_PAGED32);
   hipLaunchKernelGGL(fn, grid, dim3(256), 0, stream, p);
   return hipGetLastError();
 }
