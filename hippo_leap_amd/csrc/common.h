@@ -150,6 +150,10 @@ __device__ __forceinline__ float wave_sum(float v) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// cos and sin of a RoPE angle (up to ~max_len rad): one sincosf shares the
+// large-argument range reduction that separate cosf / sinf calls each repeat.
+__device__ __forceinline__ void rope_cs(float angle, float& c, float& s) { sincosf(angle, &s, &c); }
+
 // RoPE angle table passed by value as a kernel argument (no device memory).
 struct ThetaTable {
   float t[HL_MAX_ROPE_DIM / 2];

@@ -664,7 +664,8 @@ __global__ __launch_bounds__(256, PIPE ? (D == 64 ? 2 : 1) : 4) void decode_mfma
     // Evaluated on every lane (lanes >= half discard it), so that the
     // frequency load stays ahead of the tile loads.
     const float angle = (float)newc * theta_lane;
-    const float cs = cosf(angle), sn = sinf(angle);
+    float cs, sn;
+    rope_cs(angle, cs, sn);
 #pragma unroll
     for (int u = 0; u < VPW; ++u) {
       const int j = wave + 4 * u;

@@ -76,7 +76,9 @@ __device__ __forceinline__ void headvec_norm_rope(float* sx, int D, int lane, co
     const int half = rope_dim / 2;
     for (int i = lane; i < half; i += 64) {
       const float angle = (float)pos * theta.t[i];
-      rope_rotate(sx, i, half, rope_style, cosf(angle), sinf(angle));
+      float c, sn;
+      rope_cs(angle, c, sn);
+      rope_rotate(sx, i, half, rope_style, c, sn);
     }
     wave_lds_sync();
   }

@@ -222,7 +222,8 @@ __global__ __launch_bounds__(256) void prologue_kernel(PrologueOp op) {
     const float pos = (float)(op.start_pos + t);
     for (int i = part; i < half; i += 8) {
       const float angle = pos * op.theta.t[i];
-      const float c = cosf(angle), sn = sinf(angle);
+      float c, sn;
+      rope_cs(angle, c, sn);
       scos[i][tc] = c;
       ssin[i][tc] = sn;
       if (publish && t < T) op.rope_tab_out[(long long)i * T + t] = make_float2(c, sn);
@@ -320,8 +321,7 @@ __global__ __launch_bounds__(256) void prologue_kernel(PrologueOp op) {
           s = ssin[i][tc];
         } else {
           const float angle = pos * op.theta.t[i];
-          c = cosf(angle);
-          s = sinf(angle);
+          rope_cs(angle, c, s);
         }
         const float v0 = sx[i0][tc], v1 = sx[i1][tc];
         sx[i0][tc] = v0 * c - v1 * s;
@@ -465,7 +465,8 @@ __global__ __launch_bounds__(256) void kv_prologue_kernel(PrologueOp op) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const float angle = (float)(op.start_pos + t + e) * op.theta.t[i];
-        const float c = cosf(angle), sn = sinf(angle);
+        float c, sn;
+      rope_cs(angle, c, sn);
         const float v0 = k[0][e], v1 = k[1][e];
         k[0][e] = v0 * c - v1 * sn;
         k[1][e] = v0 * sn + v1 * c;
@@ -482,7 +483,8 @@ __global__ __launch_bounds__(256) void kv_prologue_kernel(PrologueOp op) {
           const float other = __shfl_xor(k[ps][e], 4, 64);
           if (row < op.rope_dim) {
             const float angle = (float)(op.start_pos + t + e) * op.theta.t[i];
-            const float c = cosf(angle), sn = sinf(angle);
+            float c, sn;
+      rope_cs(angle, c, sn);
             const float v0 = even ? k[ps][e] : other, v1 = even ? other : k[ps][e];
             k[ps][e] = even ? v0 * c - v1 * sn : v0 * sn + v1 * c;
             if (publish && even && t + e < T) op.rope_tab_out[(long long)i * T + t + e] = make_float2(c, sn);
