@@ -392,31 +392,36 @@ __global__ __launch_bounds__(256) void prologue_kernel(PrologueOp op) {
 // token-major readout still reads contiguous 16-byte chunks).
 __device__ __forceinline__ int kt_swz(int tok) { return (tok & 16); }
 
-template <int IODT, int KDT, int D>
+// PT tokens per workgroup (32 or 64): a thread holds 8 tokens of rows
+// r + RS * ps, RS = 256 / (PT / 8); 64-token tiles read and write 128-byte
+// row segments instead of 64.
+template <int IODT, int KDT, int D, int PT>
 __global__ __launch_bounds__(256) void kv_prologue_kernel(PrologueOp op) {
-  static_assert(D == 128, "two rows per thread: r and r + 64");
-  constexpr int NP = D / 64;  // row passes: rows r + 64 * ps
-  __shared__ __attribute__((aligned(16))) uint16_t skt[kPT][D + 8];  // kt tile (fp16 bits), padded rows
-  __shared__ float sred[4][kPT];
+  static_assert(D == 128, "half-split RoPE pairs rows r and r + 64 in-thread");
+  constexpr int CPR = PT / 8;       // 8-token chunks per row
+  constexpr int RS = 256 / CPR;     // rows per pass
+  constexpr int NP = D / RS;        // row passes: rows r + RS * ps
+  __shared__ __attribute__((aligned(16))) uint16_t skt[PT][D + 8];  // kt tile (fp16 bits), padded rows
+  __shared__ float sred[4][PT];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int T = op.seq_len;
-  const int t0 = blockIdx.x * kPT;
+  const int t0 = blockIdx.x * PT;
   const int h = blockIdx.y;
-  const int r = tid >> 2, c8 = (tid & 3) * 8;
+  const int r = tid / CPR, c8 = (tid % CPR) * 8;
   const int t = t0 + c8;  // this thread's first token
   const long long hbase = (long long)h * D * T;
 
   float k[NP][8], v[NP][8];
 #pragma unroll
   for (int ps = 0; ps < NP; ++ps) {
-    load_row8_f32<IODT>(op.k, hbase + (long long)(r + 64 * ps) * T + t, t, T, k[ps]);
-    load_row8_f32<IODT>(op.v, hbase + (long long)(r + 64 * ps) * T + t, t, T, v[ps]);
+    load_row8_f32<IODT>(op.k, hbase + (long long)(r + RS * ps) * T + t, t, T, k[ps]);
+    load_row8_f32<IODT>(op.v, hbase + (long long)(r + RS * ps) * T + t, t, T, v[ps]);
   }
 
   // V: cache column block and vt, straight from registers.
 #pragma unroll
   for (int ps = 0; ps < NP; ++ps) {
-    const int row = r + 64 * ps;
+    const int row = r + RS * ps;
     if (op.v_cache)
       store_cache8<KDT>(op.v_cache, CacheMap{op.kv_layout, D, op.max_len, op.n_head_kv, op.block_table}, h, row,
                         op.start_pos + t, t, T, v[ps]);
@@ -436,12 +441,12 @@ __global__ __launch_bounds__(256) void kv_prologue_kernel(PrologueOp op) {
       float a = 0.f;
 #pragma unroll
       for (int ps = 0; ps < NP; ++ps) a += k[ps][e] * k[ps][e];
-      // lanes with the same c8 (tid % 4) hold the other rows of this wave
+      // lanes with the same c8 (tid % CPR) hold the other rows of this wave
 #pragma unroll
-      for (int m = 4; m < 64; m <<= 1) a += __shfl_xor(a, m, 64);
+      for (int m = CPR; m < 64; m <<= 1) a += __shfl_xor(a, m, 64);
       ss[e] = a;
     }
-    if (lane < 4) {
+    if (lane < CPR) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) sred[wave][c8 + e] = ss[e];
     }
@@ -451,7 +456,7 @@ __global__ __launch_bounds__(256) void kv_prologue_kernel(PrologueOp op) {
       const float tot = sred[0][c8 + e] + sred[1][c8 + e] + sred[2][c8 + e] + sred[3][c8 + e];
       const float inv = 1.0f / sqrtf(tot / (float)D + op.eps);
 #pragma unroll
-      for (int ps = 0; ps < NP; ++ps) k[ps][e] = k[ps][e] * inv * op.k_norm_w[r + 64 * ps];
+      for (int ps = 0; ps < NP; ++ps) k[ps][e] = k[ps][e] * inv * op.k_norm_w[r + RS * ps];
     }
   }
 
@@ -460,31 +465,34 @@ __global__ __launch_bounds__(256) void kv_prologue_kernel(PrologueOp op) {
   if (op.do_rope) {
     const bool publish = op.rope_tab_out && h == 0;
     const int half = op.rope_dim / 2;
-    if (op.rope_style == HL_ROPE_HALF_SPLIT) {  // rope_dim == D: pair (r, r + 64)
-      const int i = r;
+    if (op.rope_style == HL_ROPE_HALF_SPLIT) {  // rope_dim == D: pair (row, row + 64) = passes (ps, ps + NP/2)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float angle = (float)(op.start_pos + t + e) * op.theta.t[i];
-        float c, sn;
-      rope_cs(angle, c, sn);
-        const float v0 = k[0][e], v1 = k[1][e];
-        k[0][e] = v0 * c - v1 * sn;
-        k[1][e] = v0 * sn + v1 * c;
-        if (publish && t + e < T) op.rope_tab_out[(long long)i * T + t + e] = make_float2(c, sn);
+      for (int ps = 0; ps < NP / 2; ++ps) {
+        const int i = r + RS * ps;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float angle = (float)(op.start_pos + t + e) * op.theta.t[i];
+          float c, sn;
+          rope_cs(angle, c, sn);
+          const float v0 = k[ps][e], v1 = k[ps + NP / 2][e];
+          k[ps][e] = v0 * c - v1 * sn;
+          k[ps + NP / 2][e] = v0 * sn + v1 * c;
+          if (publish && t + e < T) op.rope_tab_out[(long long)i * T + t + e] = make_float2(c, sn);
+        }
       }
-    } else {  // interleaved: rows 2i and 2i + 1 are lanes 4 apart
+    } else {  // interleaved: rows 2i and 2i + 1 are lanes CPR apart
       const bool even = (r & 1) == 0;
 #pragma unroll
       for (int ps = 0; ps < NP; ++ps) {
-        const int row = r + 64 * ps;
+        const int row = r + RS * ps;
         const int i = row >> 1;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          const float other = __shfl_xor(k[ps][e], 4, 64);
+          const float other = __shfl_xor(k[ps][e], CPR, 64);
           if (row < op.rope_dim) {
             const float angle = (float)(op.start_pos + t + e) * op.theta.t[i];
             float c, sn;
-      rope_cs(angle, c, sn);
+            rope_cs(angle, c, sn);
             const float v0 = even ? k[ps][e] : other, v1 = even ? other : k[ps][e];
             k[ps][e] = even ? v0 * c - v1 * sn : v0 * sn + v1 * c;
             if (publish && even && t + e < T) op.rope_tab_out[(long long)i * T + t + e] = make_float2(c, sn);
@@ -497,7 +505,7 @@ __global__ __launch_bounds__(256) void kv_prologue_kernel(PrologueOp op) {
   // K: cache column block, and kt through LDS (token-major fp16).
 #pragma unroll
   for (int ps = 0; ps < NP; ++ps) {
-    const int row = r + 64 * ps;
+    const int row = r + RS * ps;
     if (op.k_cache)
       store_cache8<KDT>(op.k_cache, CacheMap{op.kv_layout, D, op.max_len, op.n_head_kv, op.block_table}, h, row,
                         op.start_pos + t, t, T, k[ps]);
@@ -506,7 +514,7 @@ __global__ __launch_bounds__(256) void kv_prologue_kernel(PrologueOp op) {
   }
   __syncthreads();
   constexpr int CH = D / 8;  // 16-byte chunks per token row
-  for (int idx = tid; idx < kPT * CH; idx += 256) {
+  for (int idx = tid; idx < PT * CH; idx += 256) {
     const int tt = idx / CH, ch = idx % CH;
     const int tg = t0 + tt;
     if (tg < op.t_pad) *(u16x8*)(op.kt + ((long long)h * op.t_pad + tg) * D + 8 * ch) = *(const u16x8*)&skt[tt][(8 * ch) ^ kt_swz(tt)];
@@ -526,8 +534,9 @@ static bool kv_prologue_fits(const PrologueOp& op) {
 hipError_t prologue_launch(const PrologueOp& op, hipStream_t stream) {
   const int cols = op.t_pad > op.seq_len ? op.t_pad : op.seq_len;
   if (kv_prologue_fits(op)) {
-    dim3 grid((cols + kPT - 1) / kPT, op.n_head_kv);
-#define HL_KVP(IO, KD) hipLaunchKernelGGL((kv_prologue_kernel<IO, KD, 128>), grid, dim3(256), 0, stream, op)
+    constexpr int PT = 32;  // 64-token tiles (128-byte row segments) measured 0.8% slower at c4
+    dim3 grid((cols + PT - 1) / PT, op.n_head_kv);
+#define HL_KVP(IO, KD) hipLaunchKernelGGL((kv_prologue_kernel<IO, KD, 128, PT>), grid, dim3(256), 0, stream, op)
     const int kd = op.k_cache ? op.kv_dtype : HL_BF16;
     if (op.io_dtype == HL_F16) {
       if (kd == HL_F32) HL_KVP(HL_F16, HL_F32); else if (kd == HL_F16) HL_KVP(HL_F16, HL_F16);
