@@ -544,7 +544,7 @@ def main():
             wl = DecodeWorkload(torch, A, B=16, hq=32, hkv=4, d=128, prev=32768,
                                 kv_dtype=kvdt, sigma=1.0, base=1e6, n_sets=1 if kvdt == torch.bfloat16 else 2,
                                 qknorm=True, seed=5, kv_layout=layout)
-            t = bench_decode(torch, A, wl, max(10, args.steps // 4), 3)
+            t = bench_decode(torch, A, wl, args.steps, max(3, args.warmup))
             kvname = "fp8 e4m3" if kvdt == torch.float8_e4m3fn else "bf16"
             result[key] = decode_extra(wl, t, f"c5: Qwen3-30B-A3B-shape decode, {kvname} KV, B=16, "
                                        "L=32769, Hq32/Hkv4, D128, qkNorm + RoPE 1e6")
