@@ -192,3 +192,41 @@ def test_prefill_cache_write_paged(hl, orc, case):
     assert np.array_equal(res[0][0], res[1][0])
     assert np.array_equal(res[0][1], res[1][1])
     assert np.array_equal(res[0][2], res[1][2])
+
+
+def test_decode_step_paged_fp8_graph_replay(hl, orc):
+    """The fused step on a paged fp8 cache inside a HIP graph: replays with
+    eager work in between give the eager result every time."""
+    from hippo_leap_amd import attention as A
+    B, hq, hkv, d, M = 4, 32, 4, 128, 2048
+    n = B * hkv * d * M
+    kb = torch.from_numpy(orc.to_storage(orc.normal(n, 6601), 3)).cuda()
+    vb = torch.from_numpy(orc.to_storage(orc.normal(n, 6602), 3)).cuda()
+    table, n_pages = table_for(B, M, 6603)
+    kc, vc = paged(kb, hkv, d, M, table, n_pages), paged(vb, hkv, d, M, table, n_pages)
+    qd = torch.from_numpy(orc.normal(B * hq * d, 6604)).cuda()
+    kd = torch.from_numpy(orc.normal(B * hkv * d, 6605)).cuda()
+    vd = torch.from_numpy(orc.normal(B * hkv * d, 6606)).cuda()
+    out = torch.empty(B * hq * d, device="cuda")
+    rs = A.rope_store_args(qd, kd, vd, kc, vc, hq, hkv, d, M, 1500, 1e6, kv_layout=PAGED,
+                           block_table=table)
+    at = A.decode_args(qd, kc, vc, out, hq, hkv, d, M, 1501, kv_layout=PAGED, block_table=table)
+    ws = A.decode_step_workspace(rs, at)
+    A.decode_step(rs, at, ws)
+    torch.cuda.synchronize()
+    eager = out.cpu().numpy().copy()
+    g = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        A.decode_step(rs, at, ws)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g):
+        A.decode_step(rs, at, ws)
+    for _ in range(4):
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(out.cpu().numpy(), eager)
