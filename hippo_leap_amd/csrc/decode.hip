@@ -205,7 +205,7 @@ __device__ void finish_workgroup(const DecodeParams& p, const float* sm_m, const
 // lane j scores column t0+j for every head of the chunk, then lanes switch to
 // owning output dims for the P.V product.
 // ---------------------------------------------------------------------------
-// HC: head slots per chunk (4, 8 or 16, at least the chunk's heads).  Slots
+// HC: head slots per chunk (2, 4, 8 or 16, at least the chunk's heads).  Slots
 // past the chunk's heads score a zero q row and are never written out; every
 // slot is computed without a branch, so the heads' dependency chains (dot
 // products, wave reductions) interleave instead of running one after another.
@@ -943,6 +943,7 @@ typedef void (*KernelFn)(DecodeParams);
 // loads of unaligned caches would not fit its registers).
 template <int D, bool V4>
 KernelFn pick_f32_hc(int hc) {
+  if (hc <= 2) return decode_f32_kernel<D, V4, 2>;
   return hc <= 4 ? decode_f32_kernel<D, V4, 4> : (hc <= 8 ? decode_f32_kernel<D, V4, 8> : decode_f32_kernel<D, V4, 16>);
 }
 KernelFn pick_f32(int D, bool vec, int hc) {
@@ -1026,6 +1027,20 @@ bool vec_path(const hl_decode_args* a) {
 void decode_plan(const hl_decode_args* a, DecodePlan* plan, bool step) {
   const int G = a->n_head / a->n_head_kv;
   plan->head_chunk = G < 16 ? G : 16;
+  if (a->kv_dtype == HL_F32) {
+    // fp32 (vector ALU): a wave's work per tile grows with its heads.  When
+    // the grid is small (latency-bound: fewer workgroups than half the CUs),
+    // fewer heads per workgroup spread the work over more CUs; each chunk
+    // re-reads the K/V tile, which such small caches serve from L2 (c1:
+    // 8 -> 2 heads, 12.4 -> 8.2 us).
+    const int tiles64 = (a->seq_len + 63) / 64;
+    while (plan->head_chunk > 2) {
+      const long long wgs = (long long)a->batch * a->n_head_kv * ((G + plan->head_chunk - 1) / plan->head_chunk) *
+                            (tiles64 < 64 ? tiles64 : 64);
+      if (wgs * 2 >= cu_count()) break;
+      plan->head_chunk /= 2;
+    }
+  }
   plan->n_chunks = (G + plan->head_chunk - 1) / plan->head_chunk;
   plan->vec = vec_path(a);
   plan->step = step && a->kv_dtype != HL_F32;
