@@ -32,7 +32,8 @@ Extra objects on the same JSON line:
     attention + merge) timed with HIP events on the stream it runs on.
   linear: hl_gpu_linear_col (the gpuLinearCol drop-in, fp32) at the
     projection shapes around attention: decode GEMV GB/s (weights from HBM)
-    and prefill GEMM TFLOP/s against the fp32 peak.
+    and prefill GEMM TFLOP/s against the fp32 peak; hl_gpu_linear_col_quant
+    (gpuLinearColQuant) decode GEMV GB/s over F16, Q8_0, Q4_K, Q6_K weights.
   decode_ends: greedy argmax over the logits (hl_argmax_async / hl_gpu_argmax)
     and the token embedding (hl_gpu_embedding), the ends of a decode step.
   cpu_baseline: the C oracle (single-threaded scalar fp32 restatement of the
@@ -318,6 +319,28 @@ def bench_linear(torch, A):
                      "frac_fp32_peak": round(tf / FP32_PEAK_TFLOPS, 4)}
         log(f"linear {name}: {ms*1e3:.1f} us, {tf:.1f} TFLOP/s")
         del w, x, y
+    # Quantized decode GEMV (gpuLinearColQuant drop-in): GB/s over the packed
+    # weight bytes (+ x, y).  Weights are random bytes of the packed size:
+    # the kernel has no data-dependent branches, so the rate does not depend
+    # on the values.
+    for qname, qt, qk, qb in (("f16", 1, 1, 2), ("q8_0", 8, 32, 34), ("q4_k", 12, 256, 144),
+                              ("q6_k", 14, 256, 210)):
+        for sname, M, K in (("llama8b_q", 4096, 4096), ("llama8b_ffn_up", 14336, 4096)):
+            wbytes = M * K // qk * qb
+            n = max(2, -(-(600 << 20) // wbytes))
+            ws = [torch.randint(0, 256, (wbytes,), generator=g, device="cuda", dtype=torch.uint8)
+                  for _ in range(n)]
+            x = torch.randn(K, generator=g, device="cuda")
+            y = torch.empty(M, device="cuda")
+            fn = lambda i: A.gpu_linear_col_quant(y, x, ws[i % n], K, M, qt)
+            ms = graph_time_ms(torch, fn, n_inner=max(n, 16), replays=4)
+            gbs = (wbytes + (K + M) * 4) / (ms * 1e-3) / 1e9
+            name = f"decode_{sname}_{qname}"
+            out[name] = {"shape": f"W {M}x{K} {qname}, T=1", "us": round(ms * 1e3, 3),
+                         "unit": "GB/s", "value": round(gbs, 1),
+                         "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "weight_copies": n}
+            log(f"linear {name}: {ms*1e3:.2f} us, {gbs:.0f} GB/s")
+            del ws
     torch.cuda.empty_cache()
     return out
 

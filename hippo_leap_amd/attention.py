@@ -117,6 +117,12 @@ def gpu_linear_col(dst, x, w, w_cols, w_rows, seq_len, stream=None):
                                         _stream(stream)))
 
 
+def gpu_linear_col_quant(dst, x, w_quant, w_cols, w_rows, quant_type, stream=None):
+    """gpuLinearColQuant (naive.nim:1580-1592): dst[w_rows] = dequant(w) . x, one token."""
+    check(_lib.load().hl_gpu_linear_col_quant(_p(dst), _p(x), _p(w_quant), w_cols, w_rows,
+                                              quant_type, _stream(stream)))
+
+
 def gpu_rmsnorm_cols(dst, x, weight, dim, seq_len, eps, stream=None):
     """gpuRmsnormCols (naive.nim:2834-2843) on col-major [dim, seq_len] fp32."""
     check(_lib.load().hl_gpu_rmsnorm_cols(_p(dst), _p(x), _p(weight), dim, seq_len, eps,

@@ -812,6 +812,25 @@ int hl_gpu_linear_col(float* dst, const float* x, const float* w, int w_cols, in
   return e == hipSuccess ? HL_OK : hip_fail(e, "linear_col launch");
 }
 
+int hl_gpu_linear_col_quant(float* dst, const float* x, const void* w_quant, int w_cols, int w_rows,
+                            int quant_type, void* stream) {
+  if (!dst || !x || !w_quant) return fail(HL_EINVAL, "linear_col_quant: null pointer");
+  const int qk = quant_block_elems(quant_type);
+  if (qk == 0) return fail(HL_EUNSUPPORTED, "unsupported quant type for GPU GEMV: %d", quant_type);
+  if (w_cols <= 0 || w_rows <= 0)
+    return fail(HL_EINVAL, "linear_col_quant: bad shape (w_cols=%d, w_rows=%d)", w_cols, w_rows);
+  if (w_cols % qk) {  // the reference's rowSize* messages (quant.nim:39-58)
+    const char* name = quant_type == HL_GGML_Q8_0 ? "q8_0" : quant_type == HL_GGML_Q4_K ? "q4_K"
+                       : quant_type == HL_GGML_Q6_K ? "q6_K" : "f16";
+    return fail(HL_EINVAL, "%s row size must be multiple of %d", name, qk);
+  }
+  const size_t wbytes = (size_t)quant_row_bytes(quant_type, w_cols) * w_rows;
+  if (overlaps(dst, (size_t)w_rows * 4, x, (size_t)w_cols * 4) || overlaps(dst, (size_t)w_rows * 4, w_quant, wbytes))
+    return fail(HL_EINVAL, "linear_col_quant: dst overlaps x or w");
+  hipError_t e = linear_quant_launch(dst, x, w_quant, w_cols, w_rows, quant_type, as_stream(stream));
+  return e == hipSuccess ? HL_OK : hip_fail(e, "linear_col_quant launch");
+}
+
 int hl_gpu_rmsnorm_cols(float* dst, const float* x, const float* weight, int dim, int seq_len,
                         float eps, void* stream) {
   if (!dst || !x || !weight) return fail(HL_EINVAL, "rmsnorm_cols: null pointer");

@@ -147,6 +147,12 @@ LinearPlan linear_plan(int M, int K, int T, const float* w, const float* x);
 hipError_t linear_col_launch(float* y, const float* x, const float* w, int K, int M, int T,
                              hipStream_t stream);
 
+// ---- quantized decode GEMV (linear_quant.hip) ------------------------------
+int quant_block_elems(int qtype);        // 0: type not built
+long long quant_row_bytes(int qtype, int K);
+hipError_t linear_quant_launch(float* y, const float* x, const void* w, int K, int M, int qtype,
+                               hipStream_t stream);
+
 // ---- RMSNorm of the hidden state (norm.hip) --------------------------------
 hipError_t rmsnorm_cols_launch(float* out, const float* x, const float* w, int dim, int seq,
                                float eps, hipStream_t stream);

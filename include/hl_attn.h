@@ -180,6 +180,21 @@ int hl_gpu_attention_prefill(float* dst, const float* q, const float* k,
 int hl_gpu_linear_col(float* dst, const float* x, const float* w, int w_cols,
                       int w_rows, int seq_len, void* stream);
 
+/* GGUF weight types of hl_gpu_linear_col_quant (ggml's type ids, as the
+ * reference's GgmlType* constants, model.nim:11-21).                        */
+enum { HL_GGML_F16 = 1, HL_GGML_Q8_0 = 8, HL_GGML_Q4_K = 12, HL_GGML_Q6_K = 14 };
+
+/* gpuLinearColQuant (naive.nim:1580-1592): dst[wRows] = dequant(w)[wRows,
+ * wCols] . x[wCols] for one token (the reference's quantized GEMVs are
+ * decode-only), with w the GGUF rows of quant_type: HL_GGML_F16, Q8_0, Q4_K
+ * or Q6_K (dequantisation as quant.nim:235-355).  wCols must be a multiple
+ * of the block (32; 256 for the K-quants): HL_EINVAL with the reference's
+ * row-size message otherwise.  Other types: HL_EUNSUPPORTED ("unsupported
+ * quant type for GPU GEMV: <type>").  dst must not overlap x or w.        */
+int hl_gpu_linear_col_quant(float* dst, const float* x, const void* w_quant,
+                            int w_cols, int w_rows, int quant_type,
+                            void* stream);
+
 /* gpuRmsnormCols (naive.nim:2834-2843): dst[r, t] = x[r, t] *
  * (1/sqrtf(sum_r x[r, t]^2 / dim + eps)) * weight[r] over the col-major
  * fp32 [dim, seqLen] (the norm in front of the Q/K/V projections and the

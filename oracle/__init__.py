@@ -61,6 +61,7 @@ def lib() -> ctypes.CDLL:
             "orc_store_kv": (None, [ctypes.c_void_p, _i, _fp, _i, _i, _i, _i]),
             "orc_attention_decode": (None, [_fp, _fp, _fp, _fp, _i, _i, _i, _i, _i, _f, _fp]),
             "orc_argmax": (_i, [_fp, _ll]),
+            "orc_dequant_rows": (_ll, [_i, ctypes.c_void_p, _fp, _i, _i]),
             "orc_embedding": (None, [_fp, ctypes.POINTER(_i), _fp, _i, _i]),
             "orc_attention_prefill": (None, [_fp, _fp, _fp, _fp, _i, _i, _i, _i, _f, _i, _i, _i,
                                              _i, _i, _fp]),
@@ -247,4 +248,14 @@ def embedding(w: np.ndarray, tokens, n_emb: int) -> np.ndarray:
     out = np.empty((n_emb, tok.size), np.float32)
     lib().orc_embedding(_ptr(w), tok.ctypes.data_as(ctypes.POINTER(_i)), _ptr(out), n_emb,
                         tok.size)
+    return out
+
+
+# ---- GGUF weight rows (quant.nim) -------------------------------------------------
+def dequant_rows(qtype: int, raw: np.ndarray, rows: int, k: int) -> np.ndarray:
+    """quant.nim's dequantRow* of `rows` rows of GGUF type qtype -> fp32 [rows, k]."""
+    raw = np.ascontiguousarray(raw, dtype=np.uint8)
+    out = np.empty((rows, k), np.float32)
+    rb = lib().orc_dequant_rows(qtype, raw.ctypes.data_as(ctypes.c_void_p), _ptr(out), rows, k)
+    assert rb and raw.size >= rb * rows
     return out

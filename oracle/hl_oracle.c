@@ -25,6 +25,7 @@
  *   :4066-4074             qkNorm before RoPE
  *   :1922-2127             argmax (two-pass reduction, its tie order)
  *   :2975-3001             token embedding lookup
+ * and GGUF weight rows (quant.nim:235-355: dequantRowQ8_0, Q4K, Q6K).
  *
  * Every routine is single-threaded scalar fp32 code (built -O2, no
  * fast-math), like the reference's CPU path.  fp16/bf16 inputs enter as
@@ -38,6 +39,9 @@
  *   argmax: numpy argmax on tie-free inputs, hand-derived tie winners of
  *   the reduction tree, NaN / -inf / all-invalid cases.
  *   embedding: numpy fancy indexing.
+ *   GGUF dequant: blocks packed in the tests from the GGUF format's
+ *   definition with chosen scales/mins/quants (expected values from the
+ *   format formula), including the high-index 6-bit scale packing.
  *   f32->f16/bf16 RNE: numpy / torch conversions (exhaustive over a sweep).
  *   Device transcendental functions of the reference (hippo's expf, powf,
  *   cosf, sinf) are not pinned by any reference test: parity unpinned at
@@ -482,4 +486,93 @@ void orc_embedding(const float* w, const int* tok, float* out, int n_emb, int n_
   for (int e = 0; e < n_emb; ++e)
     for (int t = 0; t < n_tokens; ++t)
       out[(int64_t)e * n_tokens + t] = w[(int64_t)tok[t] * n_emb + e];
+}
+
+/* ---------------------------------------------------------------------- */
+/* GGUF weight rows (quant.nim)                                           */
+/* ---------------------------------------------------------------------- */
+
+static float orc_half_at(const uint8_t* p) { return orc_half_to_float((uint16_t)(p[0] | (p[1] << 8))); }
+
+/* quant.nim:304-319: 34-byte blocks, fp16 d then 32 int8; x = q * d. */
+static void orc_dequant_q8_0(const uint8_t* src, float* dst, int k) {
+  for (int b = 0; b < k / 32; ++b) {
+    const uint8_t* blk = src + (int64_t)b * 34;
+    const float d = orc_half_at(blk);
+    for (int j = 0; j < 32; ++j) dst[b * 32 + j] = (float)(int8_t)blk[2 + j] * d;
+  }
+}
+
+/* quant.nim:235-242 (getScaleMinK4): 6-bit scale / min j of the 12 bytes. */
+static void orc_scale_min_k4(int j, const uint8_t* s, int* sc, int* mn) {
+  if (j < 4) {
+    *sc = s[j] & 63;
+    *mn = s[j + 4] & 63;
+  } else {
+    *sc = (s[j + 4] & 0x0F) | ((s[j - 4] >> 6) << 4);
+    *mn = (s[j + 4] >> 4) | ((s[j] >> 6) << 4);
+  }
+}
+
+/* quant.nim:244-277: 144-byte blocks of 256: d, dmin, 12 scale bytes, 128
+ * nibble bytes; each 64-element chunk uses 32 bytes, low nibbles first. */
+static void orc_dequant_q4k(const uint8_t* src, float* dst, int k) {
+  for (int b = 0; b < k / 256; ++b) {
+    const uint8_t* blk = src + (int64_t)b * 144;
+    const float d = orc_half_at(blk), dmin = orc_half_at(blk + 2);
+    const uint8_t* scales = blk + 4;
+    const uint8_t* q = blk + 16;
+    float* out = dst + b * 256;
+    for (int c = 0; c < 4; ++c) {
+      int sc, mn;
+      orc_scale_min_k4(2 * c, scales, &sc, &mn);
+      const float d1 = d * (float)sc, m1 = dmin * (float)mn;
+      orc_scale_min_k4(2 * c + 1, scales, &sc, &mn);
+      const float d2 = d * (float)sc, m2 = dmin * (float)mn;
+      for (int l = 0; l < 32; ++l) out[64 * c + l] = d1 * (float)(q[32 * c + l] & 0x0F) - m1;
+      for (int l = 0; l < 32; ++l) out[64 * c + 32 + l] = d2 * (float)(q[32 * c + l] >> 4) - m2;
+    }
+  }
+}
+
+/* quant.nim:321-355: 210-byte blocks of 256: ql[128], qh[64], int8 sc[16],
+ * fp16 d; two halves of 128 elements, four 32-element groups each. */
+static void orc_dequant_q6k(const uint8_t* src, float* dst, int k) {
+  for (int b = 0; b < k / 256; ++b) {
+    const uint8_t* blk = src + (int64_t)b * 210;
+    const uint8_t* ql = blk;
+    const uint8_t* qh = blk + 128;
+    const int8_t* sc = (const int8_t*)(blk + 192);
+    const float d = orc_half_at(blk + 208);
+    float* out = dst + b * 256;
+    for (int n = 0; n < 2; ++n) {
+      for (int l = 0; l < 32; ++l) {
+        const int is = l / 16;
+        const int q1 = (int)((ql[64 * n + l] & 0xF) | (((qh[32 * n + l] >> 0) & 3) << 4)) - 32;
+        const int q2 = (int)((ql[64 * n + l + 32] & 0xF) | (((qh[32 * n + l] >> 2) & 3) << 4)) - 32;
+        const int q3 = (int)((ql[64 * n + l] >> 4) | (((qh[32 * n + l] >> 4) & 3) << 4)) - 32;
+        const int q4 = (int)((ql[64 * n + l + 32] >> 4) | (((qh[32 * n + l] >> 6) & 3) << 4)) - 32;
+        out[128 * n + l] = d * (float)sc[8 * n + is + 0] * (float)q1;
+        out[128 * n + l + 32] = d * (float)sc[8 * n + is + 2] * (float)q2;
+        out[128 * n + l + 64] = d * (float)sc[8 * n + is + 4] * (float)q3;
+        out[128 * n + l + 96] = d * (float)sc[8 * n + is + 6] * (float)q4;
+      }
+    }
+  }
+}
+
+/* Rows of GGUF type qtype (1 F16, 8 Q8_0, 12 Q4_K, 14 Q6_K) -> fp32
+ * [rows][k]; returns the bytes per row (0: type not covered). */
+int64_t orc_dequant_rows(int qtype, const uint8_t* src, float* dst, int rows, int k) {
+  int64_t rb = qtype == 1 ? 2LL * k : qtype == 8 ? (int64_t)(k / 32) * 34
+               : qtype == 12 ? (int64_t)(k / 256) * 144 : qtype == 14 ? (int64_t)(k / 256) * 210 : 0;
+  for (int r = 0; r < rows && rb; ++r) {
+    const uint8_t* s = src + r * rb;
+    float* o = dst + (int64_t)r * k;
+    if (qtype == 1) for (int i = 0; i < k; ++i) o[i] = orc_half_at(s + 2 * i);
+    else if (qtype == 8) orc_dequant_q8_0(s, o, k);
+    else if (qtype == 12) orc_dequant_q4k(s, o, k);
+    else orc_dequant_q6k(s, o, k);
+  }
+  return rb;
 }

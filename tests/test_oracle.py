@@ -380,3 +380,49 @@ def test_e4m3_encode_matches_torch_below_overflow(orc):
     big = np.array([464.0, 480.0, 1e30, np.inf, -np.inf, -1e9], np.float32)
     assert orc.to_storage(big, orc.FP8).tolist() == [0x7E, 0x7E, 0x7E, 0x7E, 0xFE, 0xFE]
     assert orc.to_storage(np.array([np.nan], np.float32), orc.FP8)[0] & 0x7F == 0x7F
+
+
+# ---------------------------------------------------------------------------
+# GGUF weight rows (quant.nim:235-355)
+# ---------------------------------------------------------------------------
+def test_dequant_q8_0_packed(orc):
+    from gguf_pack import pack_q8_0
+    rng = np.random.default_rng(10)
+    d = np.asarray(rng.uniform(0.01, 1.0, 3), np.float16)
+    q = rng.integers(-128, 128, (3, 32))
+    got = orc.dequant_rows(8, pack_q8_0(d, q), 1, 96)
+    assert np.array_equal(got.reshape(3, 32), (q * d.astype(np.float32)[:, None]).astype(np.float32))
+
+
+def test_dequant_q4_k_packed(orc):
+    """Every 6-bit scale and min position, including the split high-index
+    ones, round-trips through the format's packing."""
+    from gguf_pack import pack_q4_k, q4_k_values
+    rng = np.random.default_rng(11)
+    nb = 4
+    d = np.asarray(rng.uniform(0.01, 0.1, nb), np.float16)
+    dmin = np.asarray(rng.uniform(0.0, 0.1, nb), np.float16)
+    sc = rng.integers(0, 64, (nb, 8))
+    mn = rng.integers(0, 64, (nb, 8))
+    sc[0] = [63, 0, 1, 62, 32, 33, 16, 47]   # top bits of every high-index scale exercised
+    mn[0] = [0, 63, 31, 32, 48, 15, 63, 1]
+    q = rng.integers(0, 16, (nb, 256))
+    got = orc.dequant_rows(12, pack_q4_k(d, dmin, sc, mn, q), 1, 256 * nb).reshape(nb, 256)
+    assert np.allclose(got, q4_k_values(d, dmin, sc, mn, q), rtol=1e-6, atol=1e-6)
+
+
+def test_dequant_q6_k_packed(orc):
+    from gguf_pack import pack_q6_k, q6_k_values
+    rng = np.random.default_rng(12)
+    nb = 3
+    d = np.asarray(rng.uniform(0.001, 0.05, nb), np.float16)
+    sc = rng.integers(-128, 128, (nb, 16))
+    q = rng.integers(-32, 32, (nb, 256))
+    q[0, :8] = [-32, 31, 0, -1, 15, 16, -17, 30]
+    got = orc.dequant_rows(14, pack_q6_k(d, sc, q), 1, 256 * nb).reshape(nb, 256)
+    assert np.allclose(got, q6_k_values(d, sc, q), rtol=1e-6, atol=1e-6)
+
+
+def test_dequant_f16(orc):
+    x = np.asarray(np.random.default_rng(13).standard_normal(64), np.float16)
+    assert np.array_equal(orc.dequant_rows(1, x.view(np.uint8), 2, 32).reshape(-1), x.astype(np.float32))
