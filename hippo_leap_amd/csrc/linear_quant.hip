@@ -205,6 +205,321 @@ __global__ __launch_bounds__(256) void quant_gemv_kernel(const uint8_t* __restri
   }
 }
 
+// ---------------------------------------------------------------------------
+// Direct kernel: no LDS.  Each wave computes R rows; lanes own fixed element
+// groups of a block (LPB lanes per block, 64 / LPB blocks per wave step), so
+// the x values a lane loads serve all R rows.  The decode is VALU-bound (a
+// wave64 VALU op takes 4 cycles of a SIMD), so the formats are laid out to
+// spend few ops per weight: per-block scale work is amortised over 16-32
+// weights per lane, nibbles and bytes go to float with v_cvt_f32_ubyte*, and
+// every row is a buffer resource (SGPRs) so the R rows share one 32-bit
+// offset per load.  Q8_0 and Q6_K blocks start at 2-byte offsets: their
+// fields are read as the dwords covering them and re-aligned with
+// v_alignbyte (only dwords holding a field's bytes are read).
+//
+// Per format: LPB lanes per block, QKB elements per block, BB bytes, NX
+// float4 of x per lane per block, NS partial sums of x per lane per block.
+template <int QT>
+struct QD;
+template <>
+struct QD<1> { static constexpr int LPB = 1, QKB = 8, BB = 16, NX = 2, NS = 0; };    // 8 halfs
+template <>
+struct QD<8> { static constexpr int LPB = 4, QKB = 32, BB = 34, NX = 2, NS = 1; };   // 8 int8
+template <>
+struct QD<12> { static constexpr int LPB = 8, QKB = 256, BB = 144, NX = 8, NS = 2; };  // 32 nibbles
+template <>
+struct QD<14> { static constexpr int LPB = 16, QKB = 256, BB = 210, NX = 4, NS = 4; }; // 16 x 6 bit
+
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+template <int QT>
+struct QRaw;
+template <>
+struct QRaw<1> { u32x4 h; };
+template <>
+struct QRaw<8> { u32x2 p; uint32_t q, d; };
+template <>
+struct QRaw<12> { u32x4 hdr, q; };
+template <>
+struct QRaw<14> { uint32_t a0, a1, b0, b1, h0, h1; u32x2 s; uint32_t s2, d; };
+
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+// Buffer resource over [base, base + bytes): raw byte addressing (stride 0),
+// dword data format; a dword load that ends past `bytes` returns 0.
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ uint32_t bl32(rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, off & ~3u, 0, 0);
+}
+__device__ __forceinline__ u32x2 bl64(rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b64(r, off & ~3u, 0, 0);
+}
+__device__ __forceinline__ u32x4 bl128(rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+}
+__device__ __forceinline__ uint32_t al(uint32_t hi, uint32_t lo, uint32_t ps) {
+  return __builtin_amdgcn_alignbyte(hi, lo, ps);
+}
+
+// Element offsets (multiples of 4) within the block of lane j's x float4s.
+template <int QT>
+__device__ __forceinline__ int x_off(int j, int k) {
+  if constexpr (QT == 1) return 4 * k;
+  else if constexpr (QT == 8) return 8 * j + 4 * k;
+  else if constexpr (QT == 12)  // sub 2c: k < 4, sub 2c+1: k >= 4; 16 of each
+    return 64 * (j >> 1) + 32 * (k >> 2) + 16 * (j & 1) + 4 * (k & 3);
+  else return 128 * (j >> 3) + 32 * k + 4 * (j & 7);
+}
+
+// off: the block's first byte relative to the (dword-aligned) resource base.
+template <int QT>
+__device__ __forceinline__ void load_raw(rsrc_t rs, uint32_t off, int j, QRaw<QT>& r) {
+  if constexpr (QT == 1) {
+    r.h = bl128(rs, off);
+  } else if constexpr (QT == 8) {
+    const uint32_t a = off + 2 + 8 * j;
+    r.p = bl64(rs, a);
+    r.q = bl32(rs, a + 7);
+    r.d = bl32(rs, off);
+  } else if constexpr (QT == 12) {
+    r.hdr = bl128(rs, off);
+    r.q = bl128(rs, off + 16 + 32 * (j >> 1) + 16 * (j & 1));
+  } else {
+    const uint32_t n = j >> 3, l0 = 4 * (j & 7);
+    r.a0 = bl32(rs, off + 64 * n + l0);
+    r.a1 = bl32(rs, off + 64 * n + l0 + 3);
+    r.b0 = bl32(rs, off + 64 * n + 32 + l0);
+    r.b1 = bl32(rs, off + 64 * n + 32 + l0 + 3);
+    r.h0 = bl32(rs, off + 128 + 32 * n + l0);
+    r.h1 = bl32(rs, off + 128 + 32 * n + l0 + 3);
+    r.s = bl64(rs, off + 192 + 8 * n);
+    r.s2 = bl32(rs, off + 192 + 8 * n + 7);
+    r.d = bl32(rs, off + 208);
+  }
+}
+
+// Byte n of v as a float, one v_cvt_f32_ubyteN (written out: after a nibble
+// mask the compiler otherwise narrows the extract to v_bfe + ubyte0, two ops).
+#define HL_CVT_UBYTE(N)                                                   \
+  __device__ __forceinline__ float cvt_ubyte##N(uint32_t v) {             \
+    float r;                                                              \
+    asm("v_cvt_f32_ubyte" #N " %0, %1" : "=v"(r) : "v"(v));               \
+    return r;                                                             \
+  }
+HL_CVT_UBYTE(0)
+HL_CVT_UBYTE(1)
+HL_CVT_UBYTE(2)
+HL_CVT_UBYTE(3)
+#undef HL_CVT_UBYTE
+
+// acc + sum of the 4 unsigned bytes of q times x.
+__device__ __forceinline__ float fma4u(uint32_t q, const f32x4& x, float acc) {
+  acc = fmaf(cvt_ubyte0(q), x.x, acc);
+  acc = fmaf(cvt_ubyte1(q), x.y, acc);
+  acc = fmaf(cvt_ubyte2(q), x.z, acc);
+  return fmaf(cvt_ubyte3(q), x.w, acc);
+}
+__device__ __forceinline__ float hsum4(const f32x4& x) { return (x.x + x.y) + (x.z + x.w); }
+
+// Per-step sums of x the formats subtract (offset-coded quants, Q4_K mins).
+template <int QT>
+__device__ __forceinline__ void x_sums(const f32x4* xv, float* xs) {
+  if constexpr (QT == 8) {
+    xs[0] = hsum4(xv[0]) + hsum4(xv[1]);
+  } else if constexpr (QT == 12) {
+    xs[0] = (hsum4(xv[0]) + hsum4(xv[1])) + (hsum4(xv[2]) + hsum4(xv[3]));
+    xs[1] = (hsum4(xv[4]) + hsum4(xv[5])) + (hsum4(xv[6]) + hsum4(xv[7]));
+  } else if constexpr (QT == 14) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) xs[k] = hsum4(xv[k]);
+  }
+}
+
+// ps: the block's first byte within its dword (0 or 2 for Q8_0 / Q6_K).
+template <int QT>
+__device__ __forceinline__ float compute_raw(const QRaw<QT>& r, int j, uint32_t ps, const f32x4* xv,
+                                             const float* xs) {
+  if constexpr (QT == 1) {
+    const uint32_t h[4] = {r.h.x, r.h.y, r.h.z, r.h.w};
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const f32x4& x = xv[i >> 1];
+      const float a = f16_bits_to_f32((uint16_t)(h[i] & 0xFFFFu));
+      const float b = f16_bits_to_f32((uint16_t)(h[i] >> 16));
+      s = fmaf(a, (i & 1) ? x.z : x.x, s);
+      s = fmaf(b, (i & 1) ? x.w : x.y, s);
+    }
+    return s;
+  } else if constexpr (QT == 8) {
+    // int8 q as the unsigned byte q ^ 0x80 = q + 128: sum((q+128) x) - 128 sum(x).
+    const uint32_t sb = (ps + 2) & 3;  // the quants start 2 bytes after the block
+    const uint32_t q0 = al(r.p.y, r.p.x, sb) ^ 0x80808080u, q1 = al(r.q, r.p.y, sb) ^ 0x80808080u;
+    const float d = f16_bits_to_f32((uint16_t)((r.d >> (8 * ps)) & 0xFFFFu));
+    return d * (fma4u(q1, xv[1], fma4u(q0, xv[0], 0.f)) - 128.f * xs[0]);
+  } else if constexpr (QT == 12) {
+    // Sub-blocks 2c (low nibbles) and 2c+1 (high nibbles); their 6-bit
+    // scales and mins are bytes 2(c&1), 2(c&1)+1 of 16-bit pairs built
+    // branch-free from the scale dwords Y = bytes 0-3, Z = 4-7, W = 8-11.
+    const int c = j >> 1;
+    const uint32_t sh = 16 * (c & 1);
+    const uint32_t Y = r.hdr.y >> sh, Z = r.hdr.z >> sh, W = r.hdr.w >> sh;
+    const bool lo = c < 2;
+    const uint32_t m1 = lo ? 0x3F3Fu : 0x0F0Fu, m2 = lo ? 0u : 0x3030u;
+    const uint32_t SC = ((lo ? Y : W) & m1) | ((Y >> 2) & m2);
+    const uint32_t MN = ((lo ? Z : (W >> 4)) & m1) | ((Z >> 2) & m2);
+    const float d = f16_bits_to_f32((uint16_t)(r.hdr.x & 0xFFFFu));
+    const float dmin = f16_bits_to_f32((uint16_t)(r.hdr.x >> 16));
+    const uint32_t q[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
+    float slo = 0.f, shi = 0.f;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      slo = fma4u(q[m] & 0x0F0F0F0Fu, xv[m], slo);
+      shi = fma4u(q[m] & 0xF0F0F0F0u, xv[4 + m], shi);  // 16 x nibble
+    }
+    const float sc0 = (float)(SC & 255u), sc1 = (float)((SC >> 8) & 255u);
+    const float mn0 = (float)(MN & 255u), mn1 = (float)((MN >> 8) & 255u);
+    return d * fmaf(sc0, slo, sc1 * 0.0625f * shi) - dmin * fmaf(mn0, xs[0], mn1 * xs[1]);
+  } else {
+    const uint32_t qa = al(r.a1, r.a0, ps), qb = al(r.b1, r.b0, ps), qh = al(r.h1, r.h0, ps);
+    const uint32_t slo = al(r.s.y, r.s.x, ps), shi = al(r.s2, r.s.y, ps);
+    const float d = f16_bits_to_f32((uint16_t)((r.d >> (8 * ps)) & 0xFFFFu));
+    const uint32_t hb = 8 * ((j & 7) >> 2);  // second scale of a 32-group for l >= 16
+    const uint32_t u0 = (qa & 0x0F0F0F0Fu) | ((qh << 4) & 0x30303030u);
+    const uint32_t u1 = (qb & 0x0F0F0F0Fu) | ((qh << 2) & 0x30303030u);
+    const uint32_t u2 = ((qa >> 4) & 0x0F0F0F0Fu) | (qh & 0x30303030u);
+    const uint32_t u3 = ((qb >> 4) & 0x0F0F0F0Fu) | ((qh >> 2) & 0x30303030u);
+    const float s0 = (float)(int8_t)((slo >> hb) & 255u);
+    const float s1 = (float)(int8_t)((slo >> (16 + hb)) & 255u);
+    const float s2 = (float)(int8_t)((shi >> hb) & 255u);
+    const float s3 = (float)(int8_t)((shi >> (16 + hb)) & 255u);
+    const float t0 = fma4u(u0, xv[0], -32.f * xs[0]);
+    const float t1 = fma4u(u1, xv[1], -32.f * xs[1]);
+    const float t2 = fma4u(u2, xv[2], -32.f * xs[2]);
+    const float t3 = fma4u(u3, xv[3], -32.f * xs[3]);
+    return d * fmaf(s0, t0, fmaf(s1, t1, fmaf(s2, t2, s3 * t3)));
+  }
+}
+
+// KS waves of the workgroup split a row group's blocks (wave s takes steps
+// s, s + KS, ...) and merge through LDS; KS == 1: four row groups per
+// workgroup.
+template <int QT, int R, int KS>
+__global__ __launch_bounds__(256) void quant_direct_kernel(const uint8_t* __restrict__ w,
+                                                           const float* __restrict__ x,
+                                                           float* __restrict__ y, int M, int K) {
+  using F = QD<QT>;
+  constexpr int BPI = 64 / F::LPB;
+  __shared__ float part[4][R];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int row0 = (KS == 1 ? blockIdx.x * 4 + wave : blockIdx.x) * R;
+  const int s0 = KS == 1 ? 0 : wave;
+  if (KS == 1 && row0 >= M) return;
+  const int j = lane % F::LPB, bl = lane / F::LPB;
+  const int nb = K / F::QKB;
+  const uint32_t rowbytes = (uint32_t)nb * F::BB;
+  const int iters = (nb + BPI - 1) / BPI;
+  // One buffer resource per row, based at the dword holding its first byte.
+  rsrc_t rs[R];
+  uint32_t ps[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const uint8_t* rp = w + (size_t)min(row0 + r, M - 1) * rowbytes;
+    ps[r] = (uint32_t)((uintptr_t)rp & 3);
+    // Whole dwords: the range check drops a dword that ends past the size.
+    rs[r] = make_rsrc(rp - ps[r], (rowbytes + ps[r] + 3) & ~3u);
+  }
+  float acc[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = 0.f;
+
+  // Two register sets used in turn (a copy between them would wait for the
+  // loads in flight): the next step's loads are issued before this step's
+  // math.
+  QRaw<QT> ra[R], rb[R];
+  f32x4 xa[F::NX], xb[F::NX];
+  auto load = [&](int it, QRaw<QT>* raw, f32x4* xv) {
+    const int b = min(it * BPI + bl, nb - 1);
+    const float* xp = x + (size_t)b * F::QKB;
+#pragma unroll
+    for (int k = 0; k < F::NX; ++k) xv[k] = *(const f32x4*)(xp + x_off<QT>(j, k));
+#pragma unroll
+    for (int r = 0; r < R; ++r) load_raw<QT>(rs[r], ps[r] + (uint32_t)b * F::BB, j, raw[r]);
+  };
+  auto compute = [&](int it, const QRaw<QT>* raw, const f32x4* xv) {
+    const bool valid = it * BPI + bl < nb;
+    const uint32_t b = (uint32_t)min(it * BPI + bl, nb - 1);
+    float xs[F::NS > 0 ? F::NS : 1];
+    x_sums<QT>(xv, xs);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const float v = compute_raw<QT>(raw[r], j, (ps[r] + b * F::BB) & 3, xv, xs);
+      acc[r] += valid ? v : 0.f;
+    }
+  };
+  // Steps of this wave (wave-uniform: the look-ahead branch is scalar).
+  const int nsteps = __builtin_amdgcn_readfirstlane(s0 < iters ? (iters - s0 + KS - 1) / KS : 0);
+  if (nsteps > 0) load(s0, ra, xa);
+  int p = 0;
+  for (; p + 1 < nsteps; p += 2) {
+    const int it = s0 + p * KS;
+    load(it + KS, rb, xb);
+    compute(it, ra, xa);
+    if (p + 2 < nsteps) load(it + 2 * KS, ra, xa);
+    compute(it + KS, rb, xb);
+  }
+  if (p < nsteps) compute(s0 + p * KS, ra, xa);
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    float a = acc[r];
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) a += __shfl_xor(a, o, 64);
+    acc[r] = a;
+  }
+  if (KS == 1) {
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+      if (lane == 0 && row0 + r < M) y[row0 + r] = acc[r];
+    return;
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) part[wave][r] = acc[r];
+  }
+  __syncthreads();
+  if (threadIdx.x < R && row0 + (int)threadIdx.x < M) {
+    const int r = threadIdx.x;
+    y[row0 + r] = (part[0][r] + part[1][r]) + (part[2][r] + part[3][r]);
+  }
+}
+
+template <int QT, int R, int KS>
+void launch_direct(const uint8_t* w, const float* x, float* y, int M, int K, hipStream_t stream) {
+  const int groups = (M + R - 1) / R;
+  const int grid = KS == 1 ? (groups + 3) / 4 : groups;
+  hipLaunchKernelGGL((quant_direct_kernel<QT, R, KS>), dim3(grid), dim3(256), 0, stream, w, x, y, M, K);
+}
+
+template <int QT>
+void launch_direct_plan(const uint8_t* w, const float* x, float* y, int M, int K, hipStream_t stream) {
+  // Four-way split of the blocks when every wave still gets a step: 4x the
+  // waves and loads in flight for decode-sized M.
+  const int iters = (K / QD<QT>::QKB + 64 / QD<QT>::LPB - 1) / (64 / QD<QT>::LPB);
+  constexpr bool r4 = QT != 14 && QT != 12;  // Q4_K / Q6_K at four rows: ~200+ VGPRs
+  if (iters >= 4) {
+    if (r4 && M >= 8192) launch_direct<QT, 4, 4>(w, x, y, M, K, stream);
+    else if (M >= 2048) launch_direct<QT, 2, 4>(w, x, y, M, K, stream);
+    else launch_direct<QT, 1, 4>(w, x, y, M, K, stream);
+  } else {
+    if (r4 && M >= 8192) launch_direct<QT, 4, 1>(w, x, y, M, K, stream);
+    else if (M >= 2048) launch_direct<QT, 2, 1>(w, x, y, M, K, stream);
+    else launch_direct<QT, 1, 1>(w, x, y, M, K, stream);
+  }
+}
+
 template <int QT, int WPR>
 void launch_q(const uint8_t* w, const float* x, float* y, int M, int K, bool aligned, bool v4,
               hipStream_t stream) {
@@ -223,6 +538,16 @@ void launch_qt(const uint8_t* w, const float* x, float* y, int M, int K, hipStre
   const long long rowbytes = (long long)(K / QFmt<QT>::QK) * QFmt<QT>::BYTES;
   const bool aligned = rowbytes % 4 == 0 && ((uintptr_t)w & 3) == 0;
   const bool v4 = ((uintptr_t)x & 15) == 0;
+  // Direct kernel when x is 16-byte aligned and the blocks are as aligned as
+  // the format allows (F16 rows of whole 8-half groups on 16 bytes, Q4_K on
+  // 16, Q8_0 / Q6_K on 2).
+  const uintptr_t wa = (uintptr_t)w;
+  const bool direct = v4 && rowbytes < (1LL << 31) && (QT == 1 ? (K % 8 == 0 && (wa & 15) == 0)
+                                     : QT == 12 ? (wa & 15) == 0 : (wa & 1) == 0);
+  if (direct) {
+    launch_direct_plan<QT>(w, x, y, M, K, stream);
+    return;
+  }
   if (M >= 2048) launch_q<QT, 1>(w, x, y, M, K, aligned, v4, stream);
   else launch_q<QT, 4>(w, x, y, M, K, aligned, v4, stream);
 }

@@ -19,6 +19,18 @@ CASES = [
     (8, 300, 4096), (8, 4096, 4096), (8, 17, 1120),     # K % 64 != 0: byte loads
     (12, 300, 4096), (12, 4096, 4096), (12, 1024, 14336), (12, 5, 256),
     (14, 300, 4096), (14, 2048, 4096), (14, 33, 768),   # K % 512 != 0: byte loads
+    # four rows per wave (M >= 8192)
+    (1, 8193, 64), (8, 8195, 256), (12, 8200, 512), (14, 8199, 512),
+]
+
+# (qtype, rows, k, byte offset of w, float offset of x): a 2-byte weight
+# offset flips the parity of every Q8_0 / Q6_K block start; an odd byte
+# offset or an x that is not 16-byte aligned takes the LDS-staged kernel.
+OFFSET_CASES = [
+    (1, 300, 512, 0, 1), (1, 300, 544, 2, 0), (1, 300, 512, 16, 0),
+    (8, 300, 1024, 2, 0), (8, 3000, 1056, 2, 0), (8, 300, 1024, 1, 0), (8, 300, 1024, 0, 3),
+    (12, 300, 1024, 4, 0), (12, 300, 1024, 16, 0), (12, 2500, 1024, 0, 2),
+    (14, 300, 1024, 2, 0), (14, 9000, 768, 2, 0), (14, 300, 1024, 3, 0), (14, 300, 768, 0, 1),
 ]
 
 
@@ -32,6 +44,25 @@ def test_linear_col_quant_matches_oracle(hl, orc, case):
     x = orc.normal(K, 7100 + case)
     y = torch.full((M,), float("nan"), device="cuda")
     A.gpu_linear_col_quant(y, torch.from_numpy(x).cuda(), torch.from_numpy(raw).cuda(), K, M, qt)
+    torch.cuda.synchronize()
+    W = orc.dequant_rows(qt, raw, M, K).astype(np.float64)
+    assert rel_err(y.cpu().numpy(), W @ x.astype(np.float64)) < TOL_F32
+
+
+@pytest.mark.parametrize("case", range(len(OFFSET_CASES)))
+def test_linear_col_quant_offsets(hl, orc, case):
+    from hippo_leap_amd import attention as A
+    qt, M, K, wo, xo = OFFSET_CASES[case]
+    print(f"quant GEMV offset case {case}: type {qt} M={M} K={K} w+{wo} x+{xo}", flush=True)
+    rng = np.random.default_rng(7200 + case)
+    raw = random_rows(rng, qt, M, K)
+    x = orc.normal(K, 7300 + case)
+    wbuf = torch.zeros(raw.size + 16, dtype=torch.uint8, device="cuda")
+    wbuf[wo:wo + raw.size] = torch.from_numpy(raw).cuda()
+    xbuf = torch.zeros(K + 4, device="cuda")
+    xbuf[xo:xo + K] = torch.from_numpy(x).cuda()
+    y = torch.full((M,), float("nan"), device="cuda")
+    A.gpu_linear_col_quant(y, xbuf[xo:], wbuf[wo:], K, M, qt)
     torch.cuda.synchronize()
     W = orc.dequant_rows(qt, raw, M, K).astype(np.float64)
     assert rel_err(y.cpu().numpy(), W @ x.astype(np.float64)) < TOL_F32
