@@ -403,9 +403,9 @@ __device__ __forceinline__ float compute_raw(const QRaw<QT>& r, int j, uint32_t 
   }
 }
 
-// KS waves of the workgroup split a row group's blocks (wave s takes steps
-// s, s + KS, ...) and merge through LDS; KS == 1: four row groups per
-// workgroup.
+// KS waves (1, 2 or 4) split a row group's blocks (wave s of the group takes
+// steps s, s + KS, ...) and merge through LDS; a workgroup holds 4 / KS
+// row groups.
 template <int QT, int R, int KS>
 __global__ __launch_bounds__(256) void quant_direct_kernel(const uint8_t* __restrict__ w,
                                                            const float* __restrict__ x,
@@ -415,9 +415,9 @@ __global__ __launch_bounds__(256) void quant_direct_kernel(const uint8_t* __rest
   __shared__ float part[4][R];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int row0 = (KS == 1 ? blockIdx.x * 4 + wave : blockIdx.x) * R;
-  const int s0 = KS == 1 ? 0 : wave;
-  if (KS == 1 && row0 >= M) return;
+  const int row0 = (blockIdx.x * (4 / KS) + wave / KS) * R;
+  const int s0 = wave % KS;
+  if (KS == 1 && row0 >= M) return;  // no barrier below for KS == 1
   const int j = lane % F::LPB, bl = lane / F::LPB;
   const int nb = K / F::QKB;
   const uint32_t rowbytes = (uint32_t)nb * F::BB;
@@ -490,34 +490,37 @@ __global__ __launch_bounds__(256) void quant_direct_kernel(const uint8_t* __rest
     for (int r = 0; r < R; ++r) part[wave][r] = acc[r];
   }
   __syncthreads();
-  if (threadIdx.x < R && row0 + (int)threadIdx.x < M) {
-    const int r = threadIdx.x;
-    y[row0 + r] = (part[0][r] + part[1][r]) + (part[2][r] + part[3][r]);
+  if (s0 == 0 && lane < R && row0 + lane < M) {
+    float t = 0.f;
+#pragma unroll
+    for (int i = 0; i < KS; ++i) t += part[wave + i][lane];
+    y[row0 + lane] = t;
   }
 }
 
 template <int QT, int R, int KS>
 void launch_direct(const uint8_t* w, const float* x, float* y, int M, int K, hipStream_t stream) {
   const int groups = (M + R - 1) / R;
-  const int grid = KS == 1 ? (groups + 3) / 4 : groups;
+  const int grid = (groups + 4 / KS - 1) / (4 / KS);
   hipLaunchKernelGGL((quant_direct_kernel<QT, R, KS>), dim3(grid), dim3(256), 0, stream, w, x, y, M, K);
+}
+
+template <int QT, int KS>
+void launch_direct_r(const uint8_t* w, const float* x, float* y, int M, int K, hipStream_t stream) {
+  constexpr bool r4 = QT != 14 && QT != 12;  // Q4_K / Q6_K at four rows: ~200+ VGPRs
+  if (r4 && M >= 8192) launch_direct<QT, 4, KS>(w, x, y, M, K, stream);
+  else if (M >= 2048) launch_direct<QT, 2, KS>(w, x, y, M, K, stream);
+  else launch_direct<QT, 1, KS>(w, x, y, M, K, stream);
 }
 
 template <int QT>
 void launch_direct_plan(const uint8_t* w, const float* x, float* y, int M, int K, hipStream_t stream) {
-  // Four-way split of the blocks when every wave still gets a step: 4x the
-  // waves and loads in flight for decode-sized M.
+  // Split a row's blocks over four waves when each gets a step: more waves
+  // and loads in flight for decode-sized M.  (A two-way split of 2-3 steps
+  // measured slower than none: Q4_K 4096x4096 5.5 -> 7.2 us.)
   const int iters = (K / QD<QT>::QKB + 64 / QD<QT>::LPB - 1) / (64 / QD<QT>::LPB);
-  constexpr bool r4 = QT != 14 && QT != 12;  // Q4_K / Q6_K at four rows: ~200+ VGPRs
-  if (iters >= 4) {
-    if (r4 && M >= 8192) launch_direct<QT, 4, 4>(w, x, y, M, K, stream);
-    else if (M >= 2048) launch_direct<QT, 2, 4>(w, x, y, M, K, stream);
-    else launch_direct<QT, 1, 4>(w, x, y, M, K, stream);
-  } else {
-    if (r4 && M >= 8192) launch_direct<QT, 4, 1>(w, x, y, M, K, stream);
-    else if (M >= 2048) launch_direct<QT, 2, 1>(w, x, y, M, K, stream);
-    else launch_direct<QT, 1, 1>(w, x, y, M, K, stream);
-  }
+  if (iters >= 4) launch_direct_r<QT, 4>(w, x, y, M, K, stream);
+  else launch_direct_r<QT, 1>(w, x, y, M, K, stream);
 }
 
 template <int QT, int WPR>

@@ -21,6 +21,8 @@ CASES = [
     (14, 300, 4096), (14, 2048, 4096), (14, 33, 768),   # K % 512 != 0: byte loads
     # four rows per wave (M >= 8192)
     (1, 8193, 64), (8, 8195, 256), (12, 8200, 512), (14, 8199, 512),
+    # K between one and four wave steps
+    (1, 300, 1024), (8, 2100, 1024), (14, 700, 2048), (12, 9000, 4096),
 ]
 
 # (qtype, rows, k, byte offset of w, float offset of x): a 2-byte weight
