@@ -15,7 +15,9 @@ HL_OK, HL_EINVAL, HL_ECAPACITY, HL_EUNSUPPORTED, HL_EHIP = 0, -1, -2, -3, -4
 HL_F32, HL_F16, HL_BF16, HL_FP8 = 0, 1, 2, 3
 HL_ROPE_HALF_SPLIT, HL_ROPE_INTERLEAVED = 0, 1
 HL_KV_COLMAJOR, HL_KV_TILED32, HL_KV_PAGED32 = 0, 1, 2
-HL_GGML_F16, HL_GGML_Q8_0, HL_GGML_Q4_K, HL_GGML_Q6_K = 1, 8, 12, 14
+HL_GGML_F16, HL_GGML_Q5_0, HL_GGML_Q5_1, HL_GGML_Q8_0 = 1, 6, 7, 8
+HL_GGML_Q2_K, HL_GGML_Q3_K, HL_GGML_Q4_K, HL_GGML_Q5_K, HL_GGML_Q6_K = 10, 11, 12, 13, 14
+HL_GGML_IQ4_NL = 20
 
 c_int, c_float, c_void_p, c_size_t, c_longlong = (
     ctypes.c_int, ctypes.c_float, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_longlong)

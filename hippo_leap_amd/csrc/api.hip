@@ -819,9 +819,19 @@ int hl_gpu_linear_col_quant(float* dst, const float* x, const void* w_quant, int
   if (qk == 0) return fail(HL_EUNSUPPORTED, "unsupported quant type for GPU GEMV: %d", quant_type);
   if (w_cols <= 0 || w_rows <= 0)
     return fail(HL_EINVAL, "linear_col_quant: bad shape (w_cols=%d, w_rows=%d)", w_cols, w_rows);
-  if (w_cols % qk) {  // the reference's rowSize* messages (quant.nim:39-58)
-    const char* name = quant_type == HL_GGML_Q8_0 ? "q8_0" : quant_type == HL_GGML_Q4_K ? "q4_K"
-                       : quant_type == HL_GGML_Q6_K ? "q6_K" : "f16";
+  if (quant_type != HL_GGML_F16 && w_cols % qk) {  // the rowSize* messages (quant.nim:27-73)
+    const char* name = "";
+    switch (quant_type) {
+      case HL_GGML_Q5_0: name = "q5_0"; break;
+      case HL_GGML_Q5_1: name = "q5_1"; break;
+      case HL_GGML_Q8_0: name = "q8_0"; break;
+      case HL_GGML_Q2_K: name = "q2_K"; break;
+      case HL_GGML_Q3_K: name = "q3_K"; break;
+      case HL_GGML_Q4_K: name = "q4_K"; break;
+      case HL_GGML_Q5_K: name = "q5_K"; break;
+      case HL_GGML_Q6_K: name = "q6_K"; break;
+      case HL_GGML_IQ4_NL: name = "iq4_nl"; break;
+    }
     return fail(HL_EINVAL, "%s row size must be multiple of %d", name, qk);
   }
   const size_t wbytes = (size_t)quant_row_bytes(quant_type, w_cols) * w_rows;

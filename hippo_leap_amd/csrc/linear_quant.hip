@@ -39,6 +39,49 @@ template <>
 struct QFmt<14> {  // Q6_K: 128 bytes ql, 64 bytes qh, 16 int8 scales, fp16 d
   static constexpr int QK = 256, BYTES = 210, SUB = 8, CHUNK = 12;
 };
+template <>
+struct QFmt<6> {  // Q5_0: fp16 d, 32 high bits, 16 nibble bytes
+  static constexpr int QK = 32, BYTES = 22, SUB = 1, CHUNK = 64;
+};
+template <>
+struct QFmt<7> {  // Q5_1: fp16 d, fp16 m, 32 high bits, 16 nibble bytes
+  static constexpr int QK = 32, BYTES = 24, SUB = 1, CHUNK = 64;
+};
+template <>
+struct QFmt<20> {  // IQ4_NL: fp16 d, 16 nibble bytes indexing a level table
+  static constexpr int QK = 32, BYTES = 18, SUB = 1, CHUNK = 64;
+};
+template <>
+struct QFmt<10> {  // Q2_K: 16 scale/min bytes, 64 bytes of 2-bit quants, d, dmin
+  static constexpr int QK = 256, BYTES = 84, SUB = 8, CHUNK = 16;
+};
+template <>
+struct QFmt<11> {  // Q3_K: hmask[32], qs[64], 12 bytes of 6-bit scales, fp16 d
+  static constexpr int QK = 256, BYTES = 110, SUB = 8, CHUNK = 16;
+};
+template <>
+struct QFmt<13> {  // Q5_K: d, dmin, 12 scale bytes, qh[32], qs[128]
+  static constexpr int QK = 256, BYTES = 176, SUB = 8, CHUNK = 16;
+};
+
+// The IQ4_NL format's 16 non-linear levels (quant.nim:16-17).
+__constant__ float kIq4nlLevels[16] = {-127.f, -104.f, -83.f, -65.f, -49.f, -35.f, -22.f, -10.f,
+                                       1.f,    13.f,   25.f,  38.f,  53.f,  69.f,  89.f,  113.f};
+
+__device__ __forceinline__ uint32_t u32_at(const uint8_t* p) {
+  return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
+}
+
+// getScaleMinK4 (quant.nim:235-242): 6-bit scale / min j of the 12 bytes.
+__device__ __forceinline__ void scale_min_k4(const uint8_t* sc, int j, int& scv, int& mnv) {
+  if (j < 4) {
+    scv = sc[j] & 63;
+    mnv = sc[j + 4] & 63;
+  } else {
+    scv = (sc[j + 4] & 0x0F) | ((sc[j - 4] >> 6) << 4);
+    mnv = (sc[j + 4] >> 4) | ((sc[j] >> 6) << 4);
+  }
+}
 
 __device__ __forceinline__ float half_at(const uint8_t* p) {
   return f16_bits_to_f32((uint16_t)(p[0] | (p[1] << 8)));
@@ -103,6 +146,77 @@ __device__ __forceinline__ float sub_dot(const uint8_t* bp, int sub, const float
       sx += xv[l];
     }
     return d * (float)scv * sq - dmin * (float)mnv * sx;
+  } else if constexpr (QT == 6 || QT == 7 || QT == 20) {
+    // One 32-element block: element j < 16 = low nibble of qs[j], element
+    // 16 + j = its high nibble; Q5_0 / Q5_1 add bit j of qh as bit 4.
+    constexpr int QS = QT == 6 ? 6 : QT == 7 ? 8 : 2;
+    const uint32_t qh = QT == 6 ? u32_at(bp + 2) : QT == 7 ? u32_at(bp + 4) : 0u;
+    float xv[32];
+    load_x32<V4>(xb, xv);
+    float sq = 0.f, sx = 0.f;
+#pragma unroll
+    for (int l = 0; l < 16; ++l) {
+      const int b = bp[QS + l];
+      if constexpr (QT == 20) {
+        sq += kIq4nlLevels[b & 15] * xv[l] + kIq4nlLevels[b >> 4] * xv[16 + l];
+      } else {
+        const int q0 = (b & 15) | (int)(((qh >> l) & 1u) << 4);
+        const int q1 = (b >> 4) | (int)(((qh >> (l + 16)) & 1u) << 4);
+        sq += (float)q0 * xv[l] + (float)q1 * xv[16 + l];
+        sx += xv[l] + xv[16 + l];
+      }
+    }
+    const float d = half_at(bp);
+    if constexpr (QT == 6) return d * (sq - 16.f * sx);  // d * (q - 16)
+    else if constexpr (QT == 7) return d * sq + half_at(bp + 2) * sx;  // d * q + m
+    else return d * sq;
+  } else if constexpr (QT == 10 || QT == 11) {
+    // Q2_K / Q3_K sub k = 4n + j: elements 32k + l, bits 2j of
+    // qs[32n + l]; scale 8n + 2j + (l >= 16).  Q3_K subtracts 4 unless bit
+    // 4n + j of hmask[l] is set, and its scales are 6-bit minus 32.
+    const int n = sub >> 2, j = sub & 3;
+    const uint8_t* qs = bp + (QT == 10 ? 16 : 32) + 32 * n;
+    float xv[32];
+    load_x32<V4>(xb + 32 * sub, xv);
+    float s0 = 0.f, s1 = 0.f, x0 = 0.f, x1 = 0.f;
+#pragma unroll
+    for (int l = 0; l < 32; ++l) {
+      int q = (qs[l] >> (2 * j)) & 3;
+      if constexpr (QT == 11) q -= ((bp[l] >> (4 * n + j)) & 1) ? 0 : 4;
+      if (l < 16) { s0 += (float)q * xv[l]; x0 += xv[l]; }
+      else { s1 += (float)q * xv[l]; x1 += xv[l]; }
+    }
+    const int i0 = 8 * n + 2 * j;
+    if constexpr (QT == 10) {
+      const float d = half_at(bp + 80), dmin = half_at(bp + 82);
+      const int c0 = bp[i0], c1 = bp[i0 + 1];
+      return d * ((float)(c0 & 15) * s0 + (float)(c1 & 15) * s1) -
+             dmin * ((float)(c0 >> 4) * x0 + (float)(c1 >> 4) * x1);
+    } else {
+      const uint8_t* sc = bp + 96;
+      auto scale = [&](int i) {
+        const int lo = i < 8 ? (sc[i] & 15) : (sc[i - 8] >> 4);
+        return (float)((lo | (((sc[8 + (i & 3)] >> (2 * (i >> 2))) & 3) << 4)) - 32);
+      };
+      return half_at(bp + 108) * (scale(i0) * s0 + scale(i0 + 1) * s1);
+    }
+  } else if constexpr (QT == 13) {
+    // Q5_K sub s: elements 32s + l, nibble s & 1 of qs[32(s/2) + l], bit s of
+    // qh[l] as bit 4, scale / min s as Q4_K.
+    int scv, mnv;
+    scale_min_k4(bp + 4, sub, scv, mnv);
+    const uint8_t* q = bp + 48 + 32 * (sub >> 1);
+    const int sh = 4 * (sub & 1);
+    float xv[32];
+    load_x32<V4>(xb + 32 * sub, xv);
+    float sq = 0.f, sx = 0.f;
+#pragma unroll
+    for (int l = 0; l < 32; ++l) {
+      const int v = ((q[l] >> sh) & 15) | (((bp[16 + l] >> sub) & 1) << 4);
+      sq += (float)v * xv[l];
+      sx += xv[l];
+    }
+    return half_at(bp) * (float)scv * sq - half_at(bp + 2) * (float)mnv * sx;
   } else {
     // Q6_K sub j = 4n + t: elements 128n + 32t + l; low 4 bits from
     // ql[64n + 32(t&1) + l] (nibble t>>1), high 2 bits from qh[32n + l]
@@ -228,6 +342,8 @@ struct QD<8> { static constexpr int LPB = 4, QKB = 32, BB = 34, NX = 2, NS = 1; 
 template <>
 struct QD<12> { static constexpr int LPB = 8, QKB = 256, BB = 144, NX = 8, NS = 2; };  // 32 nibbles
 template <>
+struct QD<13> { static constexpr int LPB = 8, QKB = 256, BB = 176, NX = 8, NS = 2; };  // 32 x 5 bit
+template <>
 struct QD<14> { static constexpr int LPB = 16, QKB = 256, BB = 210, NX = 4, NS = 4; }; // 16 x 6 bit
 
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
@@ -241,6 +357,8 @@ template <>
 struct QRaw<8> { u32x2 p; uint32_t q, d; };
 template <>
 struct QRaw<12> { u32x4 hdr, q; };
+template <>
+struct QRaw<13> { u32x4 hdr, q, h; };
 template <>
 struct QRaw<14> { uint32_t a0, a1, b0, b1, h0, h1; u32x2 s; uint32_t s2, d; };
 
@@ -268,7 +386,7 @@ template <int QT>
 __device__ __forceinline__ int x_off(int j, int k) {
   if constexpr (QT == 1) return 4 * k;
   else if constexpr (QT == 8) return 8 * j + 4 * k;
-  else if constexpr (QT == 12)  // sub 2c: k < 4, sub 2c+1: k >= 4; 16 of each
+  else if constexpr (QT == 12 || QT == 13)  // sub 2c: k < 4, sub 2c+1: k >= 4; 16 of each
     return 64 * (j >> 1) + 32 * (k >> 2) + 16 * (j & 1) + 4 * (k & 3);
   else return 128 * (j >> 3) + 32 * k + 4 * (j & 7);
 }
@@ -286,6 +404,10 @@ __device__ __forceinline__ void load_raw(rsrc_t rs, uint32_t off, int j, QRaw<QT
   } else if constexpr (QT == 12) {
     r.hdr = bl128(rs, off);
     r.q = bl128(rs, off + 16 + 32 * (j >> 1) + 16 * (j & 1));
+  } else if constexpr (QT == 13) {
+    r.hdr = bl128(rs, off);
+    r.h = bl128(rs, off + 16 + 16 * (j & 1));
+    r.q = bl128(rs, off + 48 + 32 * (j >> 1) + 16 * (j & 1));
   } else {
     const uint32_t n = j >> 3, l0 = 4 * (j & 7);
     r.a0 = bl32(rs, off + 64 * n + l0);
@@ -328,13 +450,30 @@ template <int QT>
 __device__ __forceinline__ void x_sums(const f32x4* xv, float* xs) {
   if constexpr (QT == 8) {
     xs[0] = hsum4(xv[0]) + hsum4(xv[1]);
-  } else if constexpr (QT == 12) {
+  } else if constexpr (QT == 12 || QT == 13) {
     xs[0] = (hsum4(xv[0]) + hsum4(xv[1])) + (hsum4(xv[2]) + hsum4(xv[3]));
     xs[1] = (hsum4(xv[4]) + hsum4(xv[5])) + (hsum4(xv[6]) + hsum4(xv[7]));
   } else if constexpr (QT == 14) {
 #pragma unroll
     for (int k = 0; k < 4; ++k) xs[k] = hsum4(xv[k]);
   }
+}
+
+// Q4_K / Q5_K 6-bit scales and mins of sub-blocks 2c and 2c+1: bytes
+// 2(c&1), 2(c&1)+1 of 16-bit pairs built branch-free from the scale dwords
+// Y = bytes 0-3, Z = 4-7, W = 8-11 (getScaleMinK4, quant.nim:235-242).
+__device__ __forceinline__ void k4_pair(const u32x4& hdr, int c, float& sc0, float& sc1, float& mn0,
+                                        float& mn1) {
+  const uint32_t sh = 16 * (c & 1);
+  const uint32_t Y = hdr.y >> sh, Z = hdr.z >> sh, W = hdr.w >> sh;
+  const bool lo = c < 2;
+  const uint32_t m1 = lo ? 0x3F3Fu : 0x0F0Fu, m2 = lo ? 0u : 0x3030u;
+  const uint32_t SC = ((lo ? Y : W) & m1) | ((Y >> 2) & m2);
+  const uint32_t MN = ((lo ? Z : (W >> 4)) & m1) | ((Z >> 2) & m2);
+  sc0 = (float)(SC & 255u);
+  sc1 = (float)((SC >> 8) & 255u);
+  mn0 = (float)(MN & 255u);
+  mn1 = (float)((MN >> 8) & 255u);
 }
 
 // ps: the block's first byte within its dword (0 or 2 for Q8_0 / Q6_K).
@@ -359,29 +498,34 @@ __device__ __forceinline__ float compute_raw(const QRaw<QT>& r, int j, uint32_t 
     const uint32_t q0 = al(r.p.y, r.p.x, sb) ^ 0x80808080u, q1 = al(r.q, r.p.y, sb) ^ 0x80808080u;
     const float d = f16_bits_to_f32((uint16_t)((r.d >> (8 * ps)) & 0xFFFFu));
     return d * (fma4u(q1, xv[1], fma4u(q0, xv[0], 0.f)) - 128.f * xs[0]);
-  } else if constexpr (QT == 12) {
-    // Sub-blocks 2c (low nibbles) and 2c+1 (high nibbles); their 6-bit
-    // scales and mins are bytes 2(c&1), 2(c&1)+1 of 16-bit pairs built
-    // branch-free from the scale dwords Y = bytes 0-3, Z = 4-7, W = 8-11.
+  } else if constexpr (QT == 12 || QT == 13) {
+    // Sub-blocks 2c (low nibbles) and 2c+1 (high nibbles); Q5_K adds bits
+    // 2c / 2c+1 of qh[l] as bit 4.
     const int c = j >> 1;
-    const uint32_t sh = 16 * (c & 1);
-    const uint32_t Y = r.hdr.y >> sh, Z = r.hdr.z >> sh, W = r.hdr.w >> sh;
-    const bool lo = c < 2;
-    const uint32_t m1 = lo ? 0x3F3Fu : 0x0F0Fu, m2 = lo ? 0u : 0x3030u;
-    const uint32_t SC = ((lo ? Y : W) & m1) | ((Y >> 2) & m2);
-    const uint32_t MN = ((lo ? Z : (W >> 4)) & m1) | ((Z >> 2) & m2);
+    float sc0, sc1, mn0, mn1;
+    k4_pair(r.hdr, c, sc0, sc1, mn0, mn1);
     const float d = f16_bits_to_f32((uint16_t)(r.hdr.x & 0xFFFFu));
     const float dmin = f16_bits_to_f32((uint16_t)(r.hdr.x >> 16));
     const uint32_t q[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
     float slo = 0.f, shi = 0.f;
+    if constexpr (QT == 12) {
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      slo = fma4u(q[m] & 0x0F0F0F0Fu, xv[m], slo);
-      shi = fma4u(q[m] & 0xF0F0F0F0u, xv[4 + m], shi);  // 16 x nibble
+      for (int m = 0; m < 4; ++m) {
+        slo = fma4u(q[m] & 0x0F0F0F0Fu, xv[m], slo);
+        shi = fma4u(q[m] & 0xF0F0F0F0u, xv[4 + m], shi);  // 16 x nibble
+      }
+      shi *= 0.0625f;
+    } else {
+      const uint32_t h[4] = {r.h.x, r.h.y, r.h.z, r.h.w};
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const uint32_t hl = ((h[m] >> (2 * c)) & 0x01010101u) << 4;
+        const uint32_t hh = ((h[m] >> (2 * c + 1)) & 0x01010101u) << 4;
+        slo = fma4u((q[m] & 0x0F0F0F0Fu) | hl, xv[m], slo);
+        shi = fma4u(((q[m] >> 4) & 0x0F0F0F0Fu) | hh, xv[4 + m], shi);
+      }
     }
-    const float sc0 = (float)(SC & 255u), sc1 = (float)((SC >> 8) & 255u);
-    const float mn0 = (float)(MN & 255u), mn1 = (float)((MN >> 8) & 255u);
-    return d * fmaf(sc0, slo, sc1 * 0.0625f * shi) - dmin * fmaf(mn0, xs[0], mn1 * xs[1]);
+    return d * fmaf(sc0, slo, sc1 * shi) - dmin * fmaf(mn0, xs[0], mn1 * xs[1]);
   } else {
     const uint32_t qa = al(r.a1, r.a0, ps), qb = al(r.b1, r.b0, ps), qh = al(r.h1, r.h0, ps);
     const uint32_t slo = al(r.s.y, r.s.x, ps), shi = al(r.s2, r.s.y, ps);
@@ -507,7 +651,7 @@ void launch_direct(const uint8_t* w, const float* x, float* y, int M, int K, hip
 
 template <int QT, int KS>
 void launch_direct_r(const uint8_t* w, const float* x, float* y, int M, int K, hipStream_t stream) {
-  constexpr bool r4 = QT != 14 && QT != 12;  // Q4_K / Q6_K at four rows: ~200+ VGPRs
+  constexpr bool r4 = QT == 1 || QT == 8;  // Q4_K / Q5_K / Q6_K at four rows: ~200+ VGPRs
   if (r4 && M >= 8192) launch_direct<QT, 4, KS>(w, x, y, M, K, stream);
   else if (M >= 2048) launch_direct<QT, 2, KS>(w, x, y, M, K, stream);
   else launch_direct<QT, 1, KS>(w, x, y, M, K, stream);
@@ -536,6 +680,23 @@ void launch_q(const uint8_t* w, const float* x, float* y, int M, int K, bool ali
   }
 }
 
+// F16 rows of any length (the reference's F16 GEMV, naive.nim:1342-1366,
+// takes any wCols): one wave per row, lanes stride the columns.  Used only
+// when K is not a multiple of 32; other F16 shapes take the kernels above.
+__global__ __launch_bounds__(256) void f16_gemv_any_kernel(const uint16_t* __restrict__ w,
+                                                           const float* __restrict__ x,
+                                                           float* __restrict__ y, int M, int K) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= M) return;
+  const uint16_t* wr = w + (size_t)row * K;
+  float acc = 0.f;
+  for (int c = lane; c < K; c += 64) acc = fmaf(f16_bits_to_f32(wr[c]), x[c], acc);
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) acc += __shfl_xor(acc, o, 64);
+  if (lane == 0) y[row] = acc;
+}
+
 template <int QT>
 void launch_qt(const uint8_t* w, const float* x, float* y, int M, int K, hipStream_t stream) {
   const long long rowbytes = (long long)(K / QFmt<QT>::QK) * QFmt<QT>::BYTES;
@@ -545,11 +706,15 @@ void launch_qt(const uint8_t* w, const float* x, float* y, int M, int K, hipStre
   // the format allows (F16 rows of whole 8-half groups on 16 bytes, Q4_K on
   // 16, Q8_0 / Q6_K on 2).
   const uintptr_t wa = (uintptr_t)w;
-  const bool direct = v4 && rowbytes < (1LL << 31) && (QT == 1 ? (K % 8 == 0 && (wa & 15) == 0)
-                                     : QT == 12 ? (wa & 15) == 0 : (wa & 1) == 0);
-  if (direct) {
-    launch_direct_plan<QT>(w, x, y, M, K, stream);
-    return;
+  constexpr bool has_direct = QT == 1 || QT == 8 || QT == 12 || QT == 13 || QT == 14;
+  const bool direct = has_direct && v4 && rowbytes < (1LL << 31) &&
+                      (QT == 1 ? (K % 8 == 0 && (wa & 15) == 0)
+                       : (QT == 12 || QT == 13) ? (wa & 15) == 0 : (wa & 1) == 0);
+  if constexpr (has_direct) {
+    if (direct) {
+      launch_direct_plan<QT>(w, x, y, M, K, stream);
+      return;
+    }
   }
   if (M >= 2048) launch_q<QT, 1>(w, x, y, M, K, aligned, v4, stream);
   else launch_q<QT, 4>(w, x, y, M, K, aligned, v4, stream);
@@ -559,10 +724,10 @@ void launch_qt(const uint8_t* w, const float* x, float* y, int M, int K, hipStre
 
 int quant_block_elems(int qtype) {
   switch (qtype) {
-    case HL_GGML_F16: return 32;
-    case HL_GGML_Q8_0: return 32;
-    case HL_GGML_Q4_K: return 256;
-    case HL_GGML_Q6_K: return 256;
+    case HL_GGML_F16: case HL_GGML_Q5_0: case HL_GGML_Q5_1: case HL_GGML_Q8_0: case HL_GGML_IQ4_NL:
+      return 32;
+    case HL_GGML_Q2_K: case HL_GGML_Q3_K: case HL_GGML_Q4_K: case HL_GGML_Q5_K: case HL_GGML_Q6_K:
+      return 256;
     default: return 0;
   }
 }
@@ -570,8 +735,14 @@ int quant_block_elems(int qtype) {
 long long quant_row_bytes(int qtype, int K) {
   switch (qtype) {
     case HL_GGML_F16: return 2LL * K;
+    case HL_GGML_Q5_0: return (long long)(K / 32) * 22;
+    case HL_GGML_Q5_1: return (long long)(K / 32) * 24;
     case HL_GGML_Q8_0: return (long long)(K / 32) * 34;
+    case HL_GGML_IQ4_NL: return (long long)(K / 32) * 18;
+    case HL_GGML_Q2_K: return (long long)(K / 256) * 84;
+    case HL_GGML_Q3_K: return (long long)(K / 256) * 110;
     case HL_GGML_Q4_K: return (long long)(K / 256) * 144;
+    case HL_GGML_Q5_K: return (long long)(K / 256) * 176;
     case HL_GGML_Q6_K: return (long long)(K / 256) * 210;
     default: return 0;
   }
@@ -581,10 +752,20 @@ hipError_t linear_quant_launch(float* y, const float* x, const void* w, int K, i
                                hipStream_t stream) {
   const uint8_t* wb = (const uint8_t*)w;
   switch (qtype) {
-    case HL_GGML_F16: launch_qt<1>(wb, x, y, M, K, stream); break;
+    case HL_GGML_F16:
+      if (K % 32 == 0) launch_qt<1>(wb, x, y, M, K, stream);
+      else hipLaunchKernelGGL(f16_gemv_any_kernel, dim3((M + 3) / 4), dim3(256), 0, stream,
+                              (const uint16_t*)w, x, y, M, K);
+      break;
+    case HL_GGML_Q5_0: launch_qt<6>(wb, x, y, M, K, stream); break;
+    case HL_GGML_Q5_1: launch_qt<7>(wb, x, y, M, K, stream); break;
     case HL_GGML_Q8_0: launch_qt<8>(wb, x, y, M, K, stream); break;
+    case HL_GGML_Q2_K: launch_qt<10>(wb, x, y, M, K, stream); break;
+    case HL_GGML_Q3_K: launch_qt<11>(wb, x, y, M, K, stream); break;
     case HL_GGML_Q4_K: launch_qt<12>(wb, x, y, M, K, stream); break;
+    case HL_GGML_Q5_K: launch_qt<13>(wb, x, y, M, K, stream); break;
     case HL_GGML_Q6_K: launch_qt<14>(wb, x, y, M, K, stream); break;
+    case HL_GGML_IQ4_NL: launch_qt<20>(wb, x, y, M, K, stream); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

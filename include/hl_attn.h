@@ -182,13 +182,19 @@ int hl_gpu_linear_col(float* dst, const float* x, const float* w, int w_cols,
 
 /* GGUF weight types of hl_gpu_linear_col_quant (ggml's type ids, as the
  * reference's GgmlType* constants, model.nim:11-21).                        */
-enum { HL_GGML_F16 = 1, HL_GGML_Q8_0 = 8, HL_GGML_Q4_K = 12, HL_GGML_Q6_K = 14 };
+enum {
+  HL_GGML_F16 = 1, HL_GGML_Q5_0 = 6, HL_GGML_Q5_1 = 7, HL_GGML_Q8_0 = 8,
+  HL_GGML_Q2_K = 10, HL_GGML_Q3_K = 11, HL_GGML_Q4_K = 12, HL_GGML_Q5_K = 13,
+  HL_GGML_Q6_K = 14, HL_GGML_IQ4_NL = 20
+};
 
 /* gpuLinearColQuant (naive.nim:1580-1592): dst[wRows] = dequant(w)[wRows,
  * wCols] . x[wCols] for one token (the reference's quantized GEMVs are
- * decode-only), with w the GGUF rows of quant_type: HL_GGML_F16, Q8_0, Q4_K
- * or Q6_K (dequantisation as quant.nim:235-355).  wCols must be a multiple
- * of the block (32; 256 for the K-quants): HL_EINVAL with the reference's
+ * decode-only), with w the GGUF rows of quant_type, every type the
+ * reference dispatches: F16, Q5_0, Q5_1, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K,
+ * IQ4_NL (dequantisation as quant.nim:132-441; Q5_K as the reference's GPU
+ * kernel, naive.nim:1267-1323).  wCols must be a multiple of the block (32;
+ * 256 for the K-quants; any for F16): HL_EINVAL with the reference's
  * row-size message otherwise.  Other types: HL_EUNSUPPORTED ("unsupported
  * quant type for GPU GEMV: <type>").  dst must not overlap x or w.        */
 int hl_gpu_linear_col_quant(float* dst, const float* x, const void* w_quant,

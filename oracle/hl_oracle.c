@@ -561,18 +561,169 @@ static void orc_dequant_q6k(const uint8_t* src, float* dst, int k) {
   }
 }
 
-/* Rows of GGUF type qtype (1 F16, 8 Q8_0, 12 Q4_K, 14 Q6_K) -> fp32
- * [rows][k]; returns the bytes per row (0: type not covered). */
+/* quant.nim:132-170: 84-byte blocks of 256: 16 scale bytes (low nibble
+ * scale, high nibble min), 64 bytes of 2-bit quants, fp16 d, fp16 dmin.
+ * Element 128n + 32j + 16g + l: bits 2j of qs[32n + 16g + l], scale byte
+ * 8n + 2j + g. */
+static void orc_dequant_q2k(const uint8_t* src, float* dst, int k) {
+  for (int b = 0; b < k / 256; ++b) {
+    const uint8_t* blk = src + (int64_t)b * 84;
+    const uint8_t* sc = blk;
+    const uint8_t* qs = blk + 16;
+    const float d = orc_half_at(blk + 80), dmin = orc_half_at(blk + 82);
+    float* out = dst + b * 256;
+    for (int n = 0; n < 2; ++n)
+      for (int j = 0; j < 4; ++j)
+        for (int g = 0; g < 2; ++g) {
+          const int s = sc[8 * n + 2 * j + g];
+          const float dl = d * (float)(s & 0x0F), ml = dmin * (float)(s >> 4);
+          for (int l = 0; l < 16; ++l)
+            out[128 * n + 32 * j + 16 * g + l] =
+                dl * (float)((qs[32 * n + 16 * g + l] >> (2 * j)) & 3) - ml;
+        }
+  }
+}
+
+/* quant.nim:172-233: 110-byte blocks of 256: hmask[32], qs[64], 12 bytes of
+ * 6-bit scales, fp16 d.  Element 128n + 32j + 16g + l: bits 2j of
+ * qs[32n + 16g + l], minus 4 unless bit 4n + j of hmask[16g + l] is set;
+ * scale 8n + 2j + g (6 bits, minus 32). */
+static void orc_dequant_q3k(const uint8_t* src, float* dst, int k) {
+  for (int b = 0; b < k / 256; ++b) {
+    const uint8_t* blk = src + (int64_t)b * 110;
+    const uint8_t* hm = blk;
+    const uint8_t* qs = blk + 32;
+    const uint8_t* s = blk + 96;
+    const float d = orc_half_at(blk + 108);
+    int scales[16];
+    for (int i = 0; i < 16; ++i) {
+      const int lo = i < 8 ? (s[i] & 0x0F) : (s[i - 8] >> 4);
+      const int hi = (s[8 + (i & 3)] >> (2 * (i >> 2))) & 3;
+      scales[i] = (lo | (hi << 4)) - 32;
+    }
+    float* out = dst + b * 256;
+    for (int n = 0; n < 2; ++n)
+      for (int j = 0; j < 4; ++j)
+        for (int g = 0; g < 2; ++g) {
+          const float dl = d * (float)scales[8 * n + 2 * j + g];
+          for (int l = 0; l < 16; ++l) {
+            const int q = (qs[32 * n + 16 * g + l] >> (2 * j)) & 3;
+            const int h = (hm[16 * g + l] >> (4 * n + j)) & 1 ? 0 : 4;
+            out[128 * n + 32 * j + 16 * g + l] = dl * (float)(q - h);
+          }
+        }
+  }
+}
+
+/* quant.nim:279-302: 22-byte blocks of 32: fp16 d, 32 high bits, 16 nibble
+ * bytes; element j < 16 = low nibble of qs[j], j >= 16 = high nibble of
+ * qs[j - 16], high bit j; value d * (q - 16). */
+static void orc_dequant_q5_0(const uint8_t* src, float* dst, int k) {
+  for (int b = 0; b < k / 32; ++b) {
+    const uint8_t* blk = src + (int64_t)b * 22;
+    const float d = orc_half_at(blk);
+    const uint32_t qh = blk[2] | (blk[3] << 8) | (blk[4] << 16) | ((uint32_t)blk[5] << 24);
+    for (int j = 0; j < 32; ++j) {
+      const int lo = j < 16 ? (blk[6 + j] & 0x0F) : (blk[6 + j - 16] >> 4);
+      const int q = lo | (int)(((qh >> j) & 1) << 4);
+      dst[b * 32 + j] = d * (float)(q - 16);
+    }
+  }
+}
+
+/* quant.nim:357-383: 24-byte blocks of 32: fp16 d, fp16 m, 32 high bits,
+ * 16 nibble bytes (as Q5_0); value d * q + m. */
+static void orc_dequant_q5_1(const uint8_t* src, float* dst, int k) {
+  for (int b = 0; b < k / 32; ++b) {
+    const uint8_t* blk = src + (int64_t)b * 24;
+    const float d = orc_half_at(blk), m = orc_half_at(blk + 2);
+    const uint32_t qh = blk[4] | (blk[5] << 8) | (blk[6] << 16) | ((uint32_t)blk[7] << 24);
+    for (int j = 0; j < 32; ++j) {
+      const int lo = j < 16 ? (blk[8 + j] & 0x0F) : (blk[8 + j - 16] >> 4);
+      const int q = lo | (int)(((qh >> j) & 1) << 4);
+      dst[b * 32 + j] = d * (float)q + m;
+    }
+  }
+}
+
+/* 176-byte blocks of 256: d, dmin, 12 scale bytes (as Q4_K), qh[32],
+ * qs[128].  Element 32s + l (sub-block s): nibble s & 1 of qs[32(s/2) + l]
+ * plus bit s of qh[l] as bit 4.  This is the GPU kernel's reading
+ * (backends/naive.nim:1267-1323), the one hl_gpu_linear_col_quant replaces;
+ * quant.nim:385-423 (dequantRowQ5K, CPU side) reads bits (s/2 rounded to
+ * even)/2 + s%2 and moves to qs for s >= 4 instead, which differs for s >= 2. */
+static void orc_dequant_q5k(const uint8_t* src, float* dst, int k) {
+  for (int b = 0; b < k / 256; ++b) {
+    const uint8_t* blk = src + (int64_t)b * 176;
+    const float d = orc_half_at(blk), dmin = orc_half_at(blk + 2);
+    const uint8_t* qh = blk + 16;
+    const uint8_t* qs = blk + 48;
+    float* out = dst + b * 256;
+    for (int s = 0; s < 8; ++s) {
+      int sc, mn;
+      orc_scale_min_k4(s, blk + 4, &sc, &mn);
+      const float dl = d * (float)sc, ml = dmin * (float)mn;
+      for (int l = 0; l < 32; ++l) {
+        const int nib = (s & 1) ? (qs[32 * (s / 2) + l] >> 4) : (qs[32 * (s / 2) + l] & 0x0F);
+        const int q = nib | (((qh[l] >> s) & 1) << 4);
+        out[32 * s + l] = dl * (float)q - ml;
+      }
+    }
+  }
+}
+
+/* quant.nim:16-17 (kvaluesIQ4NL), 425-441: 18-byte blocks of 32: fp16 d,
+ * 16 nibble bytes (as Q5_0) indexing a fixed non-linear table. */
+static const int8_t kOrcIq4nl[16] = {-127, -104, -83, -65, -49, -35, -22, -10,
+                                     1,    13,   25,  38,  53,  69,  89,  113};
+static void orc_dequant_iq4nl(const uint8_t* src, float* dst, int k) {
+  for (int b = 0; b < k / 32; ++b) {
+    const uint8_t* blk = src + (int64_t)b * 18;
+    const float d = orc_half_at(blk);
+    for (int j = 0; j < 16; ++j) {
+      dst[b * 32 + j] = d * (float)kOrcIq4nl[blk[2 + j] & 0x0F];
+      dst[b * 32 + j + 16] = d * (float)kOrcIq4nl[blk[2 + j] >> 4];
+    }
+  }
+}
+
+/* Bytes per row of k elements of GGUF type qtype, 0 if not covered. */
+int64_t orc_quant_row_bytes(int qtype, int k) {
+  switch (qtype) {
+    case 1: return 2LL * k;
+    case 6: return (int64_t)(k / 32) * 22;
+    case 7: return (int64_t)(k / 32) * 24;
+    case 8: return (int64_t)(k / 32) * 34;
+    case 10: return (int64_t)(k / 256) * 84;
+    case 11: return (int64_t)(k / 256) * 110;
+    case 12: return (int64_t)(k / 256) * 144;
+    case 13: return (int64_t)(k / 256) * 176;
+    case 14: return (int64_t)(k / 256) * 210;
+    case 20: return (int64_t)(k / 32) * 18;
+    default: return 0;
+  }
+}
+
+/* Rows of GGUF type qtype (1 F16, 6 Q5_0, 7 Q5_1, 8 Q8_0, 10 Q2_K, 11 Q3_K,
+ * 12 Q4_K, 13 Q5_K, 14 Q6_K, 20 IQ4_NL) -> fp32 [rows][k]; returns the
+ * bytes per row (0: type not covered). */
 int64_t orc_dequant_rows(int qtype, const uint8_t* src, float* dst, int rows, int k) {
-  int64_t rb = qtype == 1 ? 2LL * k : qtype == 8 ? (int64_t)(k / 32) * 34
-               : qtype == 12 ? (int64_t)(k / 256) * 144 : qtype == 14 ? (int64_t)(k / 256) * 210 : 0;
+  const int64_t rb = orc_quant_row_bytes(qtype, k);
   for (int r = 0; r < rows && rb; ++r) {
     const uint8_t* s = src + r * rb;
     float* o = dst + (int64_t)r * k;
-    if (qtype == 1) for (int i = 0; i < k; ++i) o[i] = orc_half_at(s + 2 * i);
-    else if (qtype == 8) orc_dequant_q8_0(s, o, k);
-    else if (qtype == 12) orc_dequant_q4k(s, o, k);
-    else orc_dequant_q6k(s, o, k);
+    switch (qtype) {
+      case 1: for (int i = 0; i < k; ++i) o[i] = orc_half_at(s + 2 * i); break;
+      case 6: orc_dequant_q5_0(s, o, k); break;
+      case 7: orc_dequant_q5_1(s, o, k); break;
+      case 8: orc_dequant_q8_0(s, o, k); break;
+      case 10: orc_dequant_q2k(s, o, k); break;
+      case 11: orc_dequant_q3k(s, o, k); break;
+      case 12: orc_dequant_q4k(s, o, k); break;
+      case 13: orc_dequant_q5k(s, o, k); break;
+      case 14: orc_dequant_q6k(s, o, k); break;
+      case 20: orc_dequant_iq4nl(s, o, k); break;
+    }
   }
   return rb;
 }

@@ -1,9 +1,11 @@
 """GPU parity of the quantized decode GEMV (hl_gpu_linear_col_quant, the
 drop-in for gpuLinearColQuant, backends/naive.nim:1580-1592) against the
 oracle's restatement of quant.nim's dequantisers (pinned in
-tests/test_oracle.py) followed by an fp64 product: F16, Q8_0, Q4_K and Q6_K
-rows, dword-aligned rows and the byte-load path (row sizes not a multiple of
-4), one and four waves per row.  Bar: 1e-4 relative (fp32)."""
+tests/test_oracle.py) followed by an fp64 product: every type the
+reference dispatches (F16, Q5_0, Q5_1, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K,
+IQ4_NL), dword-aligned rows and the byte-load path (row sizes not a
+multiple of 4), the direct and LDS-staged kernels, one to four rows per
+wave.  Bar: 1e-4 relative (fp32)."""
 import numpy as np
 import pytest
 import torch
@@ -21,6 +23,12 @@ CASES = [
     (14, 300, 4096), (14, 2048, 4096), (14, 33, 768),   # K % 512 != 0: byte loads
     # four rows per wave (M >= 8192)
     (1, 8193, 64), (8, 8195, 256), (12, 8200, 512), (14, 8199, 512),
+    # the other types of the reference's dispatcher (LDS-staged kernel;
+    # Q5_K also direct), F16 rows of any length
+    (6, 300, 4096), (6, 33, 96), (7, 300, 4096), (7, 2100, 1024), (20, 300, 4096), (20, 17, 160),
+    (10, 300, 4096), (10, 9, 768), (11, 300, 4096), (11, 2100, 512),
+    (13, 300, 4096), (13, 4096, 4096), (13, 8200, 1024), (13, 5, 256),
+    (1, 300, 100), (1, 70, 1), (1, 2050, 4100),
     # K between one and four wave steps
     (1, 300, 1024), (8, 2100, 1024), (14, 700, 2048), (12, 9000, 4096),
 ]
@@ -33,6 +41,8 @@ OFFSET_CASES = [
     (8, 300, 1024, 2, 0), (8, 3000, 1056, 2, 0), (8, 300, 1024, 1, 0), (8, 300, 1024, 0, 3),
     (12, 300, 1024, 4, 0), (12, 300, 1024, 16, 0), (12, 2500, 1024, 0, 2),
     (14, 300, 1024, 2, 0), (14, 9000, 768, 2, 0), (14, 300, 1024, 3, 0), (14, 300, 768, 0, 1),
+    (13, 300, 1024, 8, 0), (13, 300, 1024, 0, 1), (6, 300, 1024, 1, 0), (11, 300, 1024, 2, 3),
+    (20, 300, 1024, 3, 1), (10, 300, 1024, 2, 0), (7, 300, 1024, 1, 2),
 ]
 
 
@@ -77,6 +87,10 @@ def test_linear_col_quant_errors(hl):
     y = torch.zeros(8, device="cuda")
     w = torch.zeros(8 * 512, dtype=torch.uint8, device="cuda")
     with pytest.raises(HLError, match="unsupported quant type"):
-        A.gpu_linear_col_quant(y, x, w, 512, 8, 10)
+        A.gpu_linear_col_quant(y, x, w, 512, 8, 9)  # Q8_1: not in the reference dispatcher
     with pytest.raises(HLError, match="q4_K row size must be multiple of 256"):
         A.gpu_linear_col_quant(y, x, w, 300, 8, 12)
+    for qt, name, qk in ((6, "q5_0", 32), (7, "q5_1", 32), (10, "q2_K", 256), (11, "q3_K", 256),
+                         (13, "q5_K", 256), (20, "iq4_nl", 32)):
+        with pytest.raises(HLError, match=f"{name} row size must be multiple of {qk}"):
+            A.gpu_linear_col_quant(y, x, w, 300, 8, qt)

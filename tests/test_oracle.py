@@ -426,3 +426,66 @@ def test_dequant_q6_k_packed(orc):
 def test_dequant_f16(orc):
     x = np.asarray(np.random.default_rng(13).standard_normal(64), np.float16)
     assert np.array_equal(orc.dequant_rows(1, x.view(np.uint8), 2, 32).reshape(-1), x.astype(np.float32))
+
+
+def test_dequant_q5_0_q5_1_iq4nl_packed(orc):
+    from gguf_pack import IQ4NL_LEVELS, pack_iq4nl, pack_q5_0, pack_q5_1
+    rng = np.random.default_rng(14)
+    nb = 3
+    d = np.asarray(rng.uniform(0.01, 0.5, nb), np.float16)
+    m = np.asarray(rng.uniform(-1, 1, nb), np.float16)
+    q = rng.integers(0, 32, (nb, 32))
+    q[0] = np.arange(32)  # every 5-bit value, high bit in every position
+    d64 = d.astype(np.float64)[:, None]
+    got = orc.dequant_rows(6, pack_q5_0(d, q), 1, 32 * nb).reshape(nb, 32)
+    assert np.allclose(got, d64 * (q - 16), rtol=1e-6, atol=1e-7)
+    got = orc.dequant_rows(7, pack_q5_1(d, m, q), 1, 32 * nb).reshape(nb, 32)
+    assert np.allclose(got, d64 * q + m.astype(np.float64)[:, None], rtol=1e-6, atol=1e-6)
+    idx = rng.integers(0, 16, (nb, 32))
+    idx[0, :16] = np.arange(16)
+    got = orc.dequant_rows(20, pack_iq4nl(d, idx), 1, 32 * nb).reshape(nb, 32)
+    assert np.allclose(got, d64 * IQ4NL_LEVELS[idx], rtol=1e-6, atol=1e-7)
+
+
+def test_dequant_q2_k_packed(orc):
+    from gguf_pack import pack_q2_k, scaled_values
+    rng = np.random.default_rng(15)
+    nb = 3
+    d = np.asarray(rng.uniform(0.01, 0.1, nb), np.float16)
+    dmin = np.asarray(rng.uniform(0.0, 0.1, nb), np.float16)
+    sc, mn = rng.integers(0, 16, (nb, 16)), rng.integers(0, 16, (nb, 16))
+    sc[0], mn[0] = np.arange(16), np.arange(16)[::-1]
+    q = rng.integers(0, 4, (nb, 256))
+    got = orc.dequant_rows(10, pack_q2_k(d, dmin, sc, mn, q), 1, 256 * nb).reshape(nb, 256)
+    assert np.allclose(got, scaled_values(d, sc, q, 16, dmin, mn), rtol=1e-6, atol=1e-6)
+
+
+def test_dequant_q3_k_packed(orc):
+    """All 16 6-bit scales (4 low bits in two nibble halves, 2 high bits in
+    shared bytes) and every hmask bit position."""
+    from gguf_pack import pack_q3_k, scaled_values
+    rng = np.random.default_rng(16)
+    nb = 3
+    d = np.asarray(rng.uniform(0.01, 0.1, nb), np.float16)
+    sc = rng.integers(0, 64, (nb, 16))
+    sc[0] = [0, 63, 1, 62, 16, 47, 32, 31, 15, 48, 5, 58, 33, 30, 7, 56]
+    q = rng.integers(-4, 4, (nb, 256))
+    got = orc.dequant_rows(11, pack_q3_k(d, sc, q), 1, 256 * nb).reshape(nb, 256)
+    assert np.allclose(got, scaled_values(d, sc - 32, q, 16), rtol=1e-6, atol=1e-6)
+
+
+def test_dequant_q5_k_packed(orc):
+    """Q5_K as the format (and the reference's GPU kernel,
+    naive.nim:1267-1323) defines it: bit s of qh[l] is the high bit of
+    element 32s + l."""
+    from gguf_pack import pack_q5_k, scaled_values
+    rng = np.random.default_rng(17)
+    nb = 3
+    d = np.asarray(rng.uniform(0.01, 0.1, nb), np.float16)
+    dmin = np.asarray(rng.uniform(0.0, 0.1, nb), np.float16)
+    sc, mn = rng.integers(0, 64, (nb, 8)), rng.integers(0, 64, (nb, 8))
+    sc[0], mn[0] = [63, 0, 1, 62, 32, 33, 16, 47], [0, 63, 31, 32, 48, 15, 63, 1]
+    q = rng.integers(0, 32, (nb, 256))
+    q[1] = 16  # only the high bits set: a misplaced qh bit shows directly
+    got = orc.dequant_rows(13, pack_q5_k(d, dmin, sc, mn, q), 1, 256 * nb).reshape(nb, 256)
+    assert np.allclose(got, scaled_values(d, sc, q, 32, dmin, mn), rtol=1e-6, atol=1e-6)
