@@ -324,7 +324,9 @@ def bench_linear(torch, A):
     # the kernel has no data-dependent branches, so the rate does not depend
     # on the values.
     for qname, qt, qk, qb in (("f16", 1, 1, 2), ("q8_0", 8, 32, 34), ("q4_k", 12, 256, 144),
-                              ("q6_k", 14, 256, 210)):
+                              ("q6_k", 14, 256, 210), ("q5_k", 13, 256, 176),
+                              ("q5_0", 6, 32, 22), ("q5_1", 7, 32, 24), ("q2_k", 10, 256, 84),
+                              ("q3_k", 11, 256, 110), ("iq4_nl", 20, 32, 18)):
         for sname, M, K in (("llama8b_q", 4096, 4096), ("llama8b_ffn_up", 14336, 4096)):
             wbytes = M * K // qk * qb
             n = max(2, -(-(600 << 20) // wbytes))

@@ -64,9 +64,18 @@ struct QFmt<13> {  // Q5_K: d, dmin, 12 scale bytes, qh[32], qs[128]
   static constexpr int QK = 256, BYTES = 176, SUB = 8, CHUNK = 16;
 };
 
-// The IQ4_NL format's 16 non-linear levels (quant.nim:16-17).
-__constant__ float kIq4nlLevels[16] = {-127.f, -104.f, -83.f, -65.f, -49.f, -35.f, -22.f, -10.f,
-                                       1.f,    13.f,   25.f,  38.f,  53.f,  69.f,  89.f,  113.f};
+// The IQ4_NL format's 16 non-linear levels (quant.nim:16-17), as int8 bytes
+// of four dwords, looked up in registers with v_perm_b32: selector byte s
+// picks byte s of {hi:lo} (0-3 from lo, 4-7 from hi).
+__device__ __forceinline__ float iq4nl_level(uint32_t idx) {
+  constexpr uint32_t T0 = 0xBFAD9881u;  // -127, -104, -83, -65
+  constexpr uint32_t T1 = 0xF6EADDCFu;  //  -49,  -35, -22, -10
+  constexpr uint32_t T2 = 0x26190D01u;  //    1,   13,  25,  38
+  constexpr uint32_t T3 = 0x71594535u;  //   53,   69,  89, 113
+  const uint32_t lo = __builtin_amdgcn_perm(T1, T0, idx & 7u);
+  const uint32_t hi = __builtin_amdgcn_perm(T3, T2, idx & 7u);
+  return (float)(int8_t)(((idx & 8u) ? hi : lo) & 255u);
+}
 
 __device__ __forceinline__ uint32_t u32_at(const uint8_t* p) {
   return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
@@ -158,7 +167,7 @@ __device__ __forceinline__ float sub_dot(const uint8_t* bp, int sub, const float
     for (int l = 0; l < 16; ++l) {
       const int b = bp[QS + l];
       if constexpr (QT == 20) {
-        sq += kIq4nlLevels[b & 15] * xv[l] + kIq4nlLevels[b >> 4] * xv[16 + l];
+        sq += iq4nl_level((uint32_t)b & 15u) * xv[l] + iq4nl_level((uint32_t)b >> 4) * xv[16 + l];
       } else {
         const int q0 = (b & 15) | (int)(((qh >> l) & 1u) << 4);
         const int q1 = (b >> 4) | (int)(((qh >> (l + 16)) & 1u) << 4);
