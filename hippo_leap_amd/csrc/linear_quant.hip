@@ -77,6 +77,15 @@ __device__ __forceinline__ float iq4nl_level(uint32_t idx) {
   return (float)(int8_t)(((idx & 8u) ? hi : lo) & 255u);
 }
 
+// Four IQ4_NL levels at once: n4 holds one level index (0-15) per byte.
+__device__ __forceinline__ uint32_t iq4nl_levels4(uint32_t n4) {
+  constexpr uint32_t T0 = 0xBFAD9881u, T1 = 0xF6EADDCFu, T2 = 0x26190D01u, T3 = 0x71594535u;
+  const uint32_t sel = n4 & 0x07070707u;
+  const uint32_t lo = __builtin_amdgcn_perm(T1, T0, sel), hi = __builtin_amdgcn_perm(T3, T2, sel);
+  const uint32_t m = ((n4 >> 3) & 0x01010101u) * 0xFFu;  // 0xFF in bytes with index >= 8
+  return (lo & ~m) | (hi & m);
+}
+
 __device__ __forceinline__ uint32_t u32_at(const uint8_t* p) {
   return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
 }
@@ -349,6 +358,16 @@ struct QD<1> { static constexpr int LPB = 1, QKB = 8, BB = 16, NX = 2, NS = 0; }
 template <>
 struct QD<8> { static constexpr int LPB = 4, QKB = 32, BB = 34, NX = 2, NS = 1; };   // 8 int8
 template <>
+struct QD<6> { static constexpr int LPB = 4, QKB = 32, BB = 22, NX = 2, NS = 1; };   // 8 x 5 bit
+template <>
+struct QD<7> { static constexpr int LPB = 4, QKB = 32, BB = 24, NX = 2, NS = 1; };   // 8 x 5 bit
+template <>
+struct QD<20> { static constexpr int LPB = 4, QKB = 32, BB = 18, NX = 2, NS = 1; };  // 8 levels
+template <>
+struct QD<10> { static constexpr int LPB = 16, QKB = 256, BB = 84, NX = 4, NS = 4; };  // 16 x 2 bit
+template <>
+struct QD<11> { static constexpr int LPB = 16, QKB = 256, BB = 110, NX = 4, NS = 4; }; // 16 x 3 bit
+template <>
 struct QD<12> { static constexpr int LPB = 8, QKB = 256, BB = 144, NX = 8, NS = 2; };  // 32 nibbles
 template <>
 struct QD<13> { static constexpr int LPB = 8, QKB = 256, BB = 176, NX = 8, NS = 2; };  // 32 x 5 bit
@@ -364,6 +383,16 @@ template <>
 struct QRaw<1> { u32x4 h; };
 template <>
 struct QRaw<8> { u32x2 p; uint32_t q, d; };
+template <>
+struct QRaw<6> { uint32_t d, h0, h1, q0, q1; };
+template <>
+struct QRaw<7> { uint32_t dm0, dm1, h0, h1, q0, q1; };
+template <>
+struct QRaw<20> { uint32_t d, q0, q1; };
+template <>
+struct QRaw<10> { uint32_t q, dd; u32x2 sc; };
+template <>
+struct QRaw<11> { uint32_t q0, q1, h0, h1, s0, s1, s2, s3, d; };
 template <>
 struct QRaw<12> { u32x4 hdr, q; };
 template <>
@@ -395,6 +424,9 @@ template <int QT>
 __device__ __forceinline__ int x_off(int j, int k) {
   if constexpr (QT == 1) return 4 * k;
   else if constexpr (QT == 8) return 8 * j + 4 * k;
+  else if constexpr (QT == 6 || QT == 7 || QT == 20) return 16 * k + 4 * j;  // lo / hi nibbles
+  else if constexpr (QT == 10 || QT == 11)  // 2-bit plane k of qs dword (n, g, l0)
+    return 128 * (j >> 3) + 32 * k + 16 * ((j >> 2) & 1) + 4 * (j & 3);
   else if constexpr (QT == 12 || QT == 13)  // sub 2c: k < 4, sub 2c+1: k >= 4; 16 of each
     return 64 * (j >> 1) + 32 * (k >> 2) + 16 * (j & 1) + 4 * (k & 3);
   else return 128 * (j >> 3) + 32 * k + 4 * (j & 7);
@@ -410,6 +442,39 @@ __device__ __forceinline__ void load_raw(rsrc_t rs, uint32_t off, int j, QRaw<QT
     r.p = bl64(rs, a);
     r.q = bl32(rs, a + 7);
     r.d = bl32(rs, off);
+  } else if constexpr (QT == 6) {  // fp16 d, qh[4] at 2, qs[16] at 6
+    r.d = bl32(rs, off);
+    r.h0 = bl32(rs, off + 2);
+    r.h1 = bl32(rs, off + 5);
+    r.q0 = bl32(rs, off + 6 + 4 * j);
+    r.q1 = bl32(rs, off + 9 + 4 * j);
+  } else if constexpr (QT == 7) {  // fp16 d, fp16 m, qh[4] at 4, qs[16] at 8
+    r.dm0 = bl32(rs, off);
+    r.dm1 = bl32(rs, off + 3);
+    r.h0 = bl32(rs, off + 4);
+    r.h1 = bl32(rs, off + 7);
+    r.q0 = bl32(rs, off + 8 + 4 * j);
+    r.q1 = bl32(rs, off + 11 + 4 * j);
+  } else if constexpr (QT == 20) {  // fp16 d, qs[16] at 2
+    r.d = bl32(rs, off);
+    r.q0 = bl32(rs, off + 2 + 4 * j);
+    r.q1 = bl32(rs, off + 5 + 4 * j);
+  } else if constexpr (QT == 10) {  // scales[16], qs[64] at 16, d, dmin at 80
+    const uint32_t n = j >> 3, t = j & 7;  // t = 4g + l0/4
+    r.q = bl32(rs, off + 16 + 32 * n + 4 * t);
+    r.sc = bl64(rs, off + 8 * n);
+    r.dd = bl32(rs, off + 80);
+  } else if constexpr (QT == 11) {  // hmask[32], qs[64] at 32, scales[12] at 96, d at 108
+    const uint32_t n = j >> 3, t = j & 7;
+    r.q0 = bl32(rs, off + 32 + 32 * n + 4 * t);
+    r.q1 = bl32(rs, off + 35 + 32 * n + 4 * t);
+    r.h0 = bl32(rs, off + 4 * t);
+    r.h1 = bl32(rs, off + 3 + 4 * t);
+    r.s0 = bl32(rs, off + 96);
+    r.s1 = bl32(rs, off + 100);
+    r.s2 = bl32(rs, off + 104);
+    r.s3 = bl32(rs, off + 107);
+    r.d = bl32(rs, off + 108);
   } else if constexpr (QT == 12) {
     r.hdr = bl128(rs, off);
     r.q = bl128(rs, off + 16 + 32 * (j >> 1) + 16 * (j & 1));
@@ -457,12 +522,12 @@ __device__ __forceinline__ float hsum4(const f32x4& x) { return (x.x + x.y) + (x
 // Per-step sums of x the formats subtract (offset-coded quants, Q4_K mins).
 template <int QT>
 __device__ __forceinline__ void x_sums(const f32x4* xv, float* xs) {
-  if constexpr (QT == 8) {
+  if constexpr (QT == 8 || QT == 6 || QT == 7 || QT == 20) {
     xs[0] = hsum4(xv[0]) + hsum4(xv[1]);
   } else if constexpr (QT == 12 || QT == 13) {
     xs[0] = (hsum4(xv[0]) + hsum4(xv[1])) + (hsum4(xv[2]) + hsum4(xv[3]));
     xs[1] = (hsum4(xv[4]) + hsum4(xv[5])) + (hsum4(xv[6]) + hsum4(xv[7]));
-  } else if constexpr (QT == 14) {
+  } else if constexpr (QT == 14 || QT == 10 || QT == 11) {
 #pragma unroll
     for (int k = 0; k < 4; ++k) xs[k] = hsum4(xv[k]);
   }
@@ -507,6 +572,71 @@ __device__ __forceinline__ float compute_raw(const QRaw<QT>& r, int j, uint32_t 
     const uint32_t q0 = al(r.p.y, r.p.x, sb) ^ 0x80808080u, q1 = al(r.q, r.p.y, sb) ^ 0x80808080u;
     const float d = f16_bits_to_f32((uint16_t)((r.d >> (8 * ps)) & 0xFFFFu));
     return d * (fma4u(q1, xv[1], fma4u(q0, xv[0], 0.f)) - 128.f * xs[0]);
+  } else if constexpr (QT == 6 || QT == 7 || QT == 20) {
+    // Lane j: elements 4j..4j+3 (low nibbles of qs[4j..4j+3]) and
+    // 16+4j..16+4j+3 (their high nibbles).  Fields sit at 2-byte offsets:
+    // each is re-aligned by the block's own phase plus its offset.
+    constexpr uint32_t QSO = QT == 6 ? 6 : QT == 7 ? 8 : 2;
+    const uint32_t q = al(r.q1, r.q0, (ps + QSO) & 3);
+    const uint32_t lo4 = q & 0x0F0F0F0Fu, hi4 = (q >> 4) & 0x0F0F0F0Fu;
+    if constexpr (QT == 20) {
+      const float d = f16_bits_to_f32((uint16_t)((r.d >> (8 * ps)) & 0xFFFFu));
+      // levels as signed bytes, summed as unsigned (v ^ 0x80) minus 128 sum(x)
+      const uint32_t a = iq4nl_levels4(lo4) ^ 0x80808080u, b = iq4nl_levels4(hi4) ^ 0x80808080u;
+      return d * (fma4u(b, xv[1], fma4u(a, xv[0], 0.f)) - 128.f * xs[0]);
+    } else {
+      // bits 4j..4j+3 (low nibbles) and 16+4j.. (high) of qh into bit 4 of
+      // each byte: b * 0x204081 moves bit i of a nibble to bit 8i.
+      constexpr uint32_t QHO = QT == 6 ? 2 : 4;
+      const uint32_t qh = al(r.h1, r.h0, (ps + QHO) & 3);
+      const uint32_t bl = (qh >> (4 * j)) & 15u, bh = (qh >> (16 + 4 * j)) & 15u;
+      const uint32_t u0 = lo4 | (((bl * 0x00204081u) & 0x01010101u) << 4);
+      const uint32_t u1 = hi4 | (((bh * 0x00204081u) & 0x01010101u) << 4);
+      const float dot = fma4u(u1, xv[1], fma4u(u0, xv[0], 0.f));
+      if constexpr (QT == 6) {
+        const float d = f16_bits_to_f32((uint16_t)((r.d >> (8 * ps)) & 0xFFFFu));
+        return d * (dot - 16.f * xs[0]);
+      } else {
+        const uint32_t dm = al(r.dm1, r.dm0, ps);
+        const float d = f16_bits_to_f32((uint16_t)(dm & 0xFFFFu));
+        const float m = f16_bits_to_f32((uint16_t)(dm >> 16));
+        return fmaf(d, dot, m * xs[0]);
+      }
+    }
+  } else if constexpr (QT == 10 || QT == 11) {
+    // Lane j = 8n + 4g + l0/4: elements 128n + 32k + 16g + l0..l0+3 for the
+    // four 2-bit planes k of one qs dword; scale 8n + 2k + g per plane.
+    const int n = j >> 3, g = (j >> 2) & 1;
+    float acc = 0.f;
+    if constexpr (QT == 10) {
+      const float d = f16_bits_to_f32((uint16_t)(r.dd & 0xFFFFu));
+      const float dmin = f16_bits_to_f32((uint16_t)(r.dd >> 16));
+      float dsum = 0.f, msum = 0.f;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const uint32_t sb = ((k < 2 ? r.sc.x : r.sc.y) >> (8 * (2 * (k & 1) + g))) & 255u;
+        dsum = fmaf((float)(sb & 15u), fma4u((r.q >> (2 * k)) & 0x03030303u, xv[k], 0.f), dsum);
+        msum = fmaf((float)(sb >> 4), xs[k], msum);
+      }
+      acc = d * dsum - dmin * msum;
+    } else {
+      // value (q | h << 2) - 4 with h the hmask bit 4n + k; 6-bit scales:
+      // low 4 bits at bits 4n of byte 2k + g, high 2 bits at bits
+      // 2(2n + k/2) of byte 8 + 2(k&1) + g.
+      const uint32_t q = al(r.q1, r.q0, ps), hm = al(r.h1, r.h0, ps);  // fields at 32 and 0
+      const uint32_t S0 = al(r.s1, r.s0, ps), S1 = al(r.s2, r.s1, ps), S2 = al(r.s3, r.s2, ps);
+      const float d = f16_bits_to_f32((uint16_t)((r.d >> (8 * ps)) & 0xFFFFu));
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const uint32_t u = ((q >> (2 * k)) & 0x03030303u) | (((hm >> (4 * n + k)) & 0x01010101u) << 2);
+        const uint32_t lo = (((k < 2 ? S0 : S1) >> (8 * (2 * (k & 1) + g))) >> (4 * n)) & 15u;
+        const uint32_t hi = (S2 >> (8 * (2 * (k & 1) + g) + 2 * (2 * n + (k >> 1)))) & 3u;
+        const float sc = (float)(int)((lo | (hi << 4)) - 32u);
+        acc = fmaf(sc, fma4u(u, xv[k], -4.f * xs[k]), acc);
+      }
+      acc *= d;
+    }
+    return acc;
   } else if constexpr (QT == 12 || QT == 13) {
     // Sub-blocks 2c (low nibbles) and 2c+1 (high nibbles); Q5_K adds bits
     // 2c / 2c+1 of qh[l] as bit 4.
@@ -660,7 +790,7 @@ void launch_direct(const uint8_t* w, const float* x, float* y, int M, int K, hip
 
 template <int QT, int KS>
 void launch_direct_r(const uint8_t* w, const float* x, float* y, int M, int K, hipStream_t stream) {
-  constexpr bool r4 = QT == 1 || QT == 8;  // Q4_K / Q5_K / Q6_K at four rows: ~200+ VGPRs
+  constexpr bool r4 = QT != 12 && QT != 13 && QT != 14;  // the K-quants at four rows: ~200+ VGPRs
   if (r4 && M >= 8192) launch_direct<QT, 4, KS>(w, x, y, M, K, stream);
   else if (M >= 2048) launch_direct<QT, 2, KS>(w, x, y, M, K, stream);
   else launch_direct<QT, 1, KS>(w, x, y, M, K, stream);
@@ -715,10 +845,11 @@ void launch_qt(const uint8_t* w, const float* x, float* y, int M, int K, hipStre
   // the format allows (F16 rows of whole 8-half groups on 16 bytes, Q4_K on
   // 16, Q8_0 / Q6_K on 2).
   const uintptr_t wa = (uintptr_t)w;
-  constexpr bool has_direct = QT == 1 || QT == 8 || QT == 12 || QT == 13 || QT == 14;
+  constexpr bool has_direct = true;
   const bool direct = has_direct && v4 && rowbytes < (1LL << 31) &&
                       (QT == 1 ? (K % 8 == 0 && (wa & 15) == 0)
-                       : (QT == 12 || QT == 13) ? (wa & 15) == 0 : (wa & 1) == 0);
+                       : (QT == 12 || QT == 13) ? (wa & 15) == 0
+                       : QT == 10 ? (wa & 3) == 0 : (wa & 1) == 0);  // Q2_K: 84-byte blocks, no phase
   if constexpr (has_direct) {
     if (direct) {
       launch_direct_plan<QT>(w, x, y, M, K, stream);

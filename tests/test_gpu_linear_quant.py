@@ -43,6 +43,10 @@ OFFSET_CASES = [
     (14, 300, 1024, 2, 0), (14, 9000, 768, 2, 0), (14, 300, 1024, 3, 0), (14, 300, 768, 0, 1),
     (13, 300, 1024, 8, 0), (13, 300, 1024, 0, 1), (6, 300, 1024, 1, 0), (11, 300, 1024, 2, 3),
     (20, 300, 1024, 3, 1), (10, 300, 1024, 2, 0), (7, 300, 1024, 1, 2),
+    (6, 300, 1024, 2, 0), (20, 300, 1056, 2, 0), (7, 300, 1024, 2, 0), (6, 8195, 96, 2, 0),
+    (20, 8200, 544, 0, 0), (7, 8193, 160, 2, 0),
+    (10, 300, 1024, 4, 0), (10, 8200, 768, 0, 0), (11, 300, 1280, 2, 0), (11, 8200, 768, 0, 0),
+    (11, 300, 1024, 1, 0),
 ]
 
 
