@@ -98,3 +98,34 @@ def test_linear_col_quant_errors(hl):
                          (13, "q5_K", 256), (20, "iq4_nl", 32)):
         with pytest.raises(HLError, match=f"{name} row size must be multiple of {qk}"):
             A.gpu_linear_col_quant(y, x, w, 300, 8, qt)
+
+
+@pytest.mark.parametrize("qt,M,K", [(12, 4096, 4096), (14, 300, 1024), (11, 700, 512), (8, 9000, 256)])
+def test_linear_col_quant_graph_replay(hl, orc, qt, M, K):
+    """Captured in a HIP graph and replayed with new x written eagerly in
+    between: every replay matches an eager call on the same inputs."""
+    from hippo_leap_amd import attention as A
+    print(f"quant GEMV graph replay: type {qt} M={M} K={K}", flush=True)
+    rng = np.random.default_rng(7400 + qt)
+    w = torch.from_numpy(random_rows(rng, qt, M, K)).cuda()
+    x = torch.from_numpy(orc.normal(K, 7500 + qt)).cuda()
+    y = torch.zeros(M, device="cuda")
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        A.gpu_linear_col_quant(y, x, w, K, M, qt)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        A.gpu_linear_col_quant(y, x, w, K, M, qt)
+    ref = torch.empty(M, device="cuda")
+    for i in range(4):
+        x.copy_(torch.from_numpy(orc.normal(K, 7600 + 10 * qt + i)).cuda())
+        y.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        A.gpu_linear_col_quant(ref, x, w, K, M, qt)
+        torch.cuda.synchronize()
+        assert torch.equal(y, ref), f"replay {i}"
