@@ -29,6 +29,10 @@ CASES = [
     (10, 300, 4096), (10, 9, 768), (11, 300, 4096), (11, 2100, 512),
     (13, 300, 4096), (13, 4096, 4096), (13, 8200, 1024), (13, 5, 256),
     (1, 300, 100), (1, 70, 1), (1, 2050, 4100),
+    # one row; long rows (many steps per wave with the four-way split)
+    (1, 1, 4096), (6, 1, 4096), (8, 1, 32), (10, 1, 256), (11, 1, 4096), (12, 1, 4096),
+    (13, 1, 512), (14, 1, 4096), (20, 1, 32), (7, 3, 64),
+    (14, 2048, 14336), (10, 700, 14336), (11, 300, 14336), (6, 4096, 14336), (20, 2100, 14336),
     # K between one and four wave steps
     (1, 300, 1024), (8, 2100, 1024), (14, 700, 2048), (12, 9000, 4096),
 ]
