@@ -66,6 +66,26 @@ class RopeStoreArgs(ctypes.Structure):
     ]
 
 
+class LayerDesc(ctypes.Structure):
+    _fields_ = [(n, c_void_p) for n in ("attn_norm", "q_norm", "k_norm", "ffn_norm", "wq", "wk", "wv",
+                                        "wo", "w_gate", "w_up", "w_down")] + \
+               [(n, c_int) for n in ("wq_type", "wk_type", "wv_type", "wo_type", "w_gate_type",
+                                     "w_up_type", "w_down_type")] + \
+               [("k_cache", c_void_p), ("v_cache", c_void_p)]
+
+
+class ModelDesc(ctypes.Structure):
+    _fields_ = [(n, c_int) for n in ("n_layer", "n_emb", "n_head", "n_head_kv", "head_dim",
+                                     "rope_dim", "n_ff", "n_vocab", "max_len")] + \
+               [("rms_eps", c_float), ("rope_base", c_float), ("tok_emb", c_void_p),
+                ("output_norm", c_void_p), ("output", c_void_p), ("output_type", c_int),
+                ("layers", ctypes.POINTER(LayerDesc))]
+
+
+class DecodeScratch(ctypes.Structure):
+    _fields_ = [(n, c_void_p) for n in ("x", "x_norm", "tmp0", "tmp1", "tmp2")]
+
+
 class PrefillArgs(ctypes.Structure):
     _fields_ = [
         ("n_head", c_int), ("n_head_kv", c_int), ("head_dim", c_int), ("seq_len", c_int),
@@ -111,6 +131,10 @@ SIGNATURES = {
     "hl_gpu_argmax": (c_int, [c_void_p, c_int, ctypes.POINTER(ctypes.c_int32), c_void_p]),
     "hl_argmax_async": (c_int, [c_void_p, c_int, c_void_p, c_void_p]),
     "hl_gpu_embedding": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_void_p]),
+    "hl_gpu_silu_mul": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_void_p]),
+    "hl_gpu_add": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_void_p]),
+    "hl_forward_decode_token": (c_int, [ctypes.POINTER(ModelDesc), ctypes.POINTER(DecodeScratch),
+                                        c_void_p, c_int, c_void_p, c_void_p, c_void_p]),
     "hl_attn_decode_workspace_bytes": (c_size_t, [ctypes.POINTER(DecodeArgs)]),
     "hl_attn_decode": (c_int, [ctypes.POINTER(DecodeArgs), c_void_p, c_size_t, c_void_p]),
     "hl_attn_decode_workspace_init": (c_int, [c_void_p, c_size_t, c_void_p]),

@@ -123,6 +123,16 @@ def gpu_linear_col_quant(dst, x, w_quant, w_cols, w_rows, quant_type, stream=Non
                                               quant_type, _stream(stream)))
 
 
+def gpu_silu_mul(dst, gate, up, n, stream=None):
+    """gpuSiluMul (naive.nim:2179-2193): dst = silu(gate) * up, fp32."""
+    check(_lib.load().hl_gpu_silu_mul(_p(dst), _p(gate), _p(up), n, _stream(stream)))
+
+
+def gpu_add(dst, a, b, n, stream=None):
+    """gpuAdd (naive.nim:2132-2145): dst = a + b, fp32."""
+    check(_lib.load().hl_gpu_add(_p(dst), _p(a), _p(b), n, _stream(stream)))
+
+
 def gpu_rmsnorm_cols(dst, x, weight, dim, seq_len, eps, stream=None):
     """gpuRmsnormCols (naive.nim:2834-2843) on col-major [dim, seq_len] fp32."""
     check(_lib.load().hl_gpu_rmsnorm_cols(_p(dst), _p(x), _p(weight), dim, seq_len, eps,

@@ -38,6 +38,19 @@ int hip_fail(hipError_t e, const char* what) {
 
 inline hipStream_t as_stream(void* s) { return (hipStream_t)s; }
 
+}  // namespace
+
+// The thread's error message for entry points in other translation units.
+int hl::set_error(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+namespace {
+
 std::mutex g_mu;
 bool g_theta_set = false;
 int g_theta_dim = 0;

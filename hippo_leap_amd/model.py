@@ -1,0 +1,73 @@
+"""Greedy decode of a dense decoder through hl_forward_decode_token: the
+reference's forwardDecodeToken for layers of kind lkAttentionFfn
+(backends/naive.nim:4592-4760, 5520-5545).
+
+DenseDecoder holds the ctypes descriptors of one model's device tensors and
+the decode scratch; step() runs one token on the device and leaves the next
+token on the device, so steps chain without host round trips.
+"""
+from __future__ import annotations
+
+import ctypes
+
+from . import _lib
+from ._lib import check
+from .attention import _p, _stream
+
+LAYER_WEIGHTS = ("wq", "wk", "wv", "wo", "w_gate", "w_up", "w_down")
+
+
+class DenseDecoder:
+    """cfg: n_layer, n_emb, n_head, n_head_kv, head_dim, rope_dim, n_ff,
+    n_vocab, max_len, rms_eps, rope_base.  layers: one dict per layer with
+    attn_norm, ffn_norm, optional q_norm / k_norm (fp32 device tensors), the
+    seven weights (fp32 [rows, cols] tensors, or uint8 GGUF rows) and their
+    types under "<name>_type" (0 = fp32), and k_cache / v_cache fp32
+    [n_head_kv*head_dim, max_len].  tok_emb fp32 [n_vocab, n_emb];
+    output_norm [n_emb]; output weight and output_type as the layers'."""
+
+    def __init__(self, torch, cfg: dict, tok_emb, output_norm, output, output_type: int,
+                 layers: list[dict]):
+        self.torch = torch
+        self.cfg = dict(cfg)
+        self.keep = [tok_emb, output_norm, output, layers]
+        arr = (_lib.LayerDesc * len(layers))()
+        for i, L in enumerate(layers):
+            d = arr[i]
+            for n in ("attn_norm", "q_norm", "k_norm", "ffn_norm", "k_cache", "v_cache"):
+                setattr(d, n, _p(L.get(n)))
+            for n in LAYER_WEIGHTS:
+                setattr(d, n, _p(L[n]))
+                setattr(d, n + "_type", int(L.get(n + "_type", 0)))
+        self.layer_arr = arr
+        c = self.cfg
+        self.desc = _lib.ModelDesc(
+            c["n_layer"], c["n_emb"], c["n_head"], c["n_head_kv"], c["head_dim"], c["rope_dim"],
+            c["n_ff"], c["n_vocab"], c["max_len"], c["rms_eps"], c["rope_base"], _p(tok_emb),
+            _p(output_norm), _p(output), int(output_type),
+            ctypes.cast(arr, ctypes.POINTER(_lib.LayerDesc)))
+        E, q, kv, ff = c["n_emb"], c["n_head"] * c["head_dim"], c["n_head_kv"] * c["head_dim"], c["n_ff"]
+        f = lambda n: torch.zeros(n, device="cuda")
+        self.bufs = [f(E), f(max(E, q)), f(max(E, q, ff)), f(max(kv, ff)), f(max(kv, ff))]
+        self.scratch = _lib.DecodeScratch(*[_p(b) for b in self.bufs])
+        self.logits = f(c["n_vocab"])
+        self.tokens = torch.zeros(2, dtype=torch.int32, device="cuda")  # current, next
+
+    def step(self, pos: int, token_dev=None, next_dev=None, stream=None):
+        """One token at position pos: reads token_dev (default: this
+        decoder's current-token slot), writes logits and next_dev (default:
+        the next-token slot)."""
+        tok = self.tokens[0:1] if token_dev is None else token_dev
+        nxt = self.tokens[1:2] if next_dev is None else next_dev
+        check(_lib.load().hl_forward_decode_token(ctypes.byref(self.desc), ctypes.byref(self.scratch),
+                                                  _p(tok), pos, _p(self.logits), _p(nxt),
+                                                  _stream(stream)))
+
+    def generate(self, first_token: int, n_steps: int, stream=None) -> list[int]:
+        """Greedy tokens after first_token for positions 0 .. n_steps-1,
+        chained on the device (one host read at the end)."""
+        out = self.torch.zeros(n_steps + 1, dtype=self.torch.int32, device="cuda")
+        out[0] = first_token
+        for p in range(n_steps):
+            self.step(p, out[p:p + 1], out[p + 1:p + 2], stream)
+        return out.cpu().tolist()[1:]

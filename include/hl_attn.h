@@ -419,6 +419,76 @@ int hl_attn_prefill(const hl_prefill_args* a, void* workspace, size_t ws_bytes,
 int hl_kv_cache_to_f32(float* dst, const void* cache, int kv_dtype, int rows,
                        int max_len, int col0, int ncols, void* stream);
 
+/* ------------------------------------------------------------------------ */
+/* Elementwise drop-ins of the decode step (fp32).                           */
+/* ------------------------------------------------------------------------ */
+
+/* gpuSiluMul (naive.nim:2179-2193): dst[i] = gate[i] * (1/(1 + expf(-gate[i])))
+ * * up[i] for i < n.  dst may alias gate or up.                           */
+int hl_gpu_silu_mul(float* dst, const float* gate, const float* up, int n,
+                    void* stream);
+
+/* gpuAdd (naive.nim:2132-2145): dst[i] = a[i] + b[i].  dst may alias a or b. */
+int hl_gpu_add(float* dst, const float* a, const float* b, int n, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* One greedy decode step of a dense decoder (forwardDecodeToken for layers   */
+/* of kind lkAttentionFfn, naive.nim:4592-4760, 5520-5545).                  */
+/* ------------------------------------------------------------------------ */
+
+/* A weight matrix: w_type 0 = fp32 row-major [rows, cols] (gpuLinearCol),
+ * otherwise a GGUF type of hl_gpu_linear_col_quant.                        */
+typedef struct {
+  const float* attn_norm;   /* [n_emb]                                       */
+  const float* q_norm;      /* [head_dim] or NULL (no qk-norm)               */
+  const float* k_norm;      /* [head_dim] or NULL                            */
+  const float* ffn_norm;    /* [n_emb]                                       */
+  const void* wq;           /* [n_head*head_dim, n_emb]                      */
+  const void* wk;           /* [n_head_kv*head_dim, n_emb]                   */
+  const void* wv;           /* [n_head_kv*head_dim, n_emb]                   */
+  const void* wo;           /* [n_emb, n_head*head_dim]                      */
+  const void* w_gate;       /* [n_ff, n_emb]                                 */
+  const void* w_up;         /* [n_ff, n_emb]                                 */
+  const void* w_down;       /* [n_emb, n_ff]                                 */
+  int wq_type, wk_type, wv_type, wo_type, w_gate_type, w_up_type, w_down_type;
+  float* k_cache;           /* [n_head_kv*head_dim, max_len] fp32 (as a1)    */
+  float* v_cache;
+} hl_layer_desc;
+
+typedef struct {
+  int n_layer, n_emb, n_head, n_head_kv, head_dim, rope_dim, n_ff, n_vocab, max_len;
+  float rms_eps, rope_base;
+  const float* tok_emb;        /* [n_vocab, n_emb] fp32                      */
+  const float* output_norm;    /* [n_emb]                                    */
+  const void* output;          /* [n_vocab, n_emb]                           */
+  int output_type;
+  const hl_layer_desc* layers; /* host array of n_layer                      */
+} hl_model_desc;
+
+/* Caller-owned device scratch (the reference's x, xNorm and tmp buffers):
+ * x [n_emb]; x_norm [max(n_emb, n_head*head_dim)]; tmp0 [max(n_emb,
+ * n_head*head_dim, n_ff)]; tmp1, tmp2 [max(n_head_kv*head_dim, n_ff)].    */
+typedef struct {
+  float* x;
+  float* x_norm;
+  float* tmp0;
+  float* tmp1;
+  float* tmp2;
+} hl_decode_scratch;
+
+/* Runs the token at *token_dev (device int32) through every layer at
+ * position pos, writing the K/V column pos of each layer's cache, the
+ * logits [n_vocab] and the greedy next token to *next_token_dev (device;
+ * nothing waits for the stream, so next_token_dev can be the next call's
+ * token_dev).  The same kernels, in the same order, as the reference's
+ * step: embedding; rmsnorm; per layer Q/K/V projections, qk-norm, RoPE,
+ * K/V store, attention, O projection, residual + ffn norm, gate/up,
+ * SiLU * up, down, residual + next layer's norm; final norm, output
+ * projection, argmax.  Sets the RoPE table (hl_set_rope_theta).           */
+int hl_forward_decode_token(const hl_model_desc* model, const hl_decode_scratch* scratch,
+                            const int32_t* token_dev, int pos, float* logits,
+                            int32_t* next_token_dev, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
