@@ -34,6 +34,9 @@ Extra objects on the same JSON line:
     projection shapes around attention: decode GEMV GB/s (weights from HBM)
     and prefill GEMM TFLOP/s against the fp32 peak; hl_gpu_linear_col_quant
     (gpuLinearColQuant) decode GEMV GB/s over F16, Q8_0, Q4_K, Q6_K weights.
+  model_decode: greedy decode of Llama-3-8B- and Llama-3.2-1B-shaped dense
+    decoders (Q4_K weights, random values) through hl_forward_decode_token,
+    ms per token.
   decode_ends: greedy argmax over the logits (hl_argmax_async / hl_gpu_argmax)
     and the token embedding (hl_gpu_embedding), the ends of a decode step.
   cpu_baseline: the C oracle (single-threaded scalar fp32 restatement of the
@@ -347,6 +350,77 @@ def bench_linear(torch, A):
     return out
 
 
+MODEL_SHAPES = {
+    "llama-3-8b": dict(n_layer=32, n_emb=4096, n_head=32, n_head_kv=8, head_dim=128, rope_dim=128,
+                       n_ff=14336, n_vocab=128256, max_len=512, rms_eps=1e-5, rope_base=5e5),
+    # the model of the reference's own decode benchmark (Llama-3.2-1B Q4_K_M)
+    "llama-3.2-1b": dict(n_layer=16, n_emb=2048, n_head=32, n_head_kv=8, head_dim=64, rope_dim=64,
+                         n_ff=8192, n_vocab=128256, max_len=512, rms_eps=1e-5, rope_base=5e5),
+}
+
+
+def bench_models(torch):
+    return {name: bench_model(torch, name, cfg) for name, cfg in MODEL_SHAPES.items()}
+
+
+def bench_model(torch, name, cfg):
+    """Greedy decode of a dense decoder of the given shape through
+    hl_forward_decode_token: Q4_K layer weights, Q6_K output head, fp32
+    embedding, fp32 caches of 512 positions.  Weights are random bytes with
+    their fp16 block scales set to 5e-4 (finite, moderate activations).
+    Tokens chain on the device; the time is the host clock over 16 tokens
+    after 3 warm-up tokens (positions 3..18)."""
+    import numpy as np
+    from hippo_leap_amd.model import DenseDecoder
+    E, ff, kv = cfg["n_emb"], cfg["n_ff"], cfg["n_head_kv"] * cfg["head_dim"]
+    g = torch.Generator(device="cuda").manual_seed(23)
+    half = torch.from_numpy(np.array([5e-4], np.float16).view(np.uint8).copy()).cuda()
+
+    def gguf(rows, cols, bb, scale_at):
+        nb = rows * cols // 256
+        w = torch.randint(0, 256, (nb, bb), generator=g, device="cuda", dtype=torch.uint8)
+        for o in scale_at:
+            w[:, o:o + 2] = half
+        return w.reshape(-1)
+
+    q4 = lambda r, c: gguf(r, c, 144, (0, 2))  # d, dmin
+    layers, wbytes = [], 0
+    for _ in range(cfg["n_layer"]):
+        L = {"attn_norm": torch.ones(E, device="cuda"), "ffn_norm": torch.ones(E, device="cuda"),
+             "wq": q4(E, E), "wk": q4(kv, E), "wv": q4(kv, E), "wo": q4(E, E),
+             "w_gate": q4(ff, E), "w_up": q4(ff, E), "w_down": q4(E, ff),
+             "k_cache": torch.zeros(kv, cfg["max_len"], device="cuda"),
+             "v_cache": torch.zeros(kv, cfg["max_len"], device="cuda")}
+        for n in ("wq", "wk", "wv", "wo", "w_gate", "w_up", "w_down"):
+            L[n + "_type"] = 12
+            wbytes += L[n].numel()
+        layers.append(L)
+    out = gguf(cfg["n_vocab"], E, 210, (208,))
+    wbytes += out.numel()
+    emb = torch.randn(cfg["n_vocab"], E, generator=g, device="cuda")
+    m = DenseDecoder(torch, cfg, emb, torch.ones(E, device="cuda"), out, 14, layers)
+    toks = torch.zeros(20, dtype=torch.int32, device="cuda")
+    toks[0] = 128000
+    for p in range(3):
+        m.step(p, toks[p:p + 1], toks[p + 1:p + 2])
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for p in range(3, 19):
+        m.step(p, toks[p:p + 1], toks[p + 1:p + 2])
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / 16
+    valid = bool(((toks[1:] >= 0) & (toks[1:] < cfg["n_vocab"])).all().item())
+    res = {"model": f"{name} shape, Q4_K layers, Q6_K head (random weights)", "ms_per_token": round(ms, 3),
+           "tokens_per_s": round(1e3 / ms, 1), "weight_bytes": wbytes,
+           "weight_GB_per_s": round(wbytes / (ms * 1e-3) / 1e9, 1), "positions": "3..18",
+           "tokens_in_vocab": valid}
+    log(f"model decode {name}: {ms:.3f} ms/token, {1e3 / ms:.1f} tokens/s, "
+        f"{res['weight_GB_per_s']} GB/s of weights")
+    del m, layers, emb, out
+    torch.cuda.empty_cache()
+    return res
+
+
 def bench_ends(torch, A):
     """The decode step's ends: greedy argmax over a vocabulary of logits
     (hl_argmax_async, result left on the device as in a captured decode loop;
@@ -392,7 +466,7 @@ def main():
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--only", choices=["all", "decode", "prefill", "c5", "fp32", "linear"],
+    ap.add_argument("--only", choices=["all", "decode", "prefill", "c5", "fp32", "linear", "model"],
                     default="all")
     ap.add_argument("--layouts", choices=["both", "colmajor", "tiled"], default="both",
                     help="KV-cache layouts of the decode runs (the headline c3 line is column-major; "
@@ -581,6 +655,8 @@ def main():
 
     if args.only in ("all", "linear"):
         result["linear"] = bench_linear(torch, A)
+    if args.only in ("all", "model"):
+        result["model_decode"] = bench_models(torch)
         result["decode_ends"] = bench_ends(torch, A)
 
     if not args.no_cpu:
