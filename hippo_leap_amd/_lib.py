@@ -132,6 +132,10 @@ SIGNATURES = {
     "hl_argmax_async": (c_int, [c_void_p, c_int, c_void_p, c_void_p]),
     "hl_gpu_embedding": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_void_p]),
     "hl_gpu_silu_mul": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_void_p]),
+    "hl_gpu_fused_gate_up_silu_quant": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int,
+                                                c_int, c_void_p]),
+    "hl_gpu_fused_kv_linear_quant": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int,
+                                             c_int, c_int, c_int, c_void_p]),
     "hl_gpu_add": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_void_p]),
     "hl_forward_decode_token": (c_int, [ctypes.POINTER(ModelDesc), ctypes.POINTER(DecodeScratch),
                                         c_void_p, c_int, c_void_p, c_void_p, c_void_p]),

@@ -128,6 +128,19 @@ def gpu_silu_mul(dst, gate, up, n, stream=None):
     check(_lib.load().hl_gpu_silu_mul(_p(dst), _p(gate), _p(up), n, _stream(stream)))
 
 
+def gpu_fused_gate_up_silu_quant(dst, x, gate_q, up_q, w_cols, w_rows, quant_type, stream=None):
+    """gpuFusedGateUpSiluQ4K/Q3K (naive.nim:1905-1920, 1693-1708), any GGUF type."""
+    check(_lib.load().hl_gpu_fused_gate_up_silu_quant(_p(dst), _p(x), _p(gate_q), _p(up_q), w_cols,
+                                                      w_rows, quant_type, _stream(stream)))
+
+
+def gpu_fused_kv_linear_quant(k_dst, v_dst, x, k_q, v_q, w_cols, w_rows, k_type, v_type,
+                              stream=None):
+    """gpuFusedKVLinearQ4K/Q2KQ3K (naive.nim:1799-1814, 853-868), any GGUF types."""
+    check(_lib.load().hl_gpu_fused_kv_linear_quant(_p(k_dst), _p(v_dst), _p(x), _p(k_q), _p(v_q),
+                                                   w_cols, w_rows, k_type, v_type, _stream(stream)))
+
+
 def gpu_add(dst, a, b, n, stream=None):
     """gpuAdd (naive.nim:2132-2145): dst = a + b, fp32."""
     check(_lib.load().hl_gpu_add(_p(dst), _p(a), _p(b), n, _stream(stream)))

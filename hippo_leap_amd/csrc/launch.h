@@ -170,6 +170,9 @@ hipError_t argmax_launch(const float* x, int n, unsigned int* scratch, int* resu
 hipError_t embedding_launch(float* out, const float* w, const int* tok, int n_emb, int n_tok,
                             int n_vocab, hipStream_t stream);
 
+bool linear_quant_pair_launch(int pair, float* y, float* y2, const float* x, const void* wa,
+                              const void* wb, int K, int M, int qtype, hipStream_t stream);
+
 // Sets the thread's hl_last_error() message (printf format); returns code.
 int set_error(int code, const char* fmt, ...);
 

@@ -688,17 +688,22 @@ __device__ __forceinline__ float compute_raw(const QRaw<QT>& r, int j, uint32_t 
 
 // KS waves (1, 2 or 4) split a row group's blocks (wave s of the group takes
 // steps s, s + KS, ...) and merge through LDS; a workgroup holds 4 / KS
-// row groups.
-template <int QT, int R, int KS>
+// row groups.  PAIR (R = 2): the group's two rows are row m of w and row m
+// of w2, sharing the x registers; PAIR 1 stores silu(a) * b to y (fused
+// gate / up / SiLU), PAIR 2 stores a to y and b to y2 (fused K / V).
+template <int QT, int R, int KS, int PAIR = 0>
 __global__ __launch_bounds__(256) void quant_direct_kernel(const uint8_t* __restrict__ w,
                                                            const float* __restrict__ x,
-                                                           float* __restrict__ y, int M, int K) {
+                                                           float* __restrict__ y, int M, int K,
+                                                           const uint8_t* __restrict__ w2,
+                                                           float* __restrict__ y2) {
+  static_assert(PAIR == 0 || R == 2, "pairs are two rows");
   using F = QD<QT>;
   constexpr int BPI = 64 / F::LPB;
   __shared__ float part[4][R];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int row0 = (blockIdx.x * (4 / KS) + wave / KS) * R;
+  const int row0 = (blockIdx.x * (4 / KS) + wave / KS) * (PAIR ? 1 : R);
   const int s0 = wave % KS;
   if (KS == 1 && row0 >= M) return;  // no barrier below for KS == 1
   const int j = lane % F::LPB, bl = lane / F::LPB;
@@ -710,7 +715,8 @@ __global__ __launch_bounds__(256) void quant_direct_kernel(const uint8_t* __rest
   uint32_t ps[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const uint8_t* rp = w + (size_t)min(row0 + r, M - 1) * rowbytes;
+    const uint8_t* rp = PAIR ? (r == 0 ? w : w2) + (size_t)min(row0, M - 1) * rowbytes
+                             : w + (size_t)min(row0 + r, M - 1) * rowbytes;
     ps[r] = (uint32_t)((uintptr_t)rp & 3);
     // Whole dwords: the range check drops a dword that ends past the size.
     rs[r] = make_rsrc(rp - ps[r], (rowbytes + ps[r] + 3) & ~3u);
@@ -762,10 +768,22 @@ __global__ __launch_bounds__(256) void quant_direct_kernel(const uint8_t* __rest
     for (int o = 32; o >= 1; o >>= 1) a += __shfl_xor(a, o, 64);
     acc[r] = a;
   }
-  if (KS == 1) {
+  auto store = [&](const float* t) {  // lane 0 of the group's first wave
+    if constexpr (PAIR == 1) {
+      if (row0 < M) y[row0] = t[0] * (1.0f / (1.0f + expf(-t[0]))) * t[1];  // gpuSiluMul
+    } else if constexpr (PAIR == 2) {
+      if (row0 < M) {
+        y[row0] = t[0];
+        y2[row0] = t[1];
+      }
+    } else {
 #pragma unroll
-    for (int r = 0; r < R; ++r)
-      if (lane == 0 && row0 + r < M) y[row0 + r] = acc[r];
+      for (int r = 0; r < R; ++r)
+        if (row0 + r < M) y[row0 + r] = t[r];
+    }
+  };
+  if (KS == 1) {
+    if (lane == 0) store(acc);
     return;
   }
   if (lane == 0) {
@@ -773,19 +791,25 @@ __global__ __launch_bounds__(256) void quant_direct_kernel(const uint8_t* __rest
     for (int r = 0; r < R; ++r) part[wave][r] = acc[r];
   }
   __syncthreads();
-  if (s0 == 0 && lane < R && row0 + lane < M) {
-    float t = 0.f;
+  if (s0 == 0 && lane == 0) {
+    float t[R];
 #pragma unroll
-    for (int i = 0; i < KS; ++i) t += part[wave + i][lane];
-    y[row0 + lane] = t;
+    for (int r = 0; r < R; ++r) {
+      t[r] = 0.f;
+#pragma unroll
+      for (int i = 0; i < KS; ++i) t[r] += part[wave + i][r];
+    }
+    store(t);
   }
 }
 
-template <int QT, int R, int KS>
-void launch_direct(const uint8_t* w, const float* x, float* y, int M, int K, hipStream_t stream) {
-  const int groups = (M + R - 1) / R;
+template <int QT, int R, int KS, int PAIR = 0>
+void launch_direct(const uint8_t* w, const float* x, float* y, int M, int K, hipStream_t stream,
+                   const uint8_t* w2 = nullptr, float* y2 = nullptr) {
+  const int groups = PAIR ? M : (M + R - 1) / R;
   const int grid = (groups + 4 / KS - 1) / (4 / KS);
-  hipLaunchKernelGGL((quant_direct_kernel<QT, R, KS>), dim3(grid), dim3(256), 0, stream, w, x, y, M, K);
+  hipLaunchKernelGGL((quant_direct_kernel<QT, R, KS, PAIR>), dim3(grid), dim3(256), 0, stream, w, x, y,
+                     M, K, w2, y2);
 }
 
 template <int QT, int KS>
@@ -804,6 +828,23 @@ void launch_direct_plan(const uint8_t* w, const float* x, float* y, int M, int K
   const int iters = (K / QD<QT>::QKB + 64 / QD<QT>::LPB - 1) / (64 / QD<QT>::LPB);
   if (iters >= 4) launch_direct_r<QT, 4>(w, x, y, M, K, stream);
   else launch_direct_r<QT, 1>(w, x, y, M, K, stream);
+}
+
+// Two matrices of one type at once (PAIR 1 or 2), when the direct kernel
+// takes their pointers; false: the caller runs them separately.
+template <int QT, int PAIR>
+bool launch_pair_qt(const uint8_t* w, const uint8_t* w2, const float* x, float* y, float* y2, int M,
+                    int K, hipStream_t stream) {
+  const long long rowbytes = (long long)(K / QD<QT>::QKB) * QD<QT>::BB;
+  const uintptr_t a = (uintptr_t)w | (uintptr_t)w2;
+  const bool ok = ((uintptr_t)x & 15) == 0 && rowbytes < (1LL << 31) && K % QD<QT>::QKB == 0 &&
+                  (QT == 1 ? (a & 15) == 0 : (QT == 12 || QT == 13) ? (a & 15) == 0
+                   : QT == 10 ? (a & 3) == 0 : (a & 1) == 0);
+  if (!ok) return false;
+  const int iters = (K / QD<QT>::QKB + 64 / QD<QT>::LPB - 1) / (64 / QD<QT>::LPB);
+  if (iters >= 4) launch_direct<QT, 2, 4, PAIR>(w, x, y, M, K, stream, w2, y2);
+  else launch_direct<QT, 2, 1, PAIR>(w, x, y, M, K, stream, w2, y2);
+  return true;
 }
 
 template <int QT, int WPR>
@@ -886,6 +927,31 @@ long long quant_row_bytes(int qtype, int K) {
     case HL_GGML_Q6_K: return (long long)(K / 256) * 210;
     default: return 0;
   }
+}
+
+// y = silu(W_gate x) * (W_up x) (PAIR 1) or y = W_a x, y2 = W_b x (PAIR 2)
+// in one launch for two matrices of one GGUF type; returns false when the
+// pointers or the type do not allow it (the caller then runs them apart).
+bool linear_quant_pair_launch(int pair, float* y, float* y2, const float* x, const void* wa,
+                              const void* wb, int K, int M, int qtype, hipStream_t stream) {
+  const uint8_t *a = (const uint8_t*)wa, *b = (const uint8_t*)wb;
+#define HL_PAIR(QT)                                                        \
+  return pair == 1 ? launch_pair_qt<QT, 1>(a, b, x, y, nullptr, M, K, stream) \
+                   : launch_pair_qt<QT, 2>(a, b, x, y, y2, M, K, stream)
+  switch (qtype) {
+    case HL_GGML_F16: if (K % 8) return false; HL_PAIR(1);
+    case HL_GGML_Q5_0: HL_PAIR(6);
+    case HL_GGML_Q5_1: HL_PAIR(7);
+    case HL_GGML_Q8_0: HL_PAIR(8);
+    case HL_GGML_Q2_K: HL_PAIR(10);
+    case HL_GGML_Q3_K: HL_PAIR(11);
+    case HL_GGML_Q4_K: HL_PAIR(12);
+    case HL_GGML_Q5_K: HL_PAIR(13);
+    case HL_GGML_Q6_K: HL_PAIR(14);
+    case HL_GGML_IQ4_NL: HL_PAIR(20);
+    default: return false;
+  }
+#undef HL_PAIR
 }
 
 hipError_t linear_quant_launch(float* y, const float* x, const void* w, int K, int M, int qtype,

@@ -7,6 +7,8 @@
 //   * residual_rmsnorm_kernel: gpuResidualRmsnorm (naive.nim:2845-2882), the
 //     end of a decode layer (naive.nim:5530): x += residual in place, then
 //     out = rmsnorm(x) * w.
+//   * norm_vec4_kernel: both, for one aligned vector of dim % 4 == 0 (the
+//     decode step), in one 1024-thread workgroup with the vector in registers.
 // Both are HBM/latency-bound; sums of squares are fp32, reduced in a
 // different order than the reference's 256-thread LDS tree.
 #include "common.h"
@@ -90,11 +92,67 @@ __global__ __launch_bounds__(256) void residual_rmsnorm_kernel(float* __restrict
   for (int r = threadIdx.x; r < dim; r += 256) out[r] = x[r] * inv * w[r];
 }
 
+// dim % 4 == 0, 16-byte aligned vectors, dim <= 16384: 1024 threads, up to
+// four float4 chunks each, all loaded before the reduction and kept in
+// registers for the second pass (the scalar loop above runs ~16 dependent
+// load/store rounds per thread at dim 4096).
+template <bool RES>
+__global__ __launch_bounds__(1024) void norm_vec4_kernel(float* __restrict__ x,
+                                                         const float* __restrict__ res,
+                                                         const float* __restrict__ w,
+                                                         float* __restrict__ out, int dim, float eps) {
+  __shared__ float part[16];
+  const int n4 = dim >> 2, tid = threadIdx.x;
+  f32x4 v[4];
+  float ss = 0.f;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int c = tid + 1024 * k;
+    v[k] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (c < n4) {
+      v[k] = ((const f32x4*)x)[c];
+      if (RES) v[k] += ((const f32x4*)res)[c];
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int c = tid + 1024 * k;
+    if (c < n4) {
+      if (RES) ((f32x4*)x)[c] = v[k];
+      ss += (v[k].x * v[k].x + v[k].y * v[k].y) + (v[k].z * v[k].z + v[k].w * v[k].w);
+    }
+  }
+  ss = wave_sum(ss);
+  if ((tid & 63) == 0) part[tid >> 6] = ss;
+  __syncthreads();
+  float t = 0.f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) t += part[i];
+  const float inv = 1.0f / sqrtf(t / (float)dim + eps);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int c = tid + 1024 * k;
+    if (c < n4) {
+      const f32x4 wv = ((const f32x4*)w)[c];
+      ((f32x4*)out)[c] = f32x4{v[k].x * inv * wv.x, v[k].y * inv * wv.y, v[k].z * inv * wv.z,
+                               v[k].w * inv * wv.w};
+    }
+  }
+}
+
+bool vec4_ok(int dim, const void* a, const void* b, const void* c, const void* d) {
+  const uintptr_t m = (uintptr_t)a | (uintptr_t)b | (uintptr_t)c | (uintptr_t)d;
+  return dim % 4 == 0 && dim <= 16384 && (m & 15) == 0;
+}
+
 }  // namespace
 
 hipError_t rmsnorm_cols_launch(float* out, const float* x, const float* w, int dim, int seq,
                                float eps, hipStream_t stream) {
-  if (seq < 64)
+  if (seq == 1 && vec4_ok(dim, x, w, out, out))
+    hipLaunchKernelGGL(norm_vec4_kernel<false>, dim3(1), dim3(1024), 0, stream, const_cast<float*>(x),
+                       nullptr, w, out, dim, eps);
+  else if (seq < 64)
     hipLaunchKernelGGL(rmsnorm_col_kernel, dim3(seq), dim3(256), 0, stream, x, w, out, dim, seq, eps);
   else
     hipLaunchKernelGGL(rmsnorm_cols64_kernel, dim3((seq + 63) / 64), dim3(256), 0, stream, x, w,
@@ -104,7 +162,10 @@ hipError_t rmsnorm_cols_launch(float* out, const float* x, const float* w, int d
 
 hipError_t residual_rmsnorm_launch(float* out, float* x, const float* res, const float* w, int dim,
                                    float eps, hipStream_t stream) {
-  hipLaunchKernelGGL(residual_rmsnorm_kernel, dim3(1), dim3(256), 0, stream, x, res, w, out, dim, eps);
+  if (vec4_ok(dim, x, res, w, out))
+    hipLaunchKernelGGL(norm_vec4_kernel<true>, dim3(1), dim3(1024), 0, stream, x, res, w, out, dim, eps);
+  else
+    hipLaunchKernelGGL(residual_rmsnorm_kernel, dim3(1), dim3(256), 0, stream, x, res, w, out, dim, eps);
   return hipGetLastError();
 }
 

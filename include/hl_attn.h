@@ -431,6 +431,33 @@ int hl_gpu_silu_mul(float* dst, const float* gate, const float* up, int n,
 /* gpuAdd (naive.nim:2132-2145): dst[i] = a[i] + b[i].  dst may alias a or b. */
 int hl_gpu_add(float* dst, const float* a, const float* b, int n, void* stream);
 
+/* gpuFusedGateUpSiluQ4K / gpuFusedGateUpSiluQ3K (naive.nim:1905-1920,
+ * 1693-1708) for any GGUF type of hl_gpu_linear_col_quant: dst[wRows] =
+ * silu(gate . x) * (up . x), both matrices [wRows, wCols] of quant_type, in
+ * one launch (silu as gpuSiluMul).  x must be 16-byte aligned and the
+ * weights aligned to their blocks (16 bytes for F16, Q4_K, Q5_K; 4 for
+ * Q2_K; 2 otherwise): HL_EINVAL if not.                                    */
+int hl_gpu_fused_gate_up_silu_quant(float* dst, const float* x, const void* gate_q,
+                                    const void* up_q, int w_cols, int w_rows,
+                                    int quant_type, void* stream);
+int hl_gpu_fused_gate_up_silu_q4k(float* dst, const float* x, const void* gate_q,
+                                  const void* up_q, int w_cols, int w_rows, void* stream);
+int hl_gpu_fused_gate_up_silu_q3k(float* dst, const float* x, const void* gate_q,
+                                  const void* up_q, int w_cols, int w_rows, void* stream);
+
+/* gpuFusedKVLinearQ4K / gpuFusedKVLinearQ2KQ3K (naive.nim:1799-1814,
+ * 853-868) for any GGUF types: k_dst = k_q . x, v_dst = v_q . x (both
+ * [wRows, wCols]); one launch when the types match and the pointers allow
+ * it, two otherwise.                                                      */
+int hl_gpu_fused_kv_linear_quant(float* k_dst, float* v_dst, const float* x, const void* k_q,
+                                 const void* v_q, int w_cols, int w_rows, int k_type,
+                                 int v_type, void* stream);
+int hl_gpu_fused_kv_linear_q4k(float* k_dst, float* v_dst, const float* x, const void* k_q,
+                               const void* v_q, int w_cols, int w_rows, void* stream);
+int hl_gpu_fused_kv_linear_q2k_q3k(float* k_dst, float* v_dst, const float* x,
+                                   const void* k_q, const void* v_q, int w_cols,
+                                   int w_rows, void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* One greedy decode step of a dense decoder (forwardDecodeToken for layers   */
 /* of kind lkAttentionFfn, naive.nim:4592-4760, 5520-5545).                  */

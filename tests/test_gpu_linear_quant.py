@@ -133,3 +133,59 @@ def test_linear_col_quant_graph_replay(hl, orc, qt, M, K):
         A.gpu_linear_col_quant(ref, x, w, K, M, qt)
         torch.cuda.synchronize()
         assert torch.equal(y, ref), f"replay {i}"
+
+
+FUSED = [(12, 14336, 4096), (12, 300, 512), (11, 700, 1024), (13, 2100, 2048), (8, 4096, 4096),
+         (14, 900, 768), (1, 300, 512), (20, 333, 1024), (6, 64, 256), (10, 500, 512)]
+
+
+@pytest.mark.parametrize("qt,M,K", FUSED)
+def test_fused_gate_up_silu_and_kv(hl, orc, qt, M, K):
+    """gpuFusedGateUpSiluQ4K/Q3K and gpuFusedKVLinearQ4K (naive.nim:1905-1920,
+    1693-1708, 1799-1814) for every type: silu(G x) * (U x) and (K x, V x) in
+    one launch against the oracle's dequantised rows."""
+    from hippo_leap_amd import attention as A
+    print(f"fused pair: type {qt} M={M} K={K}", flush=True)
+    rng = np.random.default_rng(7700 + qt)
+    ga, ub = random_rows(rng, qt, M, K), random_rows(rng, qt, M, K)
+    x = orc.normal(K, 7800 + qt)
+    G = orc.dequant_rows(qt, ga, M, K).astype(np.float64) @ x.astype(np.float64)
+    U = orc.dequant_rows(qt, ub, M, K).astype(np.float64) @ x.astype(np.float64)
+    xd = torch.from_numpy(x).cuda()
+    gd, ud = torch.from_numpy(ga).cuda(), torch.from_numpy(ub).cuda()
+    y = torch.full((M,), float("nan"), device="cuda")
+    A.gpu_fused_gate_up_silu_quant(y, xd, gd, ud, K, M, qt)
+    y2 = torch.full((M,), float("nan"), device="cuda")
+    A.gpu_fused_kv_linear_quant(y, y2, xd, gd, ud, K, M, qt, qt)  # y reused: fused result checked below
+    torch.cuda.synchronize()
+    assert rel_err(y.cpu().numpy(), G) < TOL_F32 and rel_err(y2.cpu().numpy(), U) < TOL_F32
+    A.gpu_fused_gate_up_silu_quant(y, xd, gd, ud, K, M, qt)
+    torch.cuda.synchronize()
+    assert rel_err(y.cpu().numpy(), G / (1 + np.exp(-G)) * U) < TOL_F32
+
+
+def test_fused_kv_mixed_types_and_alignment(hl, orc):
+    """Q2_K keys with Q3_K values (gpuFusedKVLinearQ2KQ3K) and misaligned x
+    run as two launches; the fused gate/up rejects a misaligned x."""
+    from hippo_leap_amd import attention as A
+    from hippo_leap_amd._lib import HLError
+    M, K = 500, 512
+    rng = np.random.default_rng(7900)
+    ka, vb = random_rows(rng, 10, M, K), random_rows(rng, 11, M, K)
+    x = orc.normal(K, 7901)
+    xbuf = torch.zeros(K + 4, device="cuda")
+    xbuf[1:1 + K] = torch.from_numpy(x).cuda()
+    xal = torch.from_numpy(x).cuda()
+    for xd in (xal, xbuf[1:1 + K]):
+        k = torch.full((M,), float("nan"), device="cuda")
+        v = torch.full((M,), float("nan"), device="cuda")
+        A.gpu_fused_kv_linear_quant(k, v, xd, torch.from_numpy(ka).cuda(), torch.from_numpy(vb).cuda(),
+                                    K, M, 10, 11)
+        torch.cuda.synchronize()
+        assert rel_err(k.cpu().numpy(), orc.dequant_rows(10, ka, M, K).astype(np.float64) @ x) < TOL_F32
+        assert rel_err(v.cpu().numpy(), orc.dequant_rows(11, vb, M, K).astype(np.float64) @ x) < TOL_F32
+    w = torch.from_numpy(ka).cuda()
+    with pytest.raises(HLError, match="16-byte aligned"):
+        A.gpu_fused_gate_up_silu_quant(k, xbuf[1:1 + K], w, w, K, M, 10)
+    with pytest.raises(HLError, match="unsupported quant type"):
+        A.gpu_fused_gate_up_silu_quant(k, xal, w, w, K, M, 9)

@@ -96,6 +96,11 @@ CASES = [
     ("fp32_qknorm", {}, True),  # Qwen3-style per-head q/k norm
     ("gguf", {"wq": 12, "wk": 8, "wv": 14, "wo": 13, "w_gate": 12, "w_up": 11, "w_down": 14,
               "output": 14}, True),
+    # gate/up and K/V of one type: the fused launches
+    ("gguf_fused", {"wq": 12, "wk": 12, "wv": 12, "wo": 12, "w_gate": 12, "w_up": 12, "w_down": 14,
+                    "output": 14}, False),
+    ("gguf_fused_q8", {"wq": 8, "wk": 8, "wv": 8, "wo": 8, "w_gate": 8, "w_up": 8, "w_down": 8,
+                       "output": 8}, True),
 ]
 
 

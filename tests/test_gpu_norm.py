@@ -14,7 +14,7 @@ pytestmark = pytest.mark.gpu
 
 
 @pytest.mark.parametrize("dim,T", [(2048, 1), (4096, 1), (4096, 7), (2048, 64), (4096, 512),
-                                   (100, 130), (5120, 63)])
+                                   (100, 130), (5120, 63), (16384, 1), (130, 1), (16388, 1)])
 def test_rmsnorm_cols_matches_oracle(hl, orc, dim, T):
     from hippo_leap_amd import attention as A
     print(f"rmsnorm_cols dim={dim} T={T}", flush=True)
@@ -29,7 +29,7 @@ def test_rmsnorm_cols_matches_oracle(hl, orc, dim, T):
     assert rel_err(xd.cpu().numpy(), ref) < TOL_F32
 
 
-@pytest.mark.parametrize("dim", [2048, 4096, 5120, 77])
+@pytest.mark.parametrize("dim", [2048, 4096, 5120, 77, 16384, 16388, 130])
 def test_residual_rmsnorm_matches_oracle(hl, orc, dim):
     from hippo_leap_amd import attention as A
     x = orc.normal(dim, 4100 + dim)
@@ -42,3 +42,21 @@ def test_residual_rmsnorm_matches_oracle(hl, orc, dim):
     xs = x + r
     assert np.array_equal(xd.cpu().numpy(), xs)
     assert rel_err(out.cpu().numpy(), orc.rmsnorm(xs.reshape(1, dim), w, 1e-6).reshape(-1)) < TOL_F32
+
+
+def test_residual_rmsnorm_misaligned(hl, orc):
+    """Vectors not on 16 bytes take the scalar kernel; same results."""
+    from hippo_leap_amd import attention as A
+    dim = 4096
+    x = orc.normal(dim, 4400)
+    r = orc.normal(dim, 4401, 0.0, 0.5)
+    w = orc.uniform(dim, 4402, 0.5, 1.5)
+    buf = torch.zeros(dim + 4, device="cuda")
+    buf[1:1 + dim] = torch.from_numpy(x).cuda()
+    xd = buf[1:1 + dim]
+    out = torch.full((dim,), float("nan"), device="cuda")
+    A.gpu_residual_rmsnorm(out, xd, torch.from_numpy(r).cuda(), torch.from_numpy(w).cuda(), dim, 1e-6)
+    xs = x + r
+    assert np.array_equal(xd.cpu().numpy(), xs)
+    assert rel_err(out.cpu().numpy(), orc.rmsnorm(xs.reshape(1, dim), w, 1e-6).reshape(-1)) < TOL_F32
+
