@@ -136,6 +136,14 @@ SIGNATURES = {
                                                 c_int, c_void_p]),
     "hl_gpu_fused_kv_linear_quant": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int,
                                              c_int, c_int, c_int, c_void_p]),
+    "hl_gpu_fused_gate_up_silu_q4k": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int,
+                                              c_void_p]),
+    "hl_gpu_fused_gate_up_silu_q3k": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int,
+                                              c_void_p]),
+    "hl_gpu_fused_kv_linear_q4k": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int,
+                                           c_int, c_void_p]),
+    "hl_gpu_fused_kv_linear_q2k_q3k": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int,
+                                               c_int, c_void_p]),
     "hl_gpu_add": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_void_p]),
     "hl_forward_decode_token": (c_int, [ctypes.POINTER(ModelDesc), ctypes.POINTER(DecodeScratch),
                                         c_void_p, c_int, c_void_p, c_void_p, c_void_p]),
