@@ -511,7 +511,10 @@ typedef struct {
  * step: embedding; rmsnorm; per layer Q/K/V projections, qk-norm, RoPE,
  * K/V store, attention, O projection, residual + ffn norm, gate/up,
  * SiLU * up, down, residual + next layer's norm; final norm, output
- * projection, argmax.  Sets the RoPE table (hl_set_rope_theta).           */
+ * projection, argmax.  Sets the process-wide RoPE table
+ * (hl_set_rope_theta) on every call: steps of models with different RoPE
+ * parameters must not run concurrently (the reference's theta table is
+ * module-global too).                                                     */
 int hl_forward_decode_token(const hl_model_desc* model, const hl_decode_scratch* scratch,
                             const int32_t* token_dev, int pos, float* logits,
                             int32_t* next_token_dev, void* stream);
