@@ -296,3 +296,47 @@ def test_paged_kv_validation(hl):
     assert hl.hl_attn_decode(ctypes.byref(a), None, 0, None) == _lib.HL_EUNSUPPORTED
     p = _prefill_args(k_cache=FAKE, v_cache=FAKE, kv_dtype=_lib.HL_BF16, max_len=4096, kv_layout=P)
     assert hl.hl_attn_prefill(ctypes.byref(p), None, 0, None) == _lib.HL_EINVAL
+
+
+def _model_desc(layers, **kw):
+    m = _lib.ModelDesc(2, 256, 4, 2, 64, 64, 512, 300, 16, 1e-6, 1e4, FAKE, FAKE, FAKE, 0,
+                       ctypes.cast(layers, ctypes.POINTER(_lib.LayerDesc)))
+    for k, v in kw.items():
+        setattr(m, k, v)
+    return m
+
+
+def test_decode_token_validation(hl):
+    """hl_forward_decode_token's host checks (forwardDecodeToken's
+    preconditions, naive.nim:4594-4599): nulls, shapes, the cache capacity."""
+    layers = (_lib.LayerDesc * 2)()
+    s = _lib.DecodeScratch(FAKE, FAKE, FAKE, FAKE, FAKE)
+    tok = logits = nxt = FAKE
+    call = lambda m, sc=s, pos=0: hl.hl_forward_decode_token(
+        ctypes.byref(m) if m is not None else None, ctypes.byref(sc), tok, pos, logits, nxt, None)
+    assert call(None) == _lib.HL_EINVAL
+    assert call(_model_desc(layers, tok_emb=None)) == _lib.HL_EINVAL
+    assert call(_model_desc(layers), _lib.DecodeScratch(FAKE, None, FAKE, FAKE, FAKE)) == _lib.HL_EINVAL
+    assert call(_model_desc(layers, n_layer=0)) == _lib.HL_EINVAL
+    assert call(_model_desc(layers, n_head_kv=0)) == _lib.HL_EINVAL
+    assert call(_model_desc(layers), pos=16) == _lib.HL_ECAPACITY
+    assert "outside the cache" in _err(hl)
+    assert call(_model_desc(layers), pos=-1) == _lib.HL_ECAPACITY
+
+
+def test_fused_and_elementwise_validation(hl):
+    assert hl.hl_gpu_fused_gate_up_silu_quant(FAKE, FAKE, FAKE, FAKE, 512, 8, 9, None) == \
+        _lib.HL_EUNSUPPORTED
+    assert "unsupported quant type for GPU GEMV: 9" in _err(hl)
+    assert hl.hl_gpu_fused_gate_up_silu_quant(FAKE, FAKE, FAKE, FAKE, 300, 8, 12, None) == \
+        _lib.HL_EINVAL
+    assert "multiple of 256" in _err(hl)
+    assert hl.hl_gpu_fused_gate_up_silu_quant(None, FAKE, FAKE, FAKE, 512, 8, 12, None) == \
+        _lib.HL_EINVAL
+    assert hl.hl_gpu_fused_kv_linear_quant(FAKE, FAKE, FAKE, FAKE, FAKE, 512, 8, 12, 9, None) == \
+        _lib.HL_EUNSUPPORTED
+    assert hl.hl_gpu_fused_kv_linear_q2k_q3k(FAKE, None, FAKE, FAKE, FAKE, 512, 8, None) == \
+        _lib.HL_EINVAL
+    assert hl.hl_gpu_silu_mul(FAKE, FAKE, FAKE, 0, None) == _lib.HL_EINVAL
+    assert hl.hl_gpu_silu_mul(FAKE, None, FAKE, 16, None) == _lib.HL_EINVAL
+    assert hl.hl_gpu_add(FAKE, FAKE, FAKE, -1, None) == _lib.HL_EINVAL
