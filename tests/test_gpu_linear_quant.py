@@ -161,7 +161,9 @@ def test_fused_gate_up_silu_and_kv(hl, orc, qt, M, K):
     assert rel_err(y.cpu().numpy(), G) < TOL_F32 and rel_err(y2.cpu().numpy(), U) < TOL_F32
     A.gpu_fused_gate_up_silu_quant(y, xd, gd, ud, K, M, qt)
     torch.cuda.synchronize()
-    assert rel_err(y.cpu().numpy(), G / (1 + np.exp(-G)) * U) < TOL_F32
+    with np.errstate(over="ignore"):
+        ref = G / (1 + np.exp(-G)) * U
+    assert rel_err(y.cpu().numpy(), ref) < TOL_F32
 
 
 def test_fused_kv_mixed_types_and_alignment(hl, orc):

@@ -82,7 +82,8 @@ def _oracle_step(orc, cfg, ref, tok, pos):
         x = (x + mv(lw["wo"], a)).astype(np.float32)
         xn = norm(x, lw["ffn_norm"])
         g, u = mv(lw["w_gate"], xn), mv(lw["w_up"], xn)
-        h = (g * (np.float32(1) / (np.float32(1) + np.exp(-g))) * u).astype(np.float32)
+        with np.errstate(over="ignore"):  # exp(-g) -> inf gives silu's limit 0
+            h = (g * (np.float32(1) / (np.float32(1) + np.exp(-g))) * u).astype(np.float32)
         x = (x + mv(lw["w_down"], h)).astype(np.float32)
         if li + 1 < len(ref["layers"]):
             xn = norm(x, ref["layers"][li + 1]["attn_norm"])
