@@ -11,7 +11,7 @@ import os
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(PKG_DIR, "libhl_attn.so")
 
-HL_OK, HL_EINVAL, HL_ECAPACITY, HL_EUNSUPPORTED, HL_EHIP = 0, -1, -2, -3, -4
+HL_OK, HL_EINVAL, HL_ECAPACITY, HL_EUNSUPPORTED, HL_EHIP, HL_ECAPTURE = 0, -1, -2, -3, -4, -5
 HL_F32, HL_F16, HL_BF16, HL_FP8 = 0, 1, 2, 3
 HL_ROPE_HALF_SPLIT, HL_ROPE_INTERLEAVED = 0, 1
 HL_KV_COLMAJOR, HL_KV_TILED32, HL_KV_PAGED32 = 0, 1, 2

@@ -74,6 +74,18 @@ void build_theta(ThetaTable& t, int rope_dim, float base) {
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
+// The library-owned scratch of the reference-signature drop-ins is allocated
+// (with a device synchronisation) when a call first needs it; that cannot
+// happen inside a HIP graph capture, so such a call is refused instead.
+int refuse_if_capturing(void* stream, const char* what) {
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  hipError_t e = hipStreamIsCapturing(as_stream(stream), &st);
+  if (e != hipSuccess) return hip_fail(e, "hipStreamIsCapturing");
+  if (st != hipStreamCaptureStatusNone)
+    return fail(HL_ECAPTURE, "%s: the first call of this size on a device allocates; it cannot run under stream capture (call once before capturing)", what);
+  return HL_OK;
+}
+
 int check_gqa(int n_head, int n_head_kv) {
   if (n_head <= 0 || n_head_kv <= 0)
     return fail(HL_EINVAL, "head counts must be positive (n_head=%d, n_head_kv=%d)", n_head, n_head_kv);
@@ -437,10 +449,11 @@ int hl_attn_decode_workspace_init(void* workspace, size_t bytes, void* stream) {
   return e == hipSuccess ? HL_OK : hip_fail(e, "workspace init launch");
 }
 
-int hl_gpu_attention_decode(float* dst, const float* q, const float* k_cache, const float* v_cache,
-                            int n_head, int n_head_kv, int head_dim, int cur_len, int cache_cols,
-                            void* stream) {
-  hl_decode_args a;
+// The gpuAttentionDecode call contract as batched args (B = 1, fp32 caches),
+// validated and planned.
+static int dropin_decode_plan(float* dst, const float* q, const float* k_cache, const float* v_cache, int n_head,
+                              int n_head_kv, int head_dim, int cur_len, int cache_cols, hl_decode_args& a,
+                              DecodePlan& plan) {
   memset(&a, 0, sizeof(a));
   a.batch = 1;
   a.n_head = n_head;
@@ -455,8 +468,17 @@ int hl_gpu_attention_decode(float* dst, const float* q, const float* k_cache, co
   a.out = dst;
   int rc = validate_decode(&a);
   if (rc) return rc;
-  DecodePlan plan;
   decode_plan(&a, &plan);
+  return HL_OK;
+}
+
+int hl_gpu_attention_decode(float* dst, const float* q, const float* k_cache, const float* v_cache,
+                            int n_head, int n_head_kv, int head_dim, int cur_len, int cache_cols,
+                            void* stream) {
+  hl_decode_args a;
+  DecodePlan plan;
+  int rc = dropin_decode_plan(dst, q, k_cache, v_cache, n_head, n_head_kv, head_dim, cur_len, cache_cols, a, plan);
+  if (rc) return rc;
   void* ws = nullptr;
   if (plan.ws_bytes > 0) {
     int dev = 0;
@@ -466,6 +488,8 @@ int hl_gpu_attention_decode(float* dst, const float* q, const float* k_cache, co
     if ((int)g_ws.size() <= dev) g_ws.resize(dev + 1);
     DevWs& w = g_ws[dev];
     if (w.bytes < plan.ws_bytes) {
+      int rc = refuse_if_capturing(stream, "decode workspace");
+      if (rc) return rc;
       if (w.ptr) {
         e = hipDeviceSynchronize();  // an earlier launch may still read it
         if (e != hipSuccess) return hip_fail(e, "hipDeviceSynchronize");
@@ -881,7 +905,7 @@ int hl_gpu_residual_rmsnorm(float* norm_out, float* x, const float* residual, co
 
 // Library-owned argmax scratch of the current device (allocated and zeroed
 // on the first call on that device).
-static int argmax_scratch(unsigned int** out) {
+static int argmax_scratch(unsigned int** out, void* stream) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
@@ -889,6 +913,8 @@ static int argmax_scratch(unsigned int** out) {
   if ((int)g_argmax_ws.size() <= dev) g_argmax_ws.resize(dev + 1, nullptr);
   if (!g_argmax_ws[dev]) {
     void* p = nullptr;
+    int rc = refuse_if_capturing(stream, "argmax scratch");
+    if (rc) return rc;
     e = hipMalloc(&p, kArgmaxScratchBytes);
     if (e != hipSuccess) return hip_fail(e, "hipMalloc(argmax scratch)");
     e = hipMemset(p, 0, kArgmaxScratchBytes);
@@ -903,7 +929,7 @@ int hl_argmax_async(const float* logits, int n_vocab, int32_t* result_dev, void*
   if (!logits || !result_dev) return fail(HL_EINVAL, "argmax: null pointer");
   if (n_vocab < 0) return fail(HL_EINVAL, "argmax: n_vocab %d < 0", n_vocab);
   unsigned int* scratch = nullptr;
-  int rc = argmax_scratch(&scratch);
+  int rc = argmax_scratch(&scratch, stream);
   if (rc) return rc;
   hipError_t e = argmax_launch(logits, n_vocab, scratch, result_dev, as_stream(stream));
   return e == hipSuccess ? HL_OK : hip_fail(e, "argmax launch");
@@ -913,7 +939,7 @@ int hl_gpu_argmax(const float* logits, int n_vocab, int32_t* result, void* strea
   if (!logits || !result) return fail(HL_EINVAL, "argmax: null pointer");
   if (n_vocab < 0) return fail(HL_EINVAL, "argmax: n_vocab %d < 0", n_vocab);
   unsigned int* scratch = nullptr;
-  int rc = argmax_scratch(&scratch);
+  int rc = argmax_scratch(&scratch, stream);
   if (rc) return rc;
   int* slot = (int*)((char*)scratch + kArgmaxScratchBytes - 8);
   hipError_t e = argmax_launch(logits, n_vocab, scratch, slot, as_stream(stream));

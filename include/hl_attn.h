@@ -10,7 +10,12 @@
  *  - Plain pointers and sizes only; `stream` is a hipStream_t passed as void*
  *    (NULL = the null stream).  All work is enqueued asynchronously on that
  *    stream; nothing synchronises, nothing allocates device memory except
- *    hl_gpu_attention_decode's library-owned split-K workspace (grown once).
+ *    the library-owned scratch of two reference-signature drop-ins
+ *    (hl_gpu_attention_decode's split-K workspace, grown when a call needs
+ *    more; hl_gpu_argmax / hl_argmax_async's 2 KB, on the first call on a
+ *    device).  Those allocations synchronise the device; while `stream` is
+ *    being captured into a HIP graph they are refused with HL_ECAPTURE
+ *    instead (make one call of the largest shape before capturing).
  *  - The caller owns every device buffer (naive.nim:171-182).
  *  - Return value: HL_OK (0) or a negative HL_E* code.  hl_last_error()
  *    returns a thread-local message for the last failing call, mirroring the
@@ -41,7 +46,8 @@ enum {
   HL_EINVAL = -1,        /* bad shape / pointer / GQA divisibility          */
   HL_ECAPACITY = -2,     /* KV cache full, prefill longer than max_len      */
   HL_EUNSUPPORTED = -3,  /* dtype / head_dim combination not built          */
-  HL_EHIP = -4           /* HIP runtime error (launch, device query)         */
+  HL_EHIP = -4,          /* HIP runtime error (launch, device query)         */
+  HL_ECAPTURE = -5       /* would allocate while the stream is being captured */
 };
 
 /* ---- element types of activations and KV cache ------------------------- */
@@ -157,7 +163,12 @@ int hl_gpu_store_kv_pair(float* k_cache, const float* k_src, float* v_cache,
 /* gpuAttentionDecode (naive.nim:3369-3383): dst[nHead*headDim] =
  * softmax(q_h . K^T / sqrt(headDim)) . V over cache columns [0, curLen) of
  * the fp32 caches [nHeadKv*headDim, cacheCols], kv head = h / (nHead /
- * nHeadKv).  Split-K over the context with a library-owned workspace.     */
+ * nHeadKv).  Split-K over the context with a library-owned workspace, one
+ * per device and shared by every stream: like the reference, which runs
+ * the whole backend on one stream (naive.nim:241-244), callers on one
+ * device must not overlap calls on different streams.  A call that needs a
+ * larger workspace than any before it on the device allocates it
+ * (synchronising the device); under stream capture it returns HL_ECAPTURE. */
 int hl_gpu_attention_decode(float* dst, const float* q, const float* k_cache,
                             const float* v_cache, int n_head, int n_head_kv,
                             int head_dim, int cur_len, int cache_cols,
@@ -302,8 +313,8 @@ typedef struct hl_decode_args {
  * calls with any split count as long as it holds no other data in between.
  * A call whose counter region (batch x kv heads x head chunks) is larger than
  * the previous call's on the same workspace needs another init first.
- * Calls that overlap in time must not share a workspace.  Returns 0 when the
- * plan needs no workspace (a single split).                              */
+ * Calls that overlap in time (e.g. on two streams) must not share a
+ * workspace.  Returns 0 when the plan needs no workspace (a single split). */
 size_t hl_attn_decode_workspace_bytes(const hl_decode_args* a);
 
 /* Zero-fills `bytes` of workspace on `stream` (a kernel, not a memset, so it

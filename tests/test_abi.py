@@ -74,6 +74,8 @@ def test_decode_workspace_required(hl):
     # one 4-byte arrival counter per (sequence, kv head), padded to 256 bytes,
     # then (D + 2) floats per split per query head per sequence
     assert (need - 256) % ((64 + 2) * 4 * 32) == 0
+    assert hl.hl_attn_decode(ctypes.byref(a), FAKE + 2, need, None) == _lib.HL_EINVAL
+    assert "4-byte aligned" in _err(hl)
 
 
 def test_decode_null_pointer(hl):

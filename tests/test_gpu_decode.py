@@ -200,33 +200,33 @@ def test_decode_reference_dropin_matches_batched(hl, orc):
     assert rel_err(dst.cpu().numpy(), run_decode(qd, kd, vd, 1, hq, hkv, d, L, max_len)) < 1e-6
 
 
-@pytest.mark.parametrize("dt", [0, 2])
-def test_decode_workspace_reuse_and_graph_replay(hl, orc, dt):
+@pytest.mark.parametrize("dt,hq,hkv,d", [(0, 16, 4, 64), (2, 16, 4, 64), (1, 32, 2, 128)])
+def test_decode_workspace_reuse_and_graph_replay(hl, orc, dt, hq, hkv, d):
     """The fused split merge keeps arrival counters in the workspace: after
     hl_attn_decode_workspace_init (the partials may hold garbage) every call
     leaves them zero, so reuse with other split counts and graph replays stay
-    correct."""
+    correct.  (32, 2, 128): 16 heads x 128 dims per workgroup, so the last
+    arrival folds several elements per thread."""
     from hippo_leap_amd import attention as A
-    B, hq, hkv, d, L, max_len = 3, 16, 4, 64, 900, 960
+    B, L, max_len = 3, 900, 960
     q, kb, vb = make_case(orc, B, hq, hkv, d, L, max_len, dt, 1000)
     ref = oracle_decode(orc, q, kb, vb, B, hq, hkv, d, [L] * B, max_len, dt)
     qd, kd, vd = torch.from_numpy(q).cuda(), dev_bits(kb, dt), dev_bits(vb, dt)
     out = torch.full((B * hq * d,), float("nan"), device="cuda")
     args = {ns: A.decode_args(qd, kd, vd, out, hq, hkv, d, max_len, L, num_splits=ns)
-            for ns in (5, 11, 0, 16)}
+            for ns in (5, 11, 0, 16, 2)}
     nbytes = max(A.decode_workspace_bytes(a) for a in args.values())
     ws = torch.full((nbytes,), 0xAB, dtype=torch.uint8, device="cuda")
     hl.hl_attn_decode_workspace_init(ws.data_ptr(), nbytes, None)
     torch.cuda.synchronize()
     assert int(ws.sum()) == 0
     tol = TOL_F32 if dt == 0 else TOL_LOWP
-    for ns in (5, 11, 0, 16, 5):
+    for ns in (5, 11, 0, 16, 2, 5):
         out.fill_(float("nan"))
         A.attn_decode(args[ns], ws)
         torch.cuda.synchronize()
         assert rel_err(out.cpu().numpy(), ref) < tol, ns
-    # every call left the counters (the workspace head) at zero
-    assert int(ws[:B * hkv * 4].sum()) == 0
+        assert int(ws[:B * hkv * 4].count_nonzero()) == 0, ns  # the counters are zero again
     g = torch.cuda.CUDAGraph()
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
@@ -242,6 +242,49 @@ def test_decode_workspace_reuse_and_graph_replay(hl, orc, dt):
         g.replay()
         torch.cuda.synchronize()
         assert rel_err(out.cpu().numpy(), ref) < tol
+
+
+def test_decode_dropin_refuses_to_grow_under_capture(hl, orc):
+    """hl_gpu_attention_decode owns one workspace per device and grows it
+    (hipMalloc + device sync) when a call needs more.  Under stream capture
+    that call returns HL_ECAPTURE instead: the capture stays valid, and after
+    one eager call of the shape the same call captures and replays."""
+    import ctypes
+    from hippo_leap_amd import _lib, attention as A
+    # 512 query heads over 8 kv heads, D = 128, L = 8192: a split-K workspace
+    # of several MB, larger than any other test's drop-in call needs.
+    hq, hkv, d, L, max_len = 512, 8, 128, 8192, 8192
+    q, kb, vb = make_case(orc, 1, hq, hkv, d, L, max_len, 0, 1200)
+    qd, kd, vd = (torch.from_numpy(x).cuda() for x in (q, kb, vb))
+    dst = torch.full((hq * d,), float("nan"), device="cuda")
+    side = torch.cuda.Stream()
+    args = (dst.data_ptr(), qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), hq, hkv, d, L, max_len)
+    g = torch.cuda.CUDAGraph()
+    side.wait_stream(torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g, stream=side):
+        dst.fill_(float("nan"))
+        rc = hl.hl_gpu_attention_decode(*args, ctypes.c_void_p(side.cuda_stream))
+    assert rc == _lib.HL_ECAPTURE, rc
+    assert "capture" in hl.hl_last_error().decode()
+    g.replay()  # the capture (the fill alone) is still a valid graph
+    torch.cuda.synchronize()
+    assert torch.isnan(dst).all()
+    A.gpu_attention_decode(dst, qd, kd, vd, hq, hkv, d, L, max_len)  # eager: grows the workspace
+    torch.cuda.synchronize()
+    ref = dst.cpu().numpy().copy()
+    sub = orc.attention_decode(q[:16 * d], kb[:d * max_len], vb[:d * max_len], 16, 1, d, L, max_len)
+    assert rel_err(ref[:16 * d], sub) < TOL_F32  # heads 0..15 (kv head 0) against the oracle
+    g2 = torch.cuda.CUDAGraph()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.graph(g2, stream=side):
+        assert hl.hl_gpu_attention_decode(*args, ctypes.c_void_p(side.cuda_stream)) == _lib.HL_OK
+    for _ in range(3):
+        dst.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g2.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(dst.cpu().numpy(), ref)
 
 
 def test_decode_dropin_shape_changes_share_library_workspace(hl, orc):
