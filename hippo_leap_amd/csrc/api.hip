@@ -519,6 +519,65 @@ int hl_gpu_attention_decode(float* dst, const float* q, const float* k_cache, co
 }
 
 // ---------------------------------------------------------------------------
+// gpuAttentionDecode without any allocation: the split-K workspace is a
+// fixed static device array instead of library-owned hipMalloc memory.
+// ---------------------------------------------------------------------------
+// One copy per device, held until the process ends.  Only its device address
+// (hipGetSymbolAddress) is ever handed to a kernel or a fill: the array's
+// name in host code is a host-side stand-in, not a device address.
+constexpr size_t kNoAllocScratchBytes = (size_t)1 << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+namespace {
+struct NoAllocDev {
+  void* ptr = nullptr;      // device address of `scratch` on this device
+  size_t zero_prefix = 0;   // leading bytes known to hold zero arrival counters
+};
+std::vector<NoAllocDev> g_noalloc;  // per device, guarded by g_mu
+}  // namespace
+
+int hl_gpu_attention_decode_noalloc(float* dst, const float* q, const float* k_cache, const float* v_cache,
+                                    int n_head, int n_head_kv, int head_dim, int cur_len, int cache_cols,
+                                    void* stream) {
+  hl_decode_args a;
+  DecodePlan plan;
+  int rc = dropin_decode_plan(dst, q, k_cache, v_cache, n_head, n_head_kv, head_dim, cur_len, cache_cols, a, plan);
+  if (rc) return rc;
+  void* ws = nullptr;
+  if (plan.ws_bytes > 0) {
+    if (plan.ws_bytes > kNoAllocScratchBytes)
+      return fail(HL_ECAPACITY, "decode_noalloc: this shape needs %zu bytes of split-K scratch; the static scratch holds %zu",
+                  plan.ws_bytes, kNoAllocScratchBytes);
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    std::lock_guard<std::mutex> lk(g_mu);
+    if ((int)g_noalloc.size() <= dev) g_noalloc.resize(dev + 1);
+    NoAllocDev& d = g_noalloc[dev];
+    if (!d.ptr) {  // first call on this device (which is current): its copy's address, then all zero
+      void* ptr = nullptr;
+      e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+      if (e != hipSuccess || !ptr) return hip_fail(e != hipSuccess ? e : hipErrorInvalidSymbol, "hipGetSymbolAddress(scratch)");
+      e = zero_fill_launch(ptr, kNoAllocScratchBytes, as_stream(stream));
+      if (e != hipSuccess) return hip_fail(e, "decode_noalloc scratch clear");
+      d.ptr = ptr;
+      d.zero_prefix = kNoAllocScratchBytes;
+    }
+    // Every call leaves its arrival counters zero; bytes past the previous
+    // call's counters held its partials, so a call with a longer counter
+    // region clears the difference first (a fill kernel, no allocation).
+    if (plan.counters_bytes > d.zero_prefix) {
+      e = zero_fill_launch(d.ptr, plan.counters_bytes, as_stream(stream));
+      if (e != hipSuccess) return hip_fail(e, "decode_noalloc counter clear");
+    }
+    d.zero_prefix = plan.counters_bytes;
+    ws = d.ptr;
+  }
+  hipError_t e = decode_launch(&a, &plan, ws, as_stream(stream));
+  return e == hipSuccess ? HL_OK : hip_fail(e, "decode launch");
+}
+
+// ---------------------------------------------------------------------------
 // Decode-side fused qkNorm + RoPE + KV store
 // ---------------------------------------------------------------------------
 static int rope_store_op(const hl_rope_store_args* a, HeadVecOp& op) {

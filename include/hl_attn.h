@@ -174,6 +174,24 @@ int hl_gpu_attention_decode(float* dst, const float* q, const float* k_cache,
                             int head_dim, int cur_len, int cache_cols,
                             void* stream);
 
+/* hl_gpu_attention_decode without any allocation.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Same arguments, kernels and results as
+ * hl_gpu_attention_decode; its split-K workspace is a static 1 MiB device
+ * array of the library (one copy per device, held until the process ends)
+ * instead of hipMalloc memory, so it never allocates, frees or synchronises.
+ * A shape whose split-K partials (nHead * splits * (headDim + 2) * 4 bytes,
+ * plus 256) exceed 1 MiB returns HL_ECAPACITY before launching anything;
+ * that takes hundreds of query heads (32 heads need at most ~0.3 MiB).  Every
+ * call on a device shares that device's array: calls that overlap in time
+ * on one device (e.g. on two streams) race.  The first call on a device
+ * zero-fills the array with a kernel on `stream`.                       */
+int hl_gpu_attention_decode_noalloc(float* dst, const float* q, const float* k_cache,
+                                    const float* v_cache, int n_head, int n_head_kv,
+                                    int head_dim, int cur_len, int cache_cols,
+                                    void* stream);
+
 /* gpuAttentionPrefill (naive.nim:3450-3464): causal attention over the
  * col-major fp32 projections q[nHead*headDim, seqLen], k/v[nHeadKv*headDim,
  * seqLen]; dst is col-major [nHead*headDim, seqLen].  No 4096-token cap.  */
