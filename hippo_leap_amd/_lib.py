@@ -86,6 +86,19 @@ class DecodeScratch(ctypes.Structure):
     _fields_ = [(n, c_void_p) for n in ("x", "x_norm", "tmp0", "tmp1", "tmp2")]
 
 
+class KvCacheDesc(ctypes.Structure):
+    _fields_ = [(n, c_int) for n in ("n_layer", "n_head_kv", "head_dim", "max_len", "kv_dtype",
+                                     "kv_layout")] + \
+               [("k", ctypes.POINTER(c_void_p)), ("v", ctypes.POINTER(c_void_p)),
+                ("block_table", c_void_p), ("blocks_per_seq", c_int), ("cur_len", c_int)]
+
+
+class ForwardScratch(ctypes.Structure):
+    _fields_ = [("max_tokens", c_int)] + [(n, c_void_p) for n in ("x", "x_norm", "tmp0", "tmp1", "tmp2",
+                                                                    "workspace")] + \
+               [("workspace_bytes", c_size_t)]
+
+
 class PrefillArgs(ctypes.Structure):
     _fields_ = [
         ("n_head", c_int), ("n_head_kv", c_int), ("head_dim", c_int), ("seq_len", c_int),
@@ -149,6 +162,13 @@ SIGNATURES = {
     "hl_gpu_add": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_void_p]),
     "hl_forward_decode_token": (c_int, [ctypes.POINTER(ModelDesc), ctypes.POINTER(DecodeScratch),
                                         c_void_p, c_int, c_void_p, c_void_p, c_void_p]),
+    "hl_kv_cache_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int]),
+    "hl_kv_cache_init": (c_int, [ctypes.POINTER(KvCacheDesc), ctypes.POINTER(ModelDesc)]),
+    "hl_forward_workspace_bytes": (c_size_t, [ctypes.POINTER(ModelDesc), ctypes.POINTER(KvCacheDesc), c_int]),
+    "hl_forward_prefill": (c_int, [ctypes.POINTER(ModelDesc), ctypes.POINTER(KvCacheDesc),
+                                   ctypes.POINTER(ForwardScratch), c_void_p, c_int, c_void_p, c_void_p]),
+    "hl_forward_decode": (c_int, [ctypes.POINTER(ModelDesc), ctypes.POINTER(KvCacheDesc),
+                                  ctypes.POINTER(ForwardScratch), c_void_p, c_void_p, c_void_p, c_void_p]),
     "hl_attn_decode_workspace_bytes": (c_size_t, [ctypes.POINTER(DecodeArgs)]),
     "hl_attn_decode": (c_int, [ctypes.POINTER(DecodeArgs), c_void_p, c_size_t, c_void_p]),
     "hl_attn_decode_workspace_init": (c_int, [c_void_p, c_size_t, c_void_p]),

@@ -767,6 +767,26 @@ static int validate_prefill(const hl_prefill_args* a, PrefillPlan* pl) {
   return HL_OK;
 }
 
+}  // extern "C"
+
+// Validation of the composed entry points' arguments (model.hip checks every
+// layer's calls before launching anything).
+int hl::check_decode_args(const hl_decode_args* a) { return validate_decode(a); }
+int hl::check_step_args(const hl_rope_store_args* rs, const hl_decode_args* at) {
+  HeadVecOp op;
+  return validate_step(rs, at, op);
+}
+int hl::check_rope_store_args(const hl_rope_store_args* a) {
+  HeadVecOp op;
+  return rope_store_op(a, op);
+}
+int hl::check_prefill_args(const hl_prefill_args* a) {
+  PrefillPlan pl;
+  return validate_prefill(a, &pl);
+}
+
+extern "C" {
+
 size_t hl_attn_prefill_workspace_bytes(const hl_prefill_args* a) {
   PrefillPlan pl;
   if (validate_prefill(a, &pl)) return 0;

@@ -1078,10 +1078,13 @@ void decode_plan(const hl_decode_args* a, DecodePlan* plan, bool step) {
   plan->split_len = tiles_per_split * tile;
   plan->num_splits = S;
   if (plan->num_splits > 1) {
-    // Counters first, so their place depends only on (batch, kv heads, head
-    // chunks) and not on the split count: a workspace shared by calls with
-    // different split counts keeps them where the previous call left them (zero).
-    plan->counters_bytes = ((size_t)units * 4 + 255) / 256 * 256;
+    // Counters first, in a region sized for the most head chunks any plan
+    // of this shape can use (chunks of 2 heads), so that their place depends
+    // only on (batch, kv heads, group) and not on the split count or the
+    // attention length: a workspace shared by the calls of one model keeps
+    // them where the previous call left them (zero).
+    const long long max_chunks = G < 2 ? 1 : (G + 1) / 2;
+    plan->counters_bytes = ((size_t)a->batch * a->n_head_kv * max_chunks * 4 + 255) / 256 * 256;
     const size_t partial = (size_t)a->batch * a->n_head * plan->num_splits * (a->head_dim + 2) * 4;
     plan->ws_bytes = plan->counters_bytes + partial;
   } else {

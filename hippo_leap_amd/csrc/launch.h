@@ -149,6 +149,13 @@ hipError_t linear_col_launch(float* y, const float* x, const float* w, int K, in
 
 // ---- quantized decode GEMV (linear_quant.hip) ------------------------------
 int quant_block_elems(int qtype);        // 0: type not built
+
+// ---- argument validation of the C-ABI entry points (api.hip) --------------
+// HL_OK or the entry point's own error code and message.
+int check_decode_args(const hl_decode_args* a);
+int check_step_args(const hl_rope_store_args* rs, const hl_decode_args* at);
+int check_rope_store_args(const hl_rope_store_args* a);
+int check_prefill_args(const hl_prefill_args* a);
 long long quant_row_bytes(int qtype, int K);
 hipError_t linear_quant_launch(float* y, const float* x, const void* w, int K, int M, int qtype,
                                hipStream_t stream);

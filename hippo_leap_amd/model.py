@@ -14,6 +14,8 @@ from . import _lib
 from ._lib import check
 from .attention import _p, _stream
 
+c_void_p = ctypes.c_void_p
+
 LAYER_WEIGHTS = ("wq", "wk", "wv", "wo", "w_gate", "w_up", "w_down")
 
 
@@ -71,3 +73,79 @@ class DenseDecoder:
         for p in range(n_steps):
             self.step(p, out[p:p + 1], out[p + 1:p + 2], stream)
         return out.cpu().tolist()[1:]
+
+
+class KvCache:
+    """initKvCache (backends/naive.nim:3912-3931) with a storage dtype and
+    layout: one K and one V device buffer of hl_kv_cache_bytes() per layer,
+    described by an hl_kv_cache_desc checked against the model."""
+
+    def __init__(self, torch, model: "DenseDecoder", kv_dtype: int = _lib.HL_F32,
+                 kv_layout: int = _lib.HL_KV_COLMAJOR, max_len: int | None = None, block_table=None):
+        c = model.cfg
+        self.max_len = int(max_len or c["max_len"])
+        lib = _lib.load()
+        nbytes = int(lib.hl_kv_cache_bytes(c["n_head_kv"], c["head_dim"], self.max_len, kv_dtype, kv_layout))
+        if nbytes == 0:
+            raise _lib.HLError(_lib.HL_EUNSUPPORTED, f"kv cache dtype {kv_dtype} / layout {kv_layout} not built")
+        n = c["n_layer"]
+        self.k = [torch.zeros(nbytes, dtype=torch.uint8, device="cuda") for _ in range(n)]
+        self.v = [torch.zeros(nbytes, dtype=torch.uint8, device="cuda") for _ in range(n)]
+        self.table = block_table
+        self._kp = (c_void_p * n)(*[t.data_ptr() for t in self.k])
+        self._vp = (c_void_p * n)(*[t.data_ptr() for t in self.v])
+        self.desc = _lib.KvCacheDesc(n, c["n_head_kv"], c["head_dim"], self.max_len, kv_dtype, kv_layout,
+                                     self._kp, self._vp, _p(block_table),
+                                     0 if block_table is None else int(block_table.numel()), 0)
+        check(lib.hl_kv_cache_init(ctypes.byref(self.desc), ctypes.byref(model.desc)))
+
+    @property
+    def cur_len(self) -> int:
+        return int(self.desc.cur_len)
+
+
+class DenseModel(DenseDecoder):
+    """The backend contract over a KV-cache descriptor: prefill() is the
+    reference's forwardPrefill and decode() its forwardDecodeToken
+    (backends/naive.nim:3967-4590, 4592-4760) for lkAttentionFfn layers,
+    through hl_forward_prefill / hl_forward_decode.  The activation scratch
+    and attention workspace are allocated here once for max_tokens columns,
+    so no call allocates."""
+
+    def __init__(self, torch, cfg: dict, tok_emb, output_norm, output, output_type: int,
+                 layers: list[dict], cache: KvCache | None = None, max_tokens: int = 1,
+                 kv_dtype: int = _lib.HL_F32, kv_layout: int = _lib.HL_KV_COLMAJOR):
+        super().__init__(torch, cfg, tok_emb, output_norm, output, output_type, layers)
+        self.cache = cache if cache is not None else KvCache(torch, self, kv_dtype, kv_layout)
+        c, T = self.cfg, max(1, int(max_tokens))
+        E, q, kv, ff = c["n_emb"], c["n_head"] * c["head_dim"], c["n_head_kv"] * c["head_dim"], c["n_ff"]
+        f = lambda n: torch.zeros(n * T, device="cuda")
+        self.fbufs = [f(E), f(max(E, q)), f(max(E, q, ff)), f(max(kv, ff)), f(max(kv, ff))]
+        lib = _lib.load()
+        nws = int(lib.hl_forward_workspace_bytes(ctypes.byref(self.desc), ctypes.byref(self.cache.desc), T))
+        self.ws = torch.zeros(max(nws, 256), dtype=torch.uint8, device="cuda")
+        check(lib.hl_attn_decode_workspace_init(self.ws.data_ptr(), nws, None))
+        self.fscratch = _lib.ForwardScratch(T, *[_p(b) for b in self.fbufs], self.ws.data_ptr(), nws)
+        self.max_tokens = T
+
+    def prefill(self, tokens, stream=None):
+        """forwardPrefill: tokens (host list or device int32 tensor) at
+        positions 0 .. T-1; returns the logits [n_vocab, T] (device)."""
+        torch = self.torch
+        tok = tokens if torch.is_tensor(tokens) else torch.tensor(list(tokens), dtype=torch.int32, device="cuda")
+        T = int(tok.numel())
+        logits = torch.empty(self.cfg["n_vocab"], max(T, 1), device="cuda")
+        check(_lib.load().hl_forward_prefill(ctypes.byref(self.desc), ctypes.byref(self.cache.desc),
+                                             ctypes.byref(self.fscratch), _p(tok), T, _p(logits),
+                                             _stream(stream)))
+        return logits
+
+    def decode(self, token_dev=None, next_dev=None, stream=None):
+        """forwardDecodeToken at position cache.cur_len: reads token_dev
+        (default: the current-token slot), writes self.logits and next_dev
+        (default: the next-token slot), advances the cache."""
+        tok = self.tokens[0:1] if token_dev is None else token_dev
+        nxt = self.tokens[1:2] if next_dev is None else next_dev
+        check(_lib.load().hl_forward_decode(ctypes.byref(self.desc), ctypes.byref(self.cache.desc),
+                                            ctypes.byref(self.fscratch), _p(tok), _p(self.logits), _p(nxt),
+                                            _stream(stream)))

@@ -322,8 +322,9 @@ typedef struct hl_decode_args {
   int blocks_per_seq;
 } hl_decode_args;
 
-/* Workspace bytes hl_attn_decode needs for these args: one 4-byte arrival
- * counter per (sequence, kv head, 16-head chunk), rounded up to 256 bytes,
+/* Workspace bytes hl_attn_decode needs for these args: 4-byte arrival
+ * counters, one per (sequence, kv head, pair of query heads of its group),
+ * rounded up to 256 bytes,
  * then the split-K partials (running max, sum and D accumulators per split
  * per query head).  The counters must be zero before the first call
  * (hl_attn_decode_workspace_init on the freshly allocated workspace); every
@@ -512,7 +513,9 @@ typedef struct {
 } hl_layer_desc;
 
 typedef struct {
-  int n_layer, n_emb, n_head, n_head_kv, head_dim, rope_dim, n_ff, n_vocab, max_len;
+  int n_layer, n_emb, n_head, n_head_kv, head_dim;
+  int rope_dim;                /* <= 0 -> head_dim (the reference's ropeDim)  */
+  int n_ff, n_vocab, max_len;
   float rms_eps, rope_base;
   const float* tok_emb;        /* [n_vocab, n_emb] fp32                      */
   const float* output_norm;    /* [n_emb]                                    */
@@ -547,6 +550,89 @@ typedef struct {
 int hl_forward_decode_token(const hl_model_desc* model, const hl_decode_scratch* scratch,
                             const int32_t* token_dev, int pos, float* logits,
                             int32_t* next_token_dev, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* The backend contract over a KV-cache descriptor: initKvCache,             */
+/* forwardPrefill and forwardDecodeToken (naive.nim:3912-3931, 3967-4590,    */
+/* 4592-4760) for models whose layers are all of kind lkAttentionFfn.        */
+/* ------------------------------------------------------------------------ */
+
+/* A model's KV cache (KvCache / GpuKvCache, backend_types.nim:28-49) with a
+ * storage dtype and layout, which the reference's cache lacks (its caches
+ * are fp32 [kvDim, maxLen]).  The caller owns the buffers: per layer one K
+ * and one V cache of hl_kv_cache_bytes() bytes each, in device memory.     */
+typedef struct hl_kv_cache_desc {
+  int n_layer, n_head_kv, head_dim, max_len;
+  int kv_dtype;                 /* HL_F32 (the reference's) | HL_F16 | HL_BF16 |
+                                   HL_FP8 (tiled or paged layouts only)         */
+  int kv_layout;                /* HL_KV_COLMAJOR | HL_KV_TILED32 | PAGED32      */
+  void* const* k;               /* host array [n_layer] of device caches        */
+  void* const* v;
+  const int* block_table;       /* HL_KV_PAGED32: device int[blocks_per_seq]    */
+  int blocks_per_seq;
+  int cur_len;                  /* positions written (curLen): prefill sets it,
+                                   each decode step advances it by one          */
+} hl_kv_cache_desc;
+
+/* Bytes of one layer's K (or V) cache in this dtype and layout: the
+ * reference's newTensor(@[kvDim, maxLen]) of initKvCache (naive.nim:
+ * 3926-3927), which is n_head_kv * head_dim * max_len fp32 values.  0 for
+ * a combination the library does not build.                               */
+size_t hl_kv_cache_bytes(int n_head_kv, int head_dim, int max_len, int kv_dtype, int kv_layout);
+
+/* initKvCache (naive.nim:3912-3931) for a cache descriptor the caller has
+ * filled: checks it against the model (layer count, kv heads, head dim,
+ * dtype/layout/alignment rules of the decode and prefill entry points, a
+ * cache pointer per layer) and sets cur_len = 0.                           */
+int hl_kv_cache_init(hl_kv_cache_desc* cache, const hl_model_desc* model);
+
+/* Activation scratch of the forward entry points (the reference's act0/1
+ * and scratch0..2, sized for max_tokens columns) plus the attention
+ * workspace, all caller-owned device memory.  Nothing below allocates.     */
+typedef struct {
+  int max_tokens;               /* columns the activation buffers hold (>= 1) */
+  float* x;                     /* [n_emb * max_tokens]                         */
+  float* x_norm;                /* [max(n_emb, n_head*head_dim) * max_tokens]  */
+  float* tmp0;                  /* [max(n_emb, n_head*head_dim, n_ff) * max_tokens] */
+  float* tmp1;                  /* [max(n_head_kv*head_dim, n_ff) * max_tokens] */
+  float* tmp2;                  /* [max(n_head_kv*head_dim, n_ff) * max_tokens] */
+  void* workspace;              /* hl_forward_workspace_bytes() bytes, 16-byte
+                                   aligned, zero-filled once with
+                                   hl_attn_decode_workspace_init                */
+  size_t workspace_bytes;
+} hl_forward_scratch;
+
+/* Attention workspace bytes that prefills of up to max_tokens tokens and
+ * decode steps at every position < max_len need with this cache.          */
+size_t hl_forward_workspace_bytes(const hl_model_desc* model, const hl_kv_cache_desc* cache,
+                                  int max_tokens);
+
+/* forwardPrefill (naive.nim:3967-4590), lkAttentionFfn layers: the
+ * n_tokens device int32 tokens at positions 0 .. n_tokens-1 through every
+ * layer (rmsnorm, Q/K/V projections, qk-norm, RoPE, K/V into the cache,
+ * causal attention, O projection, residual, rmsnorm, gate/up, SiLU * up,
+ * down, residual), then the final norm and the output projection into
+ * logits [n_vocab, n_tokens] (device, col-major, the reference's result
+ * tensor).  Sets cache->cur_len = n_tokens.  Weights are fp32 (type 0), as
+ * the reference's prefill takes them (it uploads fp32 copies); a quantized
+ * weight returns HL_EUNSUPPORTED.  Errors: the reference's ValueErrors
+ * (GQA, empty prompt, "prefill exceeds KV cache capacity"), checked with
+ * every pointer and shape before the first launch.                        */
+int hl_forward_prefill(const hl_model_desc* model, hl_kv_cache_desc* cache,
+                       const hl_forward_scratch* scratch, const int32_t* tokens_dev,
+                       int n_tokens, float* logits, void* stream);
+
+/* forwardDecodeToken (naive.nim:4592-4760, 5520-5545): the token at
+ * *token_dev at position cache->cur_len (the K/V column written), logits
+ * [n_vocab] and the greedy next token into *next_token_dev, then
+ * cache->cur_len += 1.  fp16/bf16/fp8 caches run each layer's qk-norm,
+ * RoPE, cache write and attention as one launch (hl_decode_step); fp32
+ * caches run the reference's sequence.  Weights fp32 or any GGUF type of
+ * hl_gpu_linear_col_quant.  "KV cache full" (HL_ECAPACITY) when cur_len ==
+ * max_len.  Nothing allocates or waits for the stream.                    */
+int hl_forward_decode(const hl_model_desc* model, hl_kv_cache_desc* cache,
+                      const hl_forward_scratch* scratch, const int32_t* token_dev,
+                      float* logits, int32_t* next_token_dev, void* stream);
 
 #ifdef __cplusplus
 }

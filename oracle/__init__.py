@@ -63,6 +63,8 @@ def lib() -> ctypes.CDLL:
             "orc_argmax": (_i, [_fp, _ll]),
             "orc_dequant_rows": (_ll, [_i, ctypes.c_void_p, _fp, _i, _i]),
             "orc_embedding": (None, [_fp, ctypes.POINTER(_i), _fp, _i, _i]),
+            "orc_add": (None, [_fp, _fp, _fp, _ll]),
+            "orc_silu_mul": (None, [_fp, _fp, _fp, _ll]),
             "orc_attention_prefill": (None, [_fp, _fp, _fp, _fp, _i, _i, _i, _i, _f, _i, _i, _i,
                                              _i, _i, _fp]),
         }
@@ -231,6 +233,24 @@ def attention_prefill(q: np.ndarray, k: np.ndarray, v: np.ndarray, n_head: int, 
     r0, r1, rs = rows if rows is not None else (0, T, 1)
     lib().orc_attention_prefill(_ptr(q), _ptr(k), _ptr(v), _ptr(out), n_head, n_head_kv, head_dim,
                                 T, float(s), h0, h1, r0, r1, rs, _ptr(scores))
+    return out
+
+
+def add(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """tensor.nim add (:42-47)."""
+    a, b = _f32(a), _f32(b)
+    assert a.shape == b.shape
+    out = np.empty_like(a)
+    lib().orc_add(_ptr(a), _ptr(b), _ptr(out), a.size)
+    return out
+
+
+def silu_mul(gate: np.ndarray, up: np.ndarray) -> np.ndarray:
+    """gpuSiluMul (naive.nim:2179-2187): gate * (1 / (1 + exp(-gate))) * up."""
+    g, u = _f32(gate), _f32(up)
+    assert g.shape == u.shape
+    out = np.empty_like(g)
+    lib().orc_silu_mul(_ptr(g), _ptr(u), _ptr(out), g.size)
     return out
 
 

@@ -423,6 +423,23 @@ void orc_attention_prefill(const float* Q, const float* K, const float* V, float
   }
 }
 
+/* tensor.nim add (:42-47): out[i] = a[i] + b[i] (fp32). */
+void orc_add(const float* a, const float* b, float* out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = a[i] + b[i];
+}
+
+/* gpuSiluMul's kernel (siluMulKernel, naive.nim:2179-2187): with x = gate[i],
+ * out[i] = x * (1 / (1 + expf(-x))) * up[i], in that order (the CPU
+ * tensor.nim silu, :56-61, writes x / (1 + exp(-x)); the GPU form is the
+ * one the drop-in replaces). */
+void orc_silu_mul(const float* gate, const float* up, float* out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) {
+    const float x = gate[i];
+    const float sig = 1.0f / (1.0f + expf(-x));
+    out[i] = x * sig * up[i];
+  }
+}
+
 /* ---------------------------------------------------------------------- */
 /* Decode-step ends (backends/naive.nim)                                  */
 /* ---------------------------------------------------------------------- */

@@ -308,10 +308,24 @@ def _model_desc(layers, **kw):
     return m
 
 
+def _fake_layers(n=2, **kw):
+    """Layer descriptors whose pointers are all non-null stand-ins (the host
+    checks never dereference them)."""
+    layers = (_lib.LayerDesc * n)()
+    for L in layers:
+        for f, t in _lib.LayerDesc._fields_:
+            if t is ctypes.c_void_p and f not in ("q_norm", "k_norm"):
+                setattr(L, f, FAKE)
+        for k, v in kw.items():
+            setattr(L, k, v)
+    return layers
+
+
 def test_decode_token_validation(hl):
     """hl_forward_decode_token's host checks (forwardDecodeToken's
-    preconditions, naive.nim:4594-4599): nulls, shapes, the cache capacity."""
-    layers = (_lib.LayerDesc * 2)()
+    preconditions, naive.nim:4594-4599): nulls, shapes, every layer's
+    weights and caches, the cache capacity, all before the first launch."""
+    layers = _fake_layers()
     s = _lib.DecodeScratch(FAKE, FAKE, FAKE, FAKE, FAKE)
     tok = logits = nxt = FAKE
     call = lambda m, sc=s, pos=0: hl.hl_forward_decode_token(
@@ -321,9 +335,76 @@ def test_decode_token_validation(hl):
     assert call(_model_desc(layers), _lib.DecodeScratch(FAKE, None, FAKE, FAKE, FAKE)) == _lib.HL_EINVAL
     assert call(_model_desc(layers, n_layer=0)) == _lib.HL_EINVAL
     assert call(_model_desc(layers, n_head_kv=0)) == _lib.HL_EINVAL
+    assert call(_model_desc(layers, n_head_kv=3)) == _lib.HL_EINVAL
+    assert _err(hl) == "GQA requires head_count divisible by head_count_kv"
+    assert call(_model_desc(layers, rope_dim=70)) == _lib.HL_EINVAL  # > head_dim
+    assert call(_model_desc(_fake_layers(w_down=None))) == _lib.HL_EINVAL
+    assert "w_down" in _err(hl)
+    assert call(_model_desc(_fake_layers(wq_type=9))) == _lib.HL_EUNSUPPORTED
     assert call(_model_desc(layers), pos=16) == _lib.HL_ECAPACITY
     assert "outside the cache" in _err(hl)
     assert call(_model_desc(layers), pos=-1) == _lib.HL_ECAPACITY
+    # a layer's attention call that would fail (head_dim 96 is not built) is
+    # refused before anything is launched
+    assert call(_model_desc(layers, head_dim=96, rope_dim=0)) == _lib.HL_EUNSUPPORTED
+
+
+def _kv_desc(n_layer=2, n_head_kv=2, head_dim=64, max_len=16, dt=_lib.HL_F32, lay=0, ptrs=None):
+    p = (ctypes.c_void_p * n_layer)(*([FAKE] * n_layer if ptrs is None else ptrs))
+    d = _lib.KvCacheDesc(n_layer, n_head_kv, head_dim, max_len, dt, lay, p, p, None, 0, 7)
+    d._keep = p
+    return d
+
+
+def test_kv_cache_descriptor(hl):
+    """hl_kv_cache_bytes / hl_kv_cache_init: initKvCache's per-layer tensor
+    [kvDim, maxLen] (naive.nim:3926-3927) in each dtype and layout."""
+    assert hl.hl_kv_cache_bytes(8, 128, 4096, _lib.HL_F32, 0) == 8 * 128 * 4096 * 4
+    assert hl.hl_kv_cache_bytes(8, 128, 4096, _lib.HL_BF16, 1) == 8 * 128 * 4096 * 2
+    assert hl.hl_kv_cache_bytes(8, 128, 4096, _lib.HL_FP8, 2) == 8 * 128 * 4096
+    assert hl.hl_kv_cache_bytes(8, 128, 4096, _lib.HL_FP8, 0) == 0  # fp8 needs tiles
+    assert hl.hl_kv_cache_bytes(8, 128, 4008, _lib.HL_F16, 1) == 0  # tiles of 32 columns
+    assert hl.hl_kv_cache_bytes(8, 128, 4096, _lib.HL_F32, 1) == 0
+    m = _model_desc(_fake_layers())
+    c = _kv_desc()
+    assert hl.hl_kv_cache_init(ctypes.byref(c), ctypes.byref(m)) == _lib.HL_OK
+    assert c.cur_len == 0
+    c = _kv_desc(n_layer=3)
+    assert hl.hl_kv_cache_init(ctypes.byref(c), ctypes.byref(m)) == _lib.HL_EINVAL
+    assert "does not match" in _err(hl)
+    c = _kv_desc(ptrs=[FAKE, None])
+    assert hl.hl_kv_cache_init(ctypes.byref(c), ctypes.byref(m)) == _lib.HL_EINVAL
+    c = _kv_desc(dt=_lib.HL_FP8, lay=0)
+    assert hl.hl_kv_cache_init(ctypes.byref(c), ctypes.byref(m)) == _lib.HL_EUNSUPPORTED
+    c = _kv_desc(dt=_lib.HL_BF16, lay=1, max_len=64)  # tiled: 16-byte aligned stand-ins
+    assert hl.hl_kv_cache_init(ctypes.byref(c), ctypes.byref(m)) == _lib.HL_OK
+
+
+def test_forward_prefill_and_decode_validation(hl):
+    """hl_forward_prefill / hl_forward_decode refuse with the reference's
+    ValueError messages (naive.nim:3969-3976, 4598-4599) before launching."""
+    m = _model_desc(_fake_layers())
+    c = _kv_desc()
+    assert hl.hl_kv_cache_init(ctypes.byref(c), ctypes.byref(m)) == _lib.HL_OK
+    s = _lib.ForwardScratch(16, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 1 << 30)
+    pre = lambda mm, T: hl.hl_forward_prefill(ctypes.byref(mm), ctypes.byref(c), ctypes.byref(s), FAKE, T,
+                                              FAKE, None)
+    assert pre(m, 0) == _lib.HL_EINVAL
+    assert _err(hl) == "prefill requires at least one token"
+    assert pre(m, 17) == _lib.HL_ECAPACITY
+    assert _err(hl) == "prefill exceeds KV cache capacity"
+    assert pre(_model_desc(_fake_layers(), n_head_kv=3), 4) == _lib.HL_EINVAL
+    assert _err(hl) == "GQA requires head_count divisible by head_count_kv"
+    assert pre(_model_desc(_fake_layers(w_up_type=12)), 4) == _lib.HL_EUNSUPPORTED
+    assert "fp32 weights" in _err(hl)
+    small = _lib.ForwardScratch(3, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 1 << 30)
+    assert hl.hl_forward_prefill(ctypes.byref(m), ctypes.byref(c), ctypes.byref(small), FAKE, 4, FAKE,
+                                 None) == _lib.HL_EINVAL
+    c.cur_len = 16
+    dec = hl.hl_forward_decode(ctypes.byref(m), ctypes.byref(c), ctypes.byref(s), FAKE, FAKE, FAKE, None)
+    assert dec == _lib.HL_ECAPACITY
+    assert _err(hl) == "KV cache full"
+    assert c.cur_len == 16  # a refused call changes nothing
 
 
 def test_fused_and_elementwise_validation(hl):

@@ -126,6 +126,23 @@ def test_forward_decode_token_matches_oracle(hl, orc, name, types, qk_norm):
         tok = nxt
 
 
+def test_forward_decode_token_rope_dim_zero(hl, orc):
+    """rope_dim 0 means the whole head, as the reference's ropeDim =
+    headDim when the model file has no rope dimension (naive.nim:3979)."""
+    from hippo_leap_amd.model import DenseDecoder
+    cfg = dict(CFG, rope_dim=0)
+    dev, ref = _build(orc, cfg, {}, False, 71)
+    m = DenseDecoder(torch, cfg, dev["tok_emb"], dev["output_norm"], dev["output"], 0, dev["layers"])
+    tok = 11
+    for pos in range(3):
+        m.tokens[0] = tok
+        m.step(pos)
+        torch.cuda.synchronize()
+        logits = m.logits.cpu().numpy()
+        assert rel_err(logits, _oracle_step(orc, dict(cfg, rope_dim=cfg["head_dim"]), ref, tok, pos)) < TOL_F32
+        tok = int(m.tokens[1].item())
+
+
 def test_generate_chains_on_device(hl, orc):
     """generate() chains the steps on the device (the next token of one step
     is the next step's input, no host read in between) and gives the tokens

@@ -489,3 +489,35 @@ def test_dequant_q5_k_packed(orc):
     q[1] = 16  # only the high bits set: a misplaced qh bit shows directly
     got = orc.dequant_rows(13, pack_q5_k(d, dmin, sc, mn, q), 1, 256 * nb).reshape(nb, 256)
     assert np.allclose(got, scaled_values(d, sc, q, 32, dmin, mn), rtol=1e-6, atol=1e-6)
+
+
+def test_add_is_ieee_fp32_addition(orc):
+    """tensor.nim add (:42-47): one fp32 addition per element, so the result
+    is numpy's float32 sum bit for bit (ties, signed zeros, infinities)."""
+    a = np.concatenate([orc.normal(1000, 51), np.float32([0.0, -0.0, np.inf, 1e38, 1.0])])
+    b = np.concatenate([orc.normal(1000, 52), np.float32([-0.0, -0.0, 1.0, 1e38, np.float32(2 ** -24)])])
+    got = orc.add(a, b)
+    assert np.array_equal(got.view(np.uint32), (a + b).view(np.uint32))
+
+
+def test_silu_mul_against_fp64_and_limits(orc):
+    """gpuSiluMul (naive.nim:2179-2187): x * sigmoid(x) * up.  Pinned by an
+    fp64 evaluation, and by its limits: silu(0) = 0; for x >= 20 the fp32
+    sigmoid is exactly 1 (the result is x * up, exactly); for x <= -104,
+    exp(-x) overflows to inf and the result is a signed zero."""
+    g = orc.normal(4000, 53) * np.float32(4)
+    u = orc.normal(4000, 54)
+    got = orc.silu_mul(g, u)
+    g64, u64 = g.astype(np.float64), u.astype(np.float64)
+    ref = g64 / (1 + np.exp(-g64)) * u64
+    assert np.max(np.abs(got - ref) / np.maximum(np.abs(ref), 1e-30)) < 1e-6
+    edge_g = np.float32([0.0, 20.0, 37.5, -104.0, -200.0])
+    edge_u = np.float32([3.0, 1.25, -2.0, 5.0, -5.0])
+    e = orc.silu_mul(edge_g, edge_u)
+    assert e[0] == 0.0
+    assert e[1] == np.float32(20.0) * np.float32(1.25) and e[2] == np.float32(37.5) * np.float32(-2.0)
+    assert e[3] == 0.0 and e[4] == 0.0
+    # the GPU form x * (1/(1+e)) * u and the CPU form x / (1+e) * u differ by
+    # at most a couple of ulps: both are the same function
+    cpu_form = (g / (np.float32(1) + np.exp(-g, dtype=np.float32)) * u).astype(np.float32)
+    assert np.max(np.abs(got - cpu_form) / np.maximum(np.abs(cpu_form), 1e-30)) < 1e-6
