@@ -84,6 +84,11 @@ def event_time_ms(torch, fn, iters):
 # summary with the commands is profiles/decode_step_c3_traffic.md); to be
 # re-measured whenever the decode kernel changes.
 C3_STEP_TRAFFIC_BYTES = 35_161_600
+# The same for the c5 step kernel (column-major bf16 caches) and for one c4
+# prefill (kv_prologue_kernel + prefill_mfma_kernel):
+# profiles/decode_step_c5_traffic.md, profiles/prefill_c4_mfma_util_and_traffic.md.
+C5_STEP_TRAFFIC_BYTES = 1_116_977_918
+C4_PREFILL_TRAFFIC_BYTES = 211_279_802
 
 
 def capture(torch, fn, n, first=0):
@@ -262,6 +267,37 @@ def cpu_baseline(budget_s=12.0):
                   f"upcast to fp32) through the scalar C oracle, {t_total:.1f} s on 1 thread",
         "ms_per_step": round(t_total * 1e3 / steps, 3),
         "host_nproc": os.cpu_count(),
+    }
+
+
+def cpu_baseline_prefill():
+    """The c4 prefill's attention on the scalar C oracle, one thread, on a
+    bounded sample: query head 0 (kv head 0) over all 4096 causal rows, the
+    same bf16-stored N(0,1) inputs upcast to fp32.  The full prefill is 32
+    such heads; the rate is the sample's causal FLOPs / its time (RoPE and
+    the cache write, a few percent of the work, are not timed)."""
+    import oracle
+    oracle.lib()
+    T, hq, hkv, d = 4096, 32, 8, 128
+    up = lambda n, seed: oracle.upcast(oracle.to_storage(oracle.normal(n, seed), oracle.BF16), oracle.BF16)
+    # head 0 reads rows 0 .. d-1 of q and kv head 0's rows of k, v: only
+    # those rows are generated (the other rows are never read)
+    q = np.zeros((hq * d, T), np.float32)
+    q[:d] = up(d * T, 41).reshape(d, T)
+    k = np.zeros((hkv * d, T), np.float32)
+    v = np.zeros((hkv * d, T), np.float32)
+    k[:d] = up(d * T, 42).reshape(d, T)
+    v[:d] = up(d * T, 43).reshape(d, T)
+    t0 = time.perf_counter()
+    oracle.attention_prefill(q, k, v, hq, hkv, d, T, heads=(0, 1))
+    dt = time.perf_counter() - t0
+    flops = 4 * d * T * (T + 1) // 2  # one head
+    return {
+        "value": round(flops / dt / 1e12, 6), "unit": "TFLOP/s", "cores": 1, "kind": "port",
+        "sample": f"c4 query head 0 of 32, all {T} causal rows (D=128, bf16-stored inputs as fp32) "
+                  f"through the scalar C oracle, {dt:.1f} s on 1 thread; the full c4 prefill is "
+                  f"32 such heads ({32 * dt:.0f} s at this rate)",
+        "full_prefill_s_estimate": round(32 * dt, 1),
     }
 
 
@@ -623,11 +659,22 @@ def main():
                         "RoPE 5e5, KV cache written",
             "dtype": "bf16 in, fp16 MFMA operands, fp32 accumulation and output",
             "value": round(tf, 2), "unit": "TFLOP/s", "ms_per_step": round(ms, 4),
-            "roofline": {"bound": "mfma", "kernel": "prologue_kernel + prefill_mfma_kernel",
+            "roofline": {"bound": "mfma", "kernel": "kv_prologue_kernel + prefill_mfma_kernel",
                          "achieved": round(tf, 2), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                         "frac": round(tf / BF16_PEAK_TFLOPS, 4), "traffic": None,
+                         "frac": round(tf / BF16_PEAK_TFLOPS, 4),
+                         "traffic": C4_PREFILL_TRAFFIC_BYTES,
+                         "traffic_source": "profiles/prefill_c4_mfma_util_and_traffic.md: "
+                                           "FETCH_SIZE x 1.99981 + WRITE_SIZE of both kernels",
+                         "mfma_util_at_actual_clock": 0.463,
+                         "mfma_util_source": "same profile: SQ_VALU_MFMA_BUSY_CYCLES / "
+                                             "(GRBM_GUI_ACTIVE per XCD x 1024 SIMDs)",
                          "algorithmic_flops": pw.flops},
         }
+        if not args.no_cpu:
+            log("cpu baseline (prefill sample) ...")
+            cb = cpu_baseline_prefill()
+            cb["gpu_over_cpu"] = round(tf / cb["value"], 1)
+            result["prefill"]["cpu_baseline"] = cb
         log(f"prefill c4: {ms:.3f} ms, {tf:.1f} TFLOP/s")
         del pw
         torch.cuda.empty_cache()
@@ -647,6 +694,9 @@ def main():
             kvname = "fp8 e4m3" if kvdt == torch.float8_e4m3fn else "bf16"
             result[key] = decode_extra(wl, t, f"c5: Qwen3-30B-A3B-shape decode, {kvname} KV, B=16, "
                                        "L=32769, Hq32/Hkv4, D128, qkNorm + RoPE 1e6")
+            if key == "decode_c5":
+                result[key]["roofline"]["traffic"] = C5_STEP_TRAFFIC_BYTES
+                result[key]["roofline"]["traffic_source"] = "profiles/decode_step_c5_traffic.md"
             log(f"{key}: step {t['step']*1e3:.1f} us, step kernel {t['kernel']*1e3:.1f} us "
                 f"({result[key]['roofline']['achieved']:.0f} GB/s), attention alone "
                 f"{t['attn']*1e3:.1f} us")
