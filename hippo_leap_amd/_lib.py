@@ -163,6 +163,7 @@ SIGNATURES = {
     "hl_forward_decode_token": (c_int, [ctypes.POINTER(ModelDesc), ctypes.POINTER(DecodeScratch),
                                         c_void_p, c_int, c_void_p, c_void_p, c_void_p]),
     "hl_kv_cache_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int]),
+    "hl_kv_cache_preferred_layout": (c_int, [c_int, c_int]),
     "hl_kv_cache_init": (c_int, [ctypes.POINTER(KvCacheDesc), ctypes.POINTER(ModelDesc)]),
     "hl_forward_workspace_bytes": (c_size_t, [ctypes.POINTER(ModelDesc), ctypes.POINTER(KvCacheDesc), c_int]),
     "hl_forward_prefill": (c_int, [ctypes.POINTER(ModelDesc), ctypes.POINTER(KvCacheDesc),

@@ -299,6 +299,12 @@ size_t hl_kv_cache_bytes(int n_head_kv, int head_dim, int max_len, int kv_dtype,
   return (size_t)n_head_kv * head_dim * max_len * elem_bytes(kv_dtype);
 }
 
+int hl_kv_cache_preferred_layout(int kv_dtype, int max_len) {
+  const bool tiles = (kv_dtype == HL_F16 || kv_dtype == HL_BF16 || kv_dtype == HL_FP8) && max_len > 0 &&
+                     max_len % 32 == 0;
+  return tiles ? HL_KV_TILED32 : HL_KV_COLMAJOR;
+}
+
 // The decode step's calls for layer l at position pos (q, k, v: the new
 // token's projections; out: the attention output).
 static void step_args(hl_rope_store_args& r, hl_decode_args& a, const hl_model_desc* m, const hl_kv_cache_desc* c,

@@ -81,10 +81,14 @@ class KvCache:
     described by an hl_kv_cache_desc checked against the model."""
 
     def __init__(self, torch, model: "DenseDecoder", kv_dtype: int = _lib.HL_F32,
-                 kv_layout: int = _lib.HL_KV_COLMAJOR, max_len: int | None = None, block_table=None):
+                 kv_layout: int | None = None, max_len: int | None = None, block_table=None):
+        """kv_layout None: the library's preferred layout for the dtype (tiled
+        for fp16/bf16/fp8 when max_len % 32 == 0, else column-major)."""
         c = model.cfg
         self.max_len = int(max_len or c["max_len"])
         lib = _lib.load()
+        if kv_layout is None:
+            kv_layout = int(lib.hl_kv_cache_preferred_layout(kv_dtype, self.max_len))
         nbytes = int(lib.hl_kv_cache_bytes(c["n_head_kv"], c["head_dim"], self.max_len, kv_dtype, kv_layout))
         if nbytes == 0:
             raise _lib.HLError(_lib.HL_EUNSUPPORTED, f"kv cache dtype {kv_dtype} / layout {kv_layout} not built")
@@ -114,7 +118,7 @@ class DenseModel(DenseDecoder):
 
     def __init__(self, torch, cfg: dict, tok_emb, output_norm, output, output_type: int,
                  layers: list[dict], cache: KvCache | None = None, max_tokens: int = 1,
-                 kv_dtype: int = _lib.HL_F32, kv_layout: int = _lib.HL_KV_COLMAJOR):
+                 kv_dtype: int = _lib.HL_F32, kv_layout: int | None = None):
         super().__init__(torch, cfg, tok_emb, output_norm, output, output_type, layers)
         self.cache = cache if cache is not None else KvCache(torch, self, kv_dtype, kv_layout)
         c, T = self.cfg, max(1, int(max_tokens))

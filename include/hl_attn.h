@@ -580,6 +580,13 @@ typedef struct hl_kv_cache_desc {
  * a combination the library does not build.                               */
 size_t hl_kv_cache_bytes(int n_head_kv, int head_dim, int max_len, int kv_dtype, int kv_layout);
 
+/* The layout initKvCache should allocate for this dtype: HL_KV_TILED32
+ * for fp16/bf16/fp8 caches whose max_len is a multiple of 32 (decode
+ * streams each 32-column tile as one contiguous run: the c5 step at 67-70%
+ * of HBM against 63% column-major), HL_KV_COLMAJOR otherwise (fp32, the
+ * reference's own cache, or an odd max_len).                              */
+int hl_kv_cache_preferred_layout(int kv_dtype, int max_len);
+
 /* initKvCache (naive.nim:3912-3931) for a cache descriptor the caller has
  * filled: checks it against the model (layer count, kv heads, head dim,
  * dtype/layout/alignment rules of the decode and prefill entry points, a

@@ -365,6 +365,11 @@ def test_kv_cache_descriptor(hl):
     assert hl.hl_kv_cache_bytes(8, 128, 4096, _lib.HL_FP8, 0) == 0  # fp8 needs tiles
     assert hl.hl_kv_cache_bytes(8, 128, 4008, _lib.HL_F16, 1) == 0  # tiles of 32 columns
     assert hl.hl_kv_cache_bytes(8, 128, 4096, _lib.HL_F32, 1) == 0
+    T, C = _lib.HL_KV_TILED32, _lib.HL_KV_COLMAJOR
+    assert hl.hl_kv_cache_preferred_layout(_lib.HL_BF16, 32768) == T
+    assert hl.hl_kv_cache_preferred_layout(_lib.HL_FP8, 4096) == T
+    assert hl.hl_kv_cache_preferred_layout(_lib.HL_F16, 4100) == C
+    assert hl.hl_kv_cache_preferred_layout(_lib.HL_F32, 4096) == C
     m = _model_desc(_fake_layers())
     c = _kv_desc()
     assert hl.hl_kv_cache_init(ctypes.byref(c), ctypes.byref(m)) == _lib.HL_OK
