@@ -12,6 +12,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <atomic>
 #include <mutex>
 #include <vector>
 
@@ -706,7 +707,7 @@ struct PrefillPlan {
   bool mfma;
   bool q_in_kernel;  // MFMA kernel builds Q from the raw activations (no qt)
   int t_pad;
-  size_t off_q, off_k, off_v, off_tab, bytes;
+  size_t off_q, off_k, off_v, off_tab, off_range, bytes;
 };
 
 static int validate_prefill(const hl_prefill_args* a, PrefillPlan* pl) {
@@ -755,6 +756,8 @@ static int validate_prefill(const hl_prefill_args* a, PrefillPlan* pl) {
     pl->off_tab = pl->off_v + (size_t)a->n_head_kv * tp * D * 2;
     pl->bytes = pl->off_tab;
     if (a->apply_rope) pl->bytes += (size_t)T * (rd / 2) * 8;  // (cos, sin) table [rope_dim/2][T]
+    pl->off_range = (pl->bytes + 15) / 16 * 16;  // range record: (call id, id of a call out of range)
+    pl->bytes = pl->off_range + 16;
   } else {
     pl->t_pad = a->seq_len;
     const bool pre = a->apply_rope || a->q_norm_w || a->k_norm_w;
@@ -762,6 +765,7 @@ static int validate_prefill(const hl_prefill_args* a, PrefillPlan* pl) {
     pl->off_k = (pre && !a->write_back_qk) ? (size_t)a->n_head * T * D * 4 : 0;
     pl->off_v = 0;
     pl->off_tab = 0;
+    pl->off_range = 0;
     pl->bytes = (pre && !a->write_back_qk) ? pl->off_k + (size_t)a->n_head_kv * T * D * 4 : 0;
   }
   return HL_OK;
@@ -851,6 +855,13 @@ int hl_attn_prefill(const hl_prefill_args* a, void* workspace, size_t ws_bytes, 
       op.hv_first = a->n_head;
     }
     if (a->apply_rope) op.rope_tab_out = (float2*)(ws + pl.off_tab);  // written by the prologue
+    // Call id of the range record: nonzero, different from the previous
+    // call's on any workspace (a process-wide counter).
+    static std::atomic<unsigned> next_id{0};
+    unsigned id = ++next_id;
+    if (id == 0) id = ++next_id;
+    op.range_word = (unsigned*)(ws + pl.off_range);
+    op.range_gen = id;
     if ((e = prologue_launch(op, st)) != hipSuccess) return hip_fail(e, "prefill prologue launch");
     pf.qt = op.qt;
     pf.kt = op.kt;
@@ -864,6 +875,8 @@ int hl_attn_prefill(const hl_prefill_args* a, void* workspace, size_t ws_bytes, 
     pf.rope_dim = rope_dim;
     pf.rope_style = a->rope_style;
     pf.rope_tab = op.rope_tab_out;
+    pf.range_flag = op.range_word + 1;
+    pf.range_gen = id;
     e = prefill_mfma_launch(pf, st);
     return e == hipSuccess ? HL_OK : hip_fail(e, "prefill launch");
   }
@@ -892,6 +905,27 @@ int hl_attn_prefill(const hl_prefill_args* a, void* workspace, size_t ws_bytes, 
   pf.scale_log2 = scale * kLog2e;
   e = prefill_f32_launch(pf, st);
   return e == hipSuccess ? HL_OK : hip_fail(e, "prefill launch");
+}
+
+int hl_attn_prefill_range_check(const hl_prefill_args* a, const void* workspace, void* stream) {
+  PrefillPlan pl;
+  int rc = validate_prefill(a, &pl);
+  if (rc) return rc;
+  if (!pl.mfma) return HL_OK;
+  if (!workspace) return fail(HL_EINVAL, "prefill range check: workspace is null");
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  hipError_t e = hipStreamIsCapturing(as_stream(stream), &cs);
+  if (e != hipSuccess) return hip_fail(e, "hipStreamIsCapturing");
+  if (cs != hipStreamCaptureStatusNone)
+    return fail(HL_ECAPTURE, "prefill range check waits for the stream; it cannot run under stream capture");
+  if ((e = hipStreamSynchronize(as_stream(stream))) != hipSuccess) return hip_fail(e, "prefill range check sync");
+  unsigned w[2] = {0u, 0u};
+  if ((e = hipMemcpy(w, (const char*)workspace + pl.off_range, sizeof(w), hipMemcpyDeviceToHost)) != hipSuccess)
+    return hip_fail(e, "prefill range check read");
+  if (w[0] != 0u && w[1] == w[0])
+    return fail(HL_ERANGE, "prefill: an activation (q*scale, k or v after qkNorm/RoPE) reached 65520, beyond the "
+                           "fp16 operands of the bf16/fp16 path; use fp32 activations for this input");
+  return HL_OK;
 }
 
 int hl_gpu_attention_prefill(float* dst, const float* q, const float* k, const float* v, int n_head,

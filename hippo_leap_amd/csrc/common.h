@@ -34,6 +34,9 @@ __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
   x += 0x7FFFu + ((x >> 16) & 1u);
   return (uint16_t)(x >> 16);
 }
+// Smallest magnitude that rounds (RNE) to an fp16 infinity.
+constexpr float kF16Inf = 65520.0f;
+
 __device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
   _Float16 h = (_Float16)f;  // v_cvt_f16_f32 under the default RNE mode
   return __builtin_bit_cast(uint16_t, h);

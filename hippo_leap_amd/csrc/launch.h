@@ -95,6 +95,11 @@ struct PrologueOp {
   ThetaTable theta;
   float2* rope_tab_out;  // optional: receives the (cos, sin) table [rope_dim/2][seq_len] of
                          // positions start_pos + t (rope_dim/2 <= 64)
+  // Range record of the fp16 operands (qt / kt / vt): workgroup (0, 0)
+  // stores range_gen to range_word[0]; a thread whose operand value has
+  // magnitude >= kF16Inf stores it to range_word[1].  Null: not recorded.
+  unsigned* range_word;
+  unsigned range_gen;
 };
 hipError_t prologue_launch(const PrologueOp& op, hipStream_t stream);
 
@@ -129,6 +134,10 @@ struct PrefillLaunch {
   float eps;
   int do_rope, rope_dim, rope_style;
   const float2* rope_tab;  // [rope_dim/2][seq_len]
+  // Q built in the kernel: a lane whose Q operand value (q * scale, after
+  // qkNorm / RoPE) has magnitude >= kF16Inf stores range_gen to *range_flag.
+  unsigned* range_flag;
+  unsigned range_gen;
 };
 hipError_t prefill_f32_launch(const PrefillLaunch& p, hipStream_t stream);
 hipError_t prefill_mfma_launch(const PrefillLaunch& p, hipStream_t stream);

@@ -53,6 +53,8 @@ struct MfmaPrefillParams {
   float eps, qscale;  // qscale = scale * log2 e
   int do_rope, rope_dim, rope_style;
   const float2* rope_tab;  // [rope_dim/2][T] (cos, sin)
+  unsigned* range_flag;    // see PrefillLaunch
+  unsigned range_gen;
 };
 
 __device__ __forceinline__ f32x16 mma32(f16x8 a, f16x8 b, f32x16 c) {
@@ -167,10 +169,16 @@ __device__ __forceinline__ void build_q(const MfmaPrefillParams& p, int hq, int 
         }
     }
   }
+  float qmax = 0.f;  // a Q operand value beyond fp16's range goes to the range record
 #pragma unroll
   for (int k = 0; k < KSTEPS; ++k)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) qf[k][e] = (_Float16)(tv ? x[k][e] * p.qscale : 0.f);
+    for (int e = 0; e < 8; ++e) {
+      const float y = tv ? x[k][e] * p.qscale : 0.f;
+      qmax = fmaxf(qmax, fabsf(y));
+      qf[k][e] = (_Float16)y;
+    }
+  if (qmax >= kF16Inf && p.range_flag) *p.range_flag = p.range_gen;
 }
 
 // Ping-pong flash kernel.  A workgroup has 8 waves, two per SIMD (waves w
@@ -505,6 +513,8 @@ hipError_t prefill_mfma_launch(const PrefillLaunch& a, hipStream_t stream) {
   p.rope_dim = a.rope_dim;
   p.rope_style = a.rope_style;
   p.rope_tab = a.rope_tab;
+  p.range_flag = a.range_flag;
+  p.range_gen = a.range_gen;
   const int qin = a.qt ? 0 : a.io_dtype;
   dim3 grid(a.n_head_kv * p.n_hgrp * p.n_qblk);
 #define HL_PF(DD, OD, QI) hipLaunchKernelGGL((prefill_mfma_kernel<DD, OD, QI>), grid, dim3(512), 0, stream, p)

@@ -201,6 +201,7 @@ __device__ __forceinline__ void store_cache8(void* cache, const CacheMap& m, int
 template <int IODT, int KDT, int DMAX>
 __global__ __launch_bounds__(256) void prologue_kernel(PrologueOp op) {
   __shared__ float sx[DMAX][kPT + 1];  // DMAX >= head_dim: the tile, sized to its class
+  if (op.range_word && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) op.range_word[0] = op.range_gen;
   __shared__ float scos[kTabHalf][kPT], ssin[kTabHalf][kPT];
   __shared__ float sred[8][kPT];
   __shared__ float sinv[kPT];
@@ -345,7 +346,9 @@ __global__ __launch_bounds__(256) void prologue_kernel(PrologueOp op) {
       }
     }
 
-    // MFMA operand layouts (fp16 bits); pad rows t >= T are written as zeros
+    // MFMA operand layouts (fp16 bits); pad rows t >= T are written as zeros.
+    // A value beyond fp16's range goes to the range record.
+    float omax = 0.f;
     if (kind < 2) {
       uint16_t* dst = kind == 0 ? op.qt : op.kt;
       if (dst) {
@@ -357,8 +360,11 @@ __global__ __launch_bounds__(256) void prologue_kernel(PrologueOp op) {
           if (tg >= op.t_pad) continue;
           u16x8 w;
 #pragma unroll
-          for (int e = 0; e < 8; ++e)
-            w[e] = tg < T ? f32_to_f16_bits(sx[8 * ch + e][tt] * mul) : (uint16_t)0;
+          for (int e = 0; e < 8; ++e) {
+            const float x = tg < T ? sx[8 * ch + e][tt] * mul : 0.f;
+            omax = fmaxf(omax, fabsf(x));
+            w[e] = f32_to_f16_bits(x);
+          }
           *(u16x8*)(dst + ((long long)h * op.t_pad + tg) * D + 8 * ch) = w;
         }
       }
@@ -367,10 +373,14 @@ __global__ __launch_bounds__(256) void prologue_kernel(PrologueOp op) {
         if (t0 + c8 >= op.t_pad) continue;
         float x[8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) x[e] = (t0 + c8 + e < T) ? sx[r][c8 + e] : 0.f;
+        for (int e = 0; e < 8; ++e) {
+          x[e] = (t0 + c8 + e < T) ? sx[r][c8 + e] : 0.f;
+          omax = fmaxf(omax, fabsf(x[e]));
+        }
         store_row8<HL_F16>(op.vt, ((long long)h * D + r) * op.t_pad + t0 + c8, t0 + c8, op.t_pad, x);
       }
     }
+    if (omax >= kF16Inf && op.range_word) op.range_word[1] = op.range_gen;
   }
 }
 
@@ -410,6 +420,7 @@ __global__ __launch_bounds__(256) void kv_prologue_kernel(PrologueOp op) {
   const int r = tid / CPR, c8 = (tid % CPR) * 8;
   const int t = t0 + c8;  // this thread's first token
   const long long hbase = (long long)h * D * T;
+  if (op.range_word && blockIdx.x == 0 && h == 0 && tid == 0) op.range_word[0] = op.range_gen;
 
   float k[NP][8], v[NP][8];
 #pragma unroll
@@ -418,7 +429,9 @@ __global__ __launch_bounds__(256) void kv_prologue_kernel(PrologueOp op) {
     load_row8_f32<IODT>(op.v, hbase + (long long)(r + RS * ps) * T + t, t, T, v[ps]);
   }
 
-  // V: cache column block and vt, straight from registers.
+  // V: cache column block and vt, straight from registers.  omax: the
+  // largest operand magnitude this thread converts (range record).
+  float omax = 0.f;
 #pragma unroll
   for (int ps = 0; ps < NP; ++ps) {
     const int row = r + RS * ps;
@@ -428,7 +441,10 @@ __global__ __launch_bounds__(256) void kv_prologue_kernel(PrologueOp op) {
     if (t < op.t_pad) {
       float x[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) x[e] = t + e < T ? v[ps][e] : 0.f;
+      for (int e = 0; e < 8; ++e) {
+        x[e] = t + e < T ? v[ps][e] : 0.f;
+        omax = fmaxf(omax, fabsf(x[e]));
+      }
       store_row8<HL_F16>(op.vt, ((long long)h * D + row) * op.t_pad + t, t, op.t_pad, x);
     }
   }
@@ -510,8 +526,13 @@ __global__ __launch_bounds__(256) void kv_prologue_kernel(PrologueOp op) {
       store_cache8<KDT>(op.k_cache, CacheMap{op.kv_layout, D, op.max_len, op.n_head_kv, op.block_table}, h, row,
                         op.start_pos + t, t, T, k[ps]);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) skt[c8 + e][row ^ kt_swz(c8 + e)] = t + e < T ? f32_to_f16_bits(k[ps][e]) : (uint16_t)0;
+    for (int e = 0; e < 8; ++e) {
+      const float x = t + e < T ? k[ps][e] : 0.f;
+      omax = fmaxf(omax, fabsf(x));
+      skt[c8 + e][row ^ kt_swz(c8 + e)] = f32_to_f16_bits(x);
+    }
   }
+  if (omax >= kF16Inf && op.range_word) op.range_word[1] = op.range_gen;
   __syncthreads();
   constexpr int CH = D / 8;  // 16-byte chunks per token row
   for (int idx = tid; idx < PT * CH; idx += 256) {

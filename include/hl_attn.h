@@ -47,7 +47,9 @@ enum {
   HL_ECAPACITY = -2,     /* KV cache full, prefill longer than max_len      */
   HL_EUNSUPPORTED = -3,  /* dtype / head_dim combination not built          */
   HL_EHIP = -4,          /* HIP runtime error (launch, device query)         */
-  HL_ECAPTURE = -5       /* would allocate while the stream is being captured */
+  HL_ECAPTURE = -5,      /* would allocate while the stream is being captured */
+  HL_ERANGE = -6         /* a bf16/fp16 prefill met an activation beyond the
+                            fp16 operand range (hl_attn_prefill_range_check) */
 };
 
 /* ---- element types of activations and KV cache ------------------------- */
@@ -442,6 +444,20 @@ size_t hl_attn_prefill_workspace_bytes(const hl_prefill_args* a);
  * (naive.nim:3975-3976).                                                  */
 int hl_attn_prefill(const hl_prefill_args* a, void* workspace, size_t ws_bytes,
                     void* stream);
+
+/* The MFMA prefill (bf16/fp16 activations) rounds Q * scale, K and V, after
+ * qkNorm and RoPE, to fp16 operands: a value of magnitude >= 65520 has no
+ * fp16 form, and the output of such a call is not valid (inf/NaN where the
+ * value is used).  The kernels record such a value, at no cost to the
+ * computation, in the call's workspace; this function waits for `stream`
+ * (the one the prefill ran on), reads the record of the last
+ * hl_attn_prefill on `workspace` with these args and returns HL_ERANGE if
+ * it met such a value, HL_OK if not (always for fp32 activations, whose
+ * path has no such limit; the reference computes in fp32,
+ * naive.nim:3385-3464).  Under stream capture it returns HL_ECAPTURE.
+ * No counterpart in the reference; callers with bf16 activations that may
+ * exceed fp16's range check each call, or use fp32 activations.           */
+int hl_attn_prefill_range_check(const hl_prefill_args* a, const void* workspace, void* stream);
 
 /* Reads cache columns [col0, col0+ncols) of a [rows, max_len] cache of
  * kv_dtype into fp32 dst[rows, ncols] (exact upcast; halfToFloat semantics,
