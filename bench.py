@@ -569,6 +569,27 @@ def main():
         # Cache-resident ("warm") figure, labelled as such: one cache set
         # (33.6 MB) replayed, so its K/V stay in the 256 MB MALL.
         warm_ms = graph_time_ms(torch, lambda i: wl.step(0))
+        # The floor of any one kernel that reads 33.6 MB: a plain streaming
+        # read of the same byte count (16 rotating buffers, past the MALL),
+        # at a few grid sizes; the best is the floor the step is compared to.
+        bufs = [torch.empty(wl.kv_bytes, dtype=torch.uint8, device="cuda") for _ in range(16)]
+        for b_ in bufs:
+            b_.fill_(1)
+        sink = torch.zeros(4, dtype=torch.int32, device="cuda")
+        floor = {}
+        for nblk in (512, 1024, 2048, 4096):
+            floor[nblk] = graph_time_ms(torch, lambda i, nb=nblk: A.probe_stream_read(bufs[i % 16], sink, nb))
+        best = min(floor.values())
+        result["stream_floor_c3"] = {
+            "bytes": wl.kv_bytes, "us": round(best * 1e3, 3),
+            "GBs": round(wl.kv_bytes / (best * 1e-3) / 1e9, 1),
+            "frac_hbm": round(wl.kv_bytes / (best * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "us_by_workgroups": {str(k): round(v * 1e3, 3) for k, v in floor.items()},
+            "step_kernel_over_floor": round(t["kernel"] / best, 3),
+            "note": "hl_probe_stream_read: one launch that only streams the c3 byte count"}
+        log(f"stream floor c3: {best*1e3:.2f} us ({wl.kv_bytes / (best * 1e-3) / 1e9:.0f} GB/s); "
+            f"by workgroups {', '.join(f'{k}: {v*1e3:.2f}' for k, v in floor.items())}")
+        del bufs
         result["warm_cache_resident"] = {
             "value": round(wl.kv_bytes / (warm_ms * 1e-3) / 1e9, 2), "unit": "GB/s",
             "ms_per_step": round(warm_ms, 5),

@@ -181,6 +181,7 @@ SIGNATURES = {
     "hl_attn_prefill_workspace_bytes": (c_size_t, [ctypes.POINTER(PrefillArgs)]),
     "hl_attn_prefill": (c_int, [ctypes.POINTER(PrefillArgs), c_void_p, c_size_t, c_void_p]),
     "hl_attn_prefill_range_check": (c_int, [ctypes.POINTER(PrefillArgs), c_void_p, c_void_p]),
+    "hl_probe_stream_read": (c_int, [c_void_p, c_size_t, c_int, c_void_p, c_void_p]),
     "hl_kv_cache_to_f32": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p]),
 }
 

@@ -385,6 +385,12 @@ def prefill_range_check(args: PrefillArgs, workspace=None, stream=None) -> int:
     return rc
 
 
+def probe_stream_read(buf: torch.Tensor, sink: torch.Tensor, blocks: int = 0, stream=None) -> None:
+    """One launch that only streams `buf` (measurement probe)."""
+    nbytes = buf.numel() * buf.element_size()
+    check(_lib.load().hl_probe_stream_read(buf.data_ptr(), nbytes, blocks, sink.data_ptr(), _stream(stream)))
+
+
 def workspace(nbytes: int, device="cuda") -> torch.Tensor | None:
     """Allocates a caller-owned workspace (GpuContext.attnScratch's role)."""
     if nbytes <= 0:

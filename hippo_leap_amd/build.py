@@ -18,7 +18,7 @@ CSRC = os.path.join(PKG_DIR, "csrc")
 INCLUDE = os.path.join(ROOT, "include")
 LIB_NAME = "libhl_attn.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
-SOURCES = ["api.hip", "decode.hip", "linear.hip", "linear_quant.hip", "model.hip", "norm.hip", "prefill.hip", "rope_store.hip", "tokens.hip"]
+SOURCES = ["api.hip", "decode.hip", "linear.hip", "linear_quant.hip", "model.hip", "norm.hip", "prefill.hip", "probe.hip", "rope_store.hip", "tokens.hip"]
 ARCH = "gfx950"
 
 

@@ -96,6 +96,14 @@ typedef struct hl_device_info {
  * reference (which has no roofline reporting); used by the benchmark.     */
 int hl_device_info_get(hl_device_info* info);
 
+/* Measurement probe, no counterpart in the reference: one launch of
+ * `blocks` workgroups (0 -> 1024) that streams `bytes` (a multiple of 16,
+ * 16-byte aligned) from device memory with 16-byte loads and computes
+ * nothing else (`sink`: a device word it practically never writes).  It is
+ * the floor a kernel reading that many bytes once reaches on this part,
+ * timed beside the decode kernels at their byte counts.                    */
+int hl_probe_stream_read(const void* buf, size_t bytes, int blocks, unsigned* sink, void* stream);
+
 /* Host-side RoPE theta table: theta[i] = powf(1/base, 2i/rope_dim) for
  * i < rope_dim/2, computed in fp32 exactly as naive.nim:3850-3861.       */
 int hl_rope_theta_table(float* theta_out, int rope_dim, float rope_base);
