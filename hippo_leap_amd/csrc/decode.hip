@@ -935,6 +935,24 @@ hipError_t zero_fill_launch(void* ws, size_t bytes, hipStream_t stream) {
 // ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
+// CUs of the current device (cached per device).
+int cu_count() {
+  static std::mutex mu;
+  static std::map<int, int> cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 256;
+  std::lock_guard<std::mutex> lk(mu);
+  auto it = cache.find(dev);
+  if (it != cache.end()) return it->second;
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) {
+    (void)hipGetLastError();
+    return 256;
+  }
+  cache[dev] = cus;
+  return cus;
+}
+
 namespace {
 
 typedef void (*KernelFn)(DecodeParams);
@@ -994,23 +1012,6 @@ int capacity(KernelFn fn) {
   }
   cache[key] = per_cu * cus;
   return per_cu * cus;
-}
-
-int cu_count() {
-  static std::mutex mu;
-  static std::map<int, int> cache;
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return 256;
-  std::lock_guard<std::mutex> lk(mu);
-  auto it = cache.find(dev);
-  if (it != cache.end()) return it->second;
-  int cus = 0;
-  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) {
-    (void)hipGetLastError();
-    return 256;
-  }
-  cache[dev] = cus;
-  return cus;
 }
 
 bool vec_path(const hl_decode_args* a) {

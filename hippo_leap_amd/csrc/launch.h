@@ -157,6 +157,7 @@ hipError_t linear_col_launch(float* y, const float* x, const float* w, int K, in
                              hipStream_t stream);
 
 // ---- quantized decode GEMV (linear_quant.hip) ------------------------------
+int cu_count();                          // CUs of the current device (cached)
 int quant_block_elems(int qtype);        // 0: type not built
 
 // ---- argument validation of the C-ABI entry points (api.hip) --------------

@@ -15,6 +15,8 @@
 // per-block scale and min factor out of the inner sums.  Rows whose byte
 // size is not a multiple of 4 (Q8_0 with K % 64, Q6_K with K % 512) load
 // bytes instead of dwords.
+#include <algorithm>
+
 #include "common.h"
 #include "launch.h"
 
@@ -803,6 +805,306 @@ __global__ __launch_bounds__(256) void quant_direct_kernel(const uint8_t* __rest
   }
 }
 
+// ---------------------------------------------------------------------------
+// Q4_K on MFMA (v_mfma_f32_16x16x32_f16): the products go to the matrix core,
+// the VALU only unpacks nibbles.
+//
+// A step of a wave is 2 weight rows x 8 consecutive blocks (4096 weights):
+// each load instruction reads 1152 contiguous bytes of each of the two rows.
+// (The same bytes read as one block of each of 16 rows stream at ~3 TB/s.)
+// The 16 MFMA columns n = 8 r + b are block b of row r; the 16 MFMA rows
+// i = 2 b + c are part c of block b's x:
+//   B[k][n] = quant at k of column n's block times its sub-block scale, as an
+//             f16 bit pattern: q sc 2^-24 (<= 945 2^-24, exact; the low nibble
+//             is one AND, the high nibble (16 q) is scaled by sc / 16),
+//   A[i][k] = x of block b at k as x 2^s = h + m 2^-11 (two f16, 22
+//             significant bits; s per block puts its largest |x| in
+//             [2^13, 2^14)),
+// so C[2b][n] + 2^-11 C[2b + 1][n] with b = n % 8 is the sum of sc q x over
+// column n's block (exact products, fp32 accumulation); the rest of C is not
+// used.  Lane 16 t + n holds quants group t of column n's block (sub-blocks
+// 2t and 2t + 1: bytes 32 t..32 t + 31; MFMA j < 4 takes the low nibbles of
+// bytes 8 j..8 j + 7, in k order 0,2,1,3,4,6,5,7, MFMA 4 + j the high ones),
+// and C[2b..2b+1][n] lands in lane 16 (b / 2) + n, registers 2 (b % 2) and
+// 2 (b % 2) + 1: that lane adds d 2^(24 - s) (C[2b] + 2^-11 C[2b+1]), and every
+// lane subtracts dmin (mn0 X0 + mn1 X1) for its two sub-blocks (X: sums of
+// x; getScaleMinK4 and dequantRowQ4K, quant.nim:235-277).
+//
+// Workgroups are persistent (about two per CU): x is converted once per
+// workgroup into LDS in the A register layout (a wave keeps the 32 VGPRs of
+// its 8-block group for all its steps).  The groups of a row go to different
+// waves, the row pairs of the workgroup to the rest; partial sums meet in LDS.
+// ---------------------------------------------------------------------------
+constexpr int kQ4gA = 8 * 64 * 16;  // A of one 8-block group: [mfma 8][lane 64] x 16 B
+constexpr int kQ4gX = 8 * 8 * 4;    // sub-block sums of x: [block 8][sub-block 8] floats
+constexpr int kQ4gF = 8 * 4;        // 2^(24 - s) per block
+constexpr int kQ4gBytes = kQ4gA + kQ4gX + kQ4gF;
+constexpr int kQ4MaxGroups = 16;    // K <= 32768 (a workgroup of at most 16 waves)
+
+typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+// Buffer descriptor over [base, base + bytes) (raw bytes, dword loads; an
+// access past `bytes` reads zeros), in SGPRs.
+__device__ __forceinline__ v4i buf_desc(const void* base, uint32_t bytes) {
+  const uintptr_t b = (uintptr_t)base;
+  return v4i{__builtin_amdgcn_readfirstlane((int)(uint32_t)b),
+             __builtin_amdgcn_readfirstlane((int)((b >> 32) & 0xFFFFu)),
+             __builtin_amdgcn_readfirstlane((int)bytes), 0x00020000};
+}
+
+// Lane l reads lane dpp(l) of v (within rows of 16 lanes).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppHalfMirror = 0x141, kDppMirror = 0x140;
+
+// Sum over the wave's 8-lane groups {16 t + 8 h + e : e < 8, t < 4} for each
+// h: DPP within rows of 16 lanes, then the four rows.
+__device__ __forceinline__ float half_row_sum(float v) {
+  v += dpp_f32<kDppXor1>(v);
+  v += dpp_f32<kDppXor2>(v);
+  v += dpp_f32<kDppHalfMirror>(v);
+  v += __shfl_xor(v, 16, 64);
+  v += __shfl_xor(v, 32, 64);
+  return v;
+}
+
+template <int PAIR>
+__global__ __launch_bounds__(1024) void q4k_mfma_kernel(const uint8_t* __restrict__ w,
+                                                        const float* __restrict__ x,
+                                                        float* __restrict__ y, int M, int K,
+                                                        const uint8_t* __restrict__ w2,
+                                                        float* __restrict__ y2, int rows_wg) {
+  extern __shared__ __align__(16) char lds[];
+  constexpr int NP = PAIR ? 2 : 1;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nw = blockDim.x >> 6;
+  const int nb = K / 256, ng = (nb + 7) / 8;
+  float* part = (float*)(lds + ng * kQ4gBytes);  // [NP][ng][rows_wg]
+
+  const int nstream = nw / ng;  // waves per group; the rest only meet the barriers
+  const int g = wave % ng, st = wave / ng;
+  const int n = lane & 15, t = lane >> 4, b8 = n & 7, rr = n >> 3;
+  const int row0 = blockIdx.x * rows_wg;
+  const int nrows = min(rows_wg, M - row0), npairs = (nrows + 1) / 2;
+  const uint32_t rowbytes = (uint32_t)nb * 144u;
+  const uint32_t oob = (uint32_t)nrows * rowbytes;  // past the workgroup's rows
+  // Lane part of the weight offsets (a block past nb: beyond the range) and
+  // the step's row pair as a uniform offset (a step past the last: beyond
+  // the range; such loads return zeros without touching memory and a zero
+  // step adds nothing).
+  const uint32_t vb = 8 * g + b8 < nb ? (uint32_t)rr * rowbytes + (uint32_t)(8 * g + b8) * 144u : oob;
+  const uint32_t vq = vb + 16 + 32 * t;
+  v4i desc[NP];
+#pragma unroll
+  for (int pm = 0; pm < NP; ++pm) desc[pm] = buf_desc((pm ? w2 : w) + (size_t)row0 * rowbytes, oob);
+  struct Raw {
+    u32x4 hdr, q0, q1;
+  };
+  // Step k: row pair st + (k / NP) nstream of matrix k % NP.  The weight
+  // loads are issued and waited for by hand (buffer_load_dwordx4; vmcnt
+  // with the loaded registers tied to the wait): the compiler otherwise
+  // moves the next step's loads below this step's math.  Outside the x
+  // prologue no other vector memory load is in flight.
+  const int nsteps = __builtin_amdgcn_readfirstlane(
+      st < nstream && st < npairs ? ((npairs - st + nstream - 1) / nstream) * NP : 0);
+  auto load = [&](int k, Raw& r) {
+    const int pm = PAIR ? (k & 1) : 0, q = st + (PAIR ? k >> 1 : k) * nstream;
+    const uint32_t so = __builtin_amdgcn_readfirstlane(k < nsteps ? (uint32_t)(2 * q) * rowbytes : oob);
+    v4i dk = desc[0];
+    if (PAIR) {  // a uniform select, kept in SGPRs
+#pragma unroll
+      for (int e = 0; e < 4; ++e) dk[e] = __builtin_amdgcn_readfirstlane(pm ? desc[NP - 1][e] : desc[0][e]);
+    }
+    asm volatile(
+        "buffer_load_dwordx4 %0, %3, %5, %6 offen\n\t"
+        "buffer_load_dwordx4 %1, %4, %5, %6 offen\n\t"
+        "buffer_load_dwordx4 %2, %4, %5, %6 offen offset:16"
+        : "=&v"(r.hdr), "=&v"(r.q0), "=&v"(r.q1)
+        : "v"(vb), "v"(vq), "s"(dk), "s"(so));
+  };
+  // Waits until at most `pending` weight loads (of later steps) are in flight.
+  auto wait = [&](Raw& r, auto pending) {
+    asm volatile("s_waitcnt vmcnt(%3)" : "+v"(r.hdr), "+v"(r.q0), "+v"(r.q1)
+                 : "n"(decltype(pending)::value));
+  };
+
+  // x -> LDS.  Chunk c = x[8c, 8c + 8) is one A register of block bk = c / 32
+  // (group bk / 8, block bk % 8 in it), quants group t, MFMA 4 h + j
+  // (8 c mod 256 = 64 t + 32 h + 8 j); a block's 32 chunks are 32 consecutive
+  // threads.  Blocks past nb are written as zeros (their quants load as
+  // zeros too).
+  const v4i xdesc = buf_desc(x, (uint32_t)K * 4u);
+  auto x_chunk = [&](int c, f32x4& v0, f32x4& v1) {
+    asm volatile(
+        "buffer_load_dwordx4 %0, %2, %3, 0 offen\n\t"
+        "buffer_load_dwordx4 %1, %2, %3, 0 offen offset:16"
+        : "=&v"(v0), "=&v"(v1)
+        : "v"(32 * c), "s"(xdesc));
+  };
+  auto convert = [&](int c, const f32x4& v0, const f32x4& v1) {
+    const int bk = c >> 5, cb = c & 31;
+    float am = fmaxf(fmaxf(fmaxf(fabsf(v0.x), fabsf(v0.y)), fmaxf(fabsf(v0.z), fabsf(v0.w))),
+                     fmaxf(fmaxf(fabsf(v1.x), fabsf(v1.y)), fmaxf(fabsf(v1.z), fabsf(v1.w))));
+    am = fmaxf(am, dpp_f32<kDppXor1>(am));
+    am = fmaxf(am, dpp_f32<kDppXor2>(am));
+    am = fmaxf(am, dpp_f32<kDppHalfMirror>(am));
+    am = fmaxf(am, dpp_f32<kDppMirror>(am));     // 16 chunks
+    am = fmaxf(am, __shfl_xor(am, 16, 64));       // the block's 32
+    float sum = (hsum4(v0) + hsum4(v1));
+    sum += dpp_f32<kDppXor1>(sum);
+    sum += dpp_f32<kDppXor2>(sum);                // the sub-block's 4 chunks
+    // am = f 2^e, f in [0.5, 1): am 2^(14 - e) in [2^13, 2^14).  (am = 0, inf,
+    // nan: e = 0.)
+    const int s = min(max(14 - __builtin_amdgcn_frexp_expf(am), -100), 140);
+    const float xs[8] = {ldexpf(v0.x, s), ldexpf(v0.z, s), ldexpf(v0.y, s), ldexpf(v0.w, s),
+                         ldexpf(v1.x, s), ldexpf(v1.z, s), ldexpf(v1.y, s), ldexpf(v1.w, s)};
+    f16x8 hv, mv;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      hv[e] = (_Float16)xs[e];
+      mv[e] = (_Float16)((xs[e] - (float)hv[e]) * 2048.f);
+    }
+    if (c >= ng * 256) return;  // threads past the last chunk
+    const int bb = bk & 7, ct = cb >> 3, mf = cb & 7;  // mf = 4 h + j
+    char* gb = lds + (bk >> 3) * kQ4gBytes;
+    *(f16x8*)(gb + (mf * 64 + 16 * ct + 2 * bb) * 16) = hv;
+    *(f16x8*)(gb + (mf * 64 + 16 * ct + 2 * bb + 1) * 16) = mv;
+    if ((cb & 3) == 0) ((float*)(gb + kQ4gA))[bb * 8 + (cb >> 2)] = sum;  // sub-block 2t + h
+    if (cb == 0) ((float*)(gb + kQ4gA + kQ4gX))[bb] = ldexpf(1.0f, 24 - s);
+  };
+  // All of this thread's x chunks (at most 4: a workgroup has at least one
+  // wave per group), then the first three steps' weights, which stay in
+  // flight while x is converted.
+  f32x4 xv[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) x_chunk(threadIdx.x + i * blockDim.x, xv[i][0], xv[i][1]);
+  Raw ra, rb, rc;
+  load(0, ra);
+  load(1, rb);
+  load(2, rc);
+  asm volatile("s_waitcnt vmcnt(9)"
+               : "+v"(xv[0][0]), "+v"(xv[0][1]), "+v"(xv[1][0]), "+v"(xv[1][1]), "+v"(xv[2][0]),
+                 "+v"(xv[2][1]), "+v"(xv[3][0]), "+v"(xv[3][1]));  // x, not the weights
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    if ((int)(threadIdx.x & ~63u) + i * (int)blockDim.x < ng * 256)  // wave-uniform
+      convert(threadIdx.x + i * blockDim.x, xv[i][0], xv[i][1]);
+  __syncthreads();
+
+  if (st < nstream) {
+    const char* gb = lds + g * kQ4gBytes;
+    f16x8 av[8];
+#pragma unroll
+    for (int m = 0; m < 8; ++m) av[m] = *(const f16x8*)(gb + (m * 64 + lane) * 16);
+    const float2 X = *(const float2*)(gb + kQ4gA + (b8 * 8 + 2 * t) * 4);
+    const float fblk = ((const float*)(gb + kQ4gA + kQ4gX))[b8];
+    const bool diag = (b8 >> 1) == t;
+    const bool odd = b8 & 1;
+
+    auto compute = [&](int k, const Raw& r) {
+      float sc0, sc1, mn0, mn1;
+      k4_pair(r.hdr, t, sc0, sc1, mn0, mn1);
+      const float d = f16_bits_to_f32((uint16_t)(r.hdr.x & 0xFFFFu));
+      const float dmin = f16_bits_to_f32((uint16_t)(r.hdr.x >> 16));
+      const h2v s0 = {(_Float16)sc0, (_Float16)sc0};
+      const h2v s1 = {(_Float16)(sc1 * 0.0625f), (_Float16)(sc1 * 0.0625f)};
+      f32x4 c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t d0 = j < 2 ? r.q0[2 * j] : r.q1[2 * j - 4];
+        const uint32_t d1 = j < 2 ? r.q0[2 * j + 1] : r.q1[2 * j - 3];
+        const uint32_t e0 = d0 >> 8, e1 = d1 >> 8;
+        const uint32_t lq[4] = {d0 & 0x000F000Fu, e0 & 0x000F000Fu, d1 & 0x000F000Fu, e1 & 0x000F000Fu};
+        const uint32_t hq[4] = {d0 & 0x00F000F0u, e0 & 0x00F000F0u, d1 & 0x00F000F0u, e1 & 0x00F000F0u};
+        u32x4 bl, bh;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          bl[u] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2v, lq[u]) * s0);
+          bh[u] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2v, hq[u]) * s1);
+        }
+        c = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[j], __builtin_bit_cast(f16x8, bl), c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[4 + j], __builtin_bit_cast(f16x8, bh), c, 0, 0, 0);
+      }
+      const float vh = odd ? c[2] : c[0], vm = odd ? c[3] : c[1];
+      float a = -dmin * fmaf(mn0, X.x, mn1 * X.y);
+      if (diag) a = fmaf(d * fblk, fmaf(vm, 0x1p-11f, vh), a);
+      a = half_row_sum(a);  // lanes n < 8: row 0 of the pair, n >= 8: row 1
+      const int pm = PAIR ? (k & 1) : 0, q = st + (PAIR ? k >> 1 : k) * nstream;
+      if ((lane & 7) == 0 && lane < 16 && 2 * q + rr < nrows)
+        part[(pm * ng + g) * rows_wg + 2 * q + rr] = a;
+    };
+    // Three steps in flight: a step's registers are reloaded with the step
+    // three ahead right after its math.  Loads and waits are unconditional,
+    // so the counts hold on every path (loads past the last step read
+    // nothing).
+    for (int k = 0; k < nsteps; k += 3) {
+      wait(ra, std::integral_constant<int, 6>());
+      compute(k, ra);
+      load(k + 3, ra);
+      wait(rb, std::integral_constant<int, 6>());
+      if (k + 1 < nsteps) compute(k + 1, rb);
+      load(k + 4, rb);
+      wait(rc, std::integral_constant<int, 6>());
+      if (k + 2 < nsteps) compute(k + 2, rc);
+      load(k + 5, rc);
+    }
+  }
+  // every load has landed before its registers can be reused
+  wait(ra, std::integral_constant<int, 0>());
+  wait(rb, std::integral_constant<int, 0>());
+  wait(rc, std::integral_constant<int, 0>());
+  __syncthreads();
+  for (int r = threadIdx.x; r < nrows; r += blockDim.x) {
+    float a = 0.f, b = 0.f;
+    for (int gg = 0; gg < ng; ++gg) {
+      a += part[gg * rows_wg + r];
+      if (PAIR) b += part[(ng + gg) * rows_wg + r];
+    }
+    if constexpr (PAIR == 0) {
+      y[row0 + r] = a;
+    } else if constexpr (PAIR == 1) {
+      y[row0 + r] = a * (1.0f / (1.0f + expf(-a))) * b;  // gpuSiluMul
+    } else {
+      y[row0 + r] = a;
+      y2[row0 + r] = b;
+    }
+  }
+}
+
+// The MFMA kernel pays for its x prologue (~2 us of latency before the
+// first product) on matrices of 2^25 weights and more: 14336 x 4096 10.8 us
+// against 15.7, 4096 x 14336 14.2 against 17.0, but 4096 x 4096 8.3 against
+// 6.6 (kernel durations).
+bool q4k_mfma_pays(int M, int K) {
+  return K <= 256 * 8 * kQ4MaxGroups && (long long)M * K >= (1LL << 25);
+}
+
+// Workgroup: one wave per 8-block group times row-pair streams, with at
+// least one thread per x chunk when 16 waves allow it; as many workgroups
+// as are resident at once (LDS and 16 waves per CU) share the row pairs.
+template <int PAIR>
+void launch_q4k_mfma(const uint8_t* w, const float* x, float* y, int M, int K, hipStream_t stream,
+                     const uint8_t* w2 = nullptr, float* y2 = nullptr) {
+  const int nb = K / 256, ng = (nb + 7) / 8;
+  const int nw = ng <= 4 ? 4 * ng : ng;
+  const size_t a_bytes = (size_t)ng * kQ4gBytes;
+  const int per_cu = std::max(1, std::min<int>(16 / nw, (int)((160 * 1024) / (a_bytes + 4096))));
+  const int pairs = (M + 1) / 2;
+  const int wgs_target = per_cu * cu_count();
+  const int pairs_wg = (pairs + wgs_target - 1) / wgs_target;
+  const int rows = 2 * pairs_wg;
+  const size_t shm = (size_t)ng * kQ4gBytes + (size_t)(PAIR ? 2 : 1) * ng * rows * 4;
+  static const hipError_t attr = hipFuncSetAttribute((const void*)q4k_mfma_kernel<PAIR>,
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+  (void)attr;
+  hipLaunchKernelGGL((q4k_mfma_kernel<PAIR>), dim3((M + rows - 1) / rows), dim3(64 * nw), shm, stream, w, x,
+                     y, M, K, w2, y2, rows);
+}
+
 template <int QT, int R, int KS, int PAIR = 0>
 void launch_direct(const uint8_t* w, const float* x, float* y, int M, int K, hipStream_t stream,
                    const uint8_t* w2 = nullptr, float* y2 = nullptr) {
@@ -825,6 +1127,12 @@ void launch_direct_plan(const uint8_t* w, const float* x, float* y, int M, int K
   // Split a row's blocks over four waves when each gets a step: more waves
   // and loads in flight for decode-sized M.  (A two-way split of 2-3 steps
   // measured slower than none: Q4_K 4096x4096 5.5 -> 7.2 us.)
+  if constexpr (QT == 12) {
+    if (q4k_mfma_pays(M, K)) {
+      launch_q4k_mfma<0>(w, x, y, M, K, stream);
+      return;
+    }
+  }
   const int iters = (K / QD<QT>::QKB + 64 / QD<QT>::LPB - 1) / (64 / QD<QT>::LPB);
   if (iters >= 4) launch_direct_r<QT, 4>(w, x, y, M, K, stream);
   else launch_direct_r<QT, 1>(w, x, y, M, K, stream);
@@ -841,6 +1149,12 @@ bool launch_pair_qt(const uint8_t* w, const uint8_t* w2, const float* x, float* 
                   (QT == 1 ? (a & 15) == 0 : (QT == 12 || QT == 13) ? (a & 15) == 0
                    : QT == 10 ? (a & 3) == 0 : (a & 1) == 0);
   if (!ok) return false;
+  if constexpr (QT == 12) {
+    if (q4k_mfma_pays(M, K)) {
+      launch_q4k_mfma<PAIR>(w, x, y, M, K, stream, w2, y2);
+      return true;
+    }
+  }
   const int iters = (K / QD<QT>::QKB + 64 / QD<QT>::LPB - 1) / (64 / QD<QT>::LPB);
   if (iters >= 4) launch_direct<QT, 2, 4, PAIR>(w, x, y, M, K, stream, w2, y2);
   else launch_direct<QT, 2, 1, PAIR>(w, x, y, M, K, stream, w2, y2);
