@@ -893,7 +893,12 @@ __global__ __launch_bounds__(256, PIPE ? (D == 64 ? 2 : 1) : 4) void decode_mfma
   __syncthreads();
   if constexpr (STEP) {
     // The new column goes to the cache after this workgroup's arrival, so its
-    // stores neither count against the tile waits nor delay the merge.
+    // stores neither count against the tile waits nor delay the merge, as
+    // nontemporal stores: they are scattered 2-byte writes (one per cache
+    // row), and written through they leave no dirty partial lines for the
+    // end of the kernel to write back (c3 step: 12.78 -> 12.64 us; issued
+    // before the tiles instead, the plain stores cost as much, because the
+    // tile waits count them).
     finish_workgroup<D>(p, sm_m, sm_l, sm_o, hc, b, kvh, chunk, hq0, split, HS, [&]() {
       if (has_new && chunk == 0) {
         for (int i = tid; i < 2 * D; i += 256) {
@@ -902,9 +907,9 @@ __global__ __launch_bounds__(256, PIPE ? (D == 64 ? 2 : 1) : 4) void decode_mfma
           if constexpr (paged) at = kv_paged_off(p.block_table, p.bps, b, p.n_head_kv, kvh, D, dd, newc);
           else at = base + kv_off(p.kv_layout, dd, newc, D, p.max_len);
           if constexpr (DT == HL_FP8)  // snew holds the fp16 form of an e4m3 value: exact
-            ((uint8_t*)(i < D ? p.k : p.v))[at] = f32_to_e4m3(from_bits<DT>(snew[i]));
+            __builtin_nontemporal_store(f32_to_e4m3(from_bits<DT>(snew[i])), &((uint8_t*)(i < D ? p.k : p.v))[at]);
           else
-            ((uint16_t*)(i < D ? p.k : p.v))[at] = snew[i];
+            __builtin_nontemporal_store(snew[i], &((uint16_t*)(i < D ? p.k : p.v))[at]);
         }
       }
     });
