@@ -446,10 +446,32 @@ def bench_model(torch, name, cfg):
     torch.cuda.synchronize()
     ms = (time.perf_counter() - t0) * 1e3 / 16
     valid = bool(((toks[1:] >= 0) & (toks[1:] < cfg["n_vocab"])).all().item())
+    # The same 16 steps captured in one HIP graph and replayed (a serving
+    # loop's form: no per-kernel host launch cost), host clock per replay.
+    graph_ms = None
+    try:
+        st = torch.cuda.Stream()
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(st):
+            with torch.cuda.graph(gr, stream=st):
+                for p in range(3, 19):
+                    m.step(p, toks[p:p + 1], toks[p + 1:p + 2])
+        gr.replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(4):
+            gr.replay()
+        torch.cuda.synchronize()
+        graph_ms = (time.perf_counter() - t0) * 1e3 / 64
+    except Exception as e:  # noqa: BLE001 - reported, not fatal
+        log(f"model decode {name}: graph capture failed: {e}")
     res = {"model": f"{name} shape, Q4_K layers, Q6_K head (random weights)", "ms_per_token": round(ms, 3),
            "tokens_per_s": round(1e3 / ms, 1), "weight_bytes": wbytes,
            "weight_GB_per_s": round(wbytes / (ms * 1e-3) / 1e9, 1), "positions": "3..18",
            "tokens_in_vocab": valid}
+    if graph_ms is not None:
+        res["graph_ms_per_token"] = round(graph_ms, 3)
+        res["graph_weight_GB_per_s"] = round(wbytes / (graph_ms * 1e-3) / 1e9, 1)
     log(f"model decode {name}: {ms:.3f} ms/token, {1e3 / ms:.1f} tokens/s, "
         f"{res['weight_GB_per_s']} GB/s of weights")
     del m, layers, emb, out
