@@ -472,6 +472,30 @@ def bench_model(torch, name, cfg):
     if graph_ms is not None:
         res["graph_ms_per_token"] = round(graph_ms, 3)
         res["graph_weight_GB_per_s"] = round(wbytes / (graph_ms * 1e-3) / 1e9, 1)
+    # The backend contract over a cache descriptor (hl_forward_decode): the
+    # same weights, a bf16 KV cache in the library's preferred (tiled)
+    # layout, so each layer's qk-norm + RoPE + cache write + attention is one
+    # fused launch; positions 3..18 as above, and 2048..2063 (an 8K cache,
+    # attention over ~2K columns).
+    try:
+        from hippo_leap_amd import _lib as L_
+        from hippo_leap_amd.model import DenseModel, KvCache
+        cfg2 = dict(cfg, max_len=8192)
+        dm = DenseModel(torch, cfg2, emb, torch.ones(E, device="cuda"), out, 14, layers, kv_dtype=L_.HL_BF16)
+        for start, key in ((3, "fused_ms_per_token"), (2048, "fused_ms_per_token_at_2k")):
+            dm.cache.desc.cur_len = start - 3
+            for p in range(start - 3, start):
+                dm.decode(toks[0:1], toks[1:2])
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for p in range(16):
+                dm.decode(toks[0:1], toks[1:2])
+            torch.cuda.synchronize()
+            res[key] = round((time.perf_counter() - t0) * 1e3 / 16, 3)
+        res["fused_kv_cache"] = f"bf16, layout {int(dm.cache.desc.kv_layout)} (1 = tiled32), max_len 8192"
+        del dm
+    except Exception as e:  # noqa: BLE001 - reported, not fatal
+        log(f"model decode {name}: descriptor path failed: {e}")
     log(f"model decode {name}: {ms:.3f} ms/token, {1e3 / ms:.1f} tokens/s, "
         f"{res['weight_GB_per_s']} GB/s of weights")
     del m, layers, emb, out

@@ -472,7 +472,7 @@ __device__ __forceinline__ u16x8 mask_row8(u16x8 r, int col, int lim) {
 // PG: paged caches (a compile-time variant, so the other layouts carry no
 // page lookups).
 template <int D, int DT, bool VEC, bool PIPE, bool STEP, bool PG = false>
-__global__ __launch_bounds__(256, PIPE ? (D == 64 ? 2 : 1) : 4) void decode_mfma_kernel(DecodeParams p) {
+__global__ __launch_bounds__(256, PIPE ? (D == 64 ? 2 : 1) : (D == 64 ? 4 : 2)) void decode_mfma_kernel(DecodeParams p) {
   static_assert(!PG || VEC, "paged caches are read with vector loads only");
   // MFMA operand type: the storage type, except fp8 caches, which are
   // converted to fp16 (exactly) as their tiles arrive.
