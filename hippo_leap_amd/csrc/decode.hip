@@ -31,6 +31,22 @@
 
 namespace hl {
 
+// Timing instrumentation for development builds only (-DHL_STAMPS): thread 0
+// of every workgroup records s_memrealtime (100 MHz) at entry (0), the first
+// tile (1), the end of its streaming loop (2), after the 4-wave merge (3),
+// after its arrival (4) and, in the merging workgroup, after the fold (5).
+#ifdef HL_STAMPS
+__device__ unsigned long long hl_stamps[65536 * 8];
+#define HL_STAMP(i)                                                                                  \
+  do {                                                                                               \
+    if (threadIdx.x == 0)                                                                            \
+      hl_stamps[(blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z)) * 8 + (i)] =        \
+          __builtin_amdgcn_s_memrealtime();                                                          \
+  } while (0)
+#else
+#define HL_STAMP(i) ((void)0)
+#endif
+
 // Workspace layout (num_splits > 1):
 //   slots [(b*Hkv + kvh)*n_chunks + chunk]    uint32 arrival counters (first)
 //   ws_o  [((b*Hq + hq)*S + split)*D + d]     unnormalised sum p*v
@@ -157,6 +173,7 @@ __device__ void finish_workgroup(const DecodeParams& p, const float* sm_m, const
   }
   unsigned int* slot = p.slots + ((long long)b * p.n_head_kv + kvh) * p.n_chunks + chunk;
   const bool last = arrive_last(slot, S);
+  HL_STAMP(4);
   after();
   if (!last) return;
 
@@ -198,6 +215,7 @@ __device__ void finish_workgroup(const DecodeParams& p, const float* sm_m, const
     }
     p.out[row * D + d] = osum / lsum;
   }
+  HL_STAMP(5);
   if (tid == 0) __hip_atomic_store(slot, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -503,6 +521,7 @@ __global__ __launch_bounds__(256, PIPE ? (D == 64 ? 2 : 1) : (D == 64 ? 4 : 2)) 
   __shared__ __attribute__((aligned(16))) unsigned char lds_raw[LDS_BYTES];
   __shared__ uint16_t snew[STEP ? 2 * D : 1];  // new column's k, v in storage bits
 
+  HL_STAMP(0);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar branches
   const int g = lane >> 4, c = lane & 15;
@@ -741,6 +760,7 @@ __global__ __launch_bounds__(256, PIPE ? (D == 64 ? 2 : 1) : (D == 64 ? 4 : 2)) 
     }
     __syncthreads();  // sq is dead; the K tiles reuse its LDS
   }
+  HL_STAMP(1);
 
   // One 32-column tile whose K/V registers have been loaded.
   auto compute_tile = [&](int t0, u16x8* kr, u16x8* vr) {
@@ -876,6 +896,7 @@ __global__ __launch_bounds__(256, PIPE ? (D == 64 ? 2 : 1) : (D == 64 ? 4 : 2)) 
     }
   }
 
+  HL_STAMP(2);
   // Wave state -> LDS, then the 4-wave merge.
   l_run += __shfl_xor(l_run, 16, 64);
   l_run += __shfl_xor(l_run, 32, 64);
@@ -892,6 +913,7 @@ __global__ __launch_bounds__(256, PIPE ? (D == 64 ? 2 : 1) : (D == 64 ? 4 : 2)) 
 #pragma unroll
     for (int i = 0; i < 4; ++i) sm_o[(wave * HS + 4 * g + i) * D + 16 * nb + c] = o[nb][i];
   __syncthreads();
+  HL_STAMP(3);
   if constexpr (STEP) {
     // The new column goes to the cache after this workgroup's arrival, so its
     // stores neither count against the tile waits nor delay the merge, as
@@ -1156,3 +1178,9 @@ hipError_t decode_launch(const hl_decode_args* a, const DecodePlan* plan, void* 
 }
 
 }  // namespace hl
+
+#ifdef HL_STAMPS
+extern "C" int hl_debug_stamps(void* host, size_t bytes) {
+  return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(hl::hl_stamps), bytes);
+}
+#endif
