@@ -119,6 +119,34 @@ def test_decode_step_matches_two_calls_and_oracle(hl, orc, dt, case):
     assert rel_err(fo, ref) < (TOL_F32 if dt == 0 else TOL_LOWP)
 
 
+SEED_CASES = [
+    # B, hq, hkv, d, max_len, positions, splits: the split holding the new
+    # column seeds its softmax state with it, so the whole column (written to
+    # LDS by every wave) must be visible to the seeding wave
+    (2, 24, 3, 128, 160, [31, 32], 1),    # one split, new column last / first of a tile
+    (2, 32, 8, 64, 128, [31, 95], 1),
+    (3, 32, 4, 128, 256, [31, 127, 200], 0),
+]
+
+
+@pytest.mark.parametrize("dt", [1, 2])
+@pytest.mark.parametrize("case", range(len(SEED_CASES)))
+def test_decode_step_new_column_seed_repeated(hl, orc, dt, case):
+    """Regression guard: the fused step matches the two-call path on every
+    one of eight repetitions.  A missing barrier before the seeding once let
+    the seeding wave read new-column entries the other waves had not written
+    yet; the timing-dependent failure showed in the fp8 tiled step case of
+    test_gpu_kv_fp8.py (one split, D = 128, new column last in its tile)."""
+    B, hq, hkv, d, max_len, positions, splits = SEED_CASES[case]
+    print(f"decode_step seed case {case} dt {dt}", flush=True)
+    for rep in range(8):
+        outs, _ = run_both(orc, B, hq, hkv, d, max_len, dt, positions, 0, 0, False, splits,
+                           1500 + 10 * case + rep)
+        (fo, fk, fv), (so, sk, sv) = outs
+        assert np.array_equal(fk, sk) and np.array_equal(fv, sv)
+        assert rel_err(fo, so) < 1e-5, f"repetition {rep}"
+
+
 def test_decode_step_graph_replay(hl, orc):
     """The step in a HIP graph: replays with eager work in between give the
     eager result every time (the cache column is rewritten with the same bits)."""
