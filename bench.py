@@ -83,7 +83,7 @@ def event_time_ms(torch, fn, iters):
 # FETCH_SIZE / WRITE_SIZE and scaled by a copy kernel of known size (the
 # summary with the commands is profiles/decode_step_c3_traffic.md); to be
 # re-measured whenever the decode kernel changes.
-C3_STEP_TRAFFIC_BYTES = 35_161_600
+C3_STEP_TRAFFIC_BYTES = 35_169_893
 # The same for the c5 step kernel (column-major bf16 caches) and for one c4
 # prefill (kv_prologue_kernel + prefill_mfma_kernel):
 # profiles/decode_step_c5_traffic.md, profiles/prefill_c4_mfma_util_and_traffic.md.
