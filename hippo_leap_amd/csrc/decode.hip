@@ -241,6 +241,7 @@ __global__ __launch_bounds__(256) void decode_f32_kernel(DecodeParams p) {
   __shared__ __attribute__((aligned(16))) float sp[4][HC][64];
   __shared__ __attribute__((aligned(16))) float sm[SM_FLOATS];
 
+  HL_STAMP(0);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar branches
   const int b = blockIdx.z;
@@ -302,6 +303,7 @@ __global__ __launch_bounds__(256) void decode_f32_kernel(DecodeParams p) {
     for (int i = 0; i < DPL; ++i) acc[h][i] = 0.f;
   }
 
+  HL_STAMP(1);
   for (bool first = true; t0 < s1; t0 += 256, first = false) {
     if (!first) load_tile(t0);
     const int col = t0 + lane;
@@ -381,6 +383,7 @@ __global__ __launch_bounds__(256) void decode_f32_kernel(DecodeParams p) {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   }
 
+  HL_STAMP(2);
   float* sm_m = sm;
   float* sm_l = sm_m + 4 * HC;
   float* sm_o = sm_l + 4 * HC;
@@ -411,6 +414,7 @@ __global__ __launch_bounds__(256) void decode_f32_kernel(DecodeParams p) {
     }
   }
   __syncthreads();
+  HL_STAMP(3);
   finish_workgroup<D>(p, sm_m, sm_l, sm_o, hc, b, kvh, chunk, hq0, split, HC);
 }
 
