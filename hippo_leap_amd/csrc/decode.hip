@@ -39,9 +39,8 @@ namespace hl {
 __device__ unsigned long long hl_stamps[65536 * 8];
 #define HL_STAMP(i)                                                                                  \
   do {                                                                                               \
-    if (threadIdx.x == 0)                                                                            \
-      hl_stamps[(blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z)) * 8 + (i)] =        \
-          __builtin_amdgcn_s_memrealtime();                                                          \
+    const unsigned wg_ = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);            \
+    if (threadIdx.x == 0 && wg_ < 65536u) hl_stamps[wg_ * 8 + (i)] = __builtin_amdgcn_s_memrealtime(); \
   } while (0)
 #else
 #define HL_STAMP(i) ((void)0)
