@@ -189,6 +189,9 @@ hipError_t embedding_launch(float* out, const float* w, const int* tok, int n_em
 
 bool linear_quant_pair_launch(int pair, float* y, float* y2, const float* x, const void* wa,
                               const void* wb, int K, int M, int qtype, hipStream_t stream);
+// Q, K and V projections of one x in one launch (false: run them apart).
+bool linear_quant_qkv_launch(float* yq, float* yk, float* yv, const float* x, const void* wq, const void* wk,
+                             const void* wv, int K, int Mq, int Mkv, int qtype, hipStream_t stream);
 
 // Sets the thread's hl_last_error() message (printf format); returns code.
 int set_error(int code, const char* fmt, ...);

@@ -693,21 +693,31 @@ __device__ __forceinline__ float compute_raw(const QRaw<QT>& r, int j, uint32_t 
 // row groups.  PAIR (R = 2): the group's two rows are row m of w and row m
 // of w2, sharing the x registers; PAIR 1 stores silu(a) * b to y (fused
 // gate / up / SiLU), PAIR 2 stores a to y and b to y2 (fused K / V).
+// PAIR 3 (R = 2): the Q, K and V projections of one x in one launch: the
+// first ceil(M / 2) groups are row pairs of w (M rows) into y, the next M2
+// groups row m of w2 and of w3 into y2 and y3 (a wave-uniform choice of
+// pointers; the arithmetic is the same code, so the results are those of
+// the separate launches).
 template <int QT, int R, int KS, int PAIR = 0>
 __global__ __launch_bounds__(256) void quant_direct_kernel(const uint8_t* __restrict__ w,
                                                            const float* __restrict__ x,
                                                            float* __restrict__ y, int M, int K,
                                                            const uint8_t* __restrict__ w2,
-                                                           float* __restrict__ y2) {
+                                                           float* __restrict__ y2,
+                                                           const uint8_t* __restrict__ w3 = nullptr,
+                                                           float* __restrict__ y3 = nullptr, int M2 = 0) {
   static_assert(PAIR == 0 || R == 2, "pairs are two rows");
   using F = QD<QT>;
   constexpr int BPI = 64 / F::LPB;
   __shared__ float part[4][R];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int row0 = (blockIdx.x * (4 / KS) + wave / KS) * (PAIR ? 1 : R);
+  const int gi = blockIdx.x * (4 / KS) + wave / KS;  // row group
+  const int gq = (M + 1) / 2;                        // PAIR 3: groups of the first matrix
+  const bool qpart = PAIR != 3 || gi < gq;           // wave-uniform
+  const int row0 = PAIR == 3 ? (qpart ? 2 * gi : gi - gq) : gi * (PAIR ? 1 : R);
   const int s0 = wave % KS;
-  if (KS == 1 && row0 >= M) return;  // no barrier below for KS == 1
+  if (KS == 1 && (PAIR == 3 ? gi >= gq + M2 : row0 >= M)) return;  // no barrier below for KS == 1
   const int j = lane % F::LPB, bl = lane / F::LPB;
   const int nb = K / F::QKB;
   const uint32_t rowbytes = (uint32_t)nb * F::BB;
@@ -717,8 +727,10 @@ __global__ __launch_bounds__(256) void quant_direct_kernel(const uint8_t* __rest
   uint32_t ps[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const uint8_t* rp = PAIR ? (r == 0 ? w : w2) + (size_t)min(row0, M - 1) * rowbytes
-                             : w + (size_t)min(row0 + r, M - 1) * rowbytes;
+    const uint8_t* rp;
+    if (PAIR == 3 && !qpart) rp = (r == 0 ? w2 : w3) + (size_t)min(row0, M2 - 1) * rowbytes;
+    else if (PAIR == 1 || PAIR == 2) rp = (r == 0 ? w : w2) + (size_t)min(row0, M - 1) * rowbytes;
+    else rp = w + (size_t)min(row0 + r, M - 1) * rowbytes;
     ps[r] = (uint32_t)((uintptr_t)rp & 3);
     // Whole dwords: the range check drops a dword that ends past the size.
     rs[r] = make_rsrc(rp - ps[r], (rowbytes + ps[r] + 3) & ~3u);
@@ -777,6 +789,17 @@ __global__ __launch_bounds__(256) void quant_direct_kernel(const uint8_t* __rest
       if (row0 < M) {
         y[row0] = t[0];
         y2[row0] = t[1];
+      }
+    } else if constexpr (PAIR == 3) {
+      if (!qpart) {
+        if (row0 < M2) {
+          y2[row0] = t[0];
+          y3[row0] = t[1];
+        }
+      } else {
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+          if (row0 + r < M) y[row0 + r] = t[r];
       }
     } else {
 #pragma unroll
@@ -1107,11 +1130,12 @@ void launch_q4k_mfma(const uint8_t* w, const float* x, float* y, int M, int K, h
 
 template <int QT, int R, int KS, int PAIR = 0>
 void launch_direct(const uint8_t* w, const float* x, float* y, int M, int K, hipStream_t stream,
-                   const uint8_t* w2 = nullptr, float* y2 = nullptr) {
-  const int groups = PAIR ? M : (M + R - 1) / R;
+                   const uint8_t* w2 = nullptr, float* y2 = nullptr, const uint8_t* w3 = nullptr,
+                   float* y3 = nullptr, int M2 = 0) {
+  const int groups = PAIR == 3 ? (M + 1) / 2 + M2 : PAIR ? M : (M + R - 1) / R;
   const int grid = (groups + 4 / KS - 1) / (4 / KS);
   hipLaunchKernelGGL((quant_direct_kernel<QT, R, KS, PAIR>), dim3(grid), dim3(256), 0, stream, w, x, y,
-                     M, K, w2, y2);
+                     M, K, w2, y2, w3, y3, M2);
 }
 
 template <int QT, int KS>
@@ -1266,6 +1290,50 @@ bool linear_quant_pair_launch(int pair, float* y, float* y2, const float* x, con
     default: return false;
   }
 #undef HL_PAIR
+}
+
+// The Q, K and V projections of one x in one launch (three matrices of one
+// GGUF type, each K columns; Q has Mq rows, K and V have Mkv): the direct
+// kernel's PAIR 3 mode.  Returns false when the pointers, the type or the
+// shapes do not allow it (Q4_K matrices that the matrix-core kernel takes,
+// for instance); the caller then runs the projections apart.
+template <int QT>
+bool launch_qkv_qt(const uint8_t* wq, const uint8_t* wk, const uint8_t* wv, const float* x, float* yq,
+                   float* yk, float* yv, int Mq, int Mkv, int K, hipStream_t stream) {
+  const long long rowbytes = (long long)(K / QD<QT>::QKB) * QD<QT>::BB;
+  const uintptr_t a = (uintptr_t)wq | (uintptr_t)wk | (uintptr_t)wv;
+  const bool ok = ((uintptr_t)x & 15) == 0 && rowbytes < (1LL << 31) && K % QD<QT>::QKB == 0 &&
+                  (QT == 1 ? (a & 15) == 0 : (QT == 12 || QT == 13) ? (a & 15) == 0
+                   : QT == 10 ? (a & 3) == 0 : (a & 1) == 0);
+  if (!ok) return false;
+  if constexpr (QT == 12) {
+    if (q4k_mfma_pays(Mq, K) || q4k_mfma_pays(Mkv, K)) return false;
+  }
+  const int iters = (K / QD<QT>::QKB + 64 / QD<QT>::LPB - 1) / (64 / QD<QT>::LPB);
+  if (iters >= 4) launch_direct<QT, 2, 4, 3>(wq, x, yq, Mq, K, stream, wk, yk, wv, yv, Mkv);
+  else launch_direct<QT, 2, 1, 3>(wq, x, yq, Mq, K, stream, wk, yk, wv, yv, Mkv);
+  return true;
+}
+
+bool linear_quant_qkv_launch(float* yq, float* yk, float* yv, const float* x, const void* wq, const void* wk,
+                             const void* wv, int K, int Mq, int Mkv, int qtype, hipStream_t stream) {
+  const uint8_t *a = (const uint8_t*)wq, *b = (const uint8_t*)wk, *c = (const uint8_t*)wv;
+  if (Mq <= 0 || Mkv <= 0) return false;
+#define HL_QKV(QT) return launch_qkv_qt<QT>(a, b, c, x, yq, yk, yv, Mq, Mkv, K, stream)
+  switch (qtype) {
+    case HL_GGML_F16: if (K % 8) return false; HL_QKV(1);
+    case HL_GGML_Q5_0: HL_QKV(6);
+    case HL_GGML_Q5_1: HL_QKV(7);
+    case HL_GGML_Q8_0: HL_QKV(8);
+    case HL_GGML_Q2_K: HL_QKV(10);
+    case HL_GGML_Q3_K: HL_QKV(11);
+    case HL_GGML_Q4_K: HL_QKV(12);
+    case HL_GGML_Q5_K: HL_QKV(13);
+    case HL_GGML_Q6_K: HL_QKV(14);
+    case HL_GGML_IQ4_NL: HL_QKV(20);
+    default: return false;
+  }
+#undef HL_QKV
 }
 
 hipError_t linear_quant_launch(float* y, const float* x, const void* w, int K, int M, int qtype,

@@ -196,6 +196,14 @@ static bool pair_launch(int which, float* d0, float* d1, const float* x, const v
          linear_quant_pair_launch(which, d0, d1, x, wa, wb, cols, rows, ta, (hipStream_t)stream);
 }
 
+// Quantized Q, K and V of one type as one launch (the direct kernel's
+// three-matrix mode); false: run Q, then the K/V pair.
+static bool qkv_launch(float* q, float* k, float* v, const float* x, const hl_layer_desc& L, int cols, int qrows,
+                       int kvrows, void* stream) {
+  return L.wq_type != 0 && L.wq_type == L.wk_type && L.wq_type == L.wv_type && pair_fusable(L.wq_type, cols) &&
+         linear_quant_qkv_launch(q, k, v, x, L.wq, L.wk, L.wv, cols, qrows, kvrows, L.wq_type, (hipStream_t)stream);
+}
+
 #define HL_TRY(call)              \
   do {                            \
     const int rc_ = (call);       \
@@ -262,10 +270,12 @@ int hl_forward_decode_token(const hl_model_desc* m, const hl_decode_scratch* s,
   HL_TRY(hl_gpu_rmsnorm_cols(s->x_norm, s->x, m->layers[0].attn_norm, E, 1, eps, stream));
   for (int l = 0; l < m->n_layer; ++l) {
     const hl_layer_desc& L = m->layers[l];
-    HL_TRY(linear_t(s->tmp0, s->x_norm, L.wq, L.wq_type, E, qdim, 1, stream));
-    if (!pair_launch(2, s->tmp1, s->tmp2, s->x_norm, L.wk, L.wv, L.wk_type, L.wv_type, E, kvdim, stream)) {
-      HL_TRY(linear_t(s->tmp1, s->x_norm, L.wk, L.wk_type, E, kvdim, 1, stream));
-      HL_TRY(linear_t(s->tmp2, s->x_norm, L.wv, L.wv_type, E, kvdim, 1, stream));
+    if (!qkv_launch(s->tmp0, s->tmp1, s->tmp2, s->x_norm, L, E, qdim, kvdim, stream)) {
+      HL_TRY(linear_t(s->tmp0, s->x_norm, L.wq, L.wq_type, E, qdim, 1, stream));
+      if (!pair_launch(2, s->tmp1, s->tmp2, s->x_norm, L.wk, L.wv, L.wk_type, L.wv_type, E, kvdim, stream)) {
+        HL_TRY(linear_t(s->tmp1, s->x_norm, L.wk, L.wk_type, E, kvdim, 1, stream));
+        HL_TRY(linear_t(s->tmp2, s->x_norm, L.wv, L.wv_type, E, kvdim, 1, stream));
+      }
     }
     if (L.q_norm) HL_TRY(hl_gpu_qk_norm(s->tmp0, L.q_norm, m->n_head, D, eps, stream));
     if (L.k_norm) HL_TRY(hl_gpu_qk_norm(s->tmp1, L.k_norm, m->n_head_kv, D, eps, stream));
@@ -525,10 +535,12 @@ int hl_forward_decode(const hl_model_desc* m, hl_kv_cache_desc* c, const hl_forw
   HL_TRY(hl_gpu_rmsnorm_cols(s->x_norm, s->x, m->layers[0].attn_norm, E, 1, eps, stream));
   for (int l = 0; l < m->n_layer; ++l) {
     const hl_layer_desc& L = m->layers[l];
-    HL_TRY(linear_t(s->tmp0, s->x_norm, L.wq, L.wq_type, E, qdim, 1, stream));
-    if (!pair_launch(2, s->tmp1, s->tmp2, s->x_norm, L.wk, L.wv, L.wk_type, L.wv_type, E, kvdim, stream)) {
-      HL_TRY(linear_t(s->tmp1, s->x_norm, L.wk, L.wk_type, E, kvdim, 1, stream));
-      HL_TRY(linear_t(s->tmp2, s->x_norm, L.wv, L.wv_type, E, kvdim, 1, stream));
+    if (!qkv_launch(s->tmp0, s->tmp1, s->tmp2, s->x_norm, L, E, qdim, kvdim, stream)) {
+      HL_TRY(linear_t(s->tmp0, s->x_norm, L.wq, L.wq_type, E, qdim, 1, stream));
+      if (!pair_launch(2, s->tmp1, s->tmp2, s->x_norm, L.wk, L.wv, L.wk_type, L.wv_type, E, kvdim, stream)) {
+        HL_TRY(linear_t(s->tmp1, s->x_norm, L.wk, L.wk_type, E, kvdim, 1, stream));
+        HL_TRY(linear_t(s->tmp2, s->x_norm, L.wv, L.wv_type, E, kvdim, 1, stream));
+      }
     }
     // qk-norm + RoPE + the cache write at pos + attention over pos + 1
     // columns (naive.nim:4697-4717): one launch for fp16/bf16/fp8 caches

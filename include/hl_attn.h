@@ -563,8 +563,9 @@ typedef struct {
  * position pos, writing the K/V column pos of each layer's cache, the
  * logits [n_vocab] and the greedy next token to *next_token_dev (device;
  * nothing waits for the stream, so next_token_dev can be the next call's
- * token_dev).  The same kernels, in the same order, as the reference's
- * step: embedding; rmsnorm; per layer Q/K/V projections, qk-norm, RoPE,
+ * token_dev).  The reference's step, in its order: embedding; rmsnorm;
+ * per layer Q/K/V projections (one launch when the three weights share a
+ * quantized type, as K/V pairs and gate/up pairs are), qk-norm, RoPE,
  * K/V store, attention, O projection, residual + ffn norm, gate/up,
  * SiLU * up, down, residual + next layer's norm; final norm, output
  * projection, argmax.  Sets the process-wide RoPE table

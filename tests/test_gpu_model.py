@@ -126,6 +126,32 @@ def test_forward_decode_token_matches_oracle(hl, orc, name, types, qk_norm):
         tok = nxt
 
 
+# Width 2048: the direct kernels split each row's blocks over four waves
+# (the three-matrix Q/K/V launch included), F16 and Q8_0 weights.
+CFG_WIDE = dict(CFG, n_emb=2048, n_head=32, n_head_kv=8, n_ff=1024)
+
+
+@pytest.mark.parametrize("types", [{"wq": 1, "wk": 1, "wv": 1, "wo": 8, "w_gate": 8, "w_up": 8, "w_down": 8},
+                                   {"wq": 8, "wk": 8, "wv": 8, "wo": 8, "w_gate": 8, "w_up": 8, "w_down": 8}],
+                         ids=["qkv_f16", "qkv_q8_0"])
+def test_forward_decode_token_wide_fused_projections(hl, orc, types):
+    from hippo_leap_amd.model import DenseDecoder
+    print(f"decode model wide {types['wq']}", flush=True)
+    dev, ref = _build(orc, CFG_WIDE, types, False, 97)
+    m = DenseDecoder(torch, CFG_WIDE, dev["tok_emb"], dev["output_norm"], dev["output"],
+                     dev["output_type"], dev["layers"])
+    tok = 5
+    m.tokens[0] = tok
+    for pos in range(3):
+        m.step(pos, m.tokens[0:1], m.tokens[1:2])
+        torch.cuda.synchronize()
+        logits = m.logits.cpu().numpy()
+        ref_logits = _oracle_step(orc, CFG_WIDE, ref, tok, pos)
+        assert rel_err(logits, ref_logits) < TOL_F32, f"step {pos}"
+        tok = int(m.tokens[1].item())
+        m.tokens[0] = tok
+
+
 def test_forward_decode_token_rope_dim_zero(hl, orc):
     """rope_dim 0 means the whole head, as the reference's ropeDim =
     headDim when the model file has no rope dimension (naive.nim:3979)."""
