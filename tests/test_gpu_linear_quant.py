@@ -88,6 +88,24 @@ def test_linear_col_quant_offsets(hl, orc, case):
     assert rel_err(y.cpu().numpy(), W @ x.astype(np.float64)) < TOL_F32
 
 
+@pytest.mark.parametrize("qt", [14, 6])
+def test_linear_col_quant_tall(hl, orc, qt):
+    """Output-head shapes (65536+ rows): each row in one wave, all four
+    steps in it.  64 random rows repeated 1024 times."""
+    from hippo_leap_amd import attention as A
+    K, base, reps = 4096, 64, 1024
+    M = base * reps
+    print(f"quant GEMV tall: type {qt} M={M} K={K}", flush=True)
+    rng = np.random.default_rng(7300 + qt)
+    raw = random_rows(rng, qt, base, K)
+    x = orc.normal(K, 7301)
+    y = torch.full((M,), float("nan"), device="cuda")
+    A.gpu_linear_col_quant(y, torch.from_numpy(x).cuda(), torch.from_numpy(np.tile(raw, reps)).cuda(), K, M, qt)
+    torch.cuda.synchronize()
+    ref = np.tile(orc.dequant_rows(qt, raw, base, K).astype(np.float64) @ x.astype(np.float64), reps)
+    assert rel_err(y.cpu().numpy(), ref) < TOL_F32
+
+
 def test_linear_col_quant_errors(hl):
     from hippo_leap_amd import attention as A
     from hippo_leap_amd._lib import HLError
