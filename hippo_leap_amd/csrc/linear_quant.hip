@@ -1161,8 +1161,12 @@ void launch_direct_plan(const uint8_t* w, const float* x, float* y, int M, int K
   // Tall matrices (output heads: 128256 rows) keep each row in one wave:
   // with 64K+ row pairs the grid is full anyway, and a wave's four steps
   // pipeline their loads (Q6_K 128256x4096 184 -> 130 us, Q5_0 112 -> 102 us).
-  if (iters >= 4 && M < 65536) launch_direct_r<QT, 4>(w, x, y, M, K, stream);
-  else launch_direct_r<QT, 1>(w, x, y, M, K, stream);
+  // Four to seven steps per row go to two waves, two or more steps each
+  // (against four waves: Q6_K 14336x4096 20.2 -> 14.9 us, Q2_K 18.2 -> 13.8,
+  // Q4_K 2048x8192 6.1 -> 4.9, Q5_K 4096x14336 15.5 -> 14.5).
+  if (M >= 65536 || iters < 4) launch_direct_r<QT, 1>(w, x, y, M, K, stream);
+  else if (iters < 8) launch_direct_r<QT, 2>(w, x, y, M, K, stream);
+  else launch_direct_r<QT, 4>(w, x, y, M, K, stream);
 }
 
 // Two matrices of one type at once (PAIR 1 or 2), when the direct kernel
