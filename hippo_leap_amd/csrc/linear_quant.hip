@@ -1187,7 +1187,11 @@ bool launch_pair_qt(const uint8_t* w, const uint8_t* w2, const float* x, float* 
     }
   }
   const int iters = (K / QD<QT>::QKB + 64 / QD<QT>::LPB - 1) / (64 / QD<QT>::LPB);
-  if (iters >= 4) launch_direct<QT, 2, 4, PAIR>(w, x, y, M, K, stream, w2, y2);
+  // The block split follows the single-matrix rule (two waves for four to
+  // seven steps: Q6_K gate/up 14336x4096 43.0 -> 32.0 us, Q3_K 43.3 -> 30.0,
+  // Q2_K 30.4 -> 24.1).
+  if (iters >= 8) launch_direct<QT, 2, 4, PAIR>(w, x, y, M, K, stream, w2, y2);
+  else if (iters >= 4) launch_direct<QT, 2, 2, PAIR>(w, x, y, M, K, stream, w2, y2);
   else launch_direct<QT, 2, 1, PAIR>(w, x, y, M, K, stream, w2, y2);
   return true;
 }
@@ -1317,7 +1321,8 @@ bool launch_qkv_qt(const uint8_t* wq, const uint8_t* wk, const uint8_t* wv, cons
     if (q4k_mfma_pays(Mq, K) || q4k_mfma_pays(Mkv, K)) return false;
   }
   const int iters = (K / QD<QT>::QKB + 64 / QD<QT>::LPB - 1) / (64 / QD<QT>::LPB);
-  if (iters >= 4) launch_direct<QT, 2, 4, 3>(wq, x, yq, Mq, K, stream, wk, yk, wv, yv, Mkv);
+  if (iters >= 8) launch_direct<QT, 2, 4, 3>(wq, x, yq, Mq, K, stream, wk, yk, wv, yv, Mkv);
+  else if (iters >= 4) launch_direct<QT, 2, 2, 3>(wq, x, yq, Mq, K, stream, wk, yk, wv, yv, Mkv);
   else launch_direct<QT, 2, 1, 3>(wq, x, yq, Mq, K, stream, wk, yk, wv, yv, Mkv);
   return true;
 }

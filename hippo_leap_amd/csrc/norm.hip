@@ -95,7 +95,8 @@ __global__ __launch_bounds__(256) void residual_rmsnorm_kernel(float* __restrict
 // dim % 4 == 0, 16-byte aligned vectors, dim <= 16384: 1024 threads, up to
 // four float4 chunks each, all loaded before the reduction and kept in
 // registers for the second pass (the scalar loop above runs ~16 dependent
-// load/store rounds per thread at dim 4096).
+// load/store rounds per thread at dim 4096).  The weights are loaded with x,
+// so the kernel waits for memory once.
 template <bool RES>
 __global__ __launch_bounds__(1024) void norm_vec4_kernel(float* __restrict__ x,
                                                          const float* __restrict__ res,
@@ -103,15 +104,17 @@ __global__ __launch_bounds__(1024) void norm_vec4_kernel(float* __restrict__ x,
                                                          float* __restrict__ out, int dim, float eps) {
   __shared__ float part[16];
   const int n4 = dim >> 2, tid = threadIdx.x;
-  f32x4 v[4];
+  f32x4 v[4], wv[4];
   float ss = 0.f;
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     const int c = tid + 1024 * k;
     v[k] = f32x4{0.f, 0.f, 0.f, 0.f};
+    wv[k] = v[k];
     if (c < n4) {
       v[k] = ((const f32x4*)x)[c];
       if (RES) v[k] += ((const f32x4*)res)[c];
+      wv[k] = ((const f32x4*)w)[c];
     }
   }
 #pragma unroll
@@ -132,11 +135,9 @@ __global__ __launch_bounds__(1024) void norm_vec4_kernel(float* __restrict__ x,
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     const int c = tid + 1024 * k;
-    if (c < n4) {
-      const f32x4 wv = ((const f32x4*)w)[c];
-      ((f32x4*)out)[c] = f32x4{v[k].x * inv * wv.x, v[k].y * inv * wv.y, v[k].z * inv * wv.z,
-                               v[k].w * inv * wv.w};
-    }
+    if (c < n4)
+      ((f32x4*)out)[c] = f32x4{v[k].x * inv * wv[k].x, v[k].y * inv * wv[k].y,
+                               v[k].z * inv * wv[k].z, v[k].w * inv * wv[k].w};
   }
 }
 
