@@ -223,7 +223,7 @@ __device__ void finish_workgroup(const DecodeParams& p, const float* sm_m, const
 // lane j scores column t0+j for every head of the chunk, then lanes switch to
 // owning output dims for the P.V product.
 // ---------------------------------------------------------------------------
-// HC: head slots per chunk (2, 4, 8 or 16, at least the chunk's heads).  Slots
+// HC: head slots per chunk (1, 2, 4, 8 or 16, at least the chunk's heads).  Slots
 // past the chunk's heads score a zero q row and are never written out; every
 // slot is computed without a branch, so the heads' dependency chains (dot
 // products, wave reductions) interleave instead of running one after another.
@@ -1002,6 +1002,7 @@ typedef void (*KernelFn)(DecodeParams);
 // loads of unaligned caches would not fit its registers).
 template <int D, bool V4>
 KernelFn pick_f32_hc(int hc) {
+  if (hc <= 1) return decode_f32_kernel<D, V4, 1>;
   if (hc <= 2) return decode_f32_kernel<D, V4, 2>;
   return hc <= 4 ? decode_f32_kernel<D, V4, 4> : (hc <= 8 ? decode_f32_kernel<D, V4, 8> : decode_f32_kernel<D, V4, 16>);
 }
@@ -1071,15 +1072,16 @@ void decode_plan(const hl_decode_args* a, DecodePlan* plan, bool step) {
   plan->head_chunk = G < 16 ? G : 16;
   if (a->kv_dtype == HL_F32) {
     // fp32 (vector ALU): a wave's work per tile grows with its heads.  When
-    // the grid is small (latency-bound: fewer workgroups than half the CUs),
-    // fewer heads per workgroup spread the work over more CUs; each chunk
-    // re-reads the K/V tile, which such small caches serve from L2 (c1:
-    // 8 -> 2 heads, 12.4 -> 8.2 us).
+    // the grid is small (latency-bound: fewer workgroups than CUs), fewer
+    // heads per workgroup, down to one, spread the work over more CUs; each
+    // chunk re-reads the K/V tile, which such small caches serve from L2
+    // (c1: 8 -> 1 head, 12.4 -> 7.5 us; head dim 128, 8 kv heads, 1024
+    // columns: 17.2 -> 14.0 us).
     const int tiles64 = (a->seq_len + 63) / 64;
-    while (plan->head_chunk > 2) {
+    while (plan->head_chunk > 1) {
       const long long wgs = (long long)a->batch * a->n_head_kv * ((G + plan->head_chunk - 1) / plan->head_chunk) *
                             (tiles64 < 64 ? tiles64 : 64);
-      if (wgs * 2 >= cu_count()) break;
+      if (wgs >= cu_count()) break;
       plan->head_chunk /= 2;
     }
   }
@@ -1126,11 +1128,11 @@ void decode_plan(const hl_decode_args* a, DecodePlan* plan, bool step) {
   plan->num_splits = S;
   if (plan->num_splits > 1) {
     // Counters first, in a region sized for the most head chunks any plan
-    // of this shape can use (chunks of 2 heads), so that their place depends
+    // of this shape can use (chunks of one head), so that their place depends
     // only on (batch, kv heads, group) and not on the split count or the
     // attention length: a workspace shared by the calls of one model keeps
     // them where the previous call left them (zero).
-    const long long max_chunks = G < 2 ? 1 : (G + 1) / 2;
+    const long long max_chunks = G;
     plan->counters_bytes = ((size_t)a->batch * a->n_head_kv * max_chunks * 4 + 255) / 256 * 256;
     const size_t partial = (size_t)a->batch * a->n_head * plan->num_splits * (a->head_dim + 2) * 4;
     plan->ws_bytes = plan->counters_bytes + partial;

@@ -437,7 +437,7 @@ static int check_scratch(const hl_forward_scratch* s, int T) {
 // (head_dim + 2) floats per query head (the decode plan's limits).
 static size_t decode_region_bytes(const hl_model_desc* m, const hl_kv_cache_desc* c) {
   const long long G = m->n_head / m->n_head_kv;
-  const long long chunks = G < 2 ? 1 : (G + 1) / 2;
+  const long long chunks = G;
   const size_t counters = ((size_t)m->n_head_kv * chunks * 4 + 255) / 256 * 256;
   const long long tiles = (c->max_len + 31) / 32;
   const long long S = tiles < 256 ? tiles : 256;
