@@ -175,6 +175,9 @@ hipError_t rmsnorm_cols_launch(float* out, const float* x, const float* w, int d
                                float eps, hipStream_t stream);
 hipError_t residual_rmsnorm_launch(float* out, float* x, const float* res, const float* w, int dim,
                                    float eps, hipStream_t stream);
+// x_dst = x_in + res; out = rmsnorm(x_dst) * w (out may be x_in).
+hipError_t residual_rmsnorm_from_launch(float* out, float* x_dst, const float* x_in, const float* res,
+                                        const float* w, int dim, float eps, hipStream_t stream);
 
 // ---- decode-step ends: argmax and embedding (tokens.hip) -------------------
 constexpr int kArgmaxMaxGroups = 256;
@@ -192,6 +195,11 @@ bool linear_quant_pair_launch(int pair, float* y, float* y2, const float* x, con
 // Q, K and V projections of one x in one launch (false: run them apart).
 bool linear_quant_qkv_launch(float* yq, float* yk, float* yv, const float* x, const void* wq, const void* wk,
                              const void* wv, int K, int Mq, int Mkv, int qtype, hipStream_t stream);
+// xsum = x + res, then the fused gate/up/SiLU of rmsnorm(xsum) * nrm in one
+// launch (Q4_K on the matrix cores, K <= 8192); false when not applicable.
+bool linear_quant_gate_up_norm_launch(float* y, float* xsum, const float* x, const float* res, const float* nrm,
+                                      float eps, const void* wg, const void* wu, int K, int M, int qtype,
+                                      hipStream_t stream);
 
 // Sets the thread's hl_last_error() message (printf format); returns code.
 int set_error(int code, const char* fmt, ...);

@@ -894,12 +894,21 @@ __device__ __forceinline__ float half_row_sum(float v) {
   return v;
 }
 
-template <int PAIR>
+// NORM: x is first replaced by rmsnorm(x + res) * nrm over its K values
+// (gpuResidualRmsnorm, naive.nim:2845-2882, folded into the x prologue:
+// every workgroup adds and reduces the whole vector; workgroup 0 also stores
+// x + res to xsum, which no workgroup of this launch reads).  One x chunk
+// per thread: K <= 8192.
+template <int PAIR, bool NORM = false>
 __global__ __launch_bounds__(1024) void q4k_mfma_kernel(const uint8_t* __restrict__ w,
                                                         const float* __restrict__ x,
                                                         float* __restrict__ y, int M, int K,
                                                         const uint8_t* __restrict__ w2,
-                                                        float* __restrict__ y2, int rows_wg) {
+                                                        float* __restrict__ y2, int rows_wg,
+                                                        const float* __restrict__ res = nullptr,
+                                                        const float* __restrict__ nrm = nullptr,
+                                                        float* __restrict__ xsum = nullptr,
+                                                        float eps = 0.f) {
   extern __shared__ __align__(16) char lds[];
   constexpr int NP = PAIR ? 2 : 1;
   const int lane = threadIdx.x & 63;
@@ -1000,20 +1009,56 @@ __global__ __launch_bounds__(1024) void q4k_mfma_kernel(const uint8_t* __restric
     if (cb == 0) ((float*)(gb + kQ4gA + kQ4gX))[bb] = ldexpf(1.0f, 24 - s);
   };
   // All of this thread's x chunks (at most 4: a workgroup has at least one
-  // wave per group), then the first three steps' weights, which stay in
-  // flight while x is converted.
-  f32x4 xv[4][2];
+  // wave per group; NORM: one, with its res and nrm chunks), then the first
+  // three steps' weights, which stay in flight while x is converted.
+  constexpr int XC = NORM ? 1 : 4;
+  f32x4 xv[XC][2];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) x_chunk(threadIdx.x + i * blockDim.x, xv[i][0], xv[i][1]);
+  for (int i = 0; i < XC; ++i) x_chunk(threadIdx.x + i * blockDim.x, xv[i][0], xv[i][1]);
+  [[maybe_unused]] f32x4 rv[2], nv[2];
+  if constexpr (NORM) {
+    const v4i rdesc = buf_desc(res, (uint32_t)K * 4u), ndesc = buf_desc(nrm, (uint32_t)K * 4u);
+    asm volatile(
+        "buffer_load_dwordx4 %0, %4, %5, 0 offen\n\t"
+        "buffer_load_dwordx4 %1, %4, %5, 0 offen offset:16\n\t"
+        "buffer_load_dwordx4 %2, %4, %6, 0 offen\n\t"
+        "buffer_load_dwordx4 %3, %4, %6, 0 offen offset:16"
+        : "=&v"(rv[0]), "=&v"(rv[1]), "=&v"(nv[0]), "=&v"(nv[1])
+        : "v"(32 * (int)threadIdx.x), "s"(rdesc), "s"(ndesc));
+  }
   Raw ra, rb, rc;
   load(0, ra);
   load(1, rb);
   load(2, rc);
-  asm volatile("s_waitcnt vmcnt(9)"
-               : "+v"(xv[0][0]), "+v"(xv[0][1]), "+v"(xv[1][0]), "+v"(xv[1][1]), "+v"(xv[2][0]),
-                 "+v"(xv[2][1]), "+v"(xv[3][0]), "+v"(xv[3][1]));  // x, not the weights
+  if constexpr (NORM) {
+    asm volatile("s_waitcnt vmcnt(9)"
+                 : "+v"(xv[0][0]), "+v"(xv[0][1]), "+v"(rv[0]), "+v"(rv[1]), "+v"(nv[0]),
+                   "+v"(nv[1]));  // x, res, nrm, not the weights
+    // Chunks past K load as zeros and add nothing to the sum of squares.
+    const f32x4 v0 = xv[0][0] + rv[0], v1 = xv[0][1] + rv[1];
+    float ss = (v0.x * v0.x + v0.y * v0.y) + (v0.z * v0.z + v0.w * v0.w) +
+               ((v1.x * v1.x + v1.y * v1.y) + (v1.z * v1.z + v1.w * v1.w));
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+    for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
+    float* red = (float*)(lds + ng * kQ4gBytes) + NP * ng * rows_wg;
+    if (lane == 0) red[wave] = ss;
+    if (blockIdx.x == 0 && (int)threadIdx.x < K / 8) {
+      *(f32x4*)(xsum + 8 * threadIdx.x) = v0;
+      *(f32x4*)(xsum + 8 * threadIdx.x + 4) = v1;
+    }
+    __syncthreads();
+    float t = 0.f;
+    for (int i = 0; i < nw; ++i) t += red[i];
+    const float inv = 1.0f / sqrtf(t / (float)K + eps);
+    xv[0][0] = f32x4{v0.x * inv * nv[0].x, v0.y * inv * nv[0].y, v0.z * inv * nv[0].z, v0.w * inv * nv[0].w};
+    xv[0][1] = f32x4{v1.x * inv * nv[1].x, v1.y * inv * nv[1].y, v1.z * inv * nv[1].z, v1.w * inv * nv[1].w};
+  } else {
+    asm volatile("s_waitcnt vmcnt(9)"
+                 : "+v"(xv[0][0]), "+v"(xv[0][1]), "+v"(xv[1][0]), "+v"(xv[1][1]), "+v"(xv[2][0]),
+                   "+v"(xv[2][1]), "+v"(xv[3][0]), "+v"(xv[3][1]));  // x, not the weights
+  }
+#pragma unroll
+  for (int i = 0; i < XC; ++i)
     if ((int)(threadIdx.x & ~63u) + i * (int)blockDim.x < ng * 256)  // wave-uniform
       convert(threadIdx.x + i * blockDim.x, xv[i][0], xv[i][1]);
   __syncthreads();
@@ -1109,9 +1154,10 @@ bool q4k_mfma_pays(int M, int K) {
 // Workgroup: one wave per 8-block group times row-pair streams, with at
 // least one thread per x chunk when 16 waves allow it; as many workgroups
 // as are resident at once (LDS and 16 waves per CU) share the row pairs.
-template <int PAIR>
+template <int PAIR, bool NORM = false>
 void launch_q4k_mfma(const uint8_t* w, const float* x, float* y, int M, int K, hipStream_t stream,
-                     const uint8_t* w2 = nullptr, float* y2 = nullptr) {
+                     const uint8_t* w2 = nullptr, float* y2 = nullptr, const float* res = nullptr,
+                     const float* nrm = nullptr, float* xsum = nullptr, float eps = 0.f) {
   const int nb = K / 256, ng = (nb + 7) / 8;
   const int nw = ng <= 4 ? 4 * ng : ng;
   const size_t a_bytes = (size_t)ng * kQ4gBytes;
@@ -1120,12 +1166,12 @@ void launch_q4k_mfma(const uint8_t* w, const float* x, float* y, int M, int K, h
   const int wgs_target = per_cu * cu_count();
   const int pairs_wg = (pairs + wgs_target - 1) / wgs_target;
   const int rows = 2 * pairs_wg;
-  const size_t shm = (size_t)ng * kQ4gBytes + (size_t)(PAIR ? 2 : 1) * ng * rows * 4;
-  static const hipError_t attr = hipFuncSetAttribute((const void*)q4k_mfma_kernel<PAIR>,
+  const size_t shm = (size_t)ng * kQ4gBytes + (size_t)(PAIR ? 2 : 1) * ng * rows * 4 + (NORM ? 16 * 4 : 0);
+  static const hipError_t attr = hipFuncSetAttribute((const void*)q4k_mfma_kernel<PAIR, NORM>,
                                                      hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
   (void)attr;
-  hipLaunchKernelGGL((q4k_mfma_kernel<PAIR>), dim3((M + rows - 1) / rows), dim3(64 * nw), shm, stream, w, x,
-                     y, M, K, w2, y2, rows);
+  hipLaunchKernelGGL((q4k_mfma_kernel<PAIR, NORM>), dim3((M + rows - 1) / rows), dim3(64 * nw), shm, stream, w,
+                     x, y, M, K, w2, y2, rows, res, nrm, xsum, eps);
 }
 
 template <int QT, int R, int KS, int PAIR = 0>
@@ -1324,6 +1370,23 @@ bool launch_qkv_qt(const uint8_t* wq, const uint8_t* wk, const uint8_t* wv, cons
   if (iters >= 8) launch_direct<QT, 2, 4, 3>(wq, x, yq, Mq, K, stream, wk, yk, wv, yv, Mkv);
   else if (iters >= 4) launch_direct<QT, 2, 2, 3>(wq, x, yq, Mq, K, stream, wk, yk, wv, yv, Mkv);
   else launch_direct<QT, 2, 1, 3>(wq, x, yq, Mq, K, stream, wk, yk, wv, yv, Mkv);
+  return true;
+}
+
+// Residual + RMSNorm folded into the fused gate/up/SiLU GEMV (Q4_K on the
+// matrix cores, K <= 8192): xsum = x + res; y = silu(G n) * (U n) with
+// n = rmsnorm(xsum) * nrm.  false: not this kernel's case (the caller runs
+// the norm and the pair separately).
+bool linear_quant_gate_up_norm_launch(float* y, float* xsum, const float* x, const float* res, const float* nrm,
+                                      float eps, const void* wg, const void* wu, int K, int M, int qtype,
+                                      hipStream_t stream) {
+  const uintptr_t v = (uintptr_t)x | (uintptr_t)res | (uintptr_t)nrm | (uintptr_t)xsum;
+  const uintptr_t a = (uintptr_t)wg | (uintptr_t)wu;
+  if (qtype != HL_GGML_Q4_K || M <= 0 || K <= 0 || K % 256 || K > 8192 || (v & 15) || (a & 15) ||
+      !q4k_mfma_pays(M, K))
+    return false;
+  launch_q4k_mfma<1, true>((const uint8_t*)wg, x, y, M, K, stream, (const uint8_t*)wu, nullptr, res, nrm, xsum,
+                           eps);
   return true;
 }
 

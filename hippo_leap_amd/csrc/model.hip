@@ -218,15 +218,31 @@ static int decode_ffn(const hl_model_desc* m, int l, float* x, float* x_norm, fl
   const hl_layer_desc& L = m->layers[l];
   const int E = m->n_emb;
   const float eps = m->rms_eps;
-  HL_TRY(hl_gpu_residual_rmsnorm(x_norm, x, tmp0, L.ffn_norm, E, eps, stream));
-  if (!pair_launch(1, tmp2, nullptr, x_norm, L.w_gate, L.w_up, L.w_gate_type, L.w_up_type, E, m->n_ff, stream)) {
-    HL_TRY(linear_t(tmp0, x_norm, L.w_gate, L.w_gate_type, E, m->n_ff, 1, stream));
-    HL_TRY(linear_t(tmp1, x_norm, L.w_up, L.w_up_type, E, m->n_ff, 1, stream));
-    HL_TRY(hl_gpu_silu_mul(tmp2, tmp0, tmp1, m->n_ff, stream));
+  // Q4_K gate/up on the matrix cores takes the residual + norm into its own
+  // x prologue; the sum then sits in x_norm until the next residual moves it
+  // back to x.
+  const bool folded = L.w_gate_type == L.w_up_type &&
+                      linear_quant_gate_up_norm_launch(tmp2, x_norm, x, tmp0, L.ffn_norm, eps, L.w_gate, L.w_up, E,
+                                                       m->n_ff, L.w_gate_type, (hipStream_t)stream);
+  if (folded) {
+    if (hipGetLastError() != hipSuccess) return set_error(HL_EHIP, "fused norm gate/up launch failed");
+  } else {
+    HL_TRY(hl_gpu_residual_rmsnorm(x_norm, x, tmp0, L.ffn_norm, E, eps, stream));
+    if (!pair_launch(1, tmp2, nullptr, x_norm, L.w_gate, L.w_up, L.w_gate_type, L.w_up_type, E, m->n_ff, stream)) {
+      HL_TRY(linear_t(tmp0, x_norm, L.w_gate, L.w_gate_type, E, m->n_ff, 1, stream));
+      HL_TRY(linear_t(tmp1, x_norm, L.w_up, L.w_up_type, E, m->n_ff, 1, stream));
+      HL_TRY(hl_gpu_silu_mul(tmp2, tmp0, tmp1, m->n_ff, stream));
+    }
   }
   HL_TRY(linear_t(tmp0, tmp2, L.w_down, L.w_down_type, m->n_ff, E, 1, stream));
-  if (l + 1 < m->n_layer) return hl_gpu_residual_rmsnorm(x_norm, x, tmp0, m->layers[l + 1].attn_norm, E, eps, stream);
-  return hl_gpu_add(x, x, tmp0, E, stream);
+  const float* xs = folded ? x_norm : x;  // the residual stream
+  if (l + 1 < m->n_layer) {
+    if (residual_rmsnorm_from_launch(x_norm, x, xs, tmp0, m->layers[l + 1].attn_norm, E, eps, (hipStream_t)stream) !=
+        hipSuccess)
+      return set_error(HL_EHIP, "residual rmsnorm launch failed");
+    return HL_OK;
+  }
+  return hl_gpu_add(x, xs, tmp0, E, stream);
 }
 
 // The gpuAttentionDecode call of the reference's step for layer l (fp32

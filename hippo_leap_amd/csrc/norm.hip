@@ -77,14 +77,16 @@ __global__ __launch_bounds__(256) void rmsnorm_cols64_kernel(const float* __rest
     }
 }
 
-__global__ __launch_bounds__(256) void residual_rmsnorm_kernel(float* __restrict__ x,
+// x = xin + res (xin may be x), out = rmsnorm(x) * w (out may be xin: each
+// thread reads its own elements of xin before the barrier and writes them
+// after it).
+__global__ __launch_bounds__(256) void residual_rmsnorm_kernel(float* x, const float* xin,
                                                                const float* __restrict__ res,
                                                                const float* __restrict__ w,
-                                                               float* __restrict__ out, int dim,
-                                                               float eps) {
+                                                               float* out, int dim, float eps) {
   float ss = 0.f;
   for (int r = threadIdx.x; r < dim; r += 256) {
-    const float v = x[r] + res[r];
+    const float v = xin[r] + res[r];
     x[r] = v;
     ss += v * v;
   }
@@ -97,11 +99,12 @@ __global__ __launch_bounds__(256) void residual_rmsnorm_kernel(float* __restrict
 // registers for the second pass (the scalar loop above runs ~16 dependent
 // load/store rounds per thread at dim 4096).  The weights are loaded with x,
 // so the kernel waits for memory once.
+// RES: x = xin + res first (xin may be x; out may be xin, as above).
 template <bool RES>
-__global__ __launch_bounds__(1024) void norm_vec4_kernel(float* __restrict__ x,
+__global__ __launch_bounds__(1024) void norm_vec4_kernel(float* x, const float* xin,
                                                          const float* __restrict__ res,
                                                          const float* __restrict__ w,
-                                                         float* __restrict__ out, int dim, float eps) {
+                                                         float* out, int dim, float eps) {
   __shared__ float part[16];
   const int n4 = dim >> 2, tid = threadIdx.x;
   f32x4 v[4], wv[4];
@@ -112,7 +115,7 @@ __global__ __launch_bounds__(1024) void norm_vec4_kernel(float* __restrict__ x,
     v[k] = f32x4{0.f, 0.f, 0.f, 0.f};
     wv[k] = v[k];
     if (c < n4) {
-      v[k] = ((const f32x4*)x)[c];
+      v[k] = ((const f32x4*)xin)[c];
       if (RES) v[k] += ((const f32x4*)res)[c];
       wv[k] = ((const f32x4*)w)[c];
     }
@@ -151,7 +154,7 @@ bool vec4_ok(int dim, const void* a, const void* b, const void* c, const void* d
 hipError_t rmsnorm_cols_launch(float* out, const float* x, const float* w, int dim, int seq,
                                float eps, hipStream_t stream) {
   if (seq == 1 && vec4_ok(dim, x, w, out, out))
-    hipLaunchKernelGGL(norm_vec4_kernel<false>, dim3(1), dim3(1024), 0, stream, const_cast<float*>(x),
+    hipLaunchKernelGGL(norm_vec4_kernel<false>, dim3(1), dim3(1024), 0, stream, const_cast<float*>(x), x,
                        nullptr, w, out, dim, eps);
   else if (seq < 64)
     hipLaunchKernelGGL(rmsnorm_col_kernel, dim3(seq), dim3(256), 0, stream, x, w, out, dim, seq, eps);
@@ -161,13 +164,19 @@ hipError_t rmsnorm_cols_launch(float* out, const float* x, const float* w, int d
   return hipGetLastError();
 }
 
+hipError_t residual_rmsnorm_from_launch(float* out, float* x_dst, const float* x_in, const float* res,
+                                        const float* w, int dim, float eps, hipStream_t stream) {
+  if (vec4_ok(dim, x_dst, res, w, out) && ((uintptr_t)x_in & 15) == 0)
+    hipLaunchKernelGGL(norm_vec4_kernel<true>, dim3(1), dim3(1024), 0, stream, x_dst, x_in, res, w, out, dim, eps);
+  else
+    hipLaunchKernelGGL(residual_rmsnorm_kernel, dim3(1), dim3(256), 0, stream, x_dst, x_in, res, w, out, dim,
+                       eps);
+  return hipGetLastError();
+}
+
 hipError_t residual_rmsnorm_launch(float* out, float* x, const float* res, const float* w, int dim,
                                    float eps, hipStream_t stream) {
-  if (vec4_ok(dim, x, res, w, out))
-    hipLaunchKernelGGL(norm_vec4_kernel<true>, dim3(1), dim3(1024), 0, stream, x, res, w, out, dim, eps);
-  else
-    hipLaunchKernelGGL(residual_rmsnorm_kernel, dim3(1), dim3(256), 0, stream, x, res, w, out, dim, eps);
-  return hipGetLastError();
+  return residual_rmsnorm_from_launch(out, x, x, res, w, dim, eps, stream);
 }
 
 }  // namespace hl

@@ -567,7 +567,8 @@ typedef struct {
  * per layer Q/K/V projections (one launch when the three weights share a
  * quantized type, as K/V pairs and gate/up pairs are), qk-norm, RoPE,
  * K/V store, attention, O projection, residual + ffn norm, gate/up,
- * SiLU * up, down, residual + next layer's norm; final norm, output
+ * SiLU * up (the residual and norm inside the gate/up launch when that runs
+ * Q4_K on the matrix cores), down, residual + next layer's norm; final norm, output
  * projection, argmax.  Sets the process-wide RoPE table
  * (hl_set_rope_theta) on every call: steps of models with different RoPE
  * parameters must not run concurrently (the reference's theta table is
