@@ -559,7 +559,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
-                                   "(sharding is described in DESIGN.md, not built)"}))
+                                   "(multi-GPU sharding is designed but not built)"}))
         sys.exit(2)
 
     import torch
