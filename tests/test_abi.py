@@ -429,3 +429,18 @@ def test_fused_and_elementwise_validation(hl):
     assert hl.hl_gpu_silu_mul(FAKE, FAKE, FAKE, 0, None) == _lib.HL_EINVAL
     assert hl.hl_gpu_silu_mul(FAKE, None, FAKE, 16, None) == _lib.HL_EINVAL
     assert hl.hl_gpu_add(FAKE, FAKE, FAKE, -1, None) == _lib.HL_EINVAL
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py measures one GPU: --gpus above 1 exits with status 2 and one
+    JSON line that says so, before touching a device."""
+    import json
+    import os
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, os.path.join(root, "bench.py"), "--gpus", "2"],
+                       capture_output=True, text=True, timeout=120, cwd=root)
+    assert r.returncode == 2
+    msg = json.loads(r.stdout.strip().splitlines()[-1])
+    assert "one GPU" in msg["error"]
