@@ -156,7 +156,9 @@ def test_linear_col_quant_graph_replay(hl, orc, qt, M, K):
 FUSED = [(12, 14336, 4096), (12, 300, 512), (11, 700, 1024), (13, 2100, 2048), (8, 4096, 4096),
          (14, 900, 768), (1, 300, 512), (20, 333, 1024), (6, 64, 256), (10, 500, 512),
          # four to seven steps per row: each row's blocks split over two waves
-         (14, 2000, 4096), (11, 701, 6144), (10, 333, 4096), (1, 300, 2048)]
+         (14, 2000, 4096), (11, 701, 6144), (10, 333, 4096), (1, 300, 2048),
+         # a Q4_K pair of 2^24 weights per matrix: the matrix-core pair kernel
+         (12, 8192, 2048)]
 
 
 @pytest.mark.parametrize("qt,M,K", FUSED)

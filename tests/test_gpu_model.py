@@ -155,15 +155,18 @@ def test_forward_decode_token_wide_fused_projections(hl, orc, types):
 # Q4_K gate/up of 2^25 weights each: the matrix-core pair kernel with the
 # residual + FFN norm folded into its x prologue (the sum parked in the norm
 # buffer until the next residual moves it back).
+# n_ff 8192: 2^24 weights per matrix, 2^25 for the pair.
 CFG_FFN = dict(CFG, n_emb=2048, n_head=32, n_head_kv=8, n_ff=16384)
 
 
-def test_forward_decode_token_norm_folded_into_gate_up(hl, orc):
+@pytest.mark.parametrize("n_ff", [16384, 8192])
+def test_forward_decode_token_norm_folded_into_gate_up(hl, orc, n_ff):
     from hippo_leap_amd.model import DenseDecoder
     types = {"wq": 12, "wk": 12, "wv": 12, "wo": 12, "w_gate": 12, "w_up": 12, "w_down": 12}
-    print("decode model: norm folded into the Q4_K gate/up", flush=True)
-    dev, ref = _build(orc, CFG_FFN, types, False, 131)
-    m = DenseDecoder(torch, CFG_FFN, dev["tok_emb"], dev["output_norm"], dev["output"],
+    print(f"decode model: norm folded into the Q4_K gate/up, n_ff {n_ff}", flush=True)
+    cfg = dict(CFG_FFN, n_ff=n_ff)
+    dev, ref = _build(orc, cfg, types, False, 131)
+    m = DenseDecoder(torch, cfg, dev["tok_emb"], dev["output_norm"], dev["output"],
                      dev["output_type"], dev["layers"])
     tok = 9
     m.tokens[0] = tok
@@ -171,7 +174,7 @@ def test_forward_decode_token_norm_folded_into_gate_up(hl, orc):
         m.step(pos, m.tokens[0:1], m.tokens[1:2])
         torch.cuda.synchronize()
         logits = m.logits.cpu().numpy()
-        ref_logits = _oracle_step(orc, CFG_FFN, ref, tok, pos)
+        ref_logits = _oracle_step(orc, cfg, ref, tok, pos)
         assert rel_err(logits, ref_logits) < TOL_F32, f"step {pos}"
         tok = int(m.tokens[1].item())
         m.tokens[0] = tok
