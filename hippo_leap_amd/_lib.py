@@ -11,7 +11,7 @@ import os
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(PKG_DIR, "libhl_attn.so")
 
-HL_OK, HL_EINVAL, HL_ECAPACITY, HL_EUNSUPPORTED, HL_EHIP, HL_ECAPTURE, HL_ERANGE = 0, -1, -2, -3, -4, -5, -6
+HL_OK, HL_EINVAL, HL_ECAPACITY, HL_EUNSUPPORTED, HL_EHIP, HL_ECAPTURE = 0, -1, -2, -3, -4, -5
 HL_F32, HL_F16, HL_BF16, HL_FP8 = 0, 1, 2, 3
 HL_ROPE_HALF_SPLIT, HL_ROPE_INTERLEAVED = 0, 1
 HL_KV_COLMAJOR, HL_KV_TILED32, HL_KV_PAGED32 = 0, 1, 2
@@ -180,7 +180,8 @@ SIGNATURES = {
                                c_size_t, c_void_p]),
     "hl_attn_prefill_workspace_bytes": (c_size_t, [ctypes.POINTER(PrefillArgs)]),
     "hl_attn_prefill": (c_int, [ctypes.POINTER(PrefillArgs), c_void_p, c_size_t, c_void_p]),
-    "hl_attn_prefill_range_check": (c_int, [ctypes.POINTER(PrefillArgs), c_void_p, c_void_p]),
+    "hl_attn_prefill_fallback_ran": (c_int, [ctypes.POINTER(PrefillArgs), c_void_p,
+                                             ctypes.POINTER(c_int), c_void_p]),
     "hl_probe_stream_read": (c_int, [c_void_p, c_size_t, c_int, c_void_p, c_void_p]),
     "hl_kv_cache_to_f32": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p]),
 }

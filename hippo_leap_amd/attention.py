@@ -27,7 +27,7 @@ import torch
 from . import _lib
 from ._lib import (HL_BF16, HL_F16, HL_F32, HL_FP8, HL_KV_COLMAJOR, HL_KV_PAGED32,  # noqa: F401
                    HL_KV_TILED32, HL_ROPE_HALF_SPLIT, DecodeArgs, PrefillArgs, RopeStoreArgs,
-                   HL_ERANGE, HL_OK, check)
+                   HL_OK, check)
 
 _DT = {torch.float32: HL_F32, torch.float16: HL_F16, torch.bfloat16: HL_BF16,
        torch.float8_e4m3fn: HL_FP8, torch.uint8: HL_FP8}
@@ -374,15 +374,15 @@ def attn_prefill(args: PrefillArgs, workspace=None, stream=None) -> None:
     check(_lib.load().hl_attn_prefill(ctypes.byref(args), ws, nbytes, _stream(stream)))
 
 
-def prefill_range_check(args: PrefillArgs, workspace=None, stream=None) -> int:
-    """Waits for the stream and returns HL_OK, or HL_ERANGE when the last
-    hl_attn_prefill on `workspace` with these args met an activation beyond
-    the fp16 operand range (other errors raise)."""
+def prefill_fallback_ran(args: PrefillArgs, workspace=None, stream=None) -> bool:
+    """Waits for the stream; True when the last hl_attn_prefill on
+    `workspace` with these args recomputed its output on the fp32 fallback
+    (an fp16 operand would have overflowed)."""
     ws = workspace.data_ptr() if workspace is not None else None
-    rc = _lib.load().hl_attn_prefill_range_check(ctypes.byref(args), ws, _stream(stream))
-    if rc not in (HL_OK, HL_ERANGE):
-        check(rc)
-    return rc
+    ran = ctypes.c_int(0)
+    check(_lib.load().hl_attn_prefill_fallback_ran(ctypes.byref(args), ws, ctypes.byref(ran),
+                                                   _stream(stream)))
+    return bool(ran.value)
 
 
 def probe_stream_read(buf: torch.Tensor, sink: torch.Tensor, blocks: int = 0, stream=None) -> None:
@@ -392,7 +392,7 @@ def probe_stream_read(buf: torch.Tensor, sink: torch.Tensor, blocks: int = 0, st
 
 
 def workspace(nbytes: int, device="cuda") -> torch.Tensor | None:
-    """Allocates a caller-owned workspace (GpuContext.attnScratch's role)."""
+    """Allocates a zero-filled caller-owned workspace (GpuContext.attnScratch's role)."""
     if nbytes <= 0:
         return None
-    return torch.empty(nbytes, dtype=torch.uint8, device=device)
+    return torch.zeros(nbytes, dtype=torch.uint8, device=device)

@@ -12,7 +12,6 @@
 #include <stdio.h>
 #include <string.h>
 
-#include <atomic>
 #include <mutex>
 #include <vector>
 
@@ -707,7 +706,7 @@ struct PrefillPlan {
   bool mfma;
   bool q_in_kernel;  // MFMA kernel builds Q from the raw activations (no qt)
   int t_pad;
-  size_t off_q, off_k, off_v, off_tab, off_range, bytes;
+  size_t off_q, off_k, off_v, off_tab, off_q32, off_k32, off_v32, off_range, bytes;
 };
 
 static int validate_prefill(const hl_prefill_args* a, PrefillPlan* pl) {
@@ -756,7 +755,12 @@ static int validate_prefill(const hl_prefill_args* a, PrefillPlan* pl) {
     pl->off_tab = pl->off_v + (size_t)a->n_head_kv * tp * D * 2;
     pl->bytes = pl->off_tab;
     if (a->apply_rope) pl->bytes += (size_t)T * (rd / 2) * 8;  // (cos, sin) table [rope_dim/2][T]
-    pl->off_range = (pl->bytes + 15) / 16 * 16;  // range record: (call id, id of a call out of range)
+    // fp32 Q, K, V of the fallback pass (col-major, after qkNorm / RoPE)
+    pl->off_q32 = (pl->bytes + 15) / 16 * 16;
+    pl->off_k32 = pl->off_q32 + (size_t)a->n_head * D * T * 4;
+    pl->off_v32 = pl->off_k32 + (size_t)a->n_head_kv * D * T * 4;
+    pl->bytes = pl->off_v32 + (size_t)a->n_head_kv * D * T * 4;
+    pl->off_range = (pl->bytes + 15) / 16 * 16;  // range record: flag, counter, outcome, spare
     pl->bytes = pl->off_range + 16;
   } else {
     pl->t_pad = a->seq_len;
@@ -765,6 +769,7 @@ static int validate_prefill(const hl_prefill_args* a, PrefillPlan* pl) {
     pl->off_k = (pre && !a->write_back_qk) ? (size_t)a->n_head * T * D * 4 : 0;
     pl->off_v = 0;
     pl->off_tab = 0;
+    pl->off_q32 = pl->off_k32 = pl->off_v32 = 0;
     pl->off_range = 0;
     pl->bytes = (pre && !a->write_back_qk) ? pl->off_k + (size_t)a->n_head_kv * T * D * 4 : 0;
   }
@@ -795,6 +800,52 @@ size_t hl_attn_prefill_workspace_bytes(const hl_prefill_args* a) {
   PrefillPlan pl;
   if (validate_prefill(a, &pl)) return 0;
   return pl.bytes;
+}
+
+// Fallback pass of an MFMA prefill, launched after every one: a Q*scale, K
+// or V operand of magnitude >= 65520 has no fp16 form, and the prologue or
+// the flash kernel then sets the range record's flag.  Two gated kernels
+// follow; while the flag is clear each workgroup returns at once.  When it
+// is set, the general prologue writes fp32 Q, K (after qkNorm / RoPE) and V
+// from the original activations, and the fp32 flash kernel recomputes the
+// whole output from them; its last workgroup clears the flag.  The caches
+// were already written with the exact values by the first prologue.
+static int prefill_fallback(const hl_prefill_args* a, const PrefillPlan& pl, const PrologueOp& main_op,
+                            float scale, char* ws, hipStream_t st) {
+  unsigned* record = (unsigned*)(ws + pl.off_range);
+  PrologueOp op = main_op;
+  op.q = a->q;
+  op.k = a->k;
+  op.v = a->v;
+  op.hv_first = 0;
+  op.q_inplace = (float*)(ws + pl.off_q32);
+  op.k_inplace = (float*)(ws + pl.off_k32);
+  op.v_f32 = (float*)(ws + pl.off_v32);
+  op.qt = op.kt = op.vt = nullptr;
+  op.k_cache = op.v_cache = nullptr;
+  op.block_table = nullptr;
+  op.rope_tab_out = nullptr;
+  op.range_word = nullptr;
+  op.t_pad = a->seq_len;
+  op.gate = record;
+  hipError_t e = prologue_launch(op, st);
+  if (e != hipSuccess) return hip_fail(e, "prefill fallback prologue launch");
+  PrefillLaunch pf;
+  memset(&pf, 0, sizeof(pf));
+  pf.q = op.q_inplace;
+  pf.k = op.k_inplace;
+  pf.v = op.v_f32;
+  pf.out = a->out;
+  pf.out_dtype = a->out_dtype;
+  pf.n_head = a->n_head;
+  pf.n_head_kv = a->n_head_kv;
+  pf.head_dim = a->head_dim;
+  pf.seq_len = a->seq_len;
+  pf.t_pad = a->seq_len;
+  pf.scale_log2 = scale * kLog2e;
+  pf.fallback_record = record;
+  e = prefill_f32_launch(pf, st);
+  return e == hipSuccess ? HL_OK : hip_fail(e, "prefill fallback launch");
 }
 
 int hl_attn_prefill(const hl_prefill_args* a, void* workspace, size_t ws_bytes, void* stream) {
@@ -855,13 +906,8 @@ int hl_attn_prefill(const hl_prefill_args* a, void* workspace, size_t ws_bytes, 
       op.hv_first = a->n_head;
     }
     if (a->apply_rope) op.rope_tab_out = (float2*)(ws + pl.off_tab);  // written by the prologue
-    // Call id of the range record: nonzero, different from the previous
-    // call's on any workspace (a process-wide counter).
-    static std::atomic<unsigned> next_id{0};
-    unsigned id = ++next_id;
-    if (id == 0) id = ++next_id;
-    op.range_word = (unsigned*)(ws + pl.off_range);
-    op.range_gen = id;
+    unsigned* record = (unsigned*)(ws + pl.off_range);
+    op.range_word = record;
     if ((e = prologue_launch(op, st)) != hipSuccess) return hip_fail(e, "prefill prologue launch");
     pf.qt = op.qt;
     pf.kt = op.kt;
@@ -875,10 +921,9 @@ int hl_attn_prefill(const hl_prefill_args* a, void* workspace, size_t ws_bytes, 
     pf.rope_dim = rope_dim;
     pf.rope_style = a->rope_style;
     pf.rope_tab = op.rope_tab_out;
-    pf.range_flag = op.range_word + 1;
-    pf.range_gen = id;
-    e = prefill_mfma_launch(pf, st);
-    return e == hipSuccess ? HL_OK : hip_fail(e, "prefill launch");
+    pf.range_flag = record;
+    if ((e = prefill_mfma_launch(pf, st)) != hipSuccess) return hip_fail(e, "prefill launch");
+    return prefill_fallback(a, pl, op, scale, ws, st);
   }
   // fp32: normed/roped q,k either in place or in the workspace
   const bool pre = a->apply_rope || a->q_norm_w || a->k_norm_w;
@@ -907,24 +952,24 @@ int hl_attn_prefill(const hl_prefill_args* a, void* workspace, size_t ws_bytes, 
   return e == hipSuccess ? HL_OK : hip_fail(e, "prefill launch");
 }
 
-int hl_attn_prefill_range_check(const hl_prefill_args* a, const void* workspace, void* stream) {
+int hl_attn_prefill_fallback_ran(const hl_prefill_args* a, const void* workspace, int* ran, void* stream) {
   PrefillPlan pl;
   int rc = validate_prefill(a, &pl);
   if (rc) return rc;
+  if (!ran) return fail(HL_EINVAL, "prefill fallback query: ran is null");
+  *ran = 0;
   if (!pl.mfma) return HL_OK;
-  if (!workspace) return fail(HL_EINVAL, "prefill range check: workspace is null");
+  if (!workspace) return fail(HL_EINVAL, "prefill fallback query: workspace is null");
   hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
   hipError_t e = hipStreamIsCapturing(as_stream(stream), &cs);
   if (e != hipSuccess) return hip_fail(e, "hipStreamIsCapturing");
   if (cs != hipStreamCaptureStatusNone)
-    return fail(HL_ECAPTURE, "prefill range check waits for the stream; it cannot run under stream capture");
-  if ((e = hipStreamSynchronize(as_stream(stream))) != hipSuccess) return hip_fail(e, "prefill range check sync");
-  unsigned w[2] = {0u, 0u};
+    return fail(HL_ECAPTURE, "prefill fallback query waits for the stream; it cannot run under stream capture");
+  if ((e = hipStreamSynchronize(as_stream(stream))) != hipSuccess) return hip_fail(e, "prefill fallback query sync");
+  unsigned w[4] = {0u, 0u, 0u, 0u};
   if ((e = hipMemcpy(w, (const char*)workspace + pl.off_range, sizeof(w), hipMemcpyDeviceToHost)) != hipSuccess)
-    return hip_fail(e, "prefill range check read");
-  if (w[0] != 0u && w[1] == w[0])
-    return fail(HL_ERANGE, "prefill: an activation (q*scale, k or v after qkNorm/RoPE) reached 65520, beyond the "
-                           "fp16 operands of the bf16/fp16 path; use fp32 activations for this input");
+    return hip_fail(e, "prefill fallback query read");
+  *ran = w[2] != 0u ? 1 : 0;
   return HL_OK;
 }
 

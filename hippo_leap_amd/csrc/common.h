@@ -37,6 +37,17 @@ __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
 // Smallest magnitude that rounds (RNE) to an fp16 infinity.
 constexpr float kF16Inf = 65520.0f;
 
+// Range record of an fp16-operand prefill (four words in the workspace):
+// [0] overflow flag, [1] arrival counter of the fallback pass, [2] whether
+// the last call took the fallback.  Agent-scope atomics: the words are read
+// by later kernels of the call on any XCD.
+__device__ __forceinline__ void range_flag_set(unsigned* rec) {
+  __hip_atomic_store(rec, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void range_counter_reset(unsigned* rec) {
+  __hip_atomic_store(rec + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 __device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
   _Float16 h = (_Float16)f;  // v_cvt_f16_f32 under the default RNE mode
   return __builtin_bit_cast(uint16_t, h);

@@ -75,6 +75,7 @@ struct PrologueOp {
   int io_dtype;
   float* q_inplace;   // fp32 write-back targets (may alias q/k) or null
   float* k_inplace;
+  float* v_f32;       // fp32 copy of v (col-major [Hkv*D, T]) or null
   uint16_t* qt;       // MFMA layouts (fp16 bits) or null
   uint16_t* kt;
   uint16_t* vt;
@@ -95,11 +96,15 @@ struct PrologueOp {
   ThetaTable theta;
   float2* rope_tab_out;  // optional: receives the (cos, sin) table [rope_dim/2][seq_len] of
                          // positions start_pos + t (rope_dim/2 <= 64)
-  // Range record of the fp16 operands (qt / kt / vt): workgroup (0, 0)
-  // stores range_gen to range_word[0]; a thread whose operand value has
-  // magnitude >= kF16Inf stores it to range_word[1].  Null: not recorded.
+  // Range record of the fp16 operands (qt / kt / vt), four words: [0] the
+  // overflow flag, [1] the fallback's arrival counter, [2] whether the last
+  // call took the fallback.  Workgroup (0, 0) zeroes the counter; a thread
+  // whose operand value has magnitude >= kF16Inf sets the flag.  Null: not
+  // recorded.
   unsigned* range_word;
-  unsigned range_gen;
+  // Fallback pass: non-null -> every workgroup returns at once unless
+  // gate[0] (the overflow flag) is set.
+  const unsigned* gate;
 };
 hipError_t prologue_launch(const PrologueOp& op, hipStream_t stream);
 
@@ -135,9 +140,14 @@ struct PrefillLaunch {
   int do_rope, rope_dim, rope_style;
   const float2* rope_tab;  // [rope_dim/2][seq_len]
   // Q built in the kernel: a lane whose Q operand value (q * scale, after
-  // qkNorm / RoPE) has magnitude >= kF16Inf stores range_gen to *range_flag.
+  // qkNorm / RoPE) has magnitude >= kF16Inf sets *range_flag.
   unsigned* range_flag;
-  unsigned range_gen;
+  // fp32 kernel as the fallback pass of an MFMA prefill: the range record
+  // (see PrologueOp).  Each workgroup reads the flag and counts itself in;
+  // the last one to arrive stores the flag to word 2 and clears words 0 and
+  // 1, so the record is clean for the next call.  Workgroups return at once
+  // when the flag is clear.
+  unsigned* fallback_record;
 };
 hipError_t prefill_f32_launch(const PrefillLaunch& p, hipStream_t stream);
 hipError_t prefill_mfma_launch(const PrefillLaunch& p, hipStream_t stream);

@@ -54,7 +54,6 @@ struct MfmaPrefillParams {
   int do_rope, rope_dim, rope_style;
   const float2* rope_tab;  // [rope_dim/2][T] (cos, sin)
   unsigned* range_flag;    // see PrefillLaunch
-  unsigned range_gen;
 };
 
 __device__ __forceinline__ f32x16 mma32(f16x8 a, f16x8 b, f32x16 c) {
@@ -178,7 +177,7 @@ __device__ __forceinline__ void build_q(const MfmaPrefillParams& p, int hq, int 
       qmax = fmaxf(qmax, fabsf(y));
       qf[k][e] = (_Float16)y;
     }
-  if (qmax >= kF16Inf && p.range_flag) *p.range_flag = p.range_gen;
+  if (qmax >= kF16Inf && p.range_flag) range_flag_set(p.range_flag);
 }
 
 // Ping-pong flash kernel.  A workgroup has 8 waves, two per SIMD (waves w
@@ -514,7 +513,6 @@ hipError_t prefill_mfma_launch(const PrefillLaunch& a, hipStream_t stream) {
   p.rope_style = a.rope_style;
   p.rope_tab = a.rope_tab;
   p.range_flag = a.range_flag;
-  p.range_gen = a.range_gen;
   const int qin = a.qt ? 0 : a.io_dtype;
   dim3 grid(a.n_head_kv * p.n_hgrp * p.n_qblk);
 #define HL_PF(DD, OD, QI) hipLaunchKernelGGL((prefill_mfma_kernel<DD, OD, QI>), grid, dim3(512), 0, stream, p)
@@ -577,6 +575,25 @@ __global__ __launch_bounds__(256) void prefill_f32mfma_kernel(PrefillLaunch p, i
   __shared__ __attribute__((aligned(16))) float sv[KSPLIT * SVN];  // [tile][h][d][ks]
 
   const int tid = threadIdx.x, lane = tid & 63;
+  if (p.fallback_record) {
+    // Fallback pass of an MFMA prefill: read the overflow flag, count this
+    // workgroup in; the last to arrive (every workgroup has read the flag by
+    // then) records the outcome and clears the flag and counter.
+    __shared__ unsigned s_go;
+    if (tid == 0) {
+      unsigned* rec = p.fallback_record;
+      const unsigned go = __hip_atomic_load(rec, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const unsigned n = __hip_atomic_fetch_add(rec + 1, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+      if (n + 1 == gridDim.x) {
+        __hip_atomic_store(rec + 2, go != 0u ? 1u : 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(rec, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(rec + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      s_go = go;
+    }
+    __syncthreads();
+    if (s_go == 0u) return;
+  }
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int ln = lane & 31, hh = lane >> 5;
   const int T = p.seq_len;
@@ -774,13 +791,17 @@ __global__ __launch_bounds__(256) void prefill_f32mfma_kernel(PrefillLaunch p, i
   if (!live) return;
   const float inv = 1.0f / l;
   if (t_abs < T) {
-    float* O = (float*)p.out + (long long)hq * D * T;
+    // fp32 output, or fp16 / bf16 when this is the fallback of an MFMA prefill
+    const long long ob = (long long)hq * D * T + t_abs;
 #pragma unroll
     for (int db = 0; db < DB; ++db)
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int d = 32 * db + 8 * (i >> 2) + 4 * hh + (i & 3);
-        O[(long long)d * T + t_abs] = o[db][i] * inv;
+        const float y = o[db][i] * inv;
+        if (p.out_dtype == HL_F16) store_elem<HL_F16>(p.out, ob + (long long)d * T, y);
+        else if (p.out_dtype == HL_BF16) store_elem<HL_BF16>(p.out, ob + (long long)d * T, y);
+        else ((float*)p.out)[ob + (long long)d * T] = y;
       }
   }
 }

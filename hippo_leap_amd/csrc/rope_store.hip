@@ -201,7 +201,8 @@ __device__ __forceinline__ void store_cache8(void* cache, const CacheMap& m, int
 template <int IODT, int KDT, int DMAX>
 __global__ __launch_bounds__(256) void prologue_kernel(PrologueOp op) {
   __shared__ float sx[DMAX][kPT + 1];  // DMAX >= head_dim: the tile, sized to its class
-  if (op.range_word && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) op.range_word[0] = op.range_gen;
+  if (op.gate && __hip_atomic_load(op.gate, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u) return;
+  if (op.range_word && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) range_counter_reset(op.range_word);
   __shared__ float scos[kTabHalf][kPT], ssin[kTabHalf][kPT];
   __shared__ float sred[8][kPT];
   __shared__ float sinv[kPT];
@@ -332,7 +333,7 @@ __global__ __launch_bounds__(256) void prologue_kernel(PrologueOp op) {
     }
 
     // row-wise outputs: fp32 write-back in place, KV-cache columns start_pos + t
-    float* inplace = kind == 0 ? op.q_inplace : (kind == 1 ? op.k_inplace : nullptr);
+    float* inplace = kind == 0 ? op.q_inplace : (kind == 1 ? op.k_inplace : op.v_f32);
     void* cache = kind == 1 ? op.k_cache : (kind == 2 ? op.v_cache : nullptr);
     if (inplace || cache) {
       for (int r = tid >> 2; r < D; r += 64) {
@@ -380,7 +381,7 @@ __global__ __launch_bounds__(256) void prologue_kernel(PrologueOp op) {
         store_row8<HL_F16>(op.vt, ((long long)h * D + r) * op.t_pad + t0 + c8, t0 + c8, op.t_pad, x);
       }
     }
-    if (omax >= kF16Inf && op.range_word) op.range_word[1] = op.range_gen;
+    if (omax >= kF16Inf && op.range_word) range_flag_set(op.range_word);
   }
 }
 
@@ -420,7 +421,7 @@ __global__ __launch_bounds__(256) void kv_prologue_kernel(PrologueOp op) {
   const int r = tid / CPR, c8 = (tid % CPR) * 8;
   const int t = t0 + c8;  // this thread's first token
   const long long hbase = (long long)h * D * T;
-  if (op.range_word && blockIdx.x == 0 && h == 0 && tid == 0) op.range_word[0] = op.range_gen;
+  if (op.range_word && blockIdx.x == 0 && h == 0 && tid == 0) range_counter_reset(op.range_word);
 
   float k[NP][8], v[NP][8];
 #pragma unroll
@@ -532,7 +533,7 @@ __global__ __launch_bounds__(256) void kv_prologue_kernel(PrologueOp op) {
       skt[c8 + e][row ^ kt_swz(c8 + e)] = f32_to_f16_bits(x);
     }
   }
-  if (omax >= kF16Inf && op.range_word) op.range_word[1] = op.range_gen;
+  if (omax >= kF16Inf && op.range_word) range_flag_set(op.range_word);
   __syncthreads();
   constexpr int CH = D / 8;  // 16-byte chunks per token row
   for (int idx = tid; idx < PT * CH; idx += 256) {
@@ -576,7 +577,8 @@ hipError_t prologue_launch(const PrologueOp& op, hipStream_t stream) {
   // prefills share one cos/sin table fill across heads.
   PrologueOp o2 = op;
   o2.hpg = kHPG;
-  while (o2.hpg > 1 && (long long)tiles * ((n_vec + o2.hpg - 1) / o2.hpg) < 2048) o2.hpg >>= 1;
+  // A gated fallback pass usually exits at once: fewest workgroups.
+  while (!op.gate && o2.hpg > 1 && (long long)tiles * ((n_vec + o2.hpg - 1) / o2.hpg) < 2048) o2.hpg >>= 1;
   dim3 grid(tiles, (n_vec + o2.hpg - 1) / o2.hpg);
 #define HL_PRO(IO, KD)                                                                          \
   if (op.head_dim <= 128) hipLaunchKernelGGL((prologue_kernel<IO, KD, 128>), grid, dim3(256), 0, stream, o2); \

@@ -47,9 +47,7 @@ enum {
   HL_ECAPACITY = -2,     /* KV cache full, prefill longer than max_len      */
   HL_EUNSUPPORTED = -3,  /* dtype / head_dim combination not built          */
   HL_EHIP = -4,          /* HIP runtime error (launch, device query)         */
-  HL_ECAPTURE = -5,      /* would allocate while the stream is being captured */
-  HL_ERANGE = -6         /* a bf16/fp16 prefill met an activation beyond the
-                            fp16 operand range (hl_attn_prefill_range_check) */
+  HL_ECAPTURE = -5       /* would allocate while the stream is being captured */
 };
 
 /* ---- element types of activations and KV cache ------------------------- */
@@ -454,18 +452,23 @@ int hl_attn_prefill(const hl_prefill_args* a, void* workspace, size_t ws_bytes,
                     void* stream);
 
 /* The MFMA prefill (bf16/fp16 activations) rounds Q * scale, K and V, after
- * qkNorm and RoPE, to fp16 operands: a value of magnitude >= 65520 has no
- * fp16 form, and the output of such a call is not valid (inf/NaN where the
- * value is used).  The kernels record such a value, at no cost to the
- * computation, in the call's workspace; this function waits for `stream`
- * (the one the prefill ran on), reads the record of the last
- * hl_attn_prefill on `workspace` with these args and returns HL_ERANGE if
- * it met such a value, HL_OK if not (always for fp32 activations, whose
- * path has no such limit; the reference computes in fp32,
- * naive.nim:3385-3464).  Under stream capture it returns HL_ECAPTURE.
- * No counterpart in the reference; callers with bf16 activations that may
- * exceed fp16's range check each call, or use fp32 activations.           */
-int hl_attn_prefill_range_check(const hl_prefill_args* a, const void* workspace, void* stream);
+ * qkNorm and RoPE, to fp16 operands.  A value of magnitude >= 65520 has no
+ * fp16 form; the kernels record such a value in the call's workspace, and
+ * two gated kernels that every MFMA prefill launches after its flash kernel
+ * then recompute the whole output from the original activations in fp32
+ * (fp32 operands and accumulation, as the reference's fp32 prefill,
+ * naive.nim:3385-3464).  While nothing overflows they return at once.  So
+ * hl_attn_prefill's output is valid over the whole range of its inputs with
+ * no call to this function, also under stream capture.  This function only
+ * reports, for tests and diagnostics, whether the last hl_attn_prefill on
+ * `workspace` with these args took that fallback: it waits for `stream`
+ * and sets *ran to 1 or 0 (always 0 for fp32 activations).  Under stream
+ * capture it returns HL_ECAPTURE.  No counterpart in the reference.
+ * A workspace whose record holds stale nonzero bytes (never used by a
+ * prefill, not zero-filled) can send its first call through the fallback:
+ * the result is the same, only slower.                                   */
+int hl_attn_prefill_fallback_ran(const hl_prefill_args* a, const void* workspace, int* ran,
+                                 void* stream);
 
 /* Reads cache columns [col0, col0+ncols) of a [rows, max_len] cache of
  * kv_dtype into fp32 dst[rows, ncols] (exact upcast; halfToFloat semantics,

@@ -117,16 +117,18 @@ def test_prefill_gqa(hl):
 def test_prefill_workspace_size(hl):
     a = _prefill_args()
     # kt [Hkv][T][D] + vt [Hkv][D][T] fp16 (the MFMA kernel builds Q itself),
-    # then the 16-byte range record of the call
-    assert hl.hl_attn_prefill_workspace_bytes(ctypes.byref(a)) == (8 + 8) * 4096 * 128 * 2 + 16
+    # the fallback's fp32 Q, K, V ([Hq*D, T], [Hkv*D, T] x 2), then the
+    # 16-byte range record of the call
+    fb = (32 + 8 + 8) * 4096 * 128 * 4
+    assert hl.hl_attn_prefill_workspace_bytes(ctypes.byref(a)) == (8 + 8) * 4096 * 128 * 2 + fb + 16
     # with RoPE: plus the (cos, sin) table [rope_dim/2][T] of float2
     r = _prefill_args(apply_rope=1, rope_base=5e5)
     assert hl.hl_attn_prefill_workspace_bytes(ctypes.byref(r)) == \
-        (8 + 8) * 4096 * 128 * 2 + 4096 * 64 * 8 + 16
+        (8 + 8) * 4096 * 128 * 2 + 4096 * 64 * 8 + fb + 16
     # half-split RoPE over part of the head: Q is prepared ahead, qt [Hq][T][D]
     h = _prefill_args(apply_rope=1, rope_base=5e5, rope_dim=64)
     assert hl.hl_attn_prefill_workspace_bytes(ctypes.byref(h)) == \
-        (32 + 8 + 8) * 4096 * 128 * 2 + 4096 * 32 * 8 + 16
+        (32 + 8 + 8) * 4096 * 128 * 2 + 4096 * 32 * 8 + fb + 16
     f = _prefill_args(io_dtype=_lib.HL_F32)
     assert hl.hl_attn_prefill_workspace_bytes(ctypes.byref(f)) == 0  # no fused ops: none needed
 

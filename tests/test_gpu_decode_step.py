@@ -178,3 +178,78 @@ def test_decode_step_graph_replay(hl, orc):
         g.replay()
         torch.cuda.synchronize()
         assert np.array_equal(out.cpu().numpy(), eager)
+
+
+@pytest.mark.parametrize("layout", [0, 1])
+def test_decode_step_c5_full_shape(hl, orc, layout):
+    """Config 5's fused step at full size, as bench.py times it: B=16,
+    Hq32/Hkv4, D128, bf16 caches, qkNorm (w ~ U(0.5, 1.5) seeded, eps 1e-6)
+    then RoPE theta 1e6 at position 32768 (angles up to 3.3e4 rad), the cache
+    write, then attention over 32769 columns (naive.nim:2887-2926, 3046-3086,
+    3149-3223, 3292-3383).  Column-major (max_len 32769) and tiled (32800)
+    caches.  The oracle checks sequences 0 and 15 in full: the written
+    column within one bf16 ulp of the oracle's rounded value (the device
+    and glibc sincosf differ by a few fp32 ulps, which can move an RNE
+    rounding by one step) and the outputs within 2e-3.  Every sequence's
+    written column equals the two-call path's bit for bit."""
+    from hippo_leap_amd import attention as A
+    B, hq, hkv, d, pos, dt = 16, 32, 4, 128, 32768, 2
+    M = 32769 if layout == 0 else 32800
+    print(f"c5 full step layout {layout}", flush=True)
+    gen = torch.Generator(device="cuda").manual_seed(3100 + layout)
+    per = hkv * d * M
+    kc0 = torch.randn(B * per, generator=gen, device="cuda").to(torch.bfloat16)
+    vc0 = torch.randn(B * per, generator=gen, device="cuda").to(torch.bfloat16)
+    host_k = {b: kc0[b * per:(b + 1) * per].view(torch.int16).cpu().numpy().view(np.uint16)
+              for b in (0, B - 1)}
+    host_v = {b: vc0[b * per:(b + 1) * per].view(torch.int16).cpu().numpy().view(np.uint16)
+              for b in (0, B - 1)}
+    qa, ka, va = orc.normal(B * hq * d, 3101), orc.normal(B * hkv * d, 3102), orc.normal(B * hkv * d, 3103)
+    wq, wk = orc.uniform(d, 3104, 0.5, 1.5), orc.uniform(d, 3105, 0.5, 1.5)
+    base = 1e6
+
+    def new_column(cache):
+        c = cache if layout == 0 else A.kv_from_tiled(cache, hkv, d, M)
+        return c.view(B, hkv * d, M)[:, :, pos].contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+    results = []
+    for fused in (True, False):
+        kc = kc0.clone() if layout == 0 else A.kv_to_tiled(kc0, hkv, d, M)
+        vc = vc0.clone() if layout == 0 else A.kv_to_tiled(vc0, hkv, d, M)
+        qd, kd, vd = dev(qa), dev(ka), dev(va)
+        out = torch.full((B * hq * d,), float("nan"), device="cuda")
+        rs = A.rope_store_args(qd, kd, vd, kc, vc, hq, hkv, d, M, pos, base,
+                               q_norm_w=dev(wq), k_norm_w=dev(wk), eps=1e-6, kv_layout=layout)
+        at = A.decode_args(qd, kc, vc, out, hq, hkv, d, M, pos + 1, kv_layout=layout)
+        if fused:
+            A.decode_step(rs, at, A.decode_step_workspace(rs, at))
+        else:
+            A.rope_store_decode(qd, kd, vd, kc, vc, hq, hkv, d, M, pos, base,
+                                q_norm_w=dev(wq), k_norm_w=dev(wk), eps=1e-6, kv_layout=layout)
+            A.attn_decode(at, A.decode_workspace(at))
+        torch.cuda.synchronize()
+        results.append((out.cpu().numpy(), new_column(kc), new_column(vc)))
+        del kc, vc
+    (fo, fk, fv), (so, sk, sv) = results
+    assert np.array_equal(fk, sk) and np.array_equal(fv, sv)
+    assert rel_err(fo, so) < 1e-5
+
+    th = orc.theta_table(d, base)
+    for b in (0, B - 1):
+        qb = orc.rope_heads(orc.qk_norm(qa[b * hq * d:(b + 1) * hq * d], wq, hq, d, 1e-6),
+                            hq, d, d, th, pos)
+        kb = orc.rope_heads(orc.qk_norm(ka[b * hkv * d:(b + 1) * hkv * d], wk, hkv, d, 1e-6),
+                            hkv, d, d, th, pos)
+        kcol = orc.to_storage(kb, dt)
+        vcol = orc.to_storage(va[b * hkv * d:(b + 1) * hkv * d], dt)
+        assert np.array_equal(fv[b], vcol)
+        ulps = np.abs(fk[b].astype(np.int32) - kcol.astype(np.int32))
+        assert ulps.max() <= 1 and (ulps > 0).mean() < 0.01, f"seq {b}: k column off by {ulps.max()} ulp"
+        kf = orc.upcast(host_k[b], dt).reshape(hkv * d, M).copy()
+        vf = orc.upcast(host_v[b], dt).reshape(hkv * d, M).copy()
+        kf[:, pos] = orc.upcast(kcol, dt)
+        vf[:, pos] = orc.upcast(vcol, dt)
+        ref = orc.attention_decode(qb, kf.reshape(-1), vf.reshape(-1), hq, hkv, d, pos + 1, M)
+        err = rel_err(fo[b * hq * d:(b + 1) * hq * d], ref)
+        print(f"c5 step layout {layout} seq {b} rel err {err:.3e}", flush=True)
+        assert err < TOL_LOWP

@@ -181,3 +181,33 @@ def test_kv_cache_to_f32_kat(hl, orc, dt):
     assert np.array_equal(out[~nan], ref[~nan])
     if dt == 1:
         assert list(out[:7]) == [0.0, 1.0, -1.0, 2.0, 0.5, np.inf, -np.inf] and np.isnan(out[7])
+
+
+@pytest.mark.parametrize("pos", [8191, 32768, 131071])
+def test_rope_dropins_large_positions(hl, orc, pos):
+    """RoPE at long-context positions (angles up to 1.3e5 rad, where the
+    argument reduction of sincosf matters), theta 1e6 and 5e5, against the
+    oracle's glibc cosf/sinf of the same fp32 angle.  The theta table is
+    installed first: hl_gpu_rope_qk_decode then uses it and ignores its
+    rope_base argument, as ropeQKDecodeKernel does (naive.nim:3046-3086)."""
+    from hippo_leap_amd import attention as A
+    H, D = 8, 128
+    for base in (1e6, 5e5):
+        th = orc.theta_table(D, base)
+        A.set_rope_theta(D, base)
+        q, k = orc.normal(H * D, 40 + pos % 7), orc.normal(2 * D, 41 + pos % 5)
+        qd, kd = dev(q), dev(k)
+        A.gpu_rope_qk_decode(qd, kd, H, 2, D, D, base, pos)
+        torch.cuda.synchronize()
+        assert rel_err(host(qd), orc.rope_heads(q, H, D, D, th, pos)) < ROPE_TOL
+        assert rel_err(host(kd), orc.rope_heads(k, 2, D, D, th, pos)) < ROPE_TOL
+        xd = dev(q)
+        A.gpu_rope_at_pos(xd, H, D, D, base, pos, 1)
+        torch.cuda.synchronize()
+        assert rel_err(host(xd), orc.rope_heads(q, H, D, D, th, pos)) < ROPE_TOL
+        T = 16
+        xc = orc.normal(H * D * T, 42).reshape(H * D, T)
+        xcd = dev(xc)
+        A.gpu_rope_at_pos_theta(xcd, H, D, D, pos - T, T)  # columns at pos-16 .. pos-1
+        torch.cuda.synchronize()
+        assert rel_err(host(xcd), orc.rope_cols(xc, H, D, T, D, th, pos - T)) < ROPE_TOL
