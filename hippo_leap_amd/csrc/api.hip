@@ -760,7 +760,7 @@ static int validate_prefill(const hl_prefill_args* a, PrefillPlan* pl) {
     pl->off_k32 = pl->off_q32 + (size_t)a->n_head * D * T * 4;
     pl->off_v32 = pl->off_k32 + (size_t)a->n_head_kv * D * T * 4;
     pl->bytes = pl->off_v32 + (size_t)a->n_head_kv * D * T * 4;
-    pl->off_range = (pl->bytes + 15) / 16 * 16;  // range record: flag, counter, outcome, spare
+    pl->off_range = (pl->bytes + 15) / 16 * 16;  // range record: mark, generation, staged generation, outcome
     pl->bytes = pl->off_range + 16;
   } else {
     pl->t_pad = a->seq_len;
@@ -808,7 +808,8 @@ size_t hl_attn_prefill_workspace_bytes(const hl_prefill_args* a) {
 // follow; while the flag is clear each workgroup returns at once.  When it
 // is set, the general prologue writes fp32 Q, K (after qkNorm / RoPE) and V
 // from the original activations, and the fp32 flash kernel recomputes the
-// whole output from them; its last workgroup clears the flag.  The caches
+// whole output from them; its workgroup 0 advances the record's generation,
+// which retires this call's mark.  The caches
 // were already written with the exact values by the first prologue.
 static int prefill_fallback(const hl_prefill_args* a, const PrefillPlan& pl, const PrologueOp& main_op,
                             float scale, char* ws, hipStream_t st) {
@@ -969,7 +970,7 @@ int hl_attn_prefill_fallback_ran(const hl_prefill_args* a, const void* workspace
   unsigned w[4] = {0u, 0u, 0u, 0u};
   if ((e = hipMemcpy(w, (const char*)workspace + pl.off_range, sizeof(w), hipMemcpyDeviceToHost)) != hipSuccess)
     return hip_fail(e, "prefill fallback query read");
-  *ran = w[2] != 0u ? 1 : 0;
+  *ran = w[3] != 0u ? 1 : 0;
   return HL_OK;
 }
 

@@ -37,16 +37,19 @@ __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
 // Smallest magnitude that rounds (RNE) to an fp16 infinity.
 constexpr float kF16Inf = 65520.0f;
 
-// Range record of an fp16-operand prefill (four words in the workspace):
-// [0] overflow flag, [1] arrival counter of the fallback pass, [2] whether
-// the last call took the fallback.  Agent-scope atomics: the words are read
-// by later kernels of the call on any XCD.
-__device__ __forceinline__ void range_flag_set(unsigned* rec) {
-  __hip_atomic_store(rec, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void range_counter_reset(unsigned* rec) {
-  __hip_atomic_store(rec + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
+// Range record of an fp16-operand prefill: four words in the workspace,
+// written and read only by the kernels of the prefill's launch sequence.
+// Each word is written in a kernel where no other workgroup reads it, so
+// stream order alone orders every access (plain loads and stores: a later
+// kernel sees an earlier kernel's stores).
+//   [0] F  overflow mark: G + 1 when this call met an operand >= 65520
+//   [1] G  call generation, advanced by the last kernel of each call
+//   [2] S  G + 1, staged by the fallback prologue for the fallback kernel
+//   [3] O  1 when the last call took the fallback, else 0
+// A stale F (from an earlier call) differs from G + 1 because G has moved
+// on since; a zero-filled record reads as "no overflow".
+// An operand of this call overflowed fp16 (prologue and flash kernel).
+__device__ __forceinline__ void range_flag_set(unsigned* rec) { rec[0] = rec[1] + 1u; }
 
 __device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
   _Float16 h = (_Float16)f;  // v_cvt_f16_f32 under the default RNE mode

@@ -93,18 +93,17 @@ struct PrologueOp {
   int t_pad;          // row count of qt/kt/vt (seq_len rounded up); pad rows zeroed
   int hv_first;       // first head vector processed (n_head: k and v heads only)
   int hpg;            // head vectors per workgroup (set by prologue_launch)
+  int n_tiles, n_hgrps;  // work items: 32-token tiles x head groups (set by prologue_launch)
   ThetaTable theta;
   float2* rope_tab_out;  // optional: receives the (cos, sin) table [rope_dim/2][seq_len] of
                          // positions start_pos + t (rope_dim/2 <= 64)
-  // Range record of the fp16 operands (qt / kt / vt), four words: [0] the
-  // overflow flag, [1] the fallback's arrival counter, [2] whether the last
-  // call took the fallback.  Workgroup (0, 0) zeroes the counter; a thread
-  // whose operand value has magnitude >= kF16Inf sets the flag.  Null: not
-  // recorded.
+  // Range record of the fp16 operands (qt / kt / vt): see range_flag_set in
+  // common.h.  A thread whose operand value has magnitude >= kF16Inf marks
+  // it.  Null: not recorded.
   unsigned* range_word;
   // Fallback pass: non-null -> every workgroup returns at once unless
   // gate[0] (the overflow flag) is set.
-  const unsigned* gate;
+  unsigned* gate;
 };
 hipError_t prologue_launch(const PrologueOp& op, hipStream_t stream);
 
@@ -142,11 +141,9 @@ struct PrefillLaunch {
   // Q built in the kernel: a lane whose Q operand value (q * scale, after
   // qkNorm / RoPE) has magnitude >= kF16Inf sets *range_flag.
   unsigned* range_flag;
-  // fp32 kernel as the fallback pass of an MFMA prefill: the range record
-  // (see PrologueOp).  Each workgroup reads the flag and counts itself in;
-  // the last one to arrive stores the flag to word 2 and clears words 0 and
-  // 1, so the record is clean for the next call.  Workgroups return at once
-  // when the flag is clear.
+  // fp32 kernel as the fallback pass of an MFMA prefill: the range record.
+  // Workgroups return at once unless the call's overflow mark is set;
+  // workgroup 0 advances the record's generation (common.h).
   unsigned* fallback_record;
 };
 hipError_t prefill_f32_launch(const PrefillLaunch& p, hipStream_t stream);

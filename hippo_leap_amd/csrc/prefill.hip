@@ -576,23 +576,22 @@ __global__ __launch_bounds__(256) void prefill_f32mfma_kernel(PrefillLaunch p, i
 
   const int tid = threadIdx.x, lane = tid & 63;
   if (p.fallback_record) {
-    // Fallback pass of an MFMA prefill: read the overflow flag, count this
-    // workgroup in; the last to arrive (every workgroup has read the flag by
-    // then) records the outcome and clears the flag and counter.
+    // Fallback pass of an MFMA prefill: runs only when the call's overflow
+    // mark F equals the staged S; workgroup 0 then advances the generation
+    // (G = S, which nothing else in this kernel reads) and records the outcome.
     __shared__ unsigned s_go;
     if (tid == 0) {
       unsigned* rec = p.fallback_record;
-      const unsigned go = __hip_atomic_load(rec, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      const unsigned n = __hip_atomic_fetch_add(rec + 1, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-      if (n + 1 == gridDim.x) {
-        __hip_atomic_store(rec + 2, go != 0u ? 1u : 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(rec, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(rec + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const unsigned sg = rec[2];
+      const unsigned go = rec[0] == sg;
+      if (blockIdx.x == 0) {
+        rec[1] = sg;
+        rec[3] = go;
       }
       s_go = go;
     }
     __syncthreads();
-    if (s_go == 0u) return;
+    if (!s_go) return;
   }
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int ln = lane & 31, hh = lane >> 5;
@@ -605,204 +604,209 @@ __global__ __launch_bounds__(256) void prefill_f32mfma_kernel(PrefillLaunch p, i
   const int n_qblk = (T + rows_wg - 1) / rows_wg;
   const int n_hgrp = group / nh;
   const int per_q = p.n_head_kv * n_hgrp;
-  const int item = blockIdx.x;
-  const int qblk = n_qblk - 1 - item / per_q;  // heaviest query blocks first
-  const int kvh = (item % per_q) / n_hgrp;
-  const int hgrp = (item % per_q) % n_hgrp;
-  const int hq = kvh * group + hgrp * nh + wave % nh;
-  const int r0 = qblk * rows_wg + ((wave / nh) % RB) * 32;
-  const int wg_last_row = min(T - 1, qblk * rows_wg + rows_wg - 1);
-  const int n_tiles = wg_last_row / BN + 1;
-  const int n_steps = (n_tiles + KSPLIT - 1) / KSPLIT;
-  const int t_abs = r0 + ln;
-  const bool live = r0 < T;
+  // One work item per workgroup, or, for the gated fallback pass, a grid of
+  // at most one workgroup per CU looping over the items.  Each item's first
+  // barrier (before its LDS fill) waits for every wave's previous item.
+  const int n_items = per_q * n_qblk;
+  for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
+    const int qblk = n_qblk - 1 - item / per_q;  // heaviest query blocks first
+    const int kvh = (item % per_q) / n_hgrp;
+    const int hgrp = (item % per_q) % n_hgrp;
+    const int hq = kvh * group + hgrp * nh + wave % nh;
+    const int r0 = qblk * rows_wg + ((wave / nh) % RB) * 32;
+    const int wg_last_row = min(T - 1, qblk * rows_wg + rows_wg - 1);
+    const int n_tiles = wg_last_row / BN + 1;
+    const int n_steps = (n_tiles + KSPLIT - 1) / KSPLIT;
+    const int t_abs = r0 + ln;
+    const bool live = r0 < T;
 
-  const float* K = p.k + (long long)kvh * D * T;
-  const float* V = p.v + (long long)kvh * D * T;
+    const float* K = p.k + (long long)kvh * D * T;
+    const float* V = p.v + (long long)kvh * D * T;
 
-  // K/V tiles: thread moves column lc (key j0 + lc) of rows d = ld0 + 4k;
-  // the next step's tiles are loaded while the current ones are computed.
-  const int lc = tid & 63, ld0 = tid >> 6;
-  float kr[KSPLIT][NL], vr[KSPLIT][NL];
-  auto load_kv = [&](int step) {
+    // K/V tiles: thread moves column lc (key j0 + lc) of rows d = ld0 + 4k;
+    // the next step's tiles are loaded while the current ones are computed.
+    const int lc = tid & 63, ld0 = tid >> 6;
+    float kr[KSPLIT][NL], vr[KSPLIT][NL];
+    auto load_kv = [&](int step) {
 #pragma unroll
-    for (int u = 0; u < KSPLIT; ++u) {
-      const int col = min((step * KSPLIT + u) * BN + lc, T - 1);
+      for (int u = 0; u < KSPLIT; ++u) {
+        const int col = min((step * KSPLIT + u) * BN + lc, T - 1);
 #pragma unroll
-      for (int k = 0; k < NL; ++k) {
-        kr[u][k] = K[(long long)(ld0 + NW * k) * T + col];
-        vr[u][k] = V[(long long)(ld0 + NW * k) * T + col];
+        for (int k = 0; k < NL; ++k) {
+          kr[u][k] = K[(long long)(ld0 + NW * k) * T + col];
+          vr[u][k] = V[(long long)(ld0 + NW * k) * T + col];
+        }
       }
+    };
+    load_kv(0);
+
+    // q operand: lane (ln, hh) holds q[t][2ks + hh] * scale * log2 e
+    float qv[KS];
+    {
+      const float* Q = p.q + (long long)hq * D * T;
+      const int t = min(t_abs, T - 1);
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) qv[ks] = Q[(long long)(2 * ks + hh) * T + t] * p.scale_log2;
     }
-  };
-  load_kv(0);
+    // Swizzled 16-byte chunk of a staged row (rows 2D or 128 bytes long).
+    auto kswz = [](int key) { return D == 64 ? (key >> 1) & 7 : key & 15; };
+    auto vswz = [](int d) { return (d >> 1) & 7; };
 
-  // q operand: lane (ln, hh) holds q[t][2ks + hh] * scale * log2 e
-  float qv[KS];
-  {
-    const float* Q = p.q + (long long)hq * D * T;
-    const int t = min(t_abs, T - 1);
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) qv[ks] = Q[(long long)(2 * ks + hh) * T + t] * p.scale_log2;
-  }
-  // Swizzled 16-byte chunk of a staged row (rows 2D or 128 bytes long).
-  auto kswz = [](int key) { return D == 64 ? (key >> 1) & 7 : key & 15; };
-  auto vswz = [](int d) { return (d >> 1) & 7; };
-
-  f32x16 o[DB];
-#pragma unroll
-  for (int db = 0; db < DB; ++db)
-#pragma unroll
-    for (int i = 0; i < 16; ++i) o[db][i] = 0.f;
-  float m_run = -INFINITY, l_run = 0.f;
-
-  for (int step = 0; step < n_steps; ++step) {
-    __syncthreads();  // the previous step's sk / sv reads are done
-#pragma unroll
-    for (int u = 0; u < KSPLIT; ++u) {
-      const bool in = (step * KSPLIT + u) * BN + lc < T;
-#pragma unroll
-      for (int k = 0; k < NL; ++k) {
-        const int d = ld0 + NW * k;
-        const float kx = in ? kr[u][k] : 0.f, vx = in ? vr[u][k] : 0.f;
-        // K: (h = d & 1, key = lc, ks = d >> 1); V: (h = lc & 1, d, ks = lc >> 1)
-        const int ksk = d >> 1, ksv = lc >> 1;
-        sk[u * SKN + ((d & 1) * BN + lc) * KS + (((ksk >> 2) ^ kswz(lc)) << 2) + (ksk & 3)] = kx;
-        sv[u * SVN + ((lc & 1) * D + d) * 32 + (((ksv >> 2) ^ vswz(d)) << 2) + (ksv & 3)] = vx;
-      }
-    }
-    if (step + 1 < n_steps) load_kv(step + 1);
-    __syncthreads();
-    const int j0 = (step * KSPLIT + kq) * BN;
-    if (!live || j0 > r0 + 31) continue;  // wave-uniform: no key of this tile is visible
-    const float* tk = sk + kq * SKN;
-    const float* tv = sv + kq * SVN;
-
-    f32x16 s[2];
-#pragma unroll
-    for (int mb = 0; mb < 2; ++mb) {
-      const int m = ln;  // A operand row = key 32mb + 8a + 2e + h for m = 8a + 4h + e
-      const int key = 32 * mb + 8 * (m >> 3) + 2 * (m & 3) + ((m >> 2) & 1);
-      const float* row = tk + (hh * BN + key) * KS;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) s[mb][i] = 0.f;
-#pragma unroll
-      for (int c = 0; c < KC; ++c) {
-        const f32x4 kf = *(const f32x4*)(row + ((c ^ kswz(key)) << 2));
-#pragma unroll
-        for (int e = 0; e < 4; ++e) s[mb] = mma32f(kf[e], qv[4 * c + e], s[mb]);
-      }
-    }
-    // Causal mask and keys beyond T: output register i = 4a + e of lane half
-    // hh in block mb is key j0 + 32mb + 8a + 2e + hh.
-    float mt = -INFINITY;
-#pragma unroll
-    for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int key = j0 + 32 * mb + 8 * (i >> 2) + 2 * (i & 3) + hh;
-        s[mb][i] = (key <= t_abs && key < T) ? s[mb][i] : -INFINITY;
-        mt = fmaxf(mt, s[mb][i]);
-      }
-    mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
-    // Finite: a visible tile starts at or before the row block (tiles are 64
-    // keys, row blocks 32 rows, both aligned), so every row sees key j0.
-    const float mn = fmaxf(m_run, mt);
-    const float alpha = fast_exp2(m_run - mn);
-    m_run = mn;
-    float ps = 0.f;
-#pragma unroll
-    for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        s[mb][i] = fast_exp2(s[mb][i] - mn);
-        ps += s[mb][i];
-      }
-    l_run = l_run * alpha + ps;
+    f32x16 o[DB];
 #pragma unroll
     for (int db = 0; db < DB; ++db)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) o[db][i] *= alpha;
-    // O^T += V^T P^T: k-step ks = 16mb + i pairs keys 2ks + h.
+      for (int i = 0; i < 16; ++i) o[db][i] = 0.f;
+    float m_run = -INFINITY, l_run = 0.f;
+
+    for (int step = 0; step < n_steps; ++step) {
+      __syncthreads();  // the previous step's sk / sv reads are done
 #pragma unroll
-    for (int db = 0; db < DB; ++db) {
-      const int d = 32 * db + ln;
-      const float* row = tv + (hh * D + d) * 32;
+      for (int u = 0; u < KSPLIT; ++u) {
+        const bool in = (step * KSPLIT + u) * BN + lc < T;
 #pragma unroll
-      for (int c = 0; c < 8; ++c) {
-        const f32x4 vf = *(const f32x4*)(row + ((c ^ vswz(d)) << 2));
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int ks = 4 * c + e;
-          o[db] = mma32f(vf[e], s[ks >> 4][ks & 15], o[db]);
+        for (int k = 0; k < NL; ++k) {
+          const int d = ld0 + NW * k;
+          const float kx = in ? kr[u][k] : 0.f, vx = in ? vr[u][k] : 0.f;
+          // K: (h = d & 1, key = lc, ks = d >> 1); V: (h = lc & 1, d, ks = lc >> 1)
+          const int ksk = d >> 1, ksv = lc >> 1;
+          sk[u * SKN + ((d & 1) * BN + lc) * KS + (((ksk >> 2) ^ kswz(lc)) << 2) + (ksk & 3)] = kx;
+          sv[u * SVN + ((lc & 1) * D + d) * 32 + (((ksv >> 2) ^ vswz(d)) << 2) + (ksv & 3)] = vx;
         }
       }
-    }
-  }
+      if (step + 1 < n_steps) load_kv(step + 1);
+      __syncthreads();
+      const int j0 = (step * KSPLIT + kq) * BN;
+      if (!live || j0 > r0 + 31) continue;  // wave-uniform: no key of this tile is visible
+      const float* tk = sk + kq * SKN;
+      const float* tv = sv + kq * SVN;
 
-  float l = l_run + __shfl_xor(l_run, 32, 64);
-  if constexpr (KSPLIT > 1) {
-    // Key groups 1.. hand (m, l, o) to group 0 through LDS (the tiles are
-    // dead); a group that saw no tile has m = -inf and weight 0.
-    __syncthreads();
-    // Slots: the waves of key groups 1.., slot = wave - nh (the launch uses
-    // the split only with one row block per workgroup, RB = 1).
-    constexpr int NSLOT = NW - NW / KSPLIT;
-    float* xm = sk;                  // [slot][lane] m
-    float* xl = xm + NSLOT * 64;     // [slot][lane] l
-    float* xo = xl + NSLOT * 64;     // [slot][db*16 + i][lane] o
-    static_assert(NSLOT * 64 * (2 + 16 * DB) <= KSPLIT * SKN, "merge buffers fit the K tiles");
-    if (kq > 0) {
-      const int sl = wave - nh;
-      xm[sl * 64 + lane] = m_run;
-      xl[sl * 64 + lane] = l;
+      f32x16 s[2];
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb) {
+        const int m = ln;  // A operand row = key 32mb + 8a + 2e + h for m = 8a + 4h + e
+        const int key = 32 * mb + 8 * (m >> 3) + 2 * (m & 3) + ((m >> 2) & 1);
+        const float* row = tk + (hh * BN + key) * KS;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) s[mb][i] = 0.f;
+#pragma unroll
+        for (int c = 0; c < KC; ++c) {
+          const f32x4 kf = *(const f32x4*)(row + ((c ^ kswz(key)) << 2));
+#pragma unroll
+          for (int e = 0; e < 4; ++e) s[mb] = mma32f(kf[e], qv[4 * c + e], s[mb]);
+        }
+      }
+      // Causal mask and keys beyond T: output register i = 4a + e of lane half
+      // hh in block mb is key j0 + 32mb + 8a + 2e + hh.
+      float mt = -INFINITY;
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int key = j0 + 32 * mb + 8 * (i >> 2) + 2 * (i & 3) + hh;
+          s[mb][i] = (key <= t_abs && key < T) ? s[mb][i] : -INFINITY;
+          mt = fmaxf(mt, s[mb][i]);
+        }
+      mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+      // Finite: a visible tile starts at or before the row block (tiles are 64
+      // keys, row blocks 32 rows, both aligned), so every row sees key j0.
+      const float mn = fmaxf(m_run, mt);
+      const float alpha = fast_exp2(m_run - mn);
+      m_run = mn;
+      float ps = 0.f;
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          s[mb][i] = fast_exp2(s[mb][i] - mn);
+          ps += s[mb][i];
+        }
+      l_run = l_run * alpha + ps;
 #pragma unroll
       for (int db = 0; db < DB; ++db)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) xo[(sl * 16 * DB + db * 16 + i) * 64 + lane] = o[db][i];
-    }
-    __syncthreads();
-    if (kq > 0) return;
-    // O^T layout: every element this lane holds belongs to its own query
-    // row t_abs, so the merge factors are per-lane scalars.
-    float mall = m_run;
+        for (int i = 0; i < 16; ++i) o[db][i] *= alpha;
+      // O^T += V^T P^T: k-step ks = 16mb + i pairs keys 2ks + h.
 #pragma unroll
-    for (int q = 1; q < KSPLIT; ++q) mall = fmaxf(mall, xm[(wave + (q - 1) * nh) * 64 + lane]);
-    const float a0 = fast_exp2(m_run - mall);
-    float aq[KSPLIT];
-    l *= a0;
+      for (int db = 0; db < DB; ++db) {
+        const int d = 32 * db + ln;
+        const float* row = tv + (hh * D + d) * 32;
 #pragma unroll
-    for (int q = 1; q < KSPLIT; ++q) {
-      const int sl = wave + (q - 1) * nh;  // slot of this row block's key group q
-      aq[q] = fast_exp2(xm[sl * 64 + lane] - mall);  // 0 for a group with no tile
-      l += aq[q] * xl[sl * 64 + lane];
-    }
+        for (int c = 0; c < 8; ++c) {
+          const f32x4 vf = *(const f32x4*)(row + ((c ^ vswz(d)) << 2));
 #pragma unroll
-    for (int db = 0; db < DB; ++db)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        float v = o[db][i] * a0;
-#pragma unroll
-        for (int q = 1; q < KSPLIT; ++q)
-          v += aq[q] * xo[((wave + (q - 1) * nh) * 16 * DB + db * 16 + i) * 64 + lane];
-        o[db][i] = v;
+          for (int e = 0; e < 4; ++e) {
+            const int ks = 4 * c + e;
+            o[db] = mma32f(vf[e], s[ks >> 4][ks & 15], o[db]);
+          }
+        }
       }
-  }
-  if (!live) return;
-  const float inv = 1.0f / l;
-  if (t_abs < T) {
-    // fp32 output, or fp16 / bf16 when this is the fallback of an MFMA prefill
-    const long long ob = (long long)hq * D * T + t_abs;
+    }
+
+    float l = l_run + __shfl_xor(l_run, 32, 64);
+    if constexpr (KSPLIT > 1) {
+      // Key groups 1.. hand (m, l, o) to group 0 through LDS (the tiles are
+      // dead); a group that saw no tile has m = -inf and weight 0.
+      __syncthreads();
+      // Slots: the waves of key groups 1.., slot = wave - nh (the launch uses
+      // the split only with one row block per workgroup, RB = 1).
+      constexpr int NSLOT = NW - NW / KSPLIT;
+      float* xm = sk;                  // [slot][lane] m
+      float* xl = xm + NSLOT * 64;     // [slot][lane] l
+      float* xo = xl + NSLOT * 64;     // [slot][db*16 + i][lane] o
+      static_assert(NSLOT * 64 * (2 + 16 * DB) <= KSPLIT * SKN, "merge buffers fit the K tiles");
+      if (kq > 0) {
+        const int sl = wave - nh;
+        xm[sl * 64 + lane] = m_run;
+        xl[sl * 64 + lane] = l;
 #pragma unroll
-    for (int db = 0; db < DB; ++db)
+        for (int db = 0; db < DB; ++db)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int d = 32 * db + 8 * (i >> 2) + 4 * hh + (i & 3);
-        const float y = o[db][i] * inv;
-        if (p.out_dtype == HL_F16) store_elem<HL_F16>(p.out, ob + (long long)d * T, y);
-        else if (p.out_dtype == HL_BF16) store_elem<HL_BF16>(p.out, ob + (long long)d * T, y);
-        else ((float*)p.out)[ob + (long long)d * T] = y;
+          for (int i = 0; i < 16; ++i) xo[(sl * 16 * DB + db * 16 + i) * 64 + lane] = o[db][i];
       }
+      __syncthreads();
+      if (kq > 0) continue;  // key groups 1.. are done with this item
+      // O^T layout: every element this lane holds belongs to its own query
+      // row t_abs, so the merge factors are per-lane scalars.
+      float mall = m_run;
+#pragma unroll
+      for (int q = 1; q < KSPLIT; ++q) mall = fmaxf(mall, xm[(wave + (q - 1) * nh) * 64 + lane]);
+      const float a0 = fast_exp2(m_run - mall);
+      float aq[KSPLIT];
+      l *= a0;
+#pragma unroll
+      for (int q = 1; q < KSPLIT; ++q) {
+        const int sl = wave + (q - 1) * nh;  // slot of this row block's key group q
+        aq[q] = fast_exp2(xm[sl * 64 + lane] - mall);  // 0 for a group with no tile
+        l += aq[q] * xl[sl * 64 + lane];
+      }
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          float v = o[db][i] * a0;
+#pragma unroll
+          for (int q = 1; q < KSPLIT; ++q)
+            v += aq[q] * xo[((wave + (q - 1) * nh) * 16 * DB + db * 16 + i) * 64 + lane];
+          o[db][i] = v;
+        }
+    }
+    if (!live) continue;
+    const float inv = 1.0f / l;
+    if (t_abs < T) {
+      // fp32 output, or fp16 / bf16 when this is the fallback of an MFMA prefill
+      const long long ob = (long long)hq * D * T + t_abs;
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int d = 32 * db + 8 * (i >> 2) + 4 * hh + (i & 3);
+          const float y = o[db][i] * inv;
+          if (p.out_dtype == HL_F16) store_elem<HL_F16>(p.out, ob + (long long)d * T, y);
+          else if (p.out_dtype == HL_BF16) store_elem<HL_BF16>(p.out, ob + (long long)d * T, y);
+          else ((float*)p.out)[ob + (long long)d * T] = y;
+        }
+    }
   }
 }
 
@@ -819,7 +823,8 @@ hipError_t prefill_f32_launch(const PrefillLaunch& p, hipStream_t stream) {
   // (A four-way split, one head per workgroup, measured 9% slower at c2.)
   const int ksp = (nh >= 2 && grid_of(nh, 1) < 256 && p.head_dim == 64) ? 2 : 1;
   if (ksp > 1) nh = 2;
-  const dim3 grid(grid_of(nh, ksp));
+  const int items = grid_of(nh, ksp);
+  const dim3 grid(p.fallback_record ? std::min(items, cu_count()) : items);
   switch (p.head_dim) {
     case 64:
       if (ksp == 2) hipLaunchKernelGGL((prefill_f32mfma_kernel<64, 2>), grid, dim3(256), 0, stream, p, nh);

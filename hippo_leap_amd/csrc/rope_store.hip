@@ -201,187 +201,203 @@ __device__ __forceinline__ void store_cache8(void* cache, const CacheMap& m, int
 template <int IODT, int KDT, int DMAX>
 __global__ __launch_bounds__(256) void prologue_kernel(PrologueOp op) {
   __shared__ float sx[DMAX][kPT + 1];  // DMAX >= head_dim: the tile, sized to its class
-  if (op.gate && __hip_atomic_load(op.gate, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u) return;
-  if (op.range_word && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) range_counter_reset(op.range_word);
+  if (op.gate) {  // fallback pass: runs only when this call's mark is set
+    __shared__ unsigned s_go;
+    if (threadIdx.x == 0) {
+      const unsigned g = op.gate[1];
+      s_go = op.gate[0] == g + 1u;
+      if (blockIdx.x == 0 && blockIdx.y == 0) op.gate[2] = g + 1u;  // S for the fallback kernel
+    }
+    __syncthreads();
+    if (!s_go) return;
+  }
   __shared__ float scos[kTabHalf][kPT], ssin[kTabHalf][kPT];
   __shared__ float sred[8][kPT];
   __shared__ float sinv[kPT];
-  const int tid = threadIdx.x;
-  const int T = op.seq_len, D = op.head_dim;
-  const int t0 = blockIdx.x * kPT;
-  const int n_vec = op.n_head + 2 * op.n_head_kv;
-  const int hv0 = op.hv_first + blockIdx.y * op.hpg;
-  const int hv1 = min(n_vec, hv0 + op.hpg);
-  const int tc = tid & (kPT - 1), part = tid / kPT;  // 8 parts of 32 lanes
-  const int t = t0 + tc;
-  const int half = op.rope_dim / 2;
-  const bool tab = op.do_rope && half <= kTabHalf && hv0 < op.n_head + op.n_head_kv;
+  // Work items (tile, head group); a launch covers them with one workgroup
+  // each, or, for the gated fallback pass, with a grid of at most one
+  // workgroup per CU that loops over them.
+  const int n_items = op.n_tiles * op.n_hgrps;
+  for (int item = blockIdx.y * gridDim.x + blockIdx.x; item < n_items; item += gridDim.x * gridDim.y) {
+  const int tile = item % op.n_tiles, hgrp = item / op.n_tiles;
+    const int tid = threadIdx.x;
+    const int T = op.seq_len, D = op.head_dim;
+    const int t0 = tile * kPT;
+    const int n_vec = op.n_head + 2 * op.n_head_kv;
+    const int hv0 = op.hv_first + hgrp * op.hpg;
+    const int hv1 = min(n_vec, hv0 + op.hpg);
+    const int tc = tid & (kPT - 1), part = tid / kPT;  // 8 parts of 32 lanes
+    const int t = t0 + tc;
+    const int half = op.rope_dim / 2;
+    const bool tab = op.do_rope && half <= kTabHalf && hv0 < op.n_head + op.n_head_kv;
 
-  if (tab) {
-    // The first head group's workgroup of each tile also publishes its slice
-    // as tab_out[i][t] for the flash kernel's Q.
-    const bool publish = op.rope_tab_out && blockIdx.y == 0;
-    const float pos = (float)(op.start_pos + t);
-    for (int i = part; i < half; i += 8) {
-      const float angle = pos * op.theta.t[i];
-      float c, sn;
-      rope_cs(angle, c, sn);
-      scos[i][tc] = c;
-      ssin[i][tc] = sn;
-      if (publish && t < T) op.rope_tab_out[(long long)i * T + t] = make_float2(c, sn);
-    }
-  }
-
-  // Head vector hv -> (kind, head index, source); kind 0 q, 1 k, 2 v.
-  auto decode_hv = [&](int hv, int& kind, int& h) {
-    if (hv < op.n_head) {
-      kind = 0;
-      h = hv;
-    } else if (hv < op.n_head + op.n_head_kv) {
-      kind = 1;
-      h = hv - op.n_head;
-    } else {
-      kind = 2;
-      h = hv - op.n_head - op.n_head_kv;
-    }
-  };
-  auto src_of = [&](int kind) { return kind == 0 ? op.q : (kind == 1 ? op.k : op.v); };
-  // Loads head hv's [D, 32] tile into registers: thread -> (row, 8-token
-  // chunk), 64 rows per pass, D <= 256 -> at most 4 passes.
-  constexpr int kPass = DMAX / 64;
-  const int c8 = (tid & 3) * 8;
-  auto load_regs = [&](int hv, float (*x)[8]) {
-    int kind, h;
-    decode_hv(hv, kind, h);
-    const void* src = src_of(kind);
-    if (!src) return;
-    const long long hbase = (long long)h * D * T;
-#pragma unroll
-    for (int ps = 0; ps < kPass; ++ps) {
-      const int r = (tid >> 2) + 64 * ps;
-      if (r < D) load_row8_f32<IODT>(src, hbase + (long long)r * T + t0 + c8, t0 + c8, T, x[ps]);
-    }
-  };
-  float xa[kPass][8], xb[kPass][8];
-  if (hv0 < hv1) load_regs(hv0, xa);
-
-  for (int hv = hv0; hv < hv1; ++hv) {
-    int kind, h;
-    decode_hv(hv, kind, h);
-    const void* src = src_of(kind);
-    // prefetch the next head's tile while this one is processed
-    if (hv + 1 < hv1) load_regs(hv + 1, xb);
-    if (!src) {  // uniform across the workgroup
-#pragma unroll
-      for (int ps = 0; ps < kPass; ++ps)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) xa[ps][e] = xb[ps][e];
-      continue;
-    }
-    const float* nw = kind == 0 ? op.q_norm_w : (kind == 1 ? op.k_norm_w : nullptr);
-    const bool rope = op.do_rope && kind < 2;
-    const long long hbase = (long long)h * D * T;
-
-    __syncthreads();  // previous head's readers of sx are done
-#pragma unroll
-    for (int ps = 0; ps < kPass; ++ps) {
-      const int r = (tid >> 2) + 64 * ps;
-      if (r < D) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) sx[r][c8 + e] = xa[ps][e];
-      }
-    }
-#pragma unroll
-    for (int ps = 0; ps < kPass; ++ps)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) xa[ps][e] = xb[ps][e];
-    __syncthreads();
-
-    if (nw) {
-      float ss = 0.f;
-      for (int d = part; d < D; d += 8) ss += sx[d][tc] * sx[d][tc];
-      sred[part][tc] = ss;
-      __syncthreads();
-      if (part == 0) {
-        float tot = 0.f;
-        for (int q = 0; q < 8; ++q) tot += sred[q][tc];
-        sinv[tc] = 1.0f / sqrtf(tot / (float)D + op.eps);
-      }
-      __syncthreads();
-      const float inv = sinv[tc];
-      for (int d = part; d < D; d += 8) sx[d][tc] = sx[d][tc] * inv * nw[d];
-      __syncthreads();
-    }
-    if (rope) {
+    if (tab) {
+      // The first head group's workgroup of each tile also publishes its slice
+      // as tab_out[i][t] for the flash kernel's Q.
+      const bool publish = op.rope_tab_out && hgrp == 0;
       const float pos = (float)(op.start_pos + t);
       for (int i = part; i < half; i += 8) {
-        int i0, i1;
-        rope_pair_index(i, half, op.rope_style, i0, i1);
-        float c, s;
-        if (tab) {
-          c = scos[i][tc];
-          s = ssin[i][tc];
-        } else {
-          const float angle = pos * op.theta.t[i];
-          rope_cs(angle, c, s);
-        }
-        const float v0 = sx[i0][tc], v1 = sx[i1][tc];
-        sx[i0][tc] = v0 * c - v1 * s;
-        sx[i1][tc] = v0 * s + v1 * c;
+        const float angle = pos * op.theta.t[i];
+        float c, sn;
+        rope_cs(angle, c, sn);
+        scos[i][tc] = c;
+        ssin[i][tc] = sn;
+        if (publish && t < T) op.rope_tab_out[(long long)i * T + t] = make_float2(c, sn);
       }
+    }
+
+    // Head vector hv -> (kind, head index, source); kind 0 q, 1 k, 2 v.
+    auto decode_hv = [&](int hv, int& kind, int& h) {
+      if (hv < op.n_head) {
+        kind = 0;
+        h = hv;
+      } else if (hv < op.n_head + op.n_head_kv) {
+        kind = 1;
+        h = hv - op.n_head;
+      } else {
+        kind = 2;
+        h = hv - op.n_head - op.n_head_kv;
+      }
+    };
+    auto src_of = [&](int kind) { return kind == 0 ? op.q : (kind == 1 ? op.k : op.v); };
+    // Loads head hv's [D, 32] tile into registers: thread -> (row, 8-token
+    // chunk), 64 rows per pass, D <= 256 -> at most 4 passes.
+    constexpr int kPass = DMAX / 64;
+    const int c8 = (tid & 3) * 8;
+    auto load_regs = [&](int hv, float (*x)[8]) {
+      int kind, h;
+      decode_hv(hv, kind, h);
+      const void* src = src_of(kind);
+      if (!src) return;
+      const long long hbase = (long long)h * D * T;
+  #pragma unroll
+      for (int ps = 0; ps < kPass; ++ps) {
+        const int r = (tid >> 2) + 64 * ps;
+        if (r < D) load_row8_f32<IODT>(src, hbase + (long long)r * T + t0 + c8, t0 + c8, T, x[ps]);
+      }
+    };
+    float xa[kPass][8], xb[kPass][8];
+    if (hv0 < hv1) load_regs(hv0, xa);
+
+    for (int hv = hv0; hv < hv1; ++hv) {
+      int kind, h;
+      decode_hv(hv, kind, h);
+      const void* src = src_of(kind);
+      // prefetch the next head's tile while this one is processed
+      if (hv + 1 < hv1) load_regs(hv + 1, xb);
+      if (!src) {  // uniform across the workgroup
+  #pragma unroll
+        for (int ps = 0; ps < kPass; ++ps)
+  #pragma unroll
+          for (int e = 0; e < 8; ++e) xa[ps][e] = xb[ps][e];
+        continue;
+      }
+      const float* nw = kind == 0 ? op.q_norm_w : (kind == 1 ? op.k_norm_w : nullptr);
+      const bool rope = op.do_rope && kind < 2;
+      const long long hbase = (long long)h * D * T;
+
+      __syncthreads();  // previous head's readers of sx are done
+  #pragma unroll
+      for (int ps = 0; ps < kPass; ++ps) {
+        const int r = (tid >> 2) + 64 * ps;
+        if (r < D) {
+  #pragma unroll
+          for (int e = 0; e < 8; ++e) sx[r][c8 + e] = xa[ps][e];
+        }
+      }
+  #pragma unroll
+      for (int ps = 0; ps < kPass; ++ps)
+  #pragma unroll
+        for (int e = 0; e < 8; ++e) xa[ps][e] = xb[ps][e];
       __syncthreads();
-    }
 
-    // row-wise outputs: fp32 write-back in place, KV-cache columns start_pos + t
-    float* inplace = kind == 0 ? op.q_inplace : (kind == 1 ? op.k_inplace : op.v_f32);
-    void* cache = kind == 1 ? op.k_cache : (kind == 2 ? op.v_cache : nullptr);
-    if (inplace || cache) {
-      for (int r = tid >> 2; r < D; r += 64) {
-        float x[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) x[e] = sx[r][c8 + e];
-        if (inplace) store_row8<HL_F32>(inplace, hbase + (long long)r * T + t0 + c8, t0 + c8, T, x);
-        if (cache)
-          store_cache8<KDT>(cache, CacheMap{op.kv_layout, D, op.max_len, op.n_head_kv, op.block_table}, h, r,
-                            op.start_pos + t0 + c8, t0 + c8, T, x);
+      if (nw) {
+        float ss = 0.f;
+        for (int d = part; d < D; d += 8) ss += sx[d][tc] * sx[d][tc];
+        sred[part][tc] = ss;
+        __syncthreads();
+        if (part == 0) {
+          float tot = 0.f;
+          for (int q = 0; q < 8; ++q) tot += sred[q][tc];
+          sinv[tc] = 1.0f / sqrtf(tot / (float)D + op.eps);
+        }
+        __syncthreads();
+        const float inv = sinv[tc];
+        for (int d = part; d < D; d += 8) sx[d][tc] = sx[d][tc] * inv * nw[d];
+        __syncthreads();
       }
-    }
-
-    // MFMA operand layouts (fp16 bits); pad rows t >= T are written as zeros.
-    // A value beyond fp16's range goes to the range record.
-    float omax = 0.f;
-    if (kind < 2) {
-      uint16_t* dst = kind == 0 ? op.qt : op.kt;
-      if (dst) {
-        const float mul = kind == 0 ? op.qt_scale : 1.0f;
-        const int chunks = D / 8;
-        for (int idx = tid; idx < kPT * chunks; idx += 256) {
-          const int tt = idx / chunks, ch = idx % chunks;
-          const int tg = t0 + tt;
-          if (tg >= op.t_pad) continue;
-          u16x8 w;
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const float x = tg < T ? sx[8 * ch + e][tt] * mul : 0.f;
-            omax = fmaxf(omax, fabsf(x));
-            w[e] = f32_to_f16_bits(x);
+      if (rope) {
+        const float pos = (float)(op.start_pos + t);
+        for (int i = part; i < half; i += 8) {
+          int i0, i1;
+          rope_pair_index(i, half, op.rope_style, i0, i1);
+          float c, s;
+          if (tab) {
+            c = scos[i][tc];
+            s = ssin[i][tc];
+          } else {
+            const float angle = pos * op.theta.t[i];
+            rope_cs(angle, c, s);
           }
-          *(u16x8*)(dst + ((long long)h * op.t_pad + tg) * D + 8 * ch) = w;
+          const float v0 = sx[i0][tc], v1 = sx[i1][tc];
+          sx[i0][tc] = v0 * c - v1 * s;
+          sx[i1][tc] = v0 * s + v1 * c;
+        }
+        __syncthreads();
+      }
+
+      // row-wise outputs: fp32 write-back in place, KV-cache columns start_pos + t
+      float* inplace = kind == 0 ? op.q_inplace : (kind == 1 ? op.k_inplace : op.v_f32);
+      void* cache = kind == 1 ? op.k_cache : (kind == 2 ? op.v_cache : nullptr);
+      if (inplace || cache) {
+        for (int r = tid >> 2; r < D; r += 64) {
+          float x[8];
+  #pragma unroll
+          for (int e = 0; e < 8; ++e) x[e] = sx[r][c8 + e];
+          if (inplace) store_row8<HL_F32>(inplace, hbase + (long long)r * T + t0 + c8, t0 + c8, T, x);
+          if (cache)
+            store_cache8<KDT>(cache, CacheMap{op.kv_layout, D, op.max_len, op.n_head_kv, op.block_table}, h, r,
+                              op.start_pos + t0 + c8, t0 + c8, T, x);
         }
       }
-    } else if (op.vt) {
-      for (int r = tid >> 2; r < D; r += 64) {
-        if (t0 + c8 >= op.t_pad) continue;
-        float x[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          x[e] = (t0 + c8 + e < T) ? sx[r][c8 + e] : 0.f;
-          omax = fmaxf(omax, fabsf(x[e]));
+
+      // MFMA operand layouts (fp16 bits); pad rows t >= T are written as zeros.
+      // A value beyond fp16's range goes to the range record.
+      float omax = 0.f;
+      if (kind < 2) {
+        uint16_t* dst = kind == 0 ? op.qt : op.kt;
+        if (dst) {
+          const float mul = kind == 0 ? op.qt_scale : 1.0f;
+          const int chunks = D / 8;
+          for (int idx = tid; idx < kPT * chunks; idx += 256) {
+            const int tt = idx / chunks, ch = idx % chunks;
+            const int tg = t0 + tt;
+            if (tg >= op.t_pad) continue;
+            u16x8 w;
+  #pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              const float x = tg < T ? sx[8 * ch + e][tt] * mul : 0.f;
+              omax = fmaxf(omax, fabsf(x));
+              w[e] = f32_to_f16_bits(x);
+            }
+            *(u16x8*)(dst + ((long long)h * op.t_pad + tg) * D + 8 * ch) = w;
+          }
         }
-        store_row8<HL_F16>(op.vt, ((long long)h * D + r) * op.t_pad + t0 + c8, t0 + c8, op.t_pad, x);
+      } else if (op.vt) {
+        for (int r = tid >> 2; r < D; r += 64) {
+          if (t0 + c8 >= op.t_pad) continue;
+          float x[8];
+  #pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            x[e] = (t0 + c8 + e < T) ? sx[r][c8 + e] : 0.f;
+            omax = fmaxf(omax, fabsf(x[e]));
+          }
+          store_row8<HL_F16>(op.vt, ((long long)h * D + r) * op.t_pad + t0 + c8, t0 + c8, op.t_pad, x);
+        }
       }
+      if (omax >= kF16Inf && op.range_word) range_flag_set(op.range_word);
     }
-    if (omax >= kF16Inf && op.range_word) range_flag_set(op.range_word);
+  __syncthreads();  // this item's LDS readers are done before the next item's fill
   }
 }
 
@@ -421,7 +437,6 @@ __global__ __launch_bounds__(256) void kv_prologue_kernel(PrologueOp op) {
   const int r = tid / CPR, c8 = (tid % CPR) * 8;
   const int t = t0 + c8;  // this thread's first token
   const long long hbase = (long long)h * D * T;
-  if (op.range_word && blockIdx.x == 0 && h == 0 && tid == 0) range_counter_reset(op.range_word);
 
   float k[NP][8], v[NP][8];
 #pragma unroll
@@ -577,9 +592,12 @@ hipError_t prologue_launch(const PrologueOp& op, hipStream_t stream) {
   // prefills share one cos/sin table fill across heads.
   PrologueOp o2 = op;
   o2.hpg = kHPG;
-  // A gated fallback pass usually exits at once: fewest workgroups.
   while (!op.gate && o2.hpg > 1 && (long long)tiles * ((n_vec + o2.hpg - 1) / o2.hpg) < 2048) o2.hpg >>= 1;
-  dim3 grid(tiles, (n_vec + o2.hpg - 1) / o2.hpg);
+  o2.n_tiles = tiles;
+  o2.n_hgrps = (n_vec + o2.hpg - 1) / o2.hpg;
+  // A gated fallback pass usually exits at once: one workgroup per CU at
+  // most (one round of gate reads), looping over the items when it runs.
+  dim3 grid = op.gate ? dim3(std::min(tiles * o2.n_hgrps, cu_count())) : dim3(tiles, o2.n_hgrps);
 #define HL_PRO(IO, KD)                                                                          \
   if (op.head_dim <= 128) hipLaunchKernelGGL((prologue_kernel<IO, KD, 128>), grid, dim3(256), 0, stream, o2); \
   else hipLaunchKernelGGL((prologue_kernel<IO, KD, HL_MAX_HEAD_DIM>), grid, dim3(256), 0, stream, o2)

@@ -464,9 +464,11 @@ int hl_attn_prefill(const hl_prefill_args* a, void* workspace, size_t ws_bytes,
  * `workspace` with these args took that fallback: it waits for `stream`
  * and sets *ran to 1 or 0 (always 0 for fp32 activations).  Under stream
  * capture it returns HL_ECAPTURE.  No counterpart in the reference.
- * A workspace whose record holds stale nonzero bytes (never used by a
- * prefill, not zero-filled) can send its first call through the fallback:
- * the result is the same, only slower.                                   */
+ * The record is 16 bytes at the end of the workspace; each call retires its
+ * own mark, so it needs no initialisation (zero-filled, or left by an
+ * earlier prefill; arbitrary bytes can at worst send one call through the
+ * fallback, with the same result).  Calls that share a workspace must not
+ * overlap (one stream, as everywhere in this library).                   */
 int hl_attn_prefill_fallback_ran(const hl_prefill_args* a, const void* workspace, int* ran,
                                  void* stream);
 
