@@ -170,6 +170,9 @@ SIGNATURES = {
                                    ctypes.POINTER(ForwardScratch), c_void_p, c_int, c_void_p, c_void_p]),
     "hl_forward_decode": (c_int, [ctypes.POINTER(ModelDesc), ctypes.POINTER(KvCacheDesc),
                                   ctypes.POINTER(ForwardScratch), c_void_p, c_void_p, c_void_p, c_void_p]),
+    "hl_forward_decode_timed": (c_int, [ctypes.POINTER(ModelDesc), ctypes.POINTER(KvCacheDesc),
+                                        ctypes.POINTER(ForwardScratch), c_void_p, c_void_p, c_void_p,
+                                        ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(c_float), c_void_p]),
     "hl_attn_decode_workspace_bytes": (c_size_t, [ctypes.POINTER(DecodeArgs)]),
     "hl_attn_decode": (c_int, [ctypes.POINTER(DecodeArgs), c_void_p, c_size_t, c_void_p]),
     "hl_attn_decode_workspace_init": (c_int, [c_void_p, c_size_t, c_void_p]),

@@ -9,6 +9,7 @@
 // without a host round trip.
 #include <cmath>
 #include <cstring>
+#include <mutex>
 
 #include "common.h"
 #include "launch.h"
@@ -571,6 +572,59 @@ int hl_forward_decode(const hl_model_desc* m, hl_kv_cache_desc* c, const hl_forw
   HL_TRY(linear_t(logits, s->x_norm, m->output, m->output_type, E, m->n_vocab, 1, stream));
   HL_TRY(hl_argmax_async(logits, m->n_vocab, next_token_dev, stream));
   c->cur_len = pos + 1;
+  return HL_OK;
+}
+
+}  // extern "C"
+
+namespace {
+// The two timing events of hl_forward_decode_timed, created on first use per
+// device and kept for the process (forwardDecodeTokenTimed's module-level
+// mkBenchEvent0/1, megakernel.nim:2516-2519).
+constexpr int kMaxDevices = 64;
+std::mutex g_ev_mu;
+hipEvent_t g_ev[kMaxDevices][2];
+
+int timing_events(hipEvent_t& e0, hipEvent_t& e1) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return set_error(HL_EHIP, "forward_decode_timed: hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return set_error(HL_EUNSUPPORTED, "forward_decode_timed: device %d", dev);
+  std::lock_guard<std::mutex> lk(g_ev_mu);
+  for (int i = 0; i < 2; ++i)
+    if (!g_ev[dev][i] && (e = hipEventCreate(&g_ev[dev][i])) != hipSuccess)
+      return set_error(HL_EHIP, "forward_decode_timed: hipEventCreate: %s", hipGetErrorString(e));
+  e0 = g_ev[dev][0];
+  e1 = g_ev[dev][1];
+  return HL_OK;
+}
+}  // namespace
+
+extern "C" {
+
+int hl_forward_decode_timed(const hl_model_desc* m, hl_kv_cache_desc* c, const hl_forward_scratch* s,
+                            const int32_t* token_dev, float* logits, int32_t* next_token_dev,
+                            int32_t* next_token, float* gpu_ms, void* stream) {
+  if (!next_token || !gpu_ms) return set_error(HL_EINVAL, "forward_decode_timed: null pointer");
+  const hipStream_t st = (hipStream_t)stream;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  hipError_t e = hipStreamIsCapturing(st, &cs);
+  if (e != hipSuccess) return set_error(HL_EHIP, "hipStreamIsCapturing: %s", hipGetErrorString(e));
+  if (cs != hipStreamCaptureStatusNone)
+    return set_error(HL_ECAPTURE, "forward_decode_timed waits for the stream; it cannot run under stream capture");
+  hipEvent_t e0, e1;
+  HL_TRY(timing_events(e0, e1));
+  if ((e = hipEventRecord(e0, st)) != hipSuccess)
+    return set_error(HL_EHIP, "forward_decode_timed: event record: %s", hipGetErrorString(e));
+  HL_TRY(hl_forward_decode(m, c, s, token_dev, logits, next_token_dev, stream));
+  if ((e = hipEventRecord(e1, st)) != hipSuccess)
+    return set_error(HL_EHIP, "forward_decode_timed: event record: %s", hipGetErrorString(e));
+  if ((e = hipMemcpyAsync(next_token, next_token_dev, sizeof(int32_t), hipMemcpyDeviceToHost, st)) != hipSuccess)
+    return set_error(HL_EHIP, "forward_decode_timed: token copy: %s", hipGetErrorString(e));
+  if ((e = hipStreamSynchronize(st)) != hipSuccess)
+    return set_error(HL_EHIP, "forward_decode_timed: sync: %s", hipGetErrorString(e));
+  if ((e = hipEventElapsedTime(gpu_ms, e0, e1)) != hipSuccess)
+    return set_error(HL_EHIP, "forward_decode_timed: elapsed time: %s", hipGetErrorString(e));
   return HL_OK;
 }
 

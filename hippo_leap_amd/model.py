@@ -153,3 +153,15 @@ class DenseModel(DenseDecoder):
         check(_lib.load().hl_forward_decode(ctypes.byref(self.desc), ctypes.byref(self.cache.desc),
                                             ctypes.byref(self.fscratch), _p(tok), _p(self.logits), _p(nxt),
                                             _stream(stream)))
+
+    def decode_timed(self, token_dev=None, stream=None) -> tuple[int, float]:
+        """forwardDecodeTokenTimed: decode() bracketed by GPU events; waits
+        for the stream and returns (next token, GPU ms)."""
+        tok = self.tokens[0:1] if token_dev is None else token_dev
+        nxt = ctypes.c_int32(0)
+        ms = ctypes.c_float(0.0)
+        check(_lib.load().hl_forward_decode_timed(ctypes.byref(self.desc), ctypes.byref(self.cache.desc),
+                                                  ctypes.byref(self.fscratch), _p(tok), _p(self.logits),
+                                                  _p(self.tokens[1:2]), ctypes.byref(nxt), ctypes.byref(ms),
+                                                  _stream(stream)))
+        return int(nxt.value), float(ms.value)

@@ -672,6 +672,20 @@ int hl_forward_decode(const hl_model_desc* model, hl_kv_cache_desc* cache,
                       const hl_forward_scratch* scratch, const int32_t* token_dev,
                       float* logits, int32_t* next_token_dev, void* stream);
 
+/* forwardDecodeTokenTimed (megakernel.nim:2514-2529, called by
+ * inference.nim:80-84): hl_forward_decode bracketed by two hipEvents on
+ * `stream` (created once per device and kept), then waits for the stream
+ * and returns the greedy next token in host *next_token (also left in
+ * *next_token_dev) and the GPU time between the events, in ms, in *gpu_ms.
+ * The events bracket the embedding through the argmax, as the reference's
+ * bracket forwardDecodeGpu + gpuArgmax.  It waits, so under stream capture
+ * it returns HL_ECAPTURE (capture hl_forward_decode itself and time the
+ * graph).  cache->cur_len advances as in hl_forward_decode.              */
+int hl_forward_decode_timed(const hl_model_desc* model, hl_kv_cache_desc* cache,
+                            const hl_forward_scratch* scratch, const int32_t* token_dev,
+                            float* logits, int32_t* next_token_dev, int32_t* next_token,
+                            float* gpu_ms, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

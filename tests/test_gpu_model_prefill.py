@@ -165,3 +165,37 @@ def test_decode_only_with_gguf_weights(hl, orc):
         tok = int(m.tokens[1].item())
         assert tok == orc.argmax(lg)
         m.tokens[0] = tok
+
+
+def test_decode_timed_matches_decode(hl, orc):
+    """hl_forward_decode_timed (forwardDecodeTokenTimed, megakernel.nim:
+    2514-2529): the same tokens and logits as hl_forward_decode on a twin
+    model, a positive GPU time below the host's wall time of the call, and
+    HL_ECAPTURE under stream capture."""
+    import time
+    from hippo_leap_amd import _lib
+    from hippo_leap_amd.model import DenseModel
+    dev, ref = _build(orc, CFG, {}, True, 321)
+    twins = [DenseModel(torch, CFG, dev["tok_emb"], dev["output_norm"], dev["output"], 0, dev["layers"],
+                        max_tokens=4, kv_dtype=2) for _ in range(2)]
+    for m in twins:
+        m.prefill([1, 2, 3, 4])
+        m.tokens[0] = 7
+    torch.cuda.synchronize()
+    for step in range(4):
+        twins[0].decode()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        tok, ms = twins[1].decode_timed()
+        wall_ms = (time.perf_counter() - t0) * 1e3
+        assert 0.0 < ms < wall_ms, (ms, wall_ms)
+        assert tok == int(twins[0].tokens[1].item()) == int(twins[1].tokens[1].item())
+        assert np.array_equal(twins[0].logits.cpu().numpy(), twins[1].logits.cpu().numpy())
+        assert twins[1].cache.cur_len == twins[0].cache.cur_len == 5 + step
+        for m in twins:
+            m.tokens[0] = tok
+    s = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    with pytest.raises(_lib.HLError, match="capture"):
+        with torch.cuda.graph(g, stream=s):
+            twins[1].decode_timed(stream=s)
