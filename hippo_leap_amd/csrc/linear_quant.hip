@@ -867,13 +867,10 @@ constexpr int kQ4MaxGroups = 16;    // K <= 32768 (a workgroup of at most 16 wav
 typedef _Float16 h2v __attribute__((ext_vector_type(2)));
 typedef int v4i __attribute__((ext_vector_type(4)));
 
-// Buffer descriptor over [base, base + bytes) (raw bytes, dword loads; an
-// access past `bytes` reads zeros), in SGPRs.
-__device__ __forceinline__ v4i buf_desc(const void* base, uint32_t bytes) {
-  const uintptr_t b = (uintptr_t)base;
-  return v4i{__builtin_amdgcn_readfirstlane((int)(uint32_t)b),
-             __builtin_amdgcn_readfirstlane((int)((b >> 32) & 0xFFFFu)),
-             __builtin_amdgcn_readfirstlane((int)bytes), 0x00020000};
+// Buffer resource over [base, base + bytes) (raw bytes; an access past
+// `bytes` reads zeros), for the buffer-load builtins.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
 }
 
 // Lane l reads lane dpp(l) of v (within rows of 16 lanes).
@@ -930,38 +927,27 @@ __global__ __launch_bounds__(1024) void q4k_mfma_kernel(const uint8_t* __restric
   // step adds nothing).
   const uint32_t vb = 8 * g + b8 < nb ? (uint32_t)rr * rowbytes + (uint32_t)(8 * g + b8) * 144u : oob;
   const uint32_t vq = vb + 16 + 32 * t;
-  v4i desc[NP];
+  const uint8_t* wbase[NP];
 #pragma unroll
-  for (int pm = 0; pm < NP; ++pm) desc[pm] = buf_desc((pm ? w2 : w) + (size_t)row0 * rowbytes, oob);
+  for (int pm = 0; pm < NP; ++pm) wbase[pm] = (pm ? w2 : w) + (size_t)row0 * rowbytes;
   struct Raw {
     u32x4 hdr, q0, q1;
   };
-  // Step k: row pair st + (k / NP) nstream of matrix k % NP.  The weight
-  // loads are issued and waited for by hand (buffer_load_dwordx4; vmcnt
-  // with the loaded registers tied to the wait): the compiler otherwise
-  // moves the next step's loads below this step's math.  Outside the x
-  // prologue no other vector memory load is in flight.
+  // Step k: row pair st + (k / NP) nstream of matrix k % NP, three buffer
+  // loads (the compiler counts them for its waits).  Scheduling barriers
+  // around each step's loads keep the next steps' loads where they are
+  // issued, three steps ahead of their math, instead of below it.
   const int nsteps = __builtin_amdgcn_readfirstlane(
       st < nstream && st < npairs ? ((npairs - st + nstream - 1) / nstream) * NP : 0);
   auto load = [&](int k, Raw& r) {
     const int pm = PAIR ? (k & 1) : 0, q = st + (PAIR ? k >> 1 : k) * nstream;
     const uint32_t so = __builtin_amdgcn_readfirstlane(k < nsteps ? (uint32_t)(2 * q) * rowbytes : oob);
-    v4i dk = desc[0];
-    if (PAIR) {  // a uniform select, kept in SGPRs
-#pragma unroll
-      for (int e = 0; e < 4; ++e) dk[e] = __builtin_amdgcn_readfirstlane(pm ? desc[NP - 1][e] : desc[0][e]);
-    }
-    asm volatile(
-        "buffer_load_dwordx4 %0, %3, %5, %6 offen\n\t"
-        "buffer_load_dwordx4 %1, %4, %5, %6 offen\n\t"
-        "buffer_load_dwordx4 %2, %4, %5, %6 offen offset:16"
-        : "=&v"(r.hdr), "=&v"(r.q0), "=&v"(r.q1)
-        : "v"(vb), "v"(vq), "s"(dk), "s"(so));
-  };
-  // Waits until at most `pending` weight loads (of later steps) are in flight.
-  auto wait = [&](Raw& r, auto pending) {
-    asm volatile("s_waitcnt vmcnt(%3)" : "+v"(r.hdr), "+v"(r.q0), "+v"(r.q1)
-                 : "n"(decltype(pending)::value));
+    const __amdgpu_buffer_rsrc_t rs = buf_rsrc(PAIR && pm ? wbase[NP - 1] : wbase[0], oob);
+    __builtin_amdgcn_sched_barrier(0);
+    r.hdr = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)vb, (int)so, 0);
+    r.q0 = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)vq, (int)so, 0);
+    r.q1 = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)vq + 16, (int)so, 0);
+    __builtin_amdgcn_sched_barrier(0);
   };
 
   // x -> LDS.  Chunk c = x[8c, 8c + 8) is one A register of block bk = c / 32
@@ -969,13 +955,10 @@ __global__ __launch_bounds__(1024) void q4k_mfma_kernel(const uint8_t* __restric
   // (8 c mod 256 = 64 t + 32 h + 8 j); a block's 32 chunks are 32 consecutive
   // threads.  Blocks past nb are written as zeros (their quants load as
   // zeros too).
-  const v4i xdesc = buf_desc(x, (uint32_t)K * 4u);
+  const __amdgpu_buffer_rsrc_t xdesc = buf_rsrc(x, (uint32_t)K * 4u);
   auto x_chunk = [&](int c, f32x4& v0, f32x4& v1) {
-    asm volatile(
-        "buffer_load_dwordx4 %0, %2, %3, 0 offen\n\t"
-        "buffer_load_dwordx4 %1, %2, %3, 0 offen offset:16"
-        : "=&v"(v0), "=&v"(v1)
-        : "v"(32 * c), "s"(xdesc));
+    v0 = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(xdesc, 32 * c, 0, 0));
+    v1 = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(xdesc, 32 * c + 16, 0, 0));
   };
   auto convert = [&](int c, const f32x4& v0, const f32x4& v1) {
     const int bk = c >> 5, cb = c & 31;
@@ -1017,23 +1000,18 @@ __global__ __launch_bounds__(1024) void q4k_mfma_kernel(const uint8_t* __restric
   for (int i = 0; i < XC; ++i) x_chunk(threadIdx.x + i * blockDim.x, xv[i][0], xv[i][1]);
   [[maybe_unused]] f32x4 rv[2], nv[2];
   if constexpr (NORM) {
-    const v4i rdesc = buf_desc(res, (uint32_t)K * 4u), ndesc = buf_desc(nrm, (uint32_t)K * 4u);
-    asm volatile(
-        "buffer_load_dwordx4 %0, %4, %5, 0 offen\n\t"
-        "buffer_load_dwordx4 %1, %4, %5, 0 offen offset:16\n\t"
-        "buffer_load_dwordx4 %2, %4, %6, 0 offen\n\t"
-        "buffer_load_dwordx4 %3, %4, %6, 0 offen offset:16"
-        : "=&v"(rv[0]), "=&v"(rv[1]), "=&v"(nv[0]), "=&v"(nv[1])
-        : "v"(32 * (int)threadIdx.x), "s"(rdesc), "s"(ndesc));
+    const __amdgpu_buffer_rsrc_t rdesc = buf_rsrc(res, (uint32_t)K * 4u), ndesc = buf_rsrc(nrm, (uint32_t)K * 4u);
+    const int o = 32 * (int)threadIdx.x;
+    rv[0] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rdesc, o, 0, 0));
+    rv[1] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rdesc, o + 16, 0, 0));
+    nv[0] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(ndesc, o, 0, 0));
+    nv[1] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(ndesc, o + 16, 0, 0));
   }
   Raw ra, rb, rc;
-  load(0, ra);
+  load(0, ra);  // the loads' scheduling barriers keep x's loads ahead of these
   load(1, rb);
   load(2, rc);
   if constexpr (NORM) {
-    asm volatile("s_waitcnt vmcnt(9)"
-                 : "+v"(xv[0][0]), "+v"(xv[0][1]), "+v"(rv[0]), "+v"(rv[1]), "+v"(nv[0]),
-                   "+v"(nv[1]));  // x, res, nrm, not the weights
     // Chunks past K load as zeros and add nothing to the sum of squares.
     const f32x4 v0 = xv[0][0] + rv[0], v1 = xv[0][1] + rv[1];
     float ss = (v0.x * v0.x + v0.y * v0.y) + (v0.z * v0.z + v0.w * v0.w) +
@@ -1052,10 +1030,6 @@ __global__ __launch_bounds__(1024) void q4k_mfma_kernel(const uint8_t* __restric
     const float inv = 1.0f / sqrtf(t / (float)K + eps);
     xv[0][0] = f32x4{v0.x * inv * nv[0].x, v0.y * inv * nv[0].y, v0.z * inv * nv[0].z, v0.w * inv * nv[0].w};
     xv[0][1] = f32x4{v1.x * inv * nv[1].x, v1.y * inv * nv[1].y, v1.z * inv * nv[1].z, v1.w * inv * nv[1].w};
-  } else {
-    asm volatile("s_waitcnt vmcnt(9)"
-                 : "+v"(xv[0][0]), "+v"(xv[0][1]), "+v"(xv[1][0]), "+v"(xv[1][1]), "+v"(xv[2][0]),
-                   "+v"(xv[2][1]), "+v"(xv[3][0]), "+v"(xv[3][1]));  // x, not the weights
   }
 #pragma unroll
   for (int i = 0; i < XC; ++i)
@@ -1110,21 +1084,14 @@ __global__ __launch_bounds__(1024) void q4k_mfma_kernel(const uint8_t* __restric
     // so the counts hold on every path (loads past the last step read
     // nothing).
     for (int k = 0; k < nsteps; k += 3) {
-      wait(ra, std::integral_constant<int, 6>());
       compute(k, ra);
       load(k + 3, ra);
-      wait(rb, std::integral_constant<int, 6>());
       if (k + 1 < nsteps) compute(k + 1, rb);
       load(k + 4, rb);
-      wait(rc, std::integral_constant<int, 6>());
       if (k + 2 < nsteps) compute(k + 2, rc);
       load(k + 5, rc);
     }
   }
-  // every load has landed before its registers can be reused
-  wait(ra, std::integral_constant<int, 0>());
-  wait(rb, std::integral_constant<int, 0>());
-  wait(rc, std::integral_constant<int, 0>());
   __syncthreads();
   for (int r = threadIdx.x; r < nrows; r += blockDim.x) {
     float a = 0.f, b = 0.f;
@@ -1150,6 +1117,8 @@ __global__ __launch_bounds__(1024) void q4k_mfma_kernel(const uint8_t* __restric
 // prologue, so pairs count 2 M rows: two 8192 x 2048 matrices (the
 // Llama-3.2-1B gate/up) move to the matrix cores, with the FFN norm folded
 // in (Llama-3.2-1B decode 0.73 -> 0.65 ms/token as a graph).
+constexpr size_t kQ4MaxLds = 160 * 1024;  // LDS per CU (gfx950)
+
 bool q4k_mfma_pays(int M, int K) {
   return K <= 256 * 8 * kQ4MaxGroups && (long long)M * K >= (1LL << 25);
 }
@@ -1158,7 +1127,7 @@ bool q4k_mfma_pays(int M, int K) {
 // least one thread per x chunk when 16 waves allow it; as many workgroups
 // as are resident at once (LDS and 16 waves per CU) share the row pairs.
 template <int PAIR, bool NORM = false>
-void launch_q4k_mfma(const uint8_t* w, const float* x, float* y, int M, int K, hipStream_t stream,
+bool launch_q4k_mfma(const uint8_t* w, const float* x, float* y, int M, int K, hipStream_t stream,
                      const uint8_t* w2 = nullptr, float* y2 = nullptr, const float* res = nullptr,
                      const float* nrm = nullptr, float* xsum = nullptr, float eps = 0.f) {
   const int nb = K / 256, ng = (nb + 7) / 8;
@@ -1167,14 +1136,27 @@ void launch_q4k_mfma(const uint8_t* w, const float* x, float* y, int M, int K, h
   const int per_cu = std::max(1, std::min<int>(16 / nw, (int)((160 * 1024) / (a_bytes + 4096))));
   const int pairs = (M + 1) / 2;
   const int wgs_target = per_cu * cu_count();
-  const int pairs_wg = (pairs + wgs_target - 1) / wgs_target;
+  int pairs_wg = (pairs + wgs_target - 1) / wgs_target;
+  // The per-row partial sums grow with the rows per workgroup: past 160 KiB
+  // of LDS the rows go to more workgroups instead (they queue behind the
+  // resident ones).
+  const size_t fixed = (size_t)ng * kQ4gBytes + (NORM ? 16 * 4 : 0);
+  const size_t per_row = (size_t)(PAIR ? 2 : 1) * ng * 4;
+  const int max_pairs = (int)((kQ4MaxLds - fixed) / per_row / 2);
+  pairs_wg = std::max(1, std::min(pairs_wg, max_pairs));
   const int rows = 2 * pairs_wg;
-  const size_t shm = (size_t)ng * kQ4gBytes + (size_t)(PAIR ? 2 : 1) * ng * rows * 4 + (NORM ? 16 * 4 : 0);
+  const size_t shm = fixed + per_row * rows;
+  // The attribute is set once per instantiation; without it only 64 KiB of
+  // dynamic LDS may be asked for, and a larger case goes to the direct kernel.
   static const hipError_t attr = hipFuncSetAttribute((const void*)q4k_mfma_kernel<PAIR, NORM>,
-                                                     hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-  (void)attr;
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)kQ4MaxLds);
+  if (shm > kQ4MaxLds || (attr != hipSuccess && shm > 64 * 1024)) {
+    (void)hipGetLastError();  // the failed attribute call's error is not this launch's
+    return false;
+  }
   hipLaunchKernelGGL((q4k_mfma_kernel<PAIR, NORM>), dim3((M + rows - 1) / rows), dim3(64 * nw), shm, stream, w,
                      x, y, M, K, w2, y2, rows, res, nrm, xsum, eps);
+  return true;
 }
 
 template <int QT, int R, int KS, int PAIR = 0>
@@ -1201,10 +1183,7 @@ void launch_direct_plan(const uint8_t* w, const float* x, float* y, int M, int K
   // and loads in flight for decode-sized M.  (A two-way split of 2-3 steps
   // measured slower than none: Q4_K 4096x4096 5.5 -> 7.2 us.)
   if constexpr (QT == 12) {
-    if (q4k_mfma_pays(M, K)) {
-      launch_q4k_mfma<0>(w, x, y, M, K, stream);
-      return;
-    }
+    if (q4k_mfma_pays(M, K) && launch_q4k_mfma<0>(w, x, y, M, K, stream)) return;
   }
   const int iters = (K / QD<QT>::QKB + 64 / QD<QT>::LPB - 1) / (64 / QD<QT>::LPB);
   // Tall matrices (output heads: 128256 rows) keep each row in one wave:
@@ -1230,10 +1209,7 @@ bool launch_pair_qt(const uint8_t* w, const uint8_t* w2, const float* x, float* 
                    : QT == 10 ? (a & 3) == 0 : (a & 1) == 0);
   if (!ok) return false;
   if constexpr (QT == 12) {
-    if (q4k_mfma_pays(2 * M, K)) {
-      launch_q4k_mfma<PAIR>(w, x, y, M, K, stream, w2, y2);
-      return true;
-    }
+    if (q4k_mfma_pays(2 * M, K) && launch_q4k_mfma<PAIR>(w, x, y, M, K, stream, w2, y2)) return true;
   }
   const int iters = (K / QD<QT>::QKB + 64 / QD<QT>::LPB - 1) / (64 / QD<QT>::LPB);
   // The block split follows the single-matrix rule (two waves for four to
@@ -1388,9 +1364,8 @@ bool linear_quant_gate_up_norm_launch(float* y, float* xsum, const float* x, con
   if (qtype != HL_GGML_Q4_K || M <= 0 || K <= 0 || K % 256 || K > 8192 || (v & 15) || (a & 15) ||
       !q4k_mfma_pays(2 * M, K))
     return false;
-  launch_q4k_mfma<1, true>((const uint8_t*)wg, x, y, M, K, stream, (const uint8_t*)wu, nullptr, res, nrm, xsum,
-                           eps);
-  return true;
+  return launch_q4k_mfma<1, true>((const uint8_t*)wg, x, y, M, K, stream, (const uint8_t*)wu, nullptr, res, nrm,
+                                  xsum, eps);
 }
 
 bool linear_quant_qkv_launch(float* yq, float* yk, float* yv, const float* x, const void* wq, const void* wk,

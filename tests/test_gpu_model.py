@@ -159,12 +159,15 @@ def test_forward_decode_token_wide_fused_projections(hl, orc, types):
 CFG_FFN = dict(CFG, n_emb=2048, n_head=32, n_head_kv=8, n_ff=16384)
 
 
-@pytest.mark.parametrize("n_ff", [16384, 8192])
-def test_forward_decode_token_norm_folded_into_gate_up(hl, orc, n_ff):
+# The fold at other widths: K = 4096 (two 8-block groups, eight waves, the
+# Llama-3-8B width), 8192 (four groups, sixteen waves) and 2560 (ten blocks:
+# a partial second group, threads past K/8 load zeros and write no sum).
+@pytest.mark.parametrize("n_emb,n_ff", [(2048, 16384), (2048, 8192), (4096, 4096), (8192, 2048), (2560, 6656)])
+def test_forward_decode_token_norm_folded_into_gate_up(hl, orc, n_emb, n_ff):
     from hippo_leap_amd.model import DenseDecoder
     types = {"wq": 12, "wk": 12, "wv": 12, "wo": 12, "w_gate": 12, "w_up": 12, "w_down": 12}
-    print(f"decode model: norm folded into the Q4_K gate/up, n_ff {n_ff}", flush=True)
-    cfg = dict(CFG_FFN, n_ff=n_ff)
+    print(f"decode model: norm folded into the Q4_K gate/up, n_emb {n_emb} n_ff {n_ff}", flush=True)
+    cfg = dict(CFG_FFN, n_emb=n_emb, n_ff=n_ff)
     dev, ref = _build(orc, cfg, types, False, 131)
     m = DenseDecoder(torch, cfg, dev["tok_emb"], dev["output_norm"], dev["output"],
                      dev["output_type"], dev["layers"])
