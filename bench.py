@@ -622,19 +622,28 @@ def main():
         for b_ in bufs:
             b_.fill_(1)
         sink = torch.zeros(4, dtype=torch.int32, device="cuda")
+        # Grid sizes x loads in flight per thread x (grid-stride, contiguous
+        # chunk per workgroup); the best of all is the floor.
         floor = {}
-        for nblk in (512, 1024, 2048, 4096):
-            floor[nblk] = graph_time_ms(torch, lambda i, nb=nblk: A.probe_stream_read(bufs[i % 16], sink, nb))
+        for nblk in (256, 512, 1024, 2048, 4096):
+            for ipt in (4, 8, 16):
+                for contig in (0, 1):
+                    floor[f"{nblk}x{ipt}{'c' if contig else 'g'}"] = graph_time_ms(
+                        torch, lambda i, nb=nblk, f=ipt, c=contig: A.probe_stream_read(
+                            bufs[i % 16], sink, nb, inflight=f, contiguous=bool(c)))
         best = min(floor.values())
+        best_cfg = min(floor, key=floor.get)
         result["stream_floor_c3"] = {
             "bytes": wl.kv_bytes, "us": round(best * 1e3, 3),
             "GBs": round(wl.kv_bytes / (best * 1e-3) / 1e9, 1),
             "frac_hbm": round(wl.kv_bytes / (best * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-            "us_by_workgroups": {str(k): round(v * 1e3, 3) for k, v in floor.items()},
+            "best_config": best_cfg,
+            "us_by_config": {k: round(v * 1e3, 3) for k, v in floor.items()},
+            "config_key": "<workgroups>x<loads in flight per thread><g: grid-stride | c: chunk per workgroup>",
             "step_kernel_over_floor": round(t["kernel"] / best, 3),
             "note": "hl_probe_stream_read: one launch that only streams the c3 byte count"}
         log(f"stream floor c3: {best*1e3:.2f} us ({wl.kv_bytes / (best * 1e-3) / 1e9:.0f} GB/s); "
-            f"by workgroups {', '.join(f'{k}: {v*1e3:.2f}' for k, v in floor.items())}")
+            f"best {best_cfg}; {', '.join(f'{k}: {v*1e3:.2f}' for k, v in floor.items())}")
         del bufs
         result["warm_cache_resident"] = {
             "value": round(wl.kv_bytes / (warm_ms * 1e-3) / 1e9, 2), "unit": "GB/s",

@@ -186,6 +186,7 @@ SIGNATURES = {
     "hl_attn_prefill_fallback_ran": (c_int, [ctypes.POINTER(PrefillArgs), c_void_p,
                                              ctypes.POINTER(c_int), c_void_p]),
     "hl_probe_stream_read": (c_int, [c_void_p, c_size_t, c_int, c_void_p, c_void_p]),
+    "hl_probe_stream_read_ex": (c_int, [c_void_p, c_size_t, c_int, c_int, c_int, c_void_p, c_void_p]),
     "hl_kv_cache_to_f32": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p]),
 }
 

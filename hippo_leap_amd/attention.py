@@ -385,10 +385,12 @@ def prefill_fallback_ran(args: PrefillArgs, workspace=None, stream=None) -> bool
     return bool(ran.value)
 
 
-def probe_stream_read(buf: torch.Tensor, sink: torch.Tensor, blocks: int = 0, stream=None) -> None:
+def probe_stream_read(buf: torch.Tensor, sink: torch.Tensor, blocks: int = 0, stream=None,
+                      inflight: int = 4, contiguous: bool = False) -> None:
     """One launch that only streams `buf` (measurement probe)."""
     nbytes = buf.numel() * buf.element_size()
-    check(_lib.load().hl_probe_stream_read(buf.data_ptr(), nbytes, blocks, sink.data_ptr(), _stream(stream)))
+    check(_lib.load().hl_probe_stream_read_ex(buf.data_ptr(), nbytes, blocks, inflight, int(contiguous),
+                                              sink.data_ptr(), _stream(stream)))
 
 
 def workspace(nbytes: int, device="cuda") -> torch.Tensor | None:

@@ -101,6 +101,11 @@ int hl_device_info_get(hl_device_info* info);
  * the floor a kernel reading that many bytes once reaches on this part,
  * timed beside the decode kernels at their byte counts.                    */
 int hl_probe_stream_read(const void* buf, size_t bytes, int blocks, unsigned* sink, void* stream);
+/* The same probe with `inflight` (4, 8 or 16) 16-byte loads per thread per
+ * iteration, and with contiguous != 0 each workgroup streaming its own
+ * contiguous chunk instead of a grid-stride sweep.                        */
+int hl_probe_stream_read_ex(const void* buf, size_t bytes, int blocks, int inflight, int contiguous,
+                            unsigned* sink, void* stream);
 
 /* Host-side RoPE theta table: theta[i] = powf(1/base, 2i/rope_dim) for
  * i < rope_dim/2, computed in fp32 exactly as naive.nim:3850-3861.       */
