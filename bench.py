@@ -217,7 +217,10 @@ def bench_decode(torch, A, wl, steps, warmup):
 # Prefill (c4)
 # ---------------------------------------------------------------------------
 class PrefillWorkload:
-    def __init__(self, torch, A, T=4096, hq=32, hkv=8, d=128, base=5e5, seed=7):
+    """c4's prefill; the KV cache in kv_layout (None: the layout the library
+    recommends for a bf16 cache of T columns, hl_kv_cache_preferred_layout,
+    which a backend's initKvCache allocates)."""
+    def __init__(self, torch, A, T=4096, hq=32, hkv=8, d=128, base=5e5, seed=7, kv_layout=None):
         g = torch.Generator(device="cuda").manual_seed(seed)
         bf = torch.bfloat16
         self.q = torch.randn(hq * d, T, generator=g, device="cuda").to(bf)
@@ -226,8 +229,12 @@ class PrefillWorkload:
         self.kc = torch.empty(hkv * d, T, dtype=bf, device="cuda")
         self.vc = torch.empty(hkv * d, T, dtype=bf, device="cuda")
         self.out = torch.empty(hq * d, T, dtype=torch.float32, device="cuda")  # fp32 like act1
+        if kv_layout is None:
+            kv_layout = int(A._lib.load().hl_kv_cache_preferred_layout(A.HL_BF16, T))
+        self.kv_layout = kv_layout
         self.a = A.prefill_args(self.q, self.k, self.v, self.out, hq, hkv, d, T, apply_rope=True,
-                                rope_base=base, k_cache=self.kc, v_cache=self.vc, max_len=T)
+                                rope_base=base, k_cache=self.kc, v_cache=self.vc, max_len=T,
+                                kv_layout=kv_layout)
         self.ws = A.workspace(A.prefill_workspace_bytes(self.a))
         self.A = A
         self.flops = 4 * hq * d * T * (T + 1) // 2
@@ -730,11 +737,22 @@ def main():
         torch.cuda.synchronize()
         ms = graph_time_ms(torch, pw.step, n_inner=8, replays=max(2, args.steps // 20))
         tf = pw.flops / (ms * 1e-3) / 1e12
+        # The same prefill writing a cache in the reference's column-major layout.
+        pc = PrefillWorkload(torch, A, kv_layout=A.HL_KV_COLMAJOR)
+        pc.step(0)
+        ms_col = graph_time_ms(torch, pc.step, n_inner=8, replays=max(2, args.steps // 20))
+        del pc
         result["prefill"] = {
             "workload": "c4: Llama-3-8B-shape causal prefill bf16, T=4096, Hq32/Hkv8, D128, "
                         "RoPE 5e5, KV cache written",
             "dtype": "bf16 in, fp16 MFMA operands, fp32 accumulation and output",
             "value": round(tf, 2), "unit": "TFLOP/s", "ms_per_step": round(ms, 4),
+            "kv_layout": {0: "colmajor", 1: "tiled32", 2: "paged32"}[pw.kv_layout] +
+                         " (hl_kv_cache_preferred_layout for a bf16 cache)",
+            "colmajor_cache": {"ms_per_step": round(ms_col, 4),
+                               "value": round(pw.flops / (ms_col * 1e-3) / 1e12, 2),
+                               "note": "the same prefill writing the reference's column-major "
+                                       "[Hkv*D, max_len] cache"},
             "roofline": {"bound": "mfma", "kernel": "kv_prologue_kernel + prefill_mfma_kernel",
                          "achieved": round(tf, 2), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(tf / BF16_PEAK_TFLOPS, 4),
@@ -751,7 +769,7 @@ def main():
             cb = cpu_baseline_prefill()
             cb["gpu_over_cpu"] = round(tf / cb["value"], 1)
             result["prefill"]["cpu_baseline"] = cb
-        log(f"prefill c4: {ms:.3f} ms, {tf:.1f} TFLOP/s")
+        log(f"prefill c4: {ms:.3f} ms, {tf:.1f} TFLOP/s (column-major cache: {ms_col:.3f} ms)")
         del pw
         torch.cuda.empty_cache()
 
