@@ -85,10 +85,10 @@ def event_time_ms(torch, fn, iters):
 # re-measured whenever the decode kernel changes.
 C3_STEP_TRAFFIC_BYTES = 35_169_893
 # The same for the c5 step kernel (column-major bf16 caches) and for one c4
-# prefill (kv_prologue_kernel + prefill_mfma_kernel):
+# prefill (kv_prologue_kernel + prefill_mfma_kernel + the gated fallback pass):
 # profiles/decode_step_c5_traffic.md, profiles/prefill_c4_mfma_util_and_traffic.md.
 C5_STEP_TRAFFIC_BYTES = 1_116_977_918
-C4_PREFILL_TRAFFIC_BYTES = 211_279_802
+C4_PREFILL_TRAFFIC_BYTES = 211_350_387
 
 
 def capture(torch, fn, n, first=0):
@@ -759,7 +759,7 @@ def main():
                          "traffic": C4_PREFILL_TRAFFIC_BYTES,
                          "traffic_source": "profiles/prefill_c4_mfma_util_and_traffic.md: "
                                            "FETCH_SIZE x 1.99981 + WRITE_SIZE of both kernels",
-                         "mfma_util_at_actual_clock": 0.463,
+                         "mfma_util_at_actual_clock": 0.465,
                          "mfma_util_source": "same profile: SQ_VALU_MFMA_BUSY_CYCLES / "
                                              "(GRBM_GUI_ACTIVE per XCD x 1024 SIMDs)",
                          "algorithmic_flops": pw.flops},
