@@ -560,7 +560,10 @@ __device__ __forceinline__ f32x16 mma32f(float a, float b, f32x16 c) {
 }
 }  // namespace
 
-template <int D, int KSPLIT>
+// FB: the gated fallback pass of an MFMA prefill (a grid of at most one
+// workgroup per CU looping over the items, output in out_dtype); otherwise
+// one item per workgroup and fp32 output, with no loop or gate in the code.
+template <int D, int KSPLIT, bool FB>
 __global__ __launch_bounds__(256) void prefill_f32mfma_kernel(PrefillLaunch p, int nh) {
   constexpr int NW = 4;             // waves
   constexpr int KS = D / 2;         // S^T k-steps (pairs of head dims)
@@ -575,7 +578,7 @@ __global__ __launch_bounds__(256) void prefill_f32mfma_kernel(PrefillLaunch p, i
   __shared__ __attribute__((aligned(16))) float sv[KSPLIT * SVN];  // [tile][h][d][ks]
 
   const int tid = threadIdx.x, lane = tid & 63;
-  if (p.fallback_record) {
+  if constexpr (FB) {
     // Fallback pass of an MFMA prefill: runs only when the call's overflow
     // mark F equals the staged S; workgroup 0 then advances the generation
     // (G = S, which nothing else in this kernel reads) and records the outcome.
@@ -604,11 +607,9 @@ __global__ __launch_bounds__(256) void prefill_f32mfma_kernel(PrefillLaunch p, i
   const int n_qblk = (T + rows_wg - 1) / rows_wg;
   const int n_hgrp = group / nh;
   const int per_q = p.n_head_kv * n_hgrp;
-  // One work item per workgroup, or, for the gated fallback pass, a grid of
-  // at most one workgroup per CU looping over the items.  Each item's first
-  // barrier (before its LDS fill) waits for every wave's previous item.
-  const int n_items = per_q * n_qblk;
-  for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
+  // Each item's first barrier (before its LDS fill) waits for every wave's
+  // previous item (fallback pass).
+  auto run_item = [&](const int item) {
     const int qblk = n_qblk - 1 - item / per_q;  // heaviest query blocks first
     const int kvh = (item % per_q) / n_hgrp;
     const int hgrp = (item % per_q) % n_hgrp;
@@ -765,7 +766,7 @@ __global__ __launch_bounds__(256) void prefill_f32mfma_kernel(PrefillLaunch p, i
           for (int i = 0; i < 16; ++i) xo[(sl * 16 * DB + db * 16 + i) * 64 + lane] = o[db][i];
       }
       __syncthreads();
-      if (kq > 0) continue;  // key groups 1.. are done with this item
+      if (kq > 0) return;  // key groups 1.. are done with this item
       // O^T layout: every element this lane holds belongs to its own query
       // row t_abs, so the merge factors are per-lane scalars.
       float mall = m_run;
@@ -791,7 +792,7 @@ __global__ __launch_bounds__(256) void prefill_f32mfma_kernel(PrefillLaunch p, i
           o[db][i] = v;
         }
     }
-    if (!live) continue;
+    if (!live) return;
     const float inv = 1.0f / l;
     if (t_abs < T) {
       // fp32 output, or fp16 / bf16 when this is the fallback of an MFMA prefill
@@ -802,11 +803,17 @@ __global__ __launch_bounds__(256) void prefill_f32mfma_kernel(PrefillLaunch p, i
         for (int i = 0; i < 16; ++i) {
           const int d = 32 * db + 8 * (i >> 2) + 4 * hh + (i & 3);
           const float y = o[db][i] * inv;
-          if (p.out_dtype == HL_F16) store_elem<HL_F16>(p.out, ob + (long long)d * T, y);
-          else if (p.out_dtype == HL_BF16) store_elem<HL_BF16>(p.out, ob + (long long)d * T, y);
+          if (FB && p.out_dtype == HL_F16) store_elem<HL_F16>(p.out, ob + (long long)d * T, y);
+          else if (FB && p.out_dtype == HL_BF16) store_elem<HL_BF16>(p.out, ob + (long long)d * T, y);
           else ((float*)p.out)[ob + (long long)d * T] = y;
         }
     }
+  };
+  if constexpr (FB) {
+    const int n_items = per_q * n_qblk;
+    for (int item = blockIdx.x; item < n_items; item += gridDim.x) run_item(item);
+  } else {
+    run_item(blockIdx.x);
   }
 }
 
@@ -825,14 +832,18 @@ hipError_t prefill_f32_launch(const PrefillLaunch& p, hipStream_t stream) {
   if (ksp > 1) nh = 2;
   const int items = grid_of(nh, ksp);
   const dim3 grid(p.fallback_record ? std::min(items, cu_count()) : items);
+#define HL_F32K(DD, KS)                                                                              \
+  if (p.fallback_record) hipLaunchKernelGGL((prefill_f32mfma_kernel<DD, KS, true>), grid, dim3(256), 0, stream, p, nh); \
+  else hipLaunchKernelGGL((prefill_f32mfma_kernel<DD, KS, false>), grid, dim3(256), 0, stream, p, nh)
   switch (p.head_dim) {
     case 64:
-      if (ksp == 2) hipLaunchKernelGGL((prefill_f32mfma_kernel<64, 2>), grid, dim3(256), 0, stream, p, nh);
-      else hipLaunchKernelGGL((prefill_f32mfma_kernel<64, 1>), grid, dim3(256), 0, stream, p, nh);
+      if (ksp == 2) HL_F32K(64, 2);
+      else HL_F32K(64, 1);
       break;
-    case 128: hipLaunchKernelGGL((prefill_f32mfma_kernel<128, 1>), grid, dim3(256), 0, stream, p, nh); break;
+    case 128: HL_F32K(128, 1); break;
     default: return hipErrorInvalidValue;
   }
+#undef HL_F32K
   return hipGetLastError();
 }
 

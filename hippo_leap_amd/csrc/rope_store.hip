@@ -198,10 +198,14 @@ __device__ __forceinline__ void store_cache8(void* cache, const CacheMap& m, int
   }
 }
 
-template <int IODT, int KDT, int DMAX>
+// GATED: the fallback pass of an MFMA prefill (returns at once unless the
+// call's overflow mark is set; a grid of at most one workgroup per CU loops
+// over the work items); otherwise one item per workgroup, with no loop or
+// gate in the code.
+template <int IODT, int KDT, int DMAX, bool GATED>
 __global__ __launch_bounds__(256) void prologue_kernel(PrologueOp op) {
   __shared__ float sx[DMAX][kPT + 1];  // DMAX >= head_dim: the tile, sized to its class
-  if (op.gate) {  // fallback pass: runs only when this call's mark is set
+  if constexpr (GATED) {  // fallback pass: runs only when this call's mark is set
     __shared__ unsigned s_go;
     if (threadIdx.x == 0) {
       const unsigned g = op.gate[1];
@@ -214,12 +218,8 @@ __global__ __launch_bounds__(256) void prologue_kernel(PrologueOp op) {
   __shared__ float scos[kTabHalf][kPT], ssin[kTabHalf][kPT];
   __shared__ float sred[8][kPT];
   __shared__ float sinv[kPT];
-  // Work items (tile, head group); a launch covers them with one workgroup
-  // each, or, for the gated fallback pass, with a grid of at most one
-  // workgroup per CU that loops over them.
-  const int n_items = op.n_tiles * op.n_hgrps;
-  for (int item = blockIdx.y * gridDim.x + blockIdx.x; item < n_items; item += gridDim.x * gridDim.y) {
-  const int tile = item % op.n_tiles, hgrp = item / op.n_tiles;
+  // Work item (tile, head group).
+  auto run_item = [&](const int tile, const int hgrp) {
     const int tid = threadIdx.x;
     const int T = op.seq_len, D = op.head_dim;
     const int t0 = tile * kPT;
@@ -397,7 +397,15 @@ __global__ __launch_bounds__(256) void prologue_kernel(PrologueOp op) {
       }
       if (omax >= kF16Inf && op.range_word) range_flag_set(op.range_word);
     }
-  __syncthreads();  // this item's LDS readers are done before the next item's fill
+  };
+  if constexpr (GATED) {
+    const int n_items = op.n_tiles * op.n_hgrps;
+    for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
+      run_item(item % op.n_tiles, item / op.n_tiles);
+      __syncthreads();  // this item's LDS readers are done before the next item's fill
+    }
+  } else {
+    run_item(blockIdx.x, blockIdx.y);
   }
 }
 
@@ -598,9 +606,15 @@ hipError_t prologue_launch(const PrologueOp& op, hipStream_t stream) {
   // A gated fallback pass usually exits at once: one workgroup per CU at
   // most (one round of gate reads), looping over the items when it runs.
   dim3 grid = op.gate ? dim3(std::min(tiles * o2.n_hgrps, cu_count())) : dim3(tiles, o2.n_hgrps);
-#define HL_PRO(IO, KD)                                                                          \
-  if (op.head_dim <= 128) hipLaunchKernelGGL((prologue_kernel<IO, KD, 128>), grid, dim3(256), 0, stream, o2); \
-  else hipLaunchKernelGGL((prologue_kernel<IO, KD, HL_MAX_HEAD_DIM>), grid, dim3(256), 0, stream, o2)
+#define HL_PRO_G(IO, KD, G)                                                                     \
+  if (op.head_dim <= 128) hipLaunchKernelGGL((prologue_kernel<IO, KD, 128, G>), grid, dim3(256), 0, stream, o2); \
+  else hipLaunchKernelGGL((prologue_kernel<IO, KD, HL_MAX_HEAD_DIM, G>), grid, dim3(256), 0, stream, o2)
+#define HL_PRO(IO, KD)             \
+  if (op.gate) {                   \
+    HL_PRO_G(IO, KD, true);        \
+  } else {                         \
+    HL_PRO_G(IO, KD, false);       \
+  }
 #define HL_PRO_IO(IO)                      \
   switch (op.kv_dtype) {                   \
     case HL_F32: HL_PRO(IO, HL_F32); break; \
@@ -615,6 +629,7 @@ hipError_t prologue_launch(const PrologueOp& op, hipStream_t stream) {
   }
 #undef HL_PRO_IO
 #undef HL_PRO
+#undef HL_PRO_G
   return hipGetLastError();
 }
 
