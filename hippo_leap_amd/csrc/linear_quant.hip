@@ -868,9 +868,15 @@ typedef _Float16 h2v __attribute__((ext_vector_type(2)));
 typedef int v4i __attribute__((ext_vector_type(4)));
 
 // Buffer resource over [base, base + bytes) (raw bytes; an access past
-// `bytes` reads zeros), for the buffer-load builtins.
+// `bytes` reads zeros), for the buffer-load builtins.  The base goes through
+// readfirstlane: a resource the compiler cannot prove wave-uniform makes it
+// wrap every load in a waterfall loop behind a full vmcnt(0) wait, which
+// drains the prefetched loads.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
+  const uintptr_t b = (uintptr_t)base;
+  const uint64_t u = (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)b) |
+                     ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(b >> 32)) << 32);
+  return __builtin_amdgcn_make_buffer_rsrc((void*)(uintptr_t)u, 0, (int)bytes, 0x00020000);
 }
 
 // Lane l reads lane dpp(l) of v (within rows of 16 lanes).
@@ -927,9 +933,8 @@ __global__ __launch_bounds__(1024) void q4k_mfma_kernel(const uint8_t* __restric
   // step adds nothing).
   const uint32_t vb = 8 * g + b8 < nb ? (uint32_t)rr * rowbytes + (uint32_t)(8 * g + b8) * 144u : oob;
   const uint32_t vq = vb + 16 + 32 * t;
-  const uint8_t* wbase[NP];
-#pragma unroll
-  for (int pm = 0; pm < NP; ++pm) wbase[pm] = (pm ? w2 : w) + (size_t)row0 * rowbytes;
+  const __amdgpu_buffer_rsrc_t rsw0 = buf_rsrc(w + (size_t)row0 * rowbytes, oob),
+                               rsw1 = buf_rsrc((PAIR ? w2 : w) + (size_t)row0 * rowbytes, oob);
   struct Raw {
     u32x4 hdr, q0, q1;
   };
@@ -942,7 +947,7 @@ __global__ __launch_bounds__(1024) void q4k_mfma_kernel(const uint8_t* __restric
   auto load = [&](int k, Raw& r) {
     const int pm = PAIR ? (k & 1) : 0, q = st + (PAIR ? k >> 1 : k) * nstream;
     const uint32_t so = __builtin_amdgcn_readfirstlane(k < nsteps ? (uint32_t)(2 * q) * rowbytes : oob);
-    const __amdgpu_buffer_rsrc_t rs = buf_rsrc(PAIR && pm ? wbase[NP - 1] : wbase[0], oob);
+    const __amdgpu_buffer_rsrc_t rs = PAIR && pm ? rsw1 : rsw0;  // a uniform select of SGPR resources
     __builtin_amdgcn_sched_barrier(0);
     r.hdr = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)vb, (int)so, 0);
     r.q0 = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)vq, (int)so, 0);
