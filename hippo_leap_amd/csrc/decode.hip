@@ -493,8 +493,14 @@ __device__ __forceinline__ u16x8 mask_row8(u16x8 r, int col, int lim) {
 
 // PG: paged caches (a compile-time variant, so the other layouts carry no
 // page lookups).
+// Launch bounds: the prefetching kernels hold two tiles per wave (one
+// workgroup per CU at head dim 128); the others fill more workgroups per CU
+// where their registers allow it without spilling.  Measured against the
+// tighter bounds that spilled: the fused step at head dim 128 (Llama-3-8B-
+// shaped layer, one sequence, 2K columns) 15.3 -> 13.0 us; the scalar-load
+// kernel at head dim 64 (c3 shape with an odd cache length) 40.5 -> 28.8 us.
 template <int D, int DT, bool VEC, bool PIPE, bool STEP, bool PG = false>
-__global__ __launch_bounds__(256, PIPE ? (D == 64 ? 2 : 1) : (D == 64 ? 4 : 2)) void decode_mfma_kernel(DecodeParams p) {
+__global__ __launch_bounds__(256, PIPE ? (D == 64 ? 2 : 1) : (D == 64 ? (VEC ? 4 : 2) : (STEP ? 1 : 2))) void decode_mfma_kernel(DecodeParams p) {
   static_assert(!PG || VEC, "paged caches are read with vector loads only");
   // MFMA operand type: the storage type, except fp8 caches, which are
   // converted to fp16 (exactly) as their tiles arrive.

@@ -610,6 +610,18 @@ __global__ __launch_bounds__(256) void prefill_f32mfma_kernel(PrefillLaunch p, i
   // Each item's first barrier (before its LDS fill) waits for every wave's
   // previous item (fallback pass).
   auto run_item = [&](const int item) {
+    // In the fallback's item loop the lane and wave ids are re-derived per
+    // item behind an empty asm: otherwise the per-lane load offsets (32 per
+    // K/V row set) are hoisted out of the loop and kept live across the
+    // whole item, which pushes the kernel into scratch at head dim 128.
+    int lane_i = lane, wave_i = wave, tid_i = tid;
+    if constexpr (FB) {
+      lane_i = (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+      asm volatile("" : "+v"(lane_i), "+s"(wave_i));
+      tid_i = wave_i * 64 + lane_i;
+    }
+    const int lane = lane_i, wave = wave_i, tid = tid_i;
+    const int ln = lane & 31, hh = lane >> 5;
     const int qblk = n_qblk - 1 - item / per_q;  // heaviest query blocks first
     const int kvh = (item % per_q) / n_hgrp;
     const int hgrp = (item % per_q) % n_hgrp;

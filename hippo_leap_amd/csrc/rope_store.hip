@@ -219,7 +219,20 @@ __global__ __launch_bounds__(256) void prologue_kernel(PrologueOp op) {
   __shared__ float sred[8][kPT];
   __shared__ float sinv[kPT];
   // Work item (tile, head group).
+  const PrologueOp& op_k = op;
   auto run_item = [&](const int tile, const int hgrp) {
+    // In the gated pass's item loop the parameters are read per item through
+    // a kernel-argument pointer the compiler cannot see through (the
+    // argument is the segment's only explicit one, at offset 0): otherwise
+    // the loads are hoisted out of the loop and their values kept in SGPRs
+    // across it, which spills them.
+    typedef const __attribute__((address_space(4))) PrologueOp* kop_t;
+    kop_t kp = nullptr;
+    if constexpr (GATED) {
+      kp = (kop_t)__builtin_amdgcn_kernarg_segment_ptr();
+      asm volatile("" : "+s"(kp));
+    }
+    const PrologueOp& op = GATED ? *(const PrologueOp*)kp : op_k;
     const int tid = threadIdx.x;
     const int T = op.seq_len, D = op.head_dim;
     const int t0 = tile * kPT;
