@@ -736,16 +736,16 @@ def main():
             pw.step(i)
         torch.cuda.synchronize()
         # The same prefill writing a cache in the reference's column-major
-        # layout, timed alternately with the preferred one (the shader clock
-        # drifts under sustained load, so whichever runs first differs):
-        # each figure is the mean of two alternating runs.
+        # layout, timed alternately with the preferred one in the order
+        # preferred, column-major, column-major, preferred (the shader clock
+        # ramps after a pause and drifts under sustained load, so a fixed
+        # order favours one of them): each figure is the mean of its two runs.
         pc = PrefillWorkload(torch, A, kv_layout=A.HL_KV_COLMAJOR)
         pc.step(0)
         reps = max(2, args.steps // 40)
         runs = {"pref": [], "col": []}
-        for _ in range(2):
-            runs["pref"].append(graph_time_ms(torch, pw.step, n_inner=8, replays=reps))
-            runs["col"].append(graph_time_ms(torch, pc.step, n_inner=8, replays=reps))
+        for key in ("pref", "col", "col", "pref"):
+            runs[key].append(graph_time_ms(torch, pw.step if key == "pref" else pc.step, n_inner=8, replays=reps))
         ms, ms_col = sum(runs["pref"]) / 2, sum(runs["col"]) / 2
         tf = pw.flops / (ms * 1e-3) / 1e12
         del pc
