@@ -558,12 +558,42 @@ namespace {
 __device__ __forceinline__ f32x16 mma32f(float a, float b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
 }
+// x ~= hi + lo * 2^-11 with hi, lo fp16: |x - hi - lo 2^-11| <= |x| 2^-22
+// for |x| < 32768 with hi normal (2^-36 absolute below fp16's normal range).
+// hi * hi' + (hi * lo' + lo * hi') 2^-11 is then the product to ~2^-21.
+__device__ __forceinline__ void split_f16x8(const float* x, f16x8& hi, f16x8& lo) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const _Float16 h = (_Float16)x[j];
+    hi[j] = h;
+    lo[j] = (_Float16)((x[j] - (float)h) * 2048.f);
+  }
+}
+// Power-of-two exponent that brings a magnitude (given as its bit pattern,
+// finite) into [2^13, 2^14): split operands scaled by it keep their hi parts
+// in fp16's normal range (the matrix cores treat fp16 subnormals as zero)
+// for every element within 2^27 of the largest.  0 for an all-zero set.
+__device__ __forceinline__ int split_shift(uint32_t max_bits) {
+  if (max_bits == 0u) return 0;
+  const int e = max_bits >= 0x00800000u ? (int)(max_bits >> 23) - 127 : -127;
+  return 13 - e;
+}
+constexpr uint32_t kInfBits = 0x7F800000u;  // |x| bit patterns at or above: inf or NaN
 }  // namespace
 
 // FB: the gated fallback pass of an MFMA prefill (a grid of at most one
 // workgroup per CU looping over the items, output in out_dtype); otherwise
 // one item per workgroup and fp32 output, with no loop or gate in the code.
-template <int D, int KSPLIT, bool FB>
+// X3: each step runs its two products as three fp16 MFMAs on a hi/lo split
+// of every fp32 operand (hi hi + (hi lo + lo hi) 2^-11, to ~2^-21 of each
+// product: within fp32 rounding of the dot products) instead of fp32 MFMAs,
+// which the matrix cores run at 1/16 of the fp16 rate.  The operands are
+// scaled by powers of two first (Q per row, K and V per tile, P by 2^14), so
+// that every element within 2^27 of its set's largest keeps a normal fp16 hi
+// part; the products are unscaled exactly.  A step whose tiles or the
+// workgroup's Q hold an inf or NaN runs the fp32 MFMAs (decided at the step's
+// first barrier from per-wave maxima).
+template <int D, int KSPLIT, bool FB, bool X3 = false>
 __global__ __launch_bounds__(256) void prefill_f32mfma_kernel(PrefillLaunch p, int nh) {
   constexpr int NW = 4;             // waves
   constexpr int KS = D / 2;         // S^T k-steps (pairs of head dims)
@@ -638,28 +668,88 @@ __global__ __launch_bounds__(256) void prefill_f32mfma_kernel(PrefillLaunch p, i
 
     // K/V tiles: thread moves column lc (key j0 + lc) of rows d = ld0 + 4k;
     // the next step's tiles are loaded while the current ones are computed.
+    // X3: K as above but rows 8 (ld0 + 4g) + j (eight consecutive dims of a
+    // key for a 16-byte fp16 chunk); V as chunks c = tid + 256 g of eight
+    // consecutive keys of row c / 8 (16-byte vector loads when rows allow).
     const int lc = tid & 63, ld0 = tid >> 6;
     float kr[KSPLIT][NL], vr[KSPLIT][NL];
+    [[maybe_unused]] const bool v_vec = (T & 3) == 0 && ((uintptr_t)p.v & 15) == 0;
     auto load_kv = [&](int step) {
 #pragma unroll
       for (int u = 0; u < KSPLIT; ++u) {
-        const int col = min((step * KSPLIT + u) * BN + lc, T - 1);
+        const int jb = (step * KSPLIT + u) * BN;
+        const int col = min(jb + lc, T - 1);
+        if constexpr (X3) {
 #pragma unroll
-        for (int k = 0; k < NL; ++k) {
-          kr[u][k] = K[(long long)(ld0 + NW * k) * T + col];
-          vr[u][k] = V[(long long)(ld0 + NW * k) * T + col];
+          for (int g = 0; g < NL / 8; ++g)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) kr[u][8 * g + j] = K[(long long)(8 * (ld0 + NW * g) + j) * T + col];
+#pragma unroll
+          for (int g = 0; g < NL / 8; ++g) {
+            const int c = tid + 256 * g, d = c >> 3, k0 = jb + 8 * (c & 7);
+            const float* row = V + (long long)d * T;
+            if (v_vec && k0 + 8 <= T) {
+              const f32x4 a = *(const f32x4*)(row + k0), b = *(const f32x4*)(row + k0 + 4);
+#pragma unroll
+              for (int j = 0; j < 4; ++j) {
+                vr[u][8 * g + j] = a[j];
+                vr[u][8 * g + 4 + j] = b[j];
+              }
+            } else {
+#pragma unroll
+              for (int j = 0; j < 8; ++j) vr[u][8 * g + j] = row[min(k0 + j, T - 1)];
+            }
+          }
+        } else {
+#pragma unroll
+          for (int k = 0; k < NL; ++k) {
+            kr[u][k] = K[(long long)(ld0 + NW * k) * T + col];
+            vr[u][k] = V[(long long)(ld0 + NW * k) * T + col];
+          }
         }
       }
     };
     load_kv(0);
 
     // q operand: lane (ln, hh) holds q[t][2ks + hh] * scale * log2 e
+    // (X3: loaded again in each fp32 step instead, so that the 2 x 32 or
+    // 2 x 64 q registers of the two forms are not both live in the loop.)
     float qv[KS];
-    {
+    auto load_qv = [&]() {
       const float* Q = p.q + (long long)hq * D * T;
       const int t = min(t_abs, T - 1);
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) qv[ks] = Q[(long long)(2 * ks + hh) * T + t] * p.scale_log2;
+    };
+    if constexpr (!X3) load_qv();
+    // X3: lane (ln, hh) also holds q[t][16 ks + 8 hh + j] * scale * log2 e *
+    // 2^sq as the fp16 hi/lo B operand of the S^T = K Q^T MFMAs, sq scaling
+    // the row's largest element (over both lane halves) into [2^13, 2^14);
+    // qbad: an inf or NaN among them.
+    [[maybe_unused]] f16x8 qh[X3 ? D / 16 : 1], ql[X3 ? D / 16 : 1];
+    [[maybe_unused]] bool qbad = false;
+    [[maybe_unused]] int sq = 0;
+    if constexpr (X3) {
+      const float* Q = p.q + (long long)hq * D * T;
+      const int t = min(t_abs, T - 1);
+      float x[D / 16][8];
+      uint32_t mq = 0u;
+#pragma unroll
+      for (int ks = 0; ks < D / 16; ++ks)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          x[ks][j] = Q[(long long)(16 * ks + 8 * hh + j) * T + t] * p.scale_log2;
+          mq = max(mq, __float_as_uint(x[ks][j]) & 0x7FFFFFFFu);
+        }
+      mq = max(mq, (uint32_t)__shfl_xor((int)mq, 32, 64));
+      qbad = live && mq >= kInfBits;
+      sq = qbad ? 0 : split_shift(mq);
+#pragma unroll
+      for (int ks = 0; ks < D / 16; ++ks) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) x[ks][j] = __builtin_amdgcn_ldexpf(x[ks][j], sq);
+        split_f16x8(x[ks], qh[ks], ql[ks]);
+      }
     }
     // Swizzled 16-byte chunk of a staged row (rows 2D or 128 bytes long).
     auto kswz = [](int key) { return D == 64 ? (key >> 1) & 7 : key & 15; };
@@ -670,21 +760,125 @@ __global__ __launch_bounds__(256) void prefill_f32mfma_kernel(PrefillLaunch p, i
     for (int db = 0; db < DB; ++db)
 #pragma unroll
       for (int i = 0; i < 16; ++i) o[db][i] = 0.f;
+    // X3: per-wave largest K and V magnitudes of a step and the wave's Q
+    // flag, gathered at the step's first barrier.
+    [[maybe_unused]] __shared__ uint32_t s_max[X3 ? NW : 1][3];
     float m_run = -INFINITY, l_run = 0.f;
 
     for (int step = 0; step < n_steps; ++step) {
-      __syncthreads();  // the previous step's sk / sv reads are done
+      // The previous step's sk / sv reads are done; X3: and the vote.
+      bool x3 = false;
+      [[maybe_unused]] int shk = 0, shv = 0;
+      if constexpr (X3) {
+        // Largest magnitudes as bit patterns (NaN above every finite value and
+        // inf), per wave into LDS.  Keys past T hold copies of key T - 1
+        // (clamped loads), real entries of the tensor.
+        uint32_t mk = 0u, mv = 0u;
 #pragma unroll
-      for (int u = 0; u < KSPLIT; ++u) {
-        const bool in = (step * KSPLIT + u) * BN + lc < T;
+        for (int u = 0; u < KSPLIT; ++u)
 #pragma unroll
-        for (int k = 0; k < NL; ++k) {
-          const int d = ld0 + NW * k;
-          const float kx = in ? kr[u][k] : 0.f, vx = in ? vr[u][k] : 0.f;
-          // K: (h = d & 1, key = lc, ks = d >> 1); V: (h = lc & 1, d, ks = lc >> 1)
-          const int ksk = d >> 1, ksv = lc >> 1;
-          sk[u * SKN + ((d & 1) * BN + lc) * KS + (((ksk >> 2) ^ kswz(lc)) << 2) + (ksk & 3)] = kx;
-          sv[u * SVN + ((lc & 1) * D + d) * 32 + (((ksv >> 2) ^ vswz(d)) << 2) + (ksv & 3)] = vx;
+          for (int e = 0; e < NL; ++e) {
+            mk = max(mk, __float_as_uint(kr[u][e]) & 0x7FFFFFFFu);
+            mv = max(mv, __float_as_uint(vr[u][e]) & 0x7FFFFFFFu);
+          }
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) {
+          mk = max(mk, (uint32_t)__shfl_xor((int)mk, o, 64));
+          mv = max(mv, (uint32_t)__shfl_xor((int)mv, o, 64));
+        }
+        const bool wq = __builtin_amdgcn_ballot_w64(qbad) != 0;
+        if (lane == 0) {
+          s_max[wave][0] = mk;
+          s_max[wave][1] = mv;
+          s_max[wave][2] = wq;
+        }
+        __syncthreads();
+        uint32_t km = 0u, vm = 0u, qb = 0u;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+          km = max(km, s_max[w][0]);
+          vm = max(vm, s_max[w][1]);
+          qb |= s_max[w][2];
+        }
+        x3 = !qb && km < kInfBits && vm < kInfBits;
+        shk = split_shift(km);
+        shv = split_shift(vm);
+      } else {
+        __syncthreads();
+      }
+      if (x3) {
+        // fp16 hi / lo tiles: K [key][D] and V^T [d][64 keys], 16-byte chunks
+        // XOR-swizzled by the row (K: key % (D/8); V: (d / 2) % 8).
+#pragma unroll
+        for (int u = 0; u < KSPLIT; ++u) {
+          const int jb = (step * KSPLIT + u) * BN;
+          uint16_t* kh = (uint16_t*)(sk + u * SKN);
+          uint16_t* kl = kh + BN * D;
+          uint16_t* vh = (uint16_t*)(sv + u * SVN);
+          uint16_t* vl = vh + D * BN;
+          const bool kin = jb + lc < T;
+#pragma unroll
+          for (int g = 0; g < NL / 8; ++g) {
+            float x[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) x[j] = kin ? __builtin_amdgcn_ldexpf(kr[u][8 * g + j], shk) : 0.f;
+            f16x8 h8, l8;
+            split_f16x8(x, h8, l8);
+            const int pos = lc * D + 8 * ((ld0 + NW * g) ^ (lc % (D / 8)));
+            *(f16x8*)(kh + pos) = h8;
+            *(f16x8*)(kl + pos) = l8;
+          }
+#pragma unroll
+          for (int g = 0; g < NL / 8; ++g) {
+            const int c = tid + 256 * g, d = c >> 3, kc = c & 7, k0 = jb + 8 * kc;
+            float x[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) x[j] = k0 + j < T ? __builtin_amdgcn_ldexpf(vr[u][8 * g + j], shv) : 0.f;
+            f16x8 h8, l8;
+            split_f16x8(x, h8, l8);
+            const int pos = d * BN + 8 * (kc ^ ((d >> 1) & 7));
+            *(f16x8*)(vh + pos) = h8;
+            *(f16x8*)(vl + pos) = l8;
+          }
+        }
+      } else if constexpr (X3) {
+        // fp32 tiles from the X3 register layout (same LDS layout as below)
+#pragma unroll
+        for (int u = 0; u < KSPLIT; ++u) {
+          const int jb = (step * KSPLIT + u) * BN;
+          const bool kin = jb + lc < T;
+#pragma unroll
+          for (int g = 0; g < NL / 8; ++g)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+              const int d = 8 * (ld0 + NW * g) + j, ksk = d >> 1;
+              sk[u * SKN + ((d & 1) * BN + lc) * KS + (((ksk >> 2) ^ kswz(lc)) << 2) + (ksk & 3)] =
+                  kin ? kr[u][8 * g + j] : 0.f;
+            }
+#pragma unroll
+          for (int g = 0; g < NL / 8; ++g) {
+            const int c = tid + 256 * g, d = c >> 3, kc = c & 7;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+              const int key = 8 * kc + j, ksv = key >> 1;
+              sv[u * SVN + ((key & 1) * D + d) * 32 + (((ksv >> 2) ^ vswz(d)) << 2) + (ksv & 3)] =
+                  jb + key < T ? vr[u][8 * g + j] : 0.f;
+            }
+          }
+        }
+      } else {
+#pragma unroll
+        for (int u = 0; u < KSPLIT; ++u) {
+          const bool in = (step * KSPLIT + u) * BN + lc < T;
+#pragma unroll
+          for (int k = 0; k < NL; ++k) {
+            const int d = ld0 + NW * k;
+            const float kx = in ? kr[u][k] : 0.f, vx = in ? vr[u][k] : 0.f;
+            // K: (h = d & 1, key = lc, ks = d >> 1); V: (h = lc & 1, d, ks = lc >> 1)
+            const int ksk = d >> 1, ksv = lc >> 1;
+            sk[u * SKN + ((d & 1) * BN + lc) * KS + (((ksk >> 2) ^ kswz(lc)) << 2) + (ksk & 3)] = kx;
+            sv[u * SVN + ((lc & 1) * D + d) * 32 + (((ksv >> 2) ^ vswz(d)) << 2) + (ksv & 3)] = vx;
+          }
         }
       }
       if (step + 1 < n_steps) load_kv(step + 1);
@@ -693,7 +887,94 @@ __global__ __launch_bounds__(256) void prefill_f32mfma_kernel(PrefillLaunch p, i
       if (!live || j0 > r0 + 31) continue;  // wave-uniform: no key of this tile is visible
       const float* tk = sk + kq * SKN;
       const float* tv = sv + kq * SVN;
+      if constexpr (X3) {
+        if (x3) {
+          const uint16_t* kh = (const uint16_t*)tk;
+          const uint16_t* kl = kh + BN * D;
+          const uint16_t* vh = (const uint16_t*)tv;
+          const uint16_t* vl = vh + D * BN;
+          // S^T = K Q^T: A row m = key 32 mb + sigma(m) (the bf16 flash kernel's
+          // permutation: P^T then feeds the P V MFMAs as it is).
+          f32x16 s[2];
+#pragma unroll
+          for (int mb = 0; mb < 2; ++mb) {
+            const int key = 32 * mb + sigma_row(ln);
+            f32x16 s1, s2;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) s1[i] = s2[i] = 0.f;
+#pragma unroll
+            for (int ks = 0; ks < D / 16; ++ks) {
+              const int pos = key * D + 8 * ((2 * ks + hh) ^ (key % (D / 8)));
+              const f16x8 ah = *(const f16x8*)(kh + pos), al = *(const f16x8*)(kl + pos);
+              s1 = mma32(ah, qh[ks], s1);
+              s2 = mma32(ah, ql[ks], s2);
+              s2 = mma32(al, qh[ks], s2);
+            }
+#pragma unroll
+            for (int i = 0; i < 16; ++i) s[mb][i] = __builtin_amdgcn_ldexpf(s1[i] + s2[i] * 0x1p-11f, -(sq + shk));
+          }
+          // Register i = 4a + e of lane half hh in block mb: key
+          // j0 + 32 mb + 16 (a >> 1) + 8 hh + 4 (a & 1) + e.
+          float mt = -INFINITY;
+#pragma unroll
+          for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+              const int a = i >> 2;
+              const int key = j0 + 32 * mb + 16 * (a >> 1) + 8 * hh + 4 * (a & 1) + (i & 3);
+              s[mb][i] = (key <= t_abs && key < T) ? s[mb][i] : -INFINITY;
+              mt = fmaxf(mt, s[mb][i]);
+            }
+          mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+          const float mn = fmaxf(m_run, mt);
+          const float alpha = fast_exp2(m_run - mn);
+          m_run = mn;
+          float ps = 0.f;
+#pragma unroll
+          for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+              s[mb][i] = fast_exp2(s[mb][i] - mn);
+              ps += s[mb][i];
+            }
+          l_run = l_run * alpha + ps;
+#pragma unroll
+          for (int db = 0; db < DB; ++db)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) o[db][i] *= alpha;
+          // O^T += V^T P^T, k-step u = keys 16 u + 8 hh + j of this lane's row,
+          // with P * 2^14 (its hi parts normal down to P = 2^-28) and V * 2^shv,
+          // into this tile's own accumulators, unscaled into o.
+          f16x8 ph[4], pl[4];
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            float x[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) x[j] = s[u >> 1][4 * (2 * (u & 1) + (j >> 2)) + (j & 3)] * 16384.f;
+            split_f16x8(x, ph[u], pl[u]);
+          }
+#pragma unroll
+          for (int db = 0; db < DB; ++db) {
+            const int d = 32 * db + ln;
+            f32x16 t1, t2;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) t1[i] = t2[i] = 0.f;
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+              const int pos = d * BN + 8 * ((2 * u + hh) ^ ((d >> 1) & 7));
+              const f16x8 vh8 = *(const f16x8*)(vh + pos), vl8 = *(const f16x8*)(vl + pos);
+              t1 = mma32(vh8, ph[u], t1);
+              t2 = mma32(vh8, pl[u], t2);
+              t2 = mma32(vl8, ph[u], t2);
+            }
+#pragma unroll
+            for (int i = 0; i < 16; ++i) o[db][i] += __builtin_amdgcn_ldexpf(t1[i] + t2[i] * 0x1p-11f, -(shv + 14));
+          }
+          continue;
+        }
+      }
 
+      if constexpr (X3) load_qv();
       f32x16 s[2];
 #pragma unroll
       for (int mb = 0; mb < 2; ++mb) {
@@ -846,7 +1127,10 @@ hipError_t prefill_f32_launch(const PrefillLaunch& p, hipStream_t stream) {
   const dim3 grid(p.fallback_record ? std::min(items, cu_count()) : items);
 #define HL_F32K(DD, KS)                                                                              \
   if (p.fallback_record) hipLaunchKernelGGL((prefill_f32mfma_kernel<DD, KS, true>), grid, dim3(256), 0, stream, p, nh); \
-  else hipLaunchKernelGGL((prefill_f32mfma_kernel<DD, KS, false>), grid, dim3(256), 0, stream, p, nh)
+  else hipLaunchKernelGGL((prefill_f32mfma_kernel<DD, KS, false, DD == 64>), grid, dim3(256), 0, stream, p, nh)
+  // The split-operand steps (X3) at head dim 64; at 128 the fp32 steps'
+  // fallback and the split steps do not fit one kernel's registers together,
+  // so that kernel keeps the fp32 MFMAs throughout.
   switch (p.head_dim) {
     case 64:
       if (ksp == 2) HL_F32K(64, 2);

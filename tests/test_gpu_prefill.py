@@ -89,6 +89,73 @@ def test_prefill_c2_full(hl, orc):
     assert np.all(kcn[:, T:] == 7.0) and np.all(vcn[:, T:] == 7.0)  # canary untouched
 
 
+@pytest.mark.parametrize("T", [1, 2, 31, 33, 63, 65, 127, 130, 257])
+def test_prefill_fp32_split_path_lengths(hl, orc, T):
+    """Head dim 64: the fp32 kernel's steps run on fp16 hi/lo splits of the
+    operands; partial tiles and lengths that are not a multiple of 4 (V read
+    element-wise) against the fp32 oracle."""
+    hq, hkv, d = 8, 2, 64
+    q = orc.normal(hq * d * T, 40 + T).reshape(hq * d, T)
+    k = orc.normal(hkv * d * T, 41 + T).reshape(hkv * d, T)
+    v = orc.normal(hkv * d * T, 42 + T).reshape(hkv * d, T)
+    ref, _, _ = oracle_prefill(orc, q, k, v, hq, hkv, d, T, base=1e4)
+    out = run_prefill(to_dev(q, 0), to_dev(k, 0), to_dev(v, 0), hq, hkv, d, T, apply_rope=True,
+                      rope_base=1e4)
+    err = rel_err(from_dev(out), ref)
+    print(f"split path T={T} rel err {err:.3e}")
+    assert err < TOL_F32 / 10
+
+
+@pytest.mark.parametrize("where", ["k_tile", "v_tile", "q_row", "tiny"])
+def test_prefill_fp32_split_path_outliers(hl, orc, where):
+    """Head dim 64, T=300: values of 2^15 and beyond in one K tile, one V tile
+    or one query row, and tiny ones, through the scaled fp16 split (each set
+    is scaled so that its largest element sits below 2^14).  Against the
+    fp32 oracle."""
+    hq, hkv, d, T = 8, 2, 64, 300
+    q = orc.normal(hq * d * T, 51).reshape(hq * d, T)
+    k = orc.normal(hkv * d * T, 52).reshape(hkv * d, T)
+    v = orc.normal(hkv * d * T, 53).reshape(hkv * d, T)
+    if where == "k_tile":
+        k[5, 70:80] = 1e5          # keys 70..79 of kv head 0 (tile 1)
+        k[d + 9, 200] = -4e4       # kv head 1, tile 3
+        q[5::d, :] = 0.0           # those dims do not reach the scores (a score
+        q[9::d, :] = 0.0           # of ~1e4 would leave the softmax ill-conditioned)
+    elif where == "v_tile":
+        v[3, 130:140] = 5e4        # tile 2 of kv head 0
+        v[d + 60, 299] = -1e6      # last key of kv head 1
+    elif where == "q_row":
+        q[2 * d + 7, 150] = 3e5    # q * scale beyond 2^15 for one row of head 2
+    else:
+        k[:, 100:110] *= 1e-30
+        v[:, 100:110] *= 1e-30
+        q[:, 40:50] *= 1e-20
+    ref, _, _ = oracle_prefill(orc, q, k, v, hq, hkv, d, T)
+    out = run_prefill(to_dev(q, 0), to_dev(k, 0), to_dev(v, 0), hq, hkv, d, T)
+    err = rel_err(from_dev(out), ref)
+    print(f"outliers {where} rel err {err:.3e}")
+    assert np.isfinite(from_dev(out)).all() and err < TOL_F32
+
+
+def test_prefill_fp32_split_path_nan_key(hl, orc):
+    """A NaN in one V entry at the first key of a 64-key tile: the steps that
+    load the tile run fp32 MFMAs, and exactly the rows that see that key come
+    out NaN, as in the oracle; the other rows match it.  (Within a tile the
+    P V product is a matrix product, so a NaN at a later key of the tile
+    also reaches the earlier rows that process the tile: 0 x NaN.)"""
+    hq, hkv, d, T = 8, 2, 64, 200
+    q = orc.normal(hq * d * T, 61).reshape(hq * d, T)
+    k = orc.normal(hkv * d * T, 62).reshape(hkv * d, T)
+    v = orc.normal(hkv * d * T, 63).reshape(hkv * d, T)
+    v[5, 128] = np.nan  # kv head 0, key 128 (first key of tile 2)
+    with np.errstate(invalid="ignore"):
+        ref, _, _ = oracle_prefill(orc, q, k, v, hq, hkv, d, T)
+    out = from_dev(run_prefill(to_dev(q, 0), to_dev(k, 0), to_dev(v, 0), hq, hkv, d, T))
+    assert np.array_equal(np.isnan(out), np.isnan(ref))
+    fin = ~np.isnan(ref)
+    assert np.abs(out[fin] - ref[fin]).max() / np.abs(ref[fin]).max() < TOL_F32
+
+
 @pytest.mark.parametrize("T", [1, 2, 31, 32, 33, 63, 64, 65, 127, 200])
 def test_prefill_fp32_lengths(hl, orc, T):
     hq, hkv, d = 8, 2, 128
