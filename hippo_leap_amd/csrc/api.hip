@@ -64,6 +64,9 @@ struct DevWs {
   size_t zero_prefix = 0;  // leading bytes known to hold zero arrival counters
 };
 std::vector<DevWs> g_ws;
+// The same for the reference-signature prefill entry point (its fp32 K/V
+// split images); grown on demand, per device.
+std::vector<DevWs> g_pws;
 std::vector<void*> g_argmax_ws;  // per device, kArgmaxScratchBytes, counter zero between calls
 
 void build_theta(ThetaTable& t, int rope_dim, float base) {
@@ -707,6 +710,7 @@ struct PrefillPlan {
   bool q_in_kernel;  // MFMA kernel builds Q from the raw activations (no qt)
   int t_pad;
   size_t off_q, off_k, off_v, off_tab, off_q32, off_k32, off_v32, off_range, bytes;
+  size_t off_split, split_bytes;  // fp32, head dim 64: the K/V split images and their tile records
 };
 
 static int validate_prefill(const hl_prefill_args* a, PrefillPlan* pl) {
@@ -742,6 +746,7 @@ static int validate_prefill(const hl_prefill_args* a, PrefillPlan* pl) {
     return fail(HL_EUNSUPPORTED, "prefill: write_back_qk needs fp32 activations");
   const size_t D = a->head_dim, T = a->seq_len;
   pl->mfma = a->io_dtype != HL_F32;
+  pl->off_split = pl->split_bytes = 0;
   const int rd = a->rope_dim ? a->rope_dim : a->head_dim;
   // The MFMA kernel applies RoPE to Q itself when every rotation pair lies in
   // one lane's registers: interleaved pairs, or half-split over all dims.
@@ -772,6 +777,9 @@ static int validate_prefill(const hl_prefill_args* a, PrefillPlan* pl) {
     pl->off_q32 = pl->off_k32 = pl->off_v32 = 0;
     pl->off_range = 0;
     pl->bytes = (pre && !a->write_back_qk) ? pl->off_k + (size_t)a->n_head_kv * T * D * 4 : 0;
+    pl->split_bytes = prefill_f32_split_bytes(a->n_head_kv, a->head_dim, a->seq_len);
+    pl->off_split = (pl->bytes + 255) / 256 * 256;
+    if (pl->split_bytes) pl->bytes = pl->off_split + pl->split_bytes;
   }
   return HL_OK;
 }
@@ -949,6 +957,10 @@ int hl_attn_prefill(const hl_prefill_args* a, void* workspace, size_t ws_bytes, 
   pf.k = ksrc;
   pf.v = (const float*)a->v;
   pf.scale_log2 = scale * kLog2e;
+  if (pl.split_bytes) {
+    pf.kv_img = ws + pl.off_split;
+    pf.kv_meta = (int*)(ws + pl.off_split + (size_t)a->n_head_kv * ((a->seq_len + 63) / 64) * 64 * a->head_dim * 8);
+  }
   e = prefill_f32_launch(pf, st);
   return e == hipSuccess ? HL_OK : hip_fail(e, "prefill launch");
 }
@@ -987,7 +999,33 @@ int hl_gpu_attention_prefill(float* dst, const float* q, const float* k, const f
   a.k = k;
   a.v = v;
   a.out = dst;
-  return hl_attn_prefill(&a, nullptr, 0, stream);
+  PrefillPlan pl;
+  int rc = validate_prefill(&a, &pl);
+  if (rc) return rc;
+  if (pl.bytes == 0) return hl_attn_prefill(&a, nullptr, 0, stream);
+  // Library-owned workspace: the lock is held through the launch, so a
+  // concurrent call that grows the buffer cannot free it under this one's
+  // launches (it synchronises the device before freeing).
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  std::lock_guard<std::mutex> lk(g_mu);
+  if ((int)g_pws.size() <= dev) g_pws.resize(dev + 1);
+  DevWs& w = g_pws[dev];
+  if (w.bytes < pl.bytes) {
+    if ((rc = refuse_if_capturing(stream, "prefill workspace"))) return rc;
+    if (w.ptr) {
+      e = hipDeviceSynchronize();  // an earlier launch may still read it
+      if (e != hipSuccess) return hip_fail(e, "hipDeviceSynchronize");
+      hipFree(w.ptr);
+      w.ptr = nullptr;
+      w.bytes = 0;
+    }
+    e = hipMalloc(&w.ptr, pl.bytes);
+    if (e != hipSuccess) return hip_fail(e, "hipMalloc(prefill workspace)");
+    w.bytes = pl.bytes;
+  }
+  return hl_attn_prefill(&a, w.ptr, w.bytes, stream);
 }
 
 static bool overlaps(const void* a, size_t abytes, const void* b, size_t bbytes) {

@@ -145,8 +145,15 @@ struct PrefillLaunch {
   // Workgroups return at once unless the call's overflow mark is set;
   // workgroup 0 advances the record's generation (common.h).
   unsigned* fallback_record;
+  // fp32 path at head dim 64 (not the fallback pass): workspace for the K/V
+  // split images prefill_f32_launch writes and its flash kernel reads,
+  // prefill_f32_split_bytes of it: [Hkv][ceil(T/64)] tiles of 32 KB, then
+  // 16 bytes of shifts and flag per tile.
+  void* kv_img;
+  int* kv_meta;
 };
 hipError_t prefill_f32_launch(const PrefillLaunch& p, hipStream_t stream);
+size_t prefill_f32_split_bytes(int n_head_kv, int head_dim, int seq_len);
 hipError_t prefill_mfma_launch(const PrefillLaunch& p, hipStream_t stream);
 int prefill_mfma_tpad(int seq_len);
 

@@ -16,7 +16,9 @@
 //    within 2e-3 of the fp32 reference; P is rounded to fp16, accumulation
 //    is fp32.
 //  * prefill_f32mfma_kernel: fp32 MFMA (v_mfma_f32_32x32x2_f32) on the
-//    reference's col-major fp32 tensors (the 1e-4 path).
+//    reference's col-major fp32 tensors (the 1e-4 path); at head dim 64,
+//    fp16 MFMAs on hi/lo splits of the operands, with K and V split once
+//    per call by kv_split_kernel.
 #include "common.h"
 #include "launch.h"
 
@@ -581,6 +583,119 @@ __device__ __forceinline__ int split_shift(uint32_t max_bits) {
 constexpr uint32_t kInfBits = 0x7F800000u;  // |x| bit patterns at or above: inf or NaN
 }  // namespace
 
+// Bytes of one 64-key tile's split image: K hi, K lo ([key][D] fp16), V hi,
+// V lo ([d][64 keys] fp16), each in the LDS layout of the flash kernel.
+template <int D>
+constexpr int kSplitTileBytes = 64 * D * 8;
+
+// kv_split_kernel: K and V of kv head blockIdx.y, keys 64 blockIdx.x ..
+// + 63, as the split-operand (X3) flash kernel's LDS images, once per call
+// instead of in every workgroup that reads the tile.  Every element is
+// scaled by a power of two per tensor and tile (its largest magnitude into
+// [2^13, 2^14)) and split into fp16 hi + lo * 2^-11; keys past T are zeros.
+// meta[4 * (h * n_tiles + tile)] = {K shift, V shift, inf/NaN flag, 0}; a
+// flagged tile's image is not written (its steps run the fp32 MFMAs).
+template <int D>
+__global__ __launch_bounds__(256) void kv_split_kernel(const float* __restrict__ k, const float* __restrict__ v,
+                                                       char* __restrict__ img, int* __restrict__ meta, int T) {
+  constexpr int BN = 64, NL = D * BN / 256;  // elements of each tensor per thread
+  __shared__ __attribute__((aligned(16))) uint16_t s_img[kSplitTileBytes<D> / 2];
+  __shared__ uint32_t s_red[4][2];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tl = blockIdx.x, h = blockIdx.y, n_kt = gridDim.x, jb = tl * BN;
+  const float* K = k + (long long)h * D * T;
+  const float* V = v + (long long)h * D * T;
+  // K: key lc, dims 8 (ld0 + 4 g) + j (one 16-byte fp16 chunk of a K row);
+  // V: chunks c = tid + 256 g, eight keys 8 (c % 8) + j of dim c / 8.
+  const int lc = tid & 63, ld0 = tid >> 6;
+  const bool kin = jb + lc < T;
+  const bool vvec = (T & 3) == 0 && ((uintptr_t)v & 15) == 0;
+  float kr[NL], vr[NL];
+  uint32_t mk = 0u, mv = 0u;
+#pragma unroll
+  for (int g = 0; g < NL / 8; ++g)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      kr[8 * g + j] = kin ? K[(long long)(8 * (ld0 + 4 * g) + j) * T + jb + lc] : 0.f;
+      mk = max(mk, __float_as_uint(kr[8 * g + j]) & 0x7FFFFFFFu);
+    }
+#pragma unroll
+  for (int g = 0; g < NL / 8; ++g) {
+    const int c = tid + 256 * g, k0 = jb + 8 * (c & 7);
+    const float* row = V + (long long)(c >> 3) * T;
+    if (vvec && k0 + 8 <= T) {
+      const f32x4 a = *(const f32x4*)(row + k0), b = *(const f32x4*)(row + k0 + 4);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        vr[8 * g + j] = a[j];
+        vr[8 * g + 4 + j] = b[j];
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) vr[8 * g + j] = k0 + j < T ? row[k0 + j] : 0.f;
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) mv = max(mv, __float_as_uint(vr[8 * g + j]) & 0x7FFFFFFFu);
+  }
+  // Largest magnitudes as bit patterns (NaN above every finite value and inf)
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    mk = max(mk, (uint32_t)__shfl_xor((int)mk, o, 64));
+    mv = max(mv, (uint32_t)__shfl_xor((int)mv, o, 64));
+  }
+  if (lane == 0) {
+    s_red[wave][0] = mk;
+    s_red[wave][1] = mv;
+  }
+  __syncthreads();
+  mk = max(max(s_red[0][0], s_red[1][0]), max(s_red[2][0], s_red[3][0]));
+  mv = max(max(s_red[0][1], s_red[1][1]), max(s_red[2][1], s_red[3][1]));
+  const bool bad = mk >= kInfBits || mv >= kInfBits;
+  const int shk = split_shift(mk), shv = split_shift(mv);
+  const long long t_idx = (long long)h * n_kt + tl;
+  if (tid == 0) *(int4*)(meta + 4 * t_idx) = make_int4(shk, shv, bad ? 1 : 0, 0);
+  if (bad) return;  // uniform
+  uint16_t* kh = s_img;
+  uint16_t* kl = kh + BN * D;
+  uint16_t* vh = kl + BN * D;
+  uint16_t* vl = vh + D * BN;
+#pragma unroll
+  for (int g = 0; g < NL / 8; ++g) {
+    float x[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) x[j] = __builtin_amdgcn_ldexpf(kr[8 * g + j], shk);
+    f16x8 h8, l8;
+    split_f16x8(x, h8, l8);
+    const int pos = lc * D + 8 * ((ld0 + 4 * g) ^ (lc % (D / 8)));
+    *(f16x8*)(kh + pos) = h8;
+    *(f16x8*)(kl + pos) = l8;
+  }
+#pragma unroll
+  for (int g = 0; g < NL / 8; ++g) {
+    const int c = tid + 256 * g, d = c >> 3, kc = c & 7;
+    float x[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) x[j] = __builtin_amdgcn_ldexpf(vr[8 * g + j], shv);
+    f16x8 h8, l8;
+    split_f16x8(x, h8, l8);
+    const int pos = d * BN + 8 * (kc ^ ((d >> 1) & 7));
+    *(f16x8*)(vh + pos) = h8;
+    *(f16x8*)(vl + pos) = l8;
+  }
+  __syncthreads();
+  char* dst = img + t_idx * kSplitTileBytes<D>;
+#pragma unroll
+  for (int i = 0; i < kSplitTileBytes<D> / 4096; ++i) {
+    const int off = (tid + 256 * i) * 16;
+    *(u32x4*)(dst + off) = *(const u32x4*)((const char*)s_img + off);
+  }
+}
+
+size_t prefill_f32_split_bytes(int n_head_kv, int head_dim, int seq_len) {
+  if (head_dim != 64) return 0;
+  return (size_t)n_head_kv * ((seq_len + 63) / 64) * (kSplitTileBytes<64> + 16);
+}
+
 // FB: the gated fallback pass of an MFMA prefill (a grid of at most one
 // workgroup per CU looping over the items, output in out_dtype); otherwise
 // one item per workgroup and fp32 output, with no loop or gate in the code.
@@ -590,9 +705,11 @@ constexpr uint32_t kInfBits = 0x7F800000u;  // |x| bit patterns at or above: inf
 // which the matrix cores run at 1/16 of the fp16 rate.  The operands are
 // scaled by powers of two first (Q per row, K and V per tile, P by 2^14), so
 // that every element within 2^27 of its set's largest keeps a normal fp16 hi
-// part; the products are unscaled exactly.  A step whose tiles or the
-// workgroup's Q hold an inf or NaN runs the fp32 MFMAs (decided at the step's
-// first barrier from per-wave maxima).
+// part; the products are unscaled exactly.  K and V arrive split, from
+// kv_split_kernel's per-tile images (two LDS sets, the next step's copied in
+// during this one); Q is split per wave.  A step whose tiles (the split
+// kernel's flags) or the workgroup's Q (a vote before the first step) hold an
+// inf or NaN runs the fp32 MFMAs on fp32 tiles loaded at that step.
 template <int D, int KSPLIT, bool FB, bool X3 = false>
 __global__ __launch_bounds__(256) void prefill_f32mfma_kernel(PrefillLaunch p, int nh) {
   constexpr int NW = 4;             // waves
@@ -604,8 +721,11 @@ __global__ __launch_bounds__(256) void prefill_f32mfma_kernel(PrefillLaunch p, i
   // KSPLIT key groups: wave w serves head w % nh and the key tiles
   // kq, kq + KSPLIT, ... (kq = w / nh); each step stages KSPLIT tiles.
   constexpr int SKN = 2 * BN * KS, SVN = 2 * D * 32;
-  __shared__ __attribute__((aligned(16))) float sk[KSPLIT * SKN];  // [tile][h][key][ks]
-  __shared__ __attribute__((aligned(16))) float sv[KSPLIT * SVN];  // [tile][h][d][ks]
+  // X3: two sets of KSPLIT tiles, the next step's copied in while this
+  // step's are read.
+  constexpr int NBUF = X3 ? 2 : 1;
+  __shared__ __attribute__((aligned(16))) float sk[NBUF * KSPLIT * SKN];  // [buf][tile][h][key][ks]
+  __shared__ __attribute__((aligned(16))) float sv[NBUF * KSPLIT * SVN];  // [buf][tile][h][d][ks]
 
   const int tid = threadIdx.x, lane = tid & 63;
   if constexpr (FB) {
@@ -665,51 +785,88 @@ __global__ __launch_bounds__(256) void prefill_f32mfma_kernel(PrefillLaunch p, i
 
     const float* K = p.k + (long long)kvh * D * T;
     const float* V = p.v + (long long)kvh * D * T;
+    // Swizzled 16-byte chunk of a staged fp32 row (rows 2D or 128 bytes long).
+    auto kswz = [](int key) { return D == 64 ? (key >> 1) & 7 : key & 15; };
+    auto vswz = [](int d) { return (d >> 1) & 7; };
 
-    // K/V tiles: thread moves column lc (key j0 + lc) of rows d = ld0 + 4k;
-    // the next step's tiles are loaded while the current ones are computed.
-    // X3: K as above but rows 8 (ld0 + 4g) + j (eight consecutive dims of a
-    // key for a 16-byte fp16 chunk); V as chunks c = tid + 256 g of eight
-    // consecutive keys of row c / 8 (16-byte vector loads when rows allow).
+    // fp32 K/V tiles: thread moves column lc (key j0 + lc) of rows
+    // d = ld0 + 4k; the next step's tiles are loaded while the current ones
+    // are computed.  X3: only a step that runs the fp32 MFMAs loads them, at
+    // the step; the split tiles come from the split kernel's images instead
+    // (kv_split_kernel), copied straight into LDS one step ahead.
     const int lc = tid & 63, ld0 = tid >> 6;
     float kr[KSPLIT][NL], vr[KSPLIT][NL];
-    [[maybe_unused]] const bool v_vec = (T & 3) == 0 && ((uintptr_t)p.v & 15) == 0;
     auto load_kv = [&](int step) {
 #pragma unroll
       for (int u = 0; u < KSPLIT; ++u) {
-        const int jb = (step * KSPLIT + u) * BN;
-        const int col = min(jb + lc, T - 1);
-        if constexpr (X3) {
+        const int col = min((step * KSPLIT + u) * BN + lc, T - 1);
 #pragma unroll
-          for (int g = 0; g < NL / 8; ++g)
-#pragma unroll
-            for (int j = 0; j < 8; ++j) kr[u][8 * g + j] = K[(long long)(8 * (ld0 + NW * g) + j) * T + col];
-#pragma unroll
-          for (int g = 0; g < NL / 8; ++g) {
-            const int c = tid + 256 * g, d = c >> 3, k0 = jb + 8 * (c & 7);
-            const float* row = V + (long long)d * T;
-            if (v_vec && k0 + 8 <= T) {
-              const f32x4 a = *(const f32x4*)(row + k0), b = *(const f32x4*)(row + k0 + 4);
-#pragma unroll
-              for (int j = 0; j < 4; ++j) {
-                vr[u][8 * g + j] = a[j];
-                vr[u][8 * g + 4 + j] = b[j];
-              }
-            } else {
-#pragma unroll
-              for (int j = 0; j < 8; ++j) vr[u][8 * g + j] = row[min(k0 + j, T - 1)];
-            }
-          }
-        } else {
-#pragma unroll
-          for (int k = 0; k < NL; ++k) {
-            kr[u][k] = K[(long long)(ld0 + NW * k) * T + col];
-            vr[u][k] = V[(long long)(ld0 + NW * k) * T + col];
-          }
+        for (int k = 0; k < NL; ++k) {
+          kr[u][k] = K[(long long)(ld0 + NW * k) * T + col];
+          vr[u][k] = V[(long long)(ld0 + NW * k) * T + col];
         }
       }
     };
-    load_kv(0);
+    // Writes the loaded tiles to LDS set b in the fp32 layout (keys past T
+    // as zeros).
+    auto stage_f32 = [&](int step, int b) {
+#pragma unroll
+      for (int u = 0; u < KSPLIT; ++u) {
+        const bool in = (step * KSPLIT + u) * BN + lc < T;
+        float* tk = sk + (b * KSPLIT + u) * SKN;
+        float* tv = sv + (b * KSPLIT + u) * SVN;
+#pragma unroll
+        for (int k = 0; k < NL; ++k) {
+          const int d = ld0 + NW * k;
+          const float kx = in ? kr[u][k] : 0.f, vx = in ? vr[u][k] : 0.f;
+          // K: (h = d & 1, key = lc, ks = d >> 1); V: (h = lc & 1, d, ks = lc >> 1)
+          const int ksk = d >> 1, ksv = lc >> 1;
+          tk[((d & 1) * BN + lc) * KS + (((ksk >> 2) ^ kswz(lc)) << 2) + (ksk & 3)] = kx;
+          tv[((lc & 1) * D + d) * 32 + (((ksv >> 2) ^ vswz(d)) << 2) + (ksv & 3)] = vx;
+        }
+      }
+    };
+    // X3: a tile's image (kv_split_kernel) into LDS set b, 1 KB per wave copy:
+    // the K image into the set's K tile, the V image into its V tile.
+    const int n_kt = (T + BN - 1) / BN;
+    [[maybe_unused]] const char* img = (const char*)p.kv_img + (long long)kvh * n_kt * kSplitTileBytes<D>;
+    [[maybe_unused]] const int* meta = p.kv_meta + (long long)kvh * n_kt * 4;
+    [[maybe_unused]] auto issue_copies = [&](int step, int b) {
+#pragma unroll
+      for (int u = 0; u < KSPLIT; ++u) {
+        const int tl = step * KSPLIT + u;
+        if (tl >= n_tiles) continue;
+        const char* src = img + (long long)tl * kSplitTileBytes<D> + lane * 16;
+        constexpr int NCH = kSplitTileBytes<D> / 1024, HALF = NCH / 2;
+#pragma unroll
+        for (int i = 0; i < NCH / NW; ++i) {
+          const int ch = wave + NW * i;
+          char* dst = ch < HALF ? (char*)(sk + (b * KSPLIT + u) * SKN) + ch * 1024
+                                : (char*)(sv + (b * KSPLIT + u) * SVN) + (ch - HALF) * 1024;
+          copy16_to_lds(src + ch * 1024, dst);
+        }
+      }
+    };
+    // X3: the step's tile records (any flag among its tiles; this wave's
+    // tile's shifts), loaded with the step's copies, a step ahead.
+    [[maybe_unused]] int m_bad = 0, m_shk = 0, m_shv = 0;
+    [[maybe_unused]] auto load_meta = [&](int step) {
+      m_bad = 0;
+#pragma unroll
+      for (int u = 0; u < KSPLIT; ++u) {
+        const int tl = min(step * KSPLIT + u, n_tiles - 1);  // a tile past the workgroup's repeats one
+        m_bad |= meta[4 * tl + 2];
+      }
+      const int tl = min(step * KSPLIT + kq, n_tiles - 1);
+      m_shk = meta[4 * tl];
+      m_shv = meta[4 * tl + 1];
+    };
+    if constexpr (X3) {
+      issue_copies(0, 0);
+      load_meta(0);
+    } else {
+      load_kv(0);
+    }
 
     // q operand: lane (ln, hh) holds q[t][2ks + hh] * scale * log2 e
     // (X3: loaded again in each fp32 step instead, so that the 2 x 32 or
@@ -751,142 +908,52 @@ __global__ __launch_bounds__(256) void prefill_f32mfma_kernel(PrefillLaunch p, i
         split_f16x8(x[ks], qh[ks], ql[ks]);
       }
     }
-    // Swizzled 16-byte chunk of a staged row (rows 2D or 128 bytes long).
-    auto kswz = [](int key) { return D == 64 ? (key >> 1) & 7 : key & 15; };
-    auto vswz = [](int d) { return (d >> 1) & 7; };
 
     f32x16 o[DB];
 #pragma unroll
     for (int db = 0; db < DB; ++db)
 #pragma unroll
       for (int i = 0; i < 16; ++i) o[db][i] = 0.f;
-    // X3: per-wave largest K and V magnitudes of a step and the wave's Q
-    // flag, gathered at the step's first barrier.
-    [[maybe_unused]] __shared__ uint32_t s_max[X3 ? NW : 1][3];
+    // X3: each wave's Q flag, read after the first step's barrier.
+    [[maybe_unused]] __shared__ uint32_t s_qbad[NW];
+    if constexpr (X3)
+      if (lane == 0) s_qbad[wave] = __builtin_amdgcn_ballot_w64(qbad) != 0;
     float m_run = -INFINITY, l_run = 0.f;
 
     for (int step = 0; step < n_steps; ++step) {
-      // The previous step's sk / sv reads are done; X3: and the vote.
+      // The previous step's sk / sv reads are done.
       bool x3 = false;
       [[maybe_unused]] int shk = 0, shv = 0;
+      const int b = X3 ? (step & 1) : 0;  // LDS set of this step
       if constexpr (X3) {
-        // Largest magnitudes as bit patterns (NaN above every finite value and
-        // inf), per wave into LDS.  Keys past T hold copies of key T - 1
-        // (clamped loads), real entries of the tensor.
-        uint32_t mk = 0u, mv = 0u;
-#pragma unroll
-        for (int u = 0; u < KSPLIT; ++u)
-#pragma unroll
-          for (int e = 0; e < NL; ++e) {
-            mk = max(mk, __float_as_uint(kr[u][e]) & 0x7FFFFFFFu);
-            mv = max(mv, __float_as_uint(vr[u][e]) & 0x7FFFFFFFu);
-          }
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) {
-          mk = max(mk, (uint32_t)__shfl_xor((int)mk, o, 64));
-          mv = max(mv, (uint32_t)__shfl_xor((int)mv, o, 64));
-        }
-        const bool wq = __builtin_amdgcn_ballot_w64(qbad) != 0;
-        if (lane == 0) {
-          s_max[wave][0] = mk;
-          s_max[wave][1] = mv;
-          s_max[wave][2] = wq;
-        }
+        // This wave's copies of the step's images have landed; after the
+        // barrier every wave's have, and the other set's readers (the previous
+        // step) are done, so the next step's copies may start.
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
         __syncthreads();
-        uint32_t km = 0u, vm = 0u, qb = 0u;
-#pragma unroll
-        for (int w = 0; w < NW; ++w) {
-          km = max(km, s_max[w][0]);
-          vm = max(vm, s_max[w][1]);
-          qb |= s_max[w][2];
+        // Split steps unless a tile of the step or the workgroup's Q holds an
+        // inf or NaN (the split kernel's flag per tile, the Q vote).
+        x3 = (m_bad | s_qbad[0] | s_qbad[1] | s_qbad[2] | s_qbad[3]) == 0;
+        shk = m_shk;
+        shv = m_shv;
+        if (step + 1 < n_steps) issue_copies(step + 1, b ^ 1);
+        load_meta(min(step + 1, n_steps - 1));  // unconditional: no join that waits for it
+        if (!x3) {
+          // fp32 MFMA step: the fp32 tiles replace this set's images
+          load_kv(step);
+          stage_f32(step, b);
+          __syncthreads();
         }
-        x3 = !qb && km < kInfBits && vm < kInfBits;
-        shk = split_shift(km);
-        shv = split_shift(vm);
       } else {
         __syncthreads();
+        stage_f32(step, 0);
+        if (step + 1 < n_steps) load_kv(step + 1);
+        __syncthreads();
       }
-      if (x3) {
-        // fp16 hi / lo tiles: K [key][D] and V^T [d][64 keys], 16-byte chunks
-        // XOR-swizzled by the row (K: key % (D/8); V: (d / 2) % 8).
-#pragma unroll
-        for (int u = 0; u < KSPLIT; ++u) {
-          const int jb = (step * KSPLIT + u) * BN;
-          uint16_t* kh = (uint16_t*)(sk + u * SKN);
-          uint16_t* kl = kh + BN * D;
-          uint16_t* vh = (uint16_t*)(sv + u * SVN);
-          uint16_t* vl = vh + D * BN;
-          const bool kin = jb + lc < T;
-#pragma unroll
-          for (int g = 0; g < NL / 8; ++g) {
-            float x[8];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) x[j] = kin ? __builtin_amdgcn_ldexpf(kr[u][8 * g + j], shk) : 0.f;
-            f16x8 h8, l8;
-            split_f16x8(x, h8, l8);
-            const int pos = lc * D + 8 * ((ld0 + NW * g) ^ (lc % (D / 8)));
-            *(f16x8*)(kh + pos) = h8;
-            *(f16x8*)(kl + pos) = l8;
-          }
-#pragma unroll
-          for (int g = 0; g < NL / 8; ++g) {
-            const int c = tid + 256 * g, d = c >> 3, kc = c & 7, k0 = jb + 8 * kc;
-            float x[8];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) x[j] = k0 + j < T ? __builtin_amdgcn_ldexpf(vr[u][8 * g + j], shv) : 0.f;
-            f16x8 h8, l8;
-            split_f16x8(x, h8, l8);
-            const int pos = d * BN + 8 * (kc ^ ((d >> 1) & 7));
-            *(f16x8*)(vh + pos) = h8;
-            *(f16x8*)(vl + pos) = l8;
-          }
-        }
-      } else if constexpr (X3) {
-        // fp32 tiles from the X3 register layout (same LDS layout as below)
-#pragma unroll
-        for (int u = 0; u < KSPLIT; ++u) {
-          const int jb = (step * KSPLIT + u) * BN;
-          const bool kin = jb + lc < T;
-#pragma unroll
-          for (int g = 0; g < NL / 8; ++g)
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-              const int d = 8 * (ld0 + NW * g) + j, ksk = d >> 1;
-              sk[u * SKN + ((d & 1) * BN + lc) * KS + (((ksk >> 2) ^ kswz(lc)) << 2) + (ksk & 3)] =
-                  kin ? kr[u][8 * g + j] : 0.f;
-            }
-#pragma unroll
-          for (int g = 0; g < NL / 8; ++g) {
-            const int c = tid + 256 * g, d = c >> 3, kc = c & 7;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-              const int key = 8 * kc + j, ksv = key >> 1;
-              sv[u * SVN + ((key & 1) * D + d) * 32 + (((ksv >> 2) ^ vswz(d)) << 2) + (ksv & 3)] =
-                  jb + key < T ? vr[u][8 * g + j] : 0.f;
-            }
-          }
-        }
-      } else {
-#pragma unroll
-        for (int u = 0; u < KSPLIT; ++u) {
-          const bool in = (step * KSPLIT + u) * BN + lc < T;
-#pragma unroll
-          for (int k = 0; k < NL; ++k) {
-            const int d = ld0 + NW * k;
-            const float kx = in ? kr[u][k] : 0.f, vx = in ? vr[u][k] : 0.f;
-            // K: (h = d & 1, key = lc, ks = d >> 1); V: (h = lc & 1, d, ks = lc >> 1)
-            const int ksk = d >> 1, ksv = lc >> 1;
-            sk[u * SKN + ((d & 1) * BN + lc) * KS + (((ksk >> 2) ^ kswz(lc)) << 2) + (ksk & 3)] = kx;
-            sv[u * SVN + ((lc & 1) * D + d) * 32 + (((ksv >> 2) ^ vswz(d)) << 2) + (ksv & 3)] = vx;
-          }
-        }
-      }
-      if (step + 1 < n_steps) load_kv(step + 1);
-      __syncthreads();
       const int j0 = (step * KSPLIT + kq) * BN;
       if (!live || j0 > r0 + 31) continue;  // wave-uniform: no key of this tile is visible
-      const float* tk = sk + kq * SKN;
-      const float* tv = sv + kq * SVN;
+      const float* tk = sk + (b * KSPLIT + kq) * SKN;
+      const float* tv = sv + (b * KSPLIT + kq) * SVN;
       if constexpr (X3) {
         if (x3) {
           const uint16_t* kh = (const uint16_t*)tk;
@@ -914,17 +981,25 @@ __global__ __launch_bounds__(256) void prefill_f32mfma_kernel(PrefillLaunch p, i
             for (int i = 0; i < 16; ++i) s[mb][i] = __builtin_amdgcn_ldexpf(s1[i] + s2[i] * 0x1p-11f, -(sq + shk));
           }
           // Register i = 4a + e of lane half hh in block mb: key
-          // j0 + 32 mb + 16 (a >> 1) + 8 hh + 4 (a & 1) + e.
+          // j0 + 32 mb + 16 (a >> 1) + 8 hh + 4 (a & 1) + e.  A tile before
+          // the row block's first row and inside T needs no mask (wave-uniform).
           float mt = -INFINITY;
+          if (j0 + BN - 1 <= r0 && j0 + BN <= T) {
 #pragma unroll
-          for (int mb = 0; mb < 2; ++mb)
+            for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-              const int a = i >> 2;
-              const int key = j0 + 32 * mb + 16 * (a >> 1) + 8 * hh + 4 * (a & 1) + (i & 3);
-              s[mb][i] = (key <= t_abs && key < T) ? s[mb][i] : -INFINITY;
-              mt = fmaxf(mt, s[mb][i]);
-            }
+              for (int i = 0; i < 16; ++i) mt = fmaxf(mt, s[mb][i]);
+          } else {
+#pragma unroll
+            for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+              for (int i = 0; i < 16; ++i) {
+                const int a = i >> 2;
+                const int key = j0 + 32 * mb + 16 * (a >> 1) + 8 * hh + 4 * (a & 1) + (i & 3);
+                s[mb][i] = (key <= t_abs && key < T) ? s[mb][i] : -INFINITY;
+                mt = fmaxf(mt, s[mb][i]);
+              }
+          }
           mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
           const float mn = fmaxf(m_run, mt);
           const float alpha = fast_exp2(m_run - mn);
@@ -1125,6 +1200,12 @@ hipError_t prefill_f32_launch(const PrefillLaunch& p, hipStream_t stream) {
   if (ksp > 1) nh = 2;
   const int items = grid_of(nh, ksp);
   const dim3 grid(p.fallback_record ? std::min(items, cu_count()) : items);
+  if (!p.fallback_record && p.head_dim == 64) {
+    // split images for the X3 kernel (after the prologue, on the same stream)
+    if (!p.kv_img || !p.kv_meta) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((kv_split_kernel<64>), dim3((p.seq_len + 63) / 64, p.n_head_kv), dim3(256), 0, stream, p.k,
+                       p.v, (char*)p.kv_img, p.kv_meta, p.seq_len);
+  }
 #define HL_F32K(DD, KS)                                                                              \
   if (p.fallback_record) hipLaunchKernelGGL((prefill_f32mfma_kernel<DD, KS, true>), grid, dim3(256), 0, stream, p, nh); \
   else hipLaunchKernelGGL((prefill_f32mfma_kernel<DD, KS, false, DD == 64>), grid, dim3(256), 0, stream, p, nh)

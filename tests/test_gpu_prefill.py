@@ -53,17 +53,20 @@ def test_prefill_golden_fp32(hl, name):
 
 
 def test_prefill_reference_dropin(hl, orc):
-    """gpuAttentionPrefill signature: already-roped fp32 projections."""
+    """gpuAttentionPrefill signature: already-roped fp32 projections.  At head
+    dim 64 the call uses a library-held workspace (the K/V split images):
+    the second length grows it, the third runs in the larger one."""
     from hippo_leap_amd import attention as A
-    hq, hkv, d, T = 32, 4, 64, 300
-    q = orc.normal(hq * d * T, 11).reshape(hq * d, T)
-    k = orc.normal(hkv * d * T, 12).reshape(hkv * d, T)
-    v = orc.normal(hkv * d * T, 13).reshape(hkv * d, T)
-    ref = orc.attention_prefill(q, k, v, hq, hkv, d, T)
-    dst = torch.empty(hq * d, T, device="cuda")
-    A.gpu_attention_prefill(dst, to_dev(q, 0), to_dev(k, 0), to_dev(v, 0), hq, hkv, d, T)
-    torch.cuda.synchronize()
-    assert rel_err(from_dev(dst), ref) < TOL_F32
+    hq, hkv, d = 32, 4, 64
+    for T in (300, 700, 65):
+        q = orc.normal(hq * d * T, 11 + T).reshape(hq * d, T)
+        k = orc.normal(hkv * d * T, 12 + T).reshape(hkv * d, T)
+        v = orc.normal(hkv * d * T, 13 + T).reshape(hkv * d, T)
+        ref = orc.attention_prefill(q, k, v, hq, hkv, d, T)
+        dst = torch.empty(hq * d, T, device="cuda")
+        A.gpu_attention_prefill(dst, to_dev(q, 0), to_dev(k, 0), to_dev(v, 0), hq, hkv, d, T)
+        torch.cuda.synchronize()
+        assert rel_err(from_dev(dst), ref) < TOL_F32, T
 
 
 def test_prefill_c2_full(hl, orc):
