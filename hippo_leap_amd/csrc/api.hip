@@ -950,6 +950,18 @@ int hl_attn_prefill(const hl_prefill_args* a, void* workspace, size_t ws_bytes, 
     if (!a->k_cache) op.k = nullptr;
   }
   if (!a->k_cache) op.v = nullptr;
+  if (pl.split_bytes) {
+    // Head dim 64: the prologue also writes the K/V split images the flash
+    // kernel reads (so it always runs, over whole 64-token tiles).
+    op.k = a->k;
+    op.v = a->v;
+    op.kv_img = ws + pl.off_split;
+    op.kv_meta = (int*)(ws + pl.off_split + (size_t)a->n_head_kv * ((a->seq_len + 63) / 64) * kSplitImgBytes);
+    op.t_pad = (a->seq_len + 63) / 64 * 64;
+    if (!op.q) op.hv_first = a->n_head;
+    pf.kv_img = op.kv_img;
+    pf.kv_meta = op.kv_meta;
+  }
   if (op.q || op.k || op.v) {
     if ((e = prologue_launch(op, st)) != hipSuccess) return hip_fail(e, "prefill prologue launch");
   }
@@ -957,10 +969,6 @@ int hl_attn_prefill(const hl_prefill_args* a, void* workspace, size_t ws_bytes, 
   pf.k = ksrc;
   pf.v = (const float*)a->v;
   pf.scale_log2 = scale * kLog2e;
-  if (pl.split_bytes) {
-    pf.kv_img = ws + pl.off_split;
-    pf.kv_meta = (int*)(ws + pl.off_split + (size_t)a->n_head_kv * ((a->seq_len + 63) / 64) * 64 * a->head_dim * 8);
-  }
   e = prefill_f32_launch(pf, st);
   return e == hipSuccess ? HL_OK : hip_fail(e, "prefill launch");
 }

@@ -176,4 +176,36 @@ struct ThetaTable {
   float t[HL_MAX_ROPE_DIM / 2];
 };
 
+// Split of fp32 operands into fp16 hi + lo * 2^-11 for three-MFMA
+// products (the fp32 prefill at head dim 64).
+// x ~= hi + lo * 2^-11 with hi, lo fp16: |x - hi - lo 2^-11| <= |x| 2^-22
+// for |x| < 32768 with hi normal (2^-36 absolute below fp16's normal range).
+// hi * hi' + (hi * lo' + lo * hi') 2^-11 is then the product to ~2^-21.
+__device__ __forceinline__ void split_f16x8(const float* x, f16x8& hi, f16x8& lo) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const _Float16 h = (_Float16)x[j];
+    hi[j] = h;
+    lo[j] = (_Float16)((x[j] - (float)h) * 2048.f);
+  }
+}
+// Power-of-two exponent that brings a magnitude (given as its bit pattern,
+// finite) into [2^13, 2^14): split operands scaled by it keep their hi parts
+// in fp16's normal range (the matrix cores treat fp16 subnormals as zero)
+// for every element within 2^27 of the largest.  0 for an all-zero set.
+__device__ __forceinline__ int split_shift(uint32_t max_bits) {
+  if (max_bits == 0u) return 0;
+  const int e = max_bits >= 0x00800000u ? (int)(max_bits >> 23) - 127 : -127;
+  return 13 - e;
+}
+constexpr uint32_t kInfBits = 0x7F800000u;  // |x| bit patterns at or above: inf or NaN
+// Split images of the fp32 prefill at head dim 64, one per (kv head, 64-key
+// tile): K hi, K lo ([key][64] fp16, 16-byte chunk c of key j at
+// c ^ (j % 8)), V hi, V lo ([d][64 keys] fp16, chunk c of dim d at
+// c ^ ((d / 2) % 8)).  Each 32-key half of a tile has its own power-of-two
+// scale per tensor; the tile's record holds 8 ints: the K shifts of halves
+// 0 and 1, the V shifts, then inf/NaN flags of K halves 0, 1 and V halves.
+constexpr int kSplitImgBytes = 64 * 64 * 8;
+constexpr int kSplitRecInts = 8;
+
 }  // namespace hl

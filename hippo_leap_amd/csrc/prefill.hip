@@ -18,7 +18,7 @@
 //  * prefill_f32mfma_kernel: fp32 MFMA (v_mfma_f32_32x32x2_f32) on the
 //    reference's col-major fp32 tensors (the 1e-4 path); at head dim 64,
 //    fp16 MFMAs on hi/lo splits of the operands, with K and V split once
-//    per call by kv_split_kernel.
+//    per call by the prologue (prologue_kernel).
 #include "common.h"
 #include "launch.h"
 
@@ -560,140 +560,11 @@ namespace {
 __device__ __forceinline__ f32x16 mma32f(float a, float b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
 }
-// x ~= hi + lo * 2^-11 with hi, lo fp16: |x - hi - lo 2^-11| <= |x| 2^-22
-// for |x| < 32768 with hi normal (2^-36 absolute below fp16's normal range).
-// hi * hi' + (hi * lo' + lo * hi') 2^-11 is then the product to ~2^-21.
-__device__ __forceinline__ void split_f16x8(const float* x, f16x8& hi, f16x8& lo) {
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const _Float16 h = (_Float16)x[j];
-    hi[j] = h;
-    lo[j] = (_Float16)((x[j] - (float)h) * 2048.f);
-  }
-}
-// Power-of-two exponent that brings a magnitude (given as its bit pattern,
-// finite) into [2^13, 2^14): split operands scaled by it keep their hi parts
-// in fp16's normal range (the matrix cores treat fp16 subnormals as zero)
-// for every element within 2^27 of the largest.  0 for an all-zero set.
-__device__ __forceinline__ int split_shift(uint32_t max_bits) {
-  if (max_bits == 0u) return 0;
-  const int e = max_bits >= 0x00800000u ? (int)(max_bits >> 23) - 127 : -127;
-  return 13 - e;
-}
-constexpr uint32_t kInfBits = 0x7F800000u;  // |x| bit patterns at or above: inf or NaN
 }  // namespace
-
-// Bytes of one 64-key tile's split image: K hi, K lo ([key][D] fp16), V hi,
-// V lo ([d][64 keys] fp16), each in the LDS layout of the flash kernel.
-template <int D>
-constexpr int kSplitTileBytes = 64 * D * 8;
-
-// kv_split_kernel: K and V of kv head blockIdx.y, keys 64 blockIdx.x ..
-// + 63, as the split-operand (X3) flash kernel's LDS images, once per call
-// instead of in every workgroup that reads the tile.  Every element is
-// scaled by a power of two per tensor and tile (its largest magnitude into
-// [2^13, 2^14)) and split into fp16 hi + lo * 2^-11; keys past T are zeros.
-// meta[4 * (h * n_tiles + tile)] = {K shift, V shift, inf/NaN flag, 0}; a
-// flagged tile's image is not written (its steps run the fp32 MFMAs).
-template <int D>
-__global__ __launch_bounds__(256) void kv_split_kernel(const float* __restrict__ k, const float* __restrict__ v,
-                                                       char* __restrict__ img, int* __restrict__ meta, int T) {
-  constexpr int BN = 64, NL = D * BN / 256;  // elements of each tensor per thread
-  __shared__ __attribute__((aligned(16))) uint16_t s_img[kSplitTileBytes<D> / 2];
-  __shared__ uint32_t s_red[4][2];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int tl = blockIdx.x, h = blockIdx.y, n_kt = gridDim.x, jb = tl * BN;
-  const float* K = k + (long long)h * D * T;
-  const float* V = v + (long long)h * D * T;
-  // K: key lc, dims 8 (ld0 + 4 g) + j (one 16-byte fp16 chunk of a K row);
-  // V: chunks c = tid + 256 g, eight keys 8 (c % 8) + j of dim c / 8.
-  const int lc = tid & 63, ld0 = tid >> 6;
-  const bool kin = jb + lc < T;
-  const bool vvec = (T & 3) == 0 && ((uintptr_t)v & 15) == 0;
-  float kr[NL], vr[NL];
-  uint32_t mk = 0u, mv = 0u;
-#pragma unroll
-  for (int g = 0; g < NL / 8; ++g)
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      kr[8 * g + j] = kin ? K[(long long)(8 * (ld0 + 4 * g) + j) * T + jb + lc] : 0.f;
-      mk = max(mk, __float_as_uint(kr[8 * g + j]) & 0x7FFFFFFFu);
-    }
-#pragma unroll
-  for (int g = 0; g < NL / 8; ++g) {
-    const int c = tid + 256 * g, k0 = jb + 8 * (c & 7);
-    const float* row = V + (long long)(c >> 3) * T;
-    if (vvec && k0 + 8 <= T) {
-      const f32x4 a = *(const f32x4*)(row + k0), b = *(const f32x4*)(row + k0 + 4);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        vr[8 * g + j] = a[j];
-        vr[8 * g + 4 + j] = b[j];
-      }
-    } else {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) vr[8 * g + j] = k0 + j < T ? row[k0 + j] : 0.f;
-    }
-#pragma unroll
-    for (int j = 0; j < 8; ++j) mv = max(mv, __float_as_uint(vr[8 * g + j]) & 0x7FFFFFFFu);
-  }
-  // Largest magnitudes as bit patterns (NaN above every finite value and inf)
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) {
-    mk = max(mk, (uint32_t)__shfl_xor((int)mk, o, 64));
-    mv = max(mv, (uint32_t)__shfl_xor((int)mv, o, 64));
-  }
-  if (lane == 0) {
-    s_red[wave][0] = mk;
-    s_red[wave][1] = mv;
-  }
-  __syncthreads();
-  mk = max(max(s_red[0][0], s_red[1][0]), max(s_red[2][0], s_red[3][0]));
-  mv = max(max(s_red[0][1], s_red[1][1]), max(s_red[2][1], s_red[3][1]));
-  const bool bad = mk >= kInfBits || mv >= kInfBits;
-  const int shk = split_shift(mk), shv = split_shift(mv);
-  const long long t_idx = (long long)h * n_kt + tl;
-  if (tid == 0) *(int4*)(meta + 4 * t_idx) = make_int4(shk, shv, bad ? 1 : 0, 0);
-  if (bad) return;  // uniform
-  uint16_t* kh = s_img;
-  uint16_t* kl = kh + BN * D;
-  uint16_t* vh = kl + BN * D;
-  uint16_t* vl = vh + D * BN;
-#pragma unroll
-  for (int g = 0; g < NL / 8; ++g) {
-    float x[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) x[j] = __builtin_amdgcn_ldexpf(kr[8 * g + j], shk);
-    f16x8 h8, l8;
-    split_f16x8(x, h8, l8);
-    const int pos = lc * D + 8 * ((ld0 + 4 * g) ^ (lc % (D / 8)));
-    *(f16x8*)(kh + pos) = h8;
-    *(f16x8*)(kl + pos) = l8;
-  }
-#pragma unroll
-  for (int g = 0; g < NL / 8; ++g) {
-    const int c = tid + 256 * g, d = c >> 3, kc = c & 7;
-    float x[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) x[j] = __builtin_amdgcn_ldexpf(vr[8 * g + j], shv);
-    f16x8 h8, l8;
-    split_f16x8(x, h8, l8);
-    const int pos = d * BN + 8 * (kc ^ ((d >> 1) & 7));
-    *(f16x8*)(vh + pos) = h8;
-    *(f16x8*)(vl + pos) = l8;
-  }
-  __syncthreads();
-  char* dst = img + t_idx * kSplitTileBytes<D>;
-#pragma unroll
-  for (int i = 0; i < kSplitTileBytes<D> / 4096; ++i) {
-    const int off = (tid + 256 * i) * 16;
-    *(u32x4*)(dst + off) = *(const u32x4*)((const char*)s_img + off);
-  }
-}
 
 size_t prefill_f32_split_bytes(int n_head_kv, int head_dim, int seq_len) {
   if (head_dim != 64) return 0;
-  return (size_t)n_head_kv * ((seq_len + 63) / 64) * (kSplitTileBytes<64> + 16);
+  return (size_t)n_head_kv * ((seq_len + 63) / 64) * (kSplitImgBytes + 4 * kSplitRecInts);
 }
 
 // FB: the gated fallback pass of an MFMA prefill (a grid of at most one
@@ -703,13 +574,14 @@ size_t prefill_f32_split_bytes(int n_head_kv, int head_dim, int seq_len) {
 // of every fp32 operand (hi hi + (hi lo + lo hi) 2^-11, to ~2^-21 of each
 // product: within fp32 rounding of the dot products) instead of fp32 MFMAs,
 // which the matrix cores run at 1/16 of the fp16 rate.  The operands are
-// scaled by powers of two first (Q per row, K and V per tile, P by 2^14), so
-// that every element within 2^27 of its set's largest keeps a normal fp16 hi
-// part; the products are unscaled exactly.  K and V arrive split, from
-// kv_split_kernel's per-tile images (two LDS sets, the next step's copied in
-// during this one); Q is split per wave.  A step whose tiles (the split
-// kernel's flags) or the workgroup's Q (a vote before the first step) hold an
-// inf or NaN runs the fp32 MFMAs on fp32 tiles loaded at that step.
+// scaled by powers of two first (Q per row, K and V per 32-key half tile, P
+// by 2^14 or less), so that every element within 2^27 of its set's largest
+// keeps a normal fp16 hi part; the products are unscaled exactly.  K and V
+// arrive split, from the prologue's per-tile images (two LDS sets, the next
+// step's copied in during this one); Q is split per wave.  A step whose
+// tiles (the prologue's flags) or the workgroup's Q (a vote before the first
+// step) hold an inf or NaN runs the fp32 MFMAs on fp32 tiles loaded at that
+// step.
 template <int D, int KSPLIT, bool FB, bool X3 = false>
 __global__ __launch_bounds__(256) void prefill_f32mfma_kernel(PrefillLaunch p, int nh) {
   constexpr int NW = 4;             // waves
@@ -793,7 +665,7 @@ __global__ __launch_bounds__(256) void prefill_f32mfma_kernel(PrefillLaunch p, i
     // d = ld0 + 4k; the next step's tiles are loaded while the current ones
     // are computed.  X3: only a step that runs the fp32 MFMAs loads them, at
     // the step; the split tiles come from the split kernel's images instead
-    // (kv_split_kernel), copied straight into LDS one step ahead.
+    // (written by the prologue), copied straight into LDS one step ahead.
     const int lc = tid & 63, ld0 = tid >> 6;
     float kr[KSPLIT][NL], vr[KSPLIT][NL];
     auto load_kv = [&](int step) {
@@ -826,18 +698,18 @@ __global__ __launch_bounds__(256) void prefill_f32mfma_kernel(PrefillLaunch p, i
         }
       }
     };
-    // X3: a tile's image (kv_split_kernel) into LDS set b, 1 KB per wave copy:
+    // X3: a tile's image into LDS set b, 1 KB per wave copy:
     // the K image into the set's K tile, the V image into its V tile.
     const int n_kt = (T + BN - 1) / BN;
-    [[maybe_unused]] const char* img = (const char*)p.kv_img + (long long)kvh * n_kt * kSplitTileBytes<D>;
-    [[maybe_unused]] const int* meta = p.kv_meta + (long long)kvh * n_kt * 4;
+    [[maybe_unused]] const char* img = (const char*)p.kv_img + (long long)kvh * n_kt * kSplitImgBytes;
+    [[maybe_unused]] const int* meta = p.kv_meta + (long long)kvh * n_kt * kSplitRecInts;
     [[maybe_unused]] auto issue_copies = [&](int step, int b) {
 #pragma unroll
       for (int u = 0; u < KSPLIT; ++u) {
         const int tl = step * KSPLIT + u;
         if (tl >= n_tiles) continue;
-        const char* src = img + (long long)tl * kSplitTileBytes<D> + lane * 16;
-        constexpr int NCH = kSplitTileBytes<D> / 1024, HALF = NCH / 2;
+        const char* src = img + (long long)tl * kSplitImgBytes + lane * 16;
+        constexpr int NCH = kSplitImgBytes / 1024, HALF = NCH / 2;
 #pragma unroll
         for (int i = 0; i < NCH / NW; ++i) {
           const int ch = wave + NW * i;
@@ -847,19 +719,23 @@ __global__ __launch_bounds__(256) void prefill_f32mfma_kernel(PrefillLaunch p, i
         }
       }
     };
-    // X3: the step's tile records (any flag among its tiles; this wave's
-    // tile's shifts), loaded with the step's copies, a step ahead.
-    [[maybe_unused]] int m_bad = 0, m_shk = 0, m_shv = 0;
+    // X3: the step's tile records (any flag among its tiles; the shifts of
+    // this wave's tile's two halves), loaded with the step's copies, a step
+    // ahead.
+    [[maybe_unused]] int m_bad = 0, m_shk0 = 0, m_shk1 = 0, m_shv0 = 0, m_shv1 = 0;
     [[maybe_unused]] auto load_meta = [&](int step) {
       m_bad = 0;
 #pragma unroll
       for (int u = 0; u < KSPLIT; ++u) {
         const int tl = min(step * KSPLIT + u, n_tiles - 1);  // a tile past the workgroup's repeats one
-        m_bad |= meta[4 * tl + 2];
+        const int4 f = *(const int4*)(meta + tl * kSplitRecInts + 4);
+        m_bad |= f.x | f.y | f.z | f.w;
       }
-      const int tl = min(step * KSPLIT + kq, n_tiles - 1);
-      m_shk = meta[4 * tl];
-      m_shv = meta[4 * tl + 1];
+      const int4 sh = *(const int4*)(meta + min(step * KSPLIT + kq, n_tiles - 1) * kSplitRecInts);
+      m_shk0 = sh.x;
+      m_shk1 = sh.y;
+      m_shv0 = sh.z;
+      m_shv1 = sh.w;
     };
     if constexpr (X3) {
       issue_copies(0, 0);
@@ -923,7 +799,7 @@ __global__ __launch_bounds__(256) void prefill_f32mfma_kernel(PrefillLaunch p, i
     for (int step = 0; step < n_steps; ++step) {
       // The previous step's sk / sv reads are done.
       bool x3 = false;
-      [[maybe_unused]] int shk = 0, shv = 0;
+      [[maybe_unused]] int shk0 = 0, shk1 = 0, shv0 = 0, shv1 = 0;
       const int b = X3 ? (step & 1) : 0;  // LDS set of this step
       if constexpr (X3) {
         // This wave's copies of the step's images have landed; after the
@@ -934,8 +810,10 @@ __global__ __launch_bounds__(256) void prefill_f32mfma_kernel(PrefillLaunch p, i
         // Split steps unless a tile of the step or the workgroup's Q holds an
         // inf or NaN (the split kernel's flag per tile, the Q vote).
         x3 = (m_bad | s_qbad[0] | s_qbad[1] | s_qbad[2] | s_qbad[3]) == 0;
-        shk = m_shk;
-        shv = m_shv;
+        shk0 = m_shk0;
+        shk1 = m_shk1;
+        shv0 = m_shv0;
+        shv1 = m_shv1;
         if (step + 1 < n_steps) issue_copies(step + 1, b ^ 1);
         load_meta(min(step + 1, n_steps - 1));  // unconditional: no join that waits for it
         if (!x3) {
@@ -978,7 +856,8 @@ __global__ __launch_bounds__(256) void prefill_f32mfma_kernel(PrefillLaunch p, i
               s2 = mma32(al, qh[ks], s2);
             }
 #pragma unroll
-            for (int i = 0; i < 16; ++i) s[mb][i] = __builtin_amdgcn_ldexpf(s1[i] + s2[i] * 0x1p-11f, -(sq + shk));
+            for (int i = 0; i < 16; ++i)
+              s[mb][i] = __builtin_amdgcn_ldexpf(s1[i] + s2[i] * 0x1p-11f, -(sq + (mb ? shk1 : shk0)));
           }
           // Register i = 4a + e of lane half hh in block mb: key
           // j0 + 32 mb + 16 (a >> 1) + 8 hh + 4 (a & 1) + e.  A tile before
@@ -1017,15 +896,21 @@ __global__ __launch_bounds__(256) void prefill_f32mfma_kernel(PrefillLaunch p, i
           for (int db = 0; db < DB; ++db)
 #pragma unroll
             for (int i = 0; i < 16; ++i) o[db][i] *= alpha;
-          // O^T += V^T P^T, k-step u = keys 16 u + 8 hh + j of this lane's row,
-          // with P * 2^14 (its hi parts normal down to P = 2^-28) and V * 2^shv,
-          // into this tile's own accumulators, unscaled into o.
+          // O^T += V^T P^T, k-step u = keys 16 u + 8 hh + j of this lane's row
+          // (key half u / 2), into this tile's own accumulators, unscaled into
+          // o.  V of half h is scaled by 2^shv_h; P of that half by
+          // 2^(14 + shv_min - shv_h), so that every product carries
+          // 2^(14 + shv_min): P * 2^14 in the half with the larger values (its
+          // hi parts normal down to P = 2^-28), less in the other.
+          const int shv_min = min(shv0, shv1);
           f16x8 ph[4], pl[4];
 #pragma unroll
           for (int u = 0; u < 4; ++u) {
+            const int pe = 14 + shv_min - ((u >> 1) ? shv1 : shv0);
             float x[8];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) x[j] = s[u >> 1][4 * (2 * (u & 1) + (j >> 2)) + (j & 3)] * 16384.f;
+            for (int j = 0; j < 8; ++j)
+              x[j] = __builtin_amdgcn_ldexpf(s[u >> 1][4 * (2 * (u & 1) + (j >> 2)) + (j & 3)], pe);
             split_f16x8(x, ph[u], pl[u]);
           }
 #pragma unroll
@@ -1043,7 +928,7 @@ __global__ __launch_bounds__(256) void prefill_f32mfma_kernel(PrefillLaunch p, i
               t2 = mma32(vl8, ph[u], t2);
             }
 #pragma unroll
-            for (int i = 0; i < 16; ++i) o[db][i] += __builtin_amdgcn_ldexpf(t1[i] + t2[i] * 0x1p-11f, -(shv + 14));
+            for (int i = 0; i < 16; ++i) o[db][i] += __builtin_amdgcn_ldexpf(t1[i] + t2[i] * 0x1p-11f, -(shv_min + 14));
           }
           continue;
         }
@@ -1200,12 +1085,8 @@ hipError_t prefill_f32_launch(const PrefillLaunch& p, hipStream_t stream) {
   if (ksp > 1) nh = 2;
   const int items = grid_of(nh, ksp);
   const dim3 grid(p.fallback_record ? std::min(items, cu_count()) : items);
-  if (!p.fallback_record && p.head_dim == 64) {
-    // split images for the X3 kernel (after the prologue, on the same stream)
-    if (!p.kv_img || !p.kv_meta) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((kv_split_kernel<64>), dim3((p.seq_len + 63) / 64, p.n_head_kv), dim3(256), 0, stream, p.k,
-                       p.v, (char*)p.kv_img, p.kv_meta, p.seq_len);
-  }
+  // the X3 kernel reads the split images the prologue wrote
+  if (!p.fallback_record && p.head_dim == 64 && (!p.kv_img || !p.kv_meta)) return hipErrorInvalidValue;
 #define HL_F32K(DD, KS)                                                                              \
   if (p.fallback_record) hipLaunchKernelGGL((prefill_f32mfma_kernel<DD, KS, true>), grid, dim3(256), 0, stream, p, nh); \
   else hipLaunchKernelGGL((prefill_f32mfma_kernel<DD, KS, false, DD == 64>), grid, dim3(256), 0, stream, p, nh)

@@ -218,6 +218,7 @@ __global__ __launch_bounds__(256) void prologue_kernel(PrologueOp op) {
   __shared__ float scos[kTabHalf][kPT], ssin[kTabHalf][kPT];
   __shared__ float sred[8][kPT];
   __shared__ float sinv[kPT];
+  __shared__ uint32_t smax[4];
   // Work item (tile, head group).
   const PrologueOp& op_k = op;
   auto run_item = [&](const int tile, const int hgrp) {
@@ -371,6 +372,53 @@ __global__ __launch_bounds__(256) void prologue_kernel(PrologueOp op) {
           if (cache)
             store_cache8<KDT>(cache, CacheMap{op.kv_layout, D, op.max_len, op.n_head_kv, op.block_table}, h, r,
                               op.start_pos + t0 + c8, t0 + c8, T, x);
+        }
+      }
+
+      // Split images of the fp32 prefill (head dim 64): this tile is half
+      // t0 / 32 % 2 of the 64-key image t0 / 64.  Scale: the largest
+      // magnitude over the half (tokens past T are zeros); a half holding an
+      // inf or NaN is flagged and not written.
+      if (op.kv_img && kind >= 1 && D == 64) {
+        const int hf = (t0 >> 5) & 1;
+        const long long img_i = (long long)h * ((T + 63) >> 6) + (t0 >> 6);
+        const int tt = tid >> 3, ch = tid & 7;  // K: key tt, dims 8 ch + e
+        const int r = tid >> 2;                 // V: dim r, keys c8 + e
+        float x[8];
+        uint32_t m = 0u;
+  #pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          x[e] = kind == 1 ? sx[8 * ch + e][tt] : sx[r][c8 + e];
+          m = max(m, __float_as_uint(x[e]) & 0x7FFFFFFFu);
+        }
+  #pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) m = max(m, (uint32_t)__shfl_xor((int)m, o, 64));
+        if ((tid & 63) == 0) smax[tid >> 6] = m;
+        __syncthreads();
+        m = max(max(smax[0], smax[1]), max(smax[2], smax[3]));
+        const bool bad = m >= kInfBits;
+        const int sh = split_shift(m);
+        if (tid == 0) {
+          int* rec = op.kv_meta + img_i * kSplitRecInts;
+          rec[(kind == 1 ? 0 : 2) + hf] = sh;
+          rec[(kind == 1 ? 4 : 6) + hf] = bad ? 1 : 0;
+        }
+        if (!bad) {
+  #pragma unroll
+          for (int e = 0; e < 8; ++e) x[e] = __builtin_amdgcn_ldexpf(x[e], sh);
+          f16x8 h8, l8;
+          split_f16x8(x, h8, l8);
+          uint16_t* base = (uint16_t*)(op.kv_img + img_i * kSplitImgBytes);
+          int pos;
+          if (kind == 1) {
+            const int key = 32 * hf + tt;
+            pos = key * 64 + 8 * (ch ^ (key & 7));
+          } else {
+            const int kc = 4 * hf + (c8 >> 3);
+            pos = 2 * 64 * 64 + r * 64 + 8 * (kc ^ ((r >> 1) & 7));
+          }
+          *(f16x8*)(base + pos) = h8;
+          *(f16x8*)(base + pos + 64 * 64) = l8;
         }
       }
 
