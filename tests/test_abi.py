@@ -132,16 +132,17 @@ def test_prefill_workspace_size(hl):
     f = _prefill_args(io_dtype=_lib.HL_F32)
     assert hl.hl_attn_prefill_workspace_bytes(ctypes.byref(f)) == 0  # no fused ops: none needed
     # fp32 at head dim 64: the K/V split images, 64 keys x 64 dims x (K, V)
-    # x (hi, lo) fp16 per tile, then 16 bytes of shifts and flag per tile
-    # (1000 tokens: 16 tiles per kv head), after the roped Q and K (256-aligned)
+    # x (hi, lo) fp16 per tile, then a record of 8 ints (shifts and flags of
+    # its two halves) per tile (1000 tokens: 16 tiles per kv head), after the
+    # roped Q and K (256-aligned)
     s = _prefill_args(io_dtype=_lib.HL_F32, head_dim=64, seq_len=1000, n_head_kv=4)
-    assert hl.hl_attn_prefill_workspace_bytes(ctypes.byref(s)) == 4 * 16 * (32768 + 16)
+    assert hl.hl_attn_prefill_workspace_bytes(ctypes.byref(s)) == 4 * 16 * (32768 + 32)
     sr = _prefill_args(io_dtype=_lib.HL_F32, head_dim=64, seq_len=1000, n_head_kv=4, apply_rope=1, rope_base=1e4)
     qk = (32 + 4) * 64 * 1000 * 4
-    assert hl.hl_attn_prefill_workspace_bytes(ctypes.byref(sr)) == (qk + 255) // 256 * 256 + 4 * 16 * (32768 + 16)
+    assert hl.hl_attn_prefill_workspace_bytes(ctypes.byref(sr)) == (qk + 255) // 256 * 256 + 4 * 16 * (32768 + 32)
     # and hl_attn_prefill asks for it
     assert hl.hl_attn_prefill(ctypes.byref(s), None, 0, None) == _lib.HL_EINVAL
-    assert "workspace of 2098176 bytes needed" in _err(hl)
+    assert "workspace of 2099200 bytes needed" in _err(hl)
 
 
 def test_rope_store_cache_full(hl):
