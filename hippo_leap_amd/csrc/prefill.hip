@@ -665,10 +665,13 @@ __global__ __launch_bounds__(256) void prefill_f32mfma_kernel(PrefillLaunch p, i
     // d = ld0 + 4k; the next step's tiles are loaded while the current ones
     // are computed.  X3: only a step that runs the fp32 MFMAs loads them, at
     // the step; the split tiles come from the split kernel's images instead
-    // (written by the prologue), copied straight into LDS one step ahead.
-    const int lc = tid & 63, ld0 = tid >> 6;
+    // (written by the prologue), copied straight into LDS one step ahead;
+    // its fp32 steps pass the thread id through an empty asm, so that their
+    // per-lane addresses are computed at the step instead of being hoisted
+    // and kept live across the loop (which costs the split steps registers).
     float kr[KSPLIT][NL], vr[KSPLIT][NL];
-    auto load_kv = [&](int step) {
+    auto load_kv = [&](int step, int tid_) {
+      const int lc = tid_ & 63, ld0 = tid_ >> 6;
 #pragma unroll
       for (int u = 0; u < KSPLIT; ++u) {
         const int col = min((step * KSPLIT + u) * BN + lc, T - 1);
@@ -681,7 +684,8 @@ __global__ __launch_bounds__(256) void prefill_f32mfma_kernel(PrefillLaunch p, i
     };
     // Writes the loaded tiles to LDS set b in the fp32 layout (keys past T
     // as zeros).
-    auto stage_f32 = [&](int step, int b) {
+    auto stage_f32 = [&](int step, int b, int tid_) {
+      const int lc = tid_ & 63, ld0 = tid_ >> 6;
 #pragma unroll
       for (int u = 0; u < KSPLIT; ++u) {
         const bool in = (step * KSPLIT + u) * BN + lc < T;
@@ -741,20 +745,20 @@ __global__ __launch_bounds__(256) void prefill_f32mfma_kernel(PrefillLaunch p, i
       issue_copies(0, 0);
       load_meta(0);
     } else {
-      load_kv(0);
+      load_kv(0, tid);
     }
 
     // q operand: lane (ln, hh) holds q[t][2ks + hh] * scale * log2 e
     // (X3: loaded again in each fp32 step instead, so that the 2 x 32 or
     // 2 x 64 q registers of the two forms are not both live in the loop.)
     float qv[KS];
-    auto load_qv = [&]() {
+    auto load_qv = [&](int lane_) {
       const float* Q = p.q + (long long)hq * D * T;
-      const int t = min(t_abs, T - 1);
+      const int t = min(r0 + (lane_ & 31), T - 1), h_ = lane_ >> 5;
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) qv[ks] = Q[(long long)(2 * ks + hh) * T + t] * p.scale_log2;
+      for (int ks = 0; ks < KS; ++ks) qv[ks] = Q[(long long)(2 * ks + h_) * T + t] * p.scale_log2;
     };
-    if constexpr (!X3) load_qv();
+    if constexpr (!X3) load_qv(lane);
     // X3: lane (ln, hh) also holds q[t][16 ks + 8 hh + j] * scale * log2 e *
     // 2^sq as the fp16 hi/lo B operand of the S^T = K Q^T MFMAs, sq scaling
     // the row's largest element (over both lane halves) into [2^13, 2^14);
@@ -818,14 +822,16 @@ __global__ __launch_bounds__(256) void prefill_f32mfma_kernel(PrefillLaunch p, i
         load_meta(min(step + 1, n_steps - 1));  // unconditional: no join that waits for it
         if (!x3) {
           // fp32 MFMA step: the fp32 tiles replace this set's images
-          load_kv(step);
-          stage_f32(step, b);
+          int tid_ = tid;
+          asm volatile("" : "+v"(tid_));
+          load_kv(step, tid_);
+          stage_f32(step, b, tid_);
           __syncthreads();
         }
       } else {
         __syncthreads();
-        stage_f32(step, 0);
-        if (step + 1 < n_steps) load_kv(step + 1);
+        stage_f32(step, 0, tid);
+        if (step + 1 < n_steps) load_kv(step + 1, tid);
         __syncthreads();
       }
       const int j0 = (step * KSPLIT + kq) * BN;
@@ -934,7 +940,11 @@ __global__ __launch_bounds__(256) void prefill_f32mfma_kernel(PrefillLaunch p, i
         }
       }
 
-      if constexpr (X3) load_qv();
+      if constexpr (X3) {
+        int lane_ = lane;
+        asm volatile("" : "+v"(lane_));
+        load_qv(lane_);
+      }
       f32x16 s[2];
 #pragma unroll
       for (int mb = 0; mb < 2; ++mb) {
