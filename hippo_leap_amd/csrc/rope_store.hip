@@ -238,27 +238,23 @@ __global__ __launch_bounds__(256) void prologue_kernel(PrologueOp op) {
     const int T = op.seq_len, D = op.head_dim;
     const int t0 = tile * kPT;
     const int n_vec = op.n_head + 2 * op.n_head_kv;
-    const int hv0 = op.hv_first + hgrp * op.hpg;
+    // Work order idx -> head vector: with every head vector to do, the K and
+    // V heads come first (the lowest workgroup ids, dispatched first: theirs
+    // is the longer chain), then Q.
+    const int nkv2 = 2 * op.n_head_kv;
+    auto hv_of = [&](int idx) {
+      if (op.hv_first != 0) return idx;
+      return idx < nkv2 ? op.n_head + idx : idx - nkv2;
+    };
+    const int hv0 = op.hv_first + hgrp * op.hpg;  // work-order indices hv0 .. hv1 - 1
     const int hv1 = min(n_vec, hv0 + op.hpg);
     const int tc = tid & (kPT - 1), part = tid / kPT;  // 8 parts of 32 lanes
     const int t = t0 + tc;
     const int half = op.rope_dim / 2;
-    const bool tab = op.do_rope && half <= kTabHalf && hv0 < op.n_head + op.n_head_kv;
-
-    if (tab) {
-      // The first head group's workgroup of each tile also publishes its slice
-      // as tab_out[i][t] for the flash kernel's Q.
-      const bool publish = op.rope_tab_out && hgrp == 0;
-      const float pos = (float)(op.start_pos + t);
-      for (int i = part; i < half; i += 8) {
-        const float angle = pos * op.theta.t[i];
-        float c, sn;
-        rope_cs(angle, c, sn);
-        scos[i][tc] = c;
-        ssin[i][tc] = sn;
-        if (publish && t < T) op.rope_tab_out[(long long)i * T + t] = make_float2(c, sn);
-      }
-    }
+    // the (cos, sin) table when a Q or K head of the group is rotated
+    const bool has_qk = op.hv_first != 0 ? hv0 < op.n_head + op.n_head_kv
+                                         : (hv0 < op.n_head_kv || hv1 > nkv2);
+    const bool tab = op.do_rope && half <= kTabHalf && has_qk;
 
     // Head vector hv -> (kind, head index, source); kind 0 q, 1 k, 2 v.
     auto decode_hv = [&](int hv, int& kind, int& h) {
@@ -291,14 +287,30 @@ __global__ __launch_bounds__(256) void prologue_kernel(PrologueOp op) {
       }
     };
     float xa[kPass][8], xb[kPass][8];
-    if (hv0 < hv1) load_regs(hv0, xa);
+    if (hv0 < hv1) load_regs(hv_of(hv0), xa);  // in flight while the table is computed
 
-    for (int hv = hv0; hv < hv1; ++hv) {
+    if (tab) {
+      // The first head group's workgroup of each tile also publishes its slice
+      // as tab_out[i][t] for the flash kernel's Q.
+      const bool publish = op.rope_tab_out && hgrp == 0;
+      const float pos = (float)(op.start_pos + t);
+      for (int i = part; i < half; i += 8) {
+        const float angle = pos * op.theta.t[i];
+        float c, sn;
+        rope_cs(angle, c, sn);
+        scos[i][tc] = c;
+        ssin[i][tc] = sn;
+        if (publish && t < T) op.rope_tab_out[(long long)i * T + t] = make_float2(c, sn);
+      }
+    }
+
+
+    for (int idx = hv0; idx < hv1; ++idx) {
       int kind, h;
-      decode_hv(hv, kind, h);
+      decode_hv(hv_of(idx), kind, h);
       const void* src = src_of(kind);
       // prefetch the next head's tile while this one is processed
-      if (hv + 1 < hv1) load_regs(hv + 1, xb);
+      if (idx + 1 < hv1) load_regs(hv_of(idx + 1), xb);
       if (!src) {  // uniform across the workgroup
   #pragma unroll
         for (int ps = 0; ps < kPass; ++ps)
