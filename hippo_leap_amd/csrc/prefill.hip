@@ -818,8 +818,12 @@ __global__ __launch_bounds__(256) void prefill_f32mfma_kernel(PrefillLaunch p, i
         shk1 = m_shk1;
         shv0 = m_shv0;
         shv1 = m_shv1;
-        if (step + 1 < n_steps) issue_copies(step + 1, b ^ 1);
-        load_meta(min(step + 1, n_steps - 1));  // unconditional: no join that waits for it
+        // A wave that runs this step's split products issues the next step's
+        // copies behind its first matrix instructions (below); the others now.
+        if (!(x3 && live && (step * KSPLIT + kq) * BN <= r0 + 31)) {
+          if (step + 1 < n_steps) issue_copies(step + 1, b ^ 1);
+          load_meta(min(step + 1, n_steps - 1));  // unconditional: no join that waits for it
+        }
         if (!x3) {
           // fp32 MFMA step: the fp32 tiles replace this set's images
           int tid_ = tid;
@@ -864,6 +868,10 @@ __global__ __launch_bounds__(256) void prefill_f32mfma_kernel(PrefillLaunch p, i
 #pragma unroll
             for (int i = 0; i < 16; ++i)
               s[mb][i] = __builtin_amdgcn_ldexpf(s1[i] + s2[i] * 0x1p-11f, -(sq + (mb ? shk1 : shk0)));
+            if (mb == 0) {
+              if (step + 1 < n_steps) issue_copies(step + 1, b ^ 1);
+              load_meta(min(step + 1, n_steps - 1));
+            }
           }
           // Register i = 4a + e of lane half hh in block mb: key
           // j0 + 32 mb + 16 (a >> 1) + 8 hh + 4 (a & 1) + e.  A tile before
