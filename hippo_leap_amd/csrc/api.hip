@@ -710,7 +710,7 @@ struct PrefillPlan {
   bool q_in_kernel;  // MFMA kernel builds Q from the raw activations (no qt)
   int t_pad;
   size_t off_q, off_k, off_v, off_tab, off_q32, off_k32, off_v32, off_range, bytes;
-  size_t off_split, split_bytes;  // fp32, head dim 64: the K/V split images and their tile records
+  size_t off_split, split_bytes;  // fp32: the K/V split images and their tile records
 };
 
 static int validate_prefill(const hl_prefill_args* a, PrefillPlan* pl) {
@@ -951,12 +951,12 @@ int hl_attn_prefill(const hl_prefill_args* a, void* workspace, size_t ws_bytes, 
   }
   if (!a->k_cache) op.v = nullptr;
   if (pl.split_bytes) {
-    // Head dim 64: the prologue also writes the K/V split images the flash
+    // The prologue also writes the K/V split images the flash
     // kernel reads (so it always runs, over whole 64-token tiles).
     op.k = a->k;
     op.v = a->v;
     op.kv_img = ws + pl.off_split;
-    op.kv_meta = (int*)(ws + pl.off_split + (size_t)a->n_head_kv * ((a->seq_len + 63) / 64) * kSplitImgBytes);
+    op.kv_meta = (int*)(ws + pl.off_split + (size_t)a->n_head_kv * ((a->seq_len + 63) / 64) * split_img_bytes(a->head_dim));
     op.t_pad = (a->seq_len + 63) / 64 * 64;
     if (!op.q) op.hv_first = a->n_head;
     pf.kv_img = op.kv_img;

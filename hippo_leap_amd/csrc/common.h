@@ -177,7 +177,7 @@ struct ThetaTable {
 };
 
 // Split of fp32 operands into fp16 hi + lo * 2^-11 for three-MFMA
-// products (the fp32 prefill at head dim 64).
+// products (the fp32 prefill).
 // x ~= hi + lo * 2^-11 with hi, lo fp16: |x - hi - lo 2^-11| <= |x| 2^-22
 // for |x| < 32768 with hi normal (2^-36 absolute below fp16's normal range).
 // hi * hi' + (hi * lo' + lo * hi') 2^-11 is then the product to ~2^-21.
@@ -199,13 +199,13 @@ __device__ __forceinline__ int split_shift(uint32_t max_bits) {
   return 13 - e;
 }
 constexpr uint32_t kInfBits = 0x7F800000u;  // |x| bit patterns at or above: inf or NaN
-// Split images of the fp32 prefill at head dim 64, one per (kv head, 64-key
-// tile): K hi, K lo ([key][64] fp16, 16-byte chunk c of key j at
-// c ^ (j % 8)), V hi, V lo ([d][64 keys] fp16, chunk c of dim d at
+// Split images of the fp32 prefill (head dim D = 64 or 128), one per (kv
+// head, 64-key tile): K hi, K lo ([key][D] fp16, 16-byte chunk c of key j at
+// c ^ (j % (D / 8))), V hi, V lo ([d][64 keys] fp16, chunk c of dim d at
 // c ^ ((d / 2) % 8)).  Each 32-key half of a tile has its own power-of-two
 // scale per tensor; the tile's record holds 8 ints: the K shifts of halves
 // 0 and 1, the V shifts, then inf/NaN flags of K halves 0, 1 and V halves.
-constexpr int kSplitImgBytes = 64 * 64 * 8;
+constexpr int split_img_bytes(int D) { return 64 * D * 8; }
 constexpr int kSplitRecInts = 8;
 
 }  // namespace hl

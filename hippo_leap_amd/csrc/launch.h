@@ -104,7 +104,7 @@ struct PrologueOp {
   // Fallback pass: non-null -> every workgroup returns at once unless
   // gate[0] (the overflow flag) is set.
   unsigned* gate;
-  // fp32 prefill at head dim 64: the K and V split images and tile records
+  // fp32 prefill: the K and V split images and tile records
   // of the flash kernel (PrefillLaunch::kv_img / kv_meta), or null.
   // t_pad must then be seq_len rounded up to 64.
   char* kv_img;
@@ -150,7 +150,7 @@ struct PrefillLaunch {
   // Workgroups return at once unless the call's overflow mark is set;
   // workgroup 0 advances the record's generation (common.h).
   unsigned* fallback_record;
-  // fp32 path at head dim 64 (not the fallback pass): the K/V split images
+  // fp32 path (not the fallback pass): the K/V split images
   // the prologue writes (PrologueOp::kv_img) and the flash kernel reads,
   // prefill_f32_split_bytes in all: [Hkv][ceil(T/64)] images of 32 KB, then
   // a record of 8 ints per image (kSplitRec*).

@@ -16,9 +16,10 @@
 //    within 2e-3 of the fp32 reference; P is rounded to fp16, accumulation
 //    is fp32.
 //  * prefill_f32mfma_kernel: fp32 MFMA (v_mfma_f32_32x32x2_f32) on the
-//    reference's col-major fp32 tensors (the 1e-4 path); at head dim 64,
-//    fp16 MFMAs on hi/lo splits of the operands, with K and V split once
-//    per call by the prologue (prologue_kernel).
+//    reference's col-major fp32 tensors (the 1e-4 path) in the fallback
+//    pass of an MFMA prefill; otherwise fp16 MFMAs on hi/lo splits of the
+//    operands, with K and V split once per call by the prologue
+//    (prologue_kernel).
 #include "common.h"
 #include "launch.h"
 
@@ -563,8 +564,8 @@ __device__ __forceinline__ f32x16 mma32f(float a, float b, f32x16 c) {
 }  // namespace
 
 size_t prefill_f32_split_bytes(int n_head_kv, int head_dim, int seq_len) {
-  if (head_dim != 64) return 0;
-  return (size_t)n_head_kv * ((seq_len + 63) / 64) * (kSplitImgBytes + 4 * kSplitRecInts);
+  if (head_dim != 64 && head_dim != 128) return 0;
+  return (size_t)n_head_kv * ((seq_len + 63) / 64) * (split_img_bytes(head_dim) + 4 * kSplitRecInts);
 }
 
 // FB: the gated fallback pass of an MFMA prefill (a grid of at most one
@@ -705,15 +706,15 @@ __global__ __launch_bounds__(256) void prefill_f32mfma_kernel(PrefillLaunch p, i
     // X3: a tile's image into LDS set b, 1 KB per wave copy:
     // the K image into the set's K tile, the V image into its V tile.
     const int n_kt = (T + BN - 1) / BN;
-    [[maybe_unused]] const char* img = (const char*)p.kv_img + (long long)kvh * n_kt * kSplitImgBytes;
+    [[maybe_unused]] const char* img = (const char*)p.kv_img + (long long)kvh * n_kt * split_img_bytes(D);
     [[maybe_unused]] const int* meta = p.kv_meta + (long long)kvh * n_kt * kSplitRecInts;
     [[maybe_unused]] auto issue_copies = [&](int step, int b) {
 #pragma unroll
       for (int u = 0; u < KSPLIT; ++u) {
         const int tl = step * KSPLIT + u;
         if (tl >= n_tiles) continue;
-        const char* src = img + (long long)tl * kSplitImgBytes + lane * 16;
-        constexpr int NCH = kSplitImgBytes / 1024, HALF = NCH / 2;
+        const char* src = img + (long long)tl * split_img_bytes(D) + lane * 16;
+        constexpr int NCH = split_img_bytes(D) / 1024, HALF = NCH / 2;
 #pragma unroll
         for (int i = 0; i < NCH / NW; ++i) {
           const int ch = wave + NW * i;
@@ -1103,14 +1104,13 @@ hipError_t prefill_f32_launch(const PrefillLaunch& p, hipStream_t stream) {
   if (ksp > 1) nh = 2;
   const int items = grid_of(nh, ksp);
   const dim3 grid(p.fallback_record ? std::min(items, cu_count()) : items);
-  // the X3 kernel reads the split images the prologue wrote
-  if (!p.fallback_record && p.head_dim == 64 && (!p.kv_img || !p.kv_meta)) return hipErrorInvalidValue;
+  // the X3 kernels read the split images the prologue wrote
+  if (!p.fallback_record && (!p.kv_img || !p.kv_meta)) return hipErrorInvalidValue;
 #define HL_F32K(DD, KS)                                                                              \
   if (p.fallback_record) hipLaunchKernelGGL((prefill_f32mfma_kernel<DD, KS, true>), grid, dim3(256), 0, stream, p, nh); \
-  else hipLaunchKernelGGL((prefill_f32mfma_kernel<DD, KS, false, DD == 64>), grid, dim3(256), 0, stream, p, nh)
-  // The split-operand steps (X3) at head dim 64; at 128 the fp32 steps'
-  // fallback and the split steps do not fit one kernel's registers together,
-  // so that kernel keeps the fp32 MFMAs throughout.
+  else hipLaunchKernelGGL((prefill_f32mfma_kernel<DD, KS, false, true>), grid, dim3(256), 0, stream, p, nh)
+  // The split-operand steps (X3) except in the fallback pass of an MFMA
+  // prefill, which keeps the fp32 MFMAs.
   switch (p.head_dim) {
     case 64:
       if (ksp == 2) HL_F32K(64, 2);

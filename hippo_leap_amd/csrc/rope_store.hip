@@ -387,22 +387,22 @@ __global__ __launch_bounds__(256) void prologue_kernel(PrologueOp op) {
         }
       }
 
-      // Split images of the fp32 prefill (head dim 64): this tile is half
+      // Split images of the fp32 prefill (head dim 64 or 128): this tile is half
       // t0 / 32 % 2 of the 64-key image t0 / 64.  Scale: the largest
       // magnitude over the half (tokens past T are zeros); a half holding an
       // inf or NaN is flagged and not written.
-      if (op.kv_img && kind >= 1 && D == 64) {
+      if (op.kv_img && kind >= 1 && (D == 64 || D == 128)) {
         const int hf = (t0 >> 5) & 1;
         const long long img_i = (long long)h * ((T + 63) >> 6) + (t0 >> 6);
-        const int tt = tid >> 3, ch = tid & 7;  // K: key tt, dims 8 ch + e
-        const int r = tid >> 2;                 // V: dim r, keys c8 + e
-        float x[8];
+        const int nper = D / 64;  // 16-byte pieces per thread: K (key, chunk), V (dim, 8 keys)
+        // piece i: K key tid / 8, dims 8 ((tid % 8) + 8 i) + e; V dim tid / 4 + 64 i, keys c8 + e
+        auto piece = [&](int i, int e) {
+          return kind == 1 ? sx[8 * ((tid & 7) + 8 * i) + e][tid >> 3] : sx[(tid >> 2) + 64 * i][c8 + e];
+        };
         uint32_t m = 0u;
+        for (int i = 0; i < nper; ++i)
   #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          x[e] = kind == 1 ? sx[8 * ch + e][tt] : sx[r][c8 + e];
-          m = max(m, __float_as_uint(x[e]) & 0x7FFFFFFFu);
-        }
+          for (int e = 0; e < 8; ++e) m = max(m, __float_as_uint(piece(i, e)) & 0x7FFFFFFFu);
   #pragma unroll
         for (int o = 32; o >= 1; o >>= 1) m = max(m, (uint32_t)__shfl_xor((int)m, o, 64));
         if ((tid & 63) == 0) smax[tid >> 6] = m;
@@ -416,21 +416,24 @@ __global__ __launch_bounds__(256) void prologue_kernel(PrologueOp op) {
           rec[(kind == 1 ? 4 : 6) + hf] = bad ? 1 : 0;
         }
         if (!bad) {
+          uint16_t* base = (uint16_t*)(op.kv_img + img_i * split_img_bytes(D));
+          for (int i = 0; i < nper; ++i) {
+            float x[8];
   #pragma unroll
-          for (int e = 0; e < 8; ++e) x[e] = __builtin_amdgcn_ldexpf(x[e], sh);
-          f16x8 h8, l8;
-          split_f16x8(x, h8, l8);
-          uint16_t* base = (uint16_t*)(op.kv_img + img_i * kSplitImgBytes);
-          int pos;
-          if (kind == 1) {
-            const int key = 32 * hf + tt;
-            pos = key * 64 + 8 * (ch ^ (key & 7));
-          } else {
-            const int kc = 4 * hf + (c8 >> 3);
-            pos = 2 * 64 * 64 + r * 64 + 8 * (kc ^ ((r >> 1) & 7));
+            for (int e = 0; e < 8; ++e) x[e] = __builtin_amdgcn_ldexpf(piece(i, e), sh);
+            f16x8 h8, l8;
+            split_f16x8(x, h8, l8);
+            int pos;
+            if (kind == 1) {
+              const int key = 32 * hf + (tid >> 3), ch = (tid & 7) + 8 * i;
+              pos = key * D + 8 * (ch ^ (key % (D / 8)));
+            } else {
+              const int r = (tid >> 2) + 64 * i, kc = 4 * hf + (c8 >> 3);
+              pos = 2 * 64 * D + r * 64 + 8 * (kc ^ ((r >> 1) & 7));
+            }
+            *(f16x8*)(base + pos) = h8;
+            *(f16x8*)(base + pos + 64 * D) = l8;
           }
-          *(f16x8*)(base + pos) = h8;
-          *(f16x8*)(base + pos + 64 * 64) = l8;
         }
       }
 

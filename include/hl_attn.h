@@ -208,7 +208,7 @@ int hl_gpu_attention_decode_noalloc(float* dst, const float* q, const float* k_c
 /* gpuAttentionPrefill (naive.nim:3450-3464): causal attention over the
  * col-major fp32 projections q[nHead*headDim, seqLen], k/v[nHeadKv*headDim,
  * seqLen]; dst is col-major [nHead*headDim, seqLen].  No 4096-token cap.
- * At head dim 64 it uses a library-owned workspace per device (the K/V
+ * It uses a library-owned workspace per device (the K/V
  * split images, hipMalloc'd when a call needs more than the last one and
  * kept; growing it waits for the device and is refused under capture).  */
 int hl_gpu_attention_prefill(float* dst, const float* q, const float* k,
@@ -451,7 +451,7 @@ typedef struct hl_prefill_args {
 
 /* Workspace hl_attn_prefill needs for these args (0: none).  It holds the
  * MFMA path's fp16 operands and fallback buffers, or, for fp32 activations,
- * the roped Q and K when RoPE / qkNorm run, and at head dim 64 the K/V
+ * the roped Q and K when RoPE / qkNorm run, and the K/V
  * split images (8 bytes per K and V element, padded to 64-token tiles).   */
 size_t hl_attn_prefill_workspace_bytes(const hl_prefill_args* a);
 

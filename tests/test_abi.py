@@ -129,12 +129,12 @@ def test_prefill_workspace_size(hl):
     h = _prefill_args(apply_rope=1, rope_base=5e5, rope_dim=64)
     assert hl.hl_attn_prefill_workspace_bytes(ctypes.byref(h)) == \
         (32 + 8 + 8) * 4096 * 128 * 2 + 4096 * 32 * 8 + fb + 16
-    f = _prefill_args(io_dtype=_lib.HL_F32)
-    assert hl.hl_attn_prefill_workspace_bytes(ctypes.byref(f)) == 0  # no fused ops: none needed
-    # fp32 at head dim 64: the K/V split images, 64 keys x 64 dims x (K, V)
+    # fp32: no fused ops, only the K/V split images, 64 keys x D dims x (K, V)
     # x (hi, lo) fp16 per tile, then a record of 8 ints (shifts and flags of
-    # its two halves) per tile (1000 tokens: 16 tiles per kv head), after the
-    # roped Q and K (256-aligned)
+    # its two halves) per tile (4096 tokens: 64 tiles per kv head)
+    f = _prefill_args(io_dtype=_lib.HL_F32)
+    assert hl.hl_attn_prefill_workspace_bytes(ctypes.byref(f)) == 8 * 64 * (64 * 128 * 8 + 32)
+    # head dim 64, 1000 tokens (16 tiles), after the roped Q and K (256-aligned)
     s = _prefill_args(io_dtype=_lib.HL_F32, head_dim=64, seq_len=1000, n_head_kv=4)
     assert hl.hl_attn_prefill_workspace_bytes(ctypes.byref(s)) == 4 * 16 * (32768 + 32)
     sr = _prefill_args(io_dtype=_lib.HL_F32, head_dim=64, seq_len=1000, n_head_kv=4, apply_rope=1, rope_base=1e4)

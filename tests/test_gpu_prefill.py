@@ -92,12 +92,13 @@ def test_prefill_c2_full(hl, orc):
     assert np.all(kcn[:, T:] == 7.0) and np.all(vcn[:, T:] == 7.0)  # canary untouched
 
 
+@pytest.mark.parametrize("d", [64, 128])
 @pytest.mark.parametrize("T", [1, 2, 31, 33, 63, 65, 127, 130, 257])
-def test_prefill_fp32_split_path_lengths(hl, orc, T):
-    """Head dim 64: the fp32 kernel's steps run on fp16 hi/lo splits of the
-    operands; partial tiles and lengths that are not a multiple of 4 (V read
-    element-wise) against the fp32 oracle."""
-    hq, hkv, d = 8, 2, 64
+def test_prefill_fp32_split_path_lengths(hl, orc, T, d):
+    """The fp32 kernel's steps run on fp16 hi/lo splits of the operands (K
+    and V split by the prologue per 32-key half tile); partial tiles and
+    lengths that are not a multiple of 4 against the fp32 oracle."""
+    hq, hkv = 8, 2
     q = orc.normal(hq * d * T, 40 + T).reshape(hq * d, T)
     k = orc.normal(hkv * d * T, 41 + T).reshape(hkv * d, T)
     v = orc.normal(hkv * d * T, 42 + T).reshape(hkv * d, T)
@@ -105,17 +106,18 @@ def test_prefill_fp32_split_path_lengths(hl, orc, T):
     out = run_prefill(to_dev(q, 0), to_dev(k, 0), to_dev(v, 0), hq, hkv, d, T, apply_rope=True,
                       rope_base=1e4)
     err = rel_err(from_dev(out), ref)
-    print(f"split path T={T} rel err {err:.3e}")
+    print(f"split path D={d} T={T} rel err {err:.3e}")
     assert err < TOL_F32 / 10
 
 
+@pytest.mark.parametrize("d", [64, 128])
 @pytest.mark.parametrize("where", ["k_tile", "v_tile", "q_row", "tiny"])
-def test_prefill_fp32_split_path_outliers(hl, orc, where):
-    """Head dim 64, T=300: values of 2^15 and beyond in one K tile, one V tile
-    or one query row, and tiny ones, through the scaled fp16 split (each set
-    is scaled so that its largest element sits below 2^14).  Against the
-    fp32 oracle."""
-    hq, hkv, d, T = 8, 2, 64, 300
+def test_prefill_fp32_split_path_outliers(hl, orc, where, d):
+    """T=300: values of 2^15 and beyond in one K tile, one V tile or one
+    query row, and tiny ones, through the scaled fp16 split (each set is
+    scaled so that its largest element sits below 2^14).  Against the fp32
+    oracle."""
+    hq, hkv, T = 8, 2, 300
     q = orc.normal(hq * d * T, 51).reshape(hq * d, T)
     k = orc.normal(hkv * d * T, 52).reshape(hkv * d, T)
     v = orc.normal(hkv * d * T, 53).reshape(hkv * d, T)
@@ -136,17 +138,18 @@ def test_prefill_fp32_split_path_outliers(hl, orc, where):
     ref, _, _ = oracle_prefill(orc, q, k, v, hq, hkv, d, T)
     out = run_prefill(to_dev(q, 0), to_dev(k, 0), to_dev(v, 0), hq, hkv, d, T)
     err = rel_err(from_dev(out), ref)
-    print(f"outliers {where} rel err {err:.3e}")
+    print(f"outliers {where} D={d} rel err {err:.3e}")
     assert np.isfinite(from_dev(out)).all() and err < TOL_F32
 
 
-def test_prefill_fp32_split_path_nan_key(hl, orc):
+@pytest.mark.parametrize("d", [64, 128])
+def test_prefill_fp32_split_path_nan_key(hl, orc, d):
     """A NaN in one V entry at the first key of a 64-key tile: the steps that
     load the tile run fp32 MFMAs, and exactly the rows that see that key come
     out NaN, as in the oracle; the other rows match it.  (Within a tile the
     P V product is a matrix product, so a NaN at a later key of the tile
     also reaches the earlier rows that process the tile: 0 x NaN.)"""
-    hq, hkv, d, T = 8, 2, 64, 200
+    hq, hkv, T = 8, 2, 200
     q = orc.normal(hq * d * T, 61).reshape(hq * d, T)
     k = orc.normal(hkv * d * T, 62).reshape(hkv * d, T)
     v = orc.normal(hkv * d * T, 63).reshape(hkv * d, T)
