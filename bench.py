@@ -28,6 +28,8 @@ Extra objects on the same JSON line:
     call contract (hl_gpu_attention_decode; fp32 prefill with RoPE 1e4 and
     the cache write), timed for reference: they are parity cases, not the
     metric.
+  prefill_fp32_llama8b: the same fp32 prefill contract at the Llama-3-8B
+    attention shape (head dim 128, T=4096).
   roofline: the fused step kernel (qkNorm/RoPE + KV write + split-K
     attention + merge) timed with HIP events on the stream it runs on.
   linear: hl_gpu_linear_col (the gpuLinearCol drop-in, fp32) at the
@@ -720,13 +722,37 @@ def main():
         f2 = 4 * 32 * 64 * T2 * (T2 + 1) // 2
         result["prefill_c2"] = {
             "workload": "c2: TinyLlama-shape causal prefill, fp32, T=512, Hq32/Hkv4, D64, RoPE 1e4, "
-                        "KV cache written (prologue + fp32-MFMA flash kernel)",
+                        "KV cache written (prologue + split-operand flash kernel)",
             "us": round(ms2 * 1e3, 3), "unit": "TFLOP/s",
             "value": round(f2 / (ms2 * 1e-3) / 1e12, 3),
             "frac_fp32_peak": round(f2 / (ms2 * 1e-3) / 1e12 / FP32_PEAK_TFLOPS, 4)}
         log(f"decode c1: {ms1*1e3:.2f} us; prefill c2: {ms2*1e3:.1f} us "
             f"({f2 / (ms2 * 1e-3) / 1e12:.2f} TFLOP/s)")
         del sets
+        # The same fp32 contract at the Llama-3-8B attention shape (head dim
+        # 128, T=4096): what gpuAttentionPrefill of the reference's fp32
+        # backend runs for that model.
+        T8, hq8, hkv8, d8 = 4096, 32, 8, 128
+        q8 = torch.randn(hq8 * d8, T8, generator=g, device="cuda")
+        k8 = torch.randn(hkv8 * d8, T8, generator=g, device="cuda")
+        v8 = torch.randn(hkv8 * d8, T8, generator=g, device="cuda")
+        kc8 = torch.empty(hkv8 * d8, T8, device="cuda")
+        vc8 = torch.empty(hkv8 * d8, T8, device="cuda")
+        o8 = torch.empty(hq8 * d8, T8, device="cuda")
+        a8 = A.prefill_args(q8, k8, v8, o8, hq8, hkv8, d8, T8, rope_base=5e5, apply_rope=True,
+                            k_cache=kc8, v_cache=vc8, max_len=T8)
+        ws8 = A.workspace(A.prefill_workspace_bytes(a8))
+        ms8 = graph_time_ms(torch, lambda i: A.attn_prefill(a8, ws8), 8, 4)
+        f8 = 4 * hq8 * d8 * T8 * (T8 + 1) // 2
+        result["prefill_fp32_llama8b"] = {
+            "workload": "Llama-3-8B-shape causal prefill, fp32, T=4096, Hq32/Hkv8, D128, RoPE 5e5, "
+                        "fp32 KV cache written (prologue + split-operand flash kernel)",
+            "us": round(ms8 * 1e3, 1), "unit": "TFLOP/s",
+            "value": round(f8 / (ms8 * 1e-3) / 1e12, 2),
+            "frac_fp32_peak": round(f8 / (ms8 * 1e-3) / 1e12 / FP32_PEAK_TFLOPS, 4),
+            "note": "the products run as three fp16 MFMAs on hi/lo splits, hence above the fp32 peak"}
+        log(f"prefill fp32 Llama-3-8B shape: {ms8*1e3:.1f} us ({f8 / (ms8 * 1e-3) / 1e12:.1f} TFLOP/s)")
+        del q8, k8, v8, kc8, vc8, o8, ws8
         torch.cuda.empty_cache()
 
     if args.only in ("all", "prefill"):
