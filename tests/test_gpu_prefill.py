@@ -110,6 +110,47 @@ def test_prefill_fp32_split_path_lengths(hl, orc, T, d):
     assert err < TOL_F32 / 10
 
 
+@pytest.mark.parametrize("T", [65, 200])
+@pytest.mark.parametrize("hq,hkv,d", [(4, 4, 64), (6, 3, 128), (16, 2, 64), (8, 2, 128), (12, 4, 64)])
+def test_prefill_fp32_split_path_gqa(hl, orc, hq, hkv, d, T):
+    """GQA groups of 1, 2, 3, 4 and 8 query heads per kv head (workgroups of
+    one, two or four heads, with and without the two-way key split) through
+    the split-operand fp32 kernel, with the KV cache written."""
+    q = orc.normal(hq * d * T, 70 + T).reshape(hq * d, T)
+    k = orc.normal(hkv * d * T, 71 + T).reshape(hkv * d, T)
+    v = orc.normal(hkv * d * T, 72 + T).reshape(hkv * d, T)
+    ref, _, kr = oracle_prefill(orc, q, k, v, hq, hkv, d, T, base=1e4)
+    kc = torch.zeros(hkv * d, T, device="cuda")
+    vc = torch.zeros(hkv * d, T, device="cuda")
+    out = run_prefill(to_dev(q, 0), to_dev(k, 0), to_dev(v, 0), hq, hkv, d, T, apply_rope=True,
+                      rope_base=1e4, k_cache=kc, v_cache=vc, max_len=T)
+    assert rel_err(from_dev(out), ref) < TOL_F32 / 10
+    assert np.array_equal(from_dev(vc), v)
+    assert rel_err(from_dev(kc), kr) < 1e-6
+
+
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("style,half_rope", [(0, False), (1, False), (0, True)])
+def test_prefill_fp32_split_path_qknorm_rope(hl, orc, d, style, half_rope):
+    """fp32 with qkNorm and RoPE (half-split, interleaved, half-split over
+    half the head) applied by the prologue before it splits K: the oracle's
+    norm and rotation, then attention."""
+    hq, hkv, T = 8, 2, 150
+    rd = d // 2 if half_rope else d
+    q = orc.normal(hq * d * T, 81).reshape(hq * d, T)
+    k = orc.normal(hkv * d * T, 82).reshape(hkv * d, T)
+    v = orc.normal(hkv * d * T, 83).reshape(hkv * d, T)
+    wq, wk = orc.uniform(d, 84, 0.5, 1.5), orc.uniform(d, 85, 0.5, 1.5)
+    ref, _, _ = oracle_prefill(orc, q, k, v, hq, hkv, d, T, base=1e6, style=style, wq=wq, wk=wk,
+                               rope_dim=rd)
+    out = run_prefill(to_dev(q, 0), to_dev(k, 0), to_dev(v, 0), hq, hkv, d, T, apply_rope=True,
+                      rope_base=1e6, rope_style=style, rope_dim=rd,
+                      q_norm_w=torch.from_numpy(wq).cuda(), k_norm_w=torch.from_numpy(wk).cuda())
+    err = rel_err(from_dev(out), ref)
+    print(f"fp32 qknorm rope D={d} style={style} rope_dim={rd} rel err {err:.3e}")
+    assert err < TOL_F32 / 10
+
+
 @pytest.mark.parametrize("d", [64, 128])
 @pytest.mark.parametrize("where", ["k_tile", "v_tile", "q_row", "tiny"])
 def test_prefill_fp32_split_path_outliers(hl, orc, where, d):
