@@ -339,3 +339,52 @@ def test_prefill_lowp_output_is_rne_of_fp32_output(hl, orc, dt):
     olp = run_prefill(*args, out_dtype=TDT[dt], apply_rope=True, rope_base=5e5)
     exp = orc.to_storage(from_dev(o32), dt)
     assert np.array_equal(olp.view(torch.int16).cpu().numpy().view(np.uint16), exp)
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_prefill_fp32_split_path_graph_replays(hl, orc, d):
+    """The fp32 prefill captured once and replayed on three inputs copied into
+    the same buffers (plain; a 1e5 outlier in a K tile; a NaN in a V tile, so
+    the split images' flags switch steps to the fp32 MFMAs and back): each
+    replay reproduces its eager result bit for bit, with the eager runs of
+    the other inputs in between."""
+    from hippo_leap_amd import attention as A
+    hq, hkv, T = 8, 2, 200
+    base = [orc.normal(h * d * T, 90 + i).reshape(h * d, T) for i, h in enumerate((hq, hkv, hkv))]
+    outl = [x.copy() for x in base]
+    outl[1][3, 70:75] = 1e5
+    nan = [x.copy() for x in base]
+    nan[2][d + 5, 150] = np.nan
+    inputs = {"plain": base, "outlier": outl, "nan": nan}
+    qd, kd, vd = (to_dev(x, 0) for x in base)
+    out = torch.empty(hq * d, T, device="cuda")
+    a = A.prefill_args(qd, kd, vd, out, hq, hkv, d, T, apply_rope=True, rope_base=1e4)
+    ws = A.workspace(A.prefill_workspace_bytes(a))
+    eager = {}
+    for name, src in inputs.items():
+        for dst, x in zip((qd, kd, vd), src):
+            dst.copy_(to_dev(x, 0))
+        A.attn_prefill(a, ws)
+        torch.cuda.synchronize()
+        eager[name] = from_dev(out).copy()
+    with np.errstate(invalid="ignore"):
+        ref, _, _ = oracle_prefill(orc, *base, hq, hkv, d, T, base=1e4)
+    assert rel_err(eager["plain"], ref) < TOL_F32 / 10
+    assert np.isnan(eager["nan"]).any() and not np.isnan(eager["outlier"]).any()
+    g = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        A.attn_prefill(a, ws)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g):
+        A.attn_prefill(a, ws)
+    for name in ("nan", "plain", "outlier", "nan", "plain"):
+        for dst, x in zip((qd, kd, vd), inputs[name]):
+            dst.copy_(to_dev(x, 0))
+        out.fill_(7.0)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(from_dev(out), eager[name], equal_nan=True), name
