@@ -665,9 +665,9 @@ __global__ __launch_bounds__(256) void prefill_f32mfma_kernel(PrefillLaunch p, i
     // fp32 K/V tiles: thread moves column lc (key j0 + lc) of rows
     // d = ld0 + 4k; the next step's tiles are loaded while the current ones
     // are computed.  X3: only a step that runs the fp32 MFMAs loads them, at
-    // the step; the split tiles come from the split kernel's images instead
-    // (written by the prologue), copied straight into LDS one step ahead;
-    // its fp32 steps pass the thread id through an empty asm, so that their
+    // the step; the split tiles come from the images the prologue wrote,
+    // copied straight into LDS one step ahead; the fp32 steps pass the
+    // thread id through an empty asm, so that their
     // per-lane addresses are computed at the step instead of being hoisted
     // and kept live across the loop (which costs the split steps registers).
     float kr[KSPLIT][NL], vr[KSPLIT][NL];
