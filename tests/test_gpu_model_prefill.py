@@ -91,10 +91,17 @@ CASES = [  # (name, kv dtype, layout, qk-norm)
 ]
 
 
-@pytest.mark.parametrize("name,dt,lay,qk", CASES, ids=[c[0] for c in CASES])
+# head dim 128 (the Llama-3-8B / Qwen3 head) with fp32 activations and caches:
+# the split-operand prefill kernel at 128 (q dim 512 != n_emb 256)
+CFG128 = dict(CFG, head_dim=128)
+CASES128 = [("fp32_colmajor_d128", 0, 0, False), ("fp32_colmajor_qknorm_d128", 0, 0, True)]
+
+
+@pytest.mark.parametrize("name,dt,lay,qk", CASES + CASES128, ids=[c[0] for c in CASES + CASES128])
 def test_prefill_then_decode_matches_oracle(hl, orc, name, dt, lay, qk):
     from hippo_leap_amd.model import DenseModel
     print(f"prefill+decode case {name}", flush=True)
+    CFG = CFG128 if name.endswith("_d128") else globals()["CFG"]
     dev, ref = _build(orc, CFG, {}, qk, 77 + len(name))
     T = 12
     m = DenseModel(torch, CFG, dev["tok_emb"], dev["output_norm"], dev["output"], 0, dev["layers"],
