@@ -152,6 +152,31 @@ def test_prefill_fp32_split_path_qknorm_rope(hl, orc, d, style, half_rope):
 
 
 @pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("style", [0, 1])
+def test_prefill_fp32_split_path_start_pos(hl, orc, d, style):
+    """fp32 chunk continuing a sequence: RoPE at positions start_pos + t, the
+    cache written from column start_pos (earlier and later columns
+    untouched), attention over the chunk's own keys."""
+    hq, hkv, T, start, max_len = 8, 2, 70, 37, 128
+    q, k, v = (orc.normal(h * d * T, 180 + i).reshape(h * d, T) for i, h in enumerate((hq, hkv, hkv)))
+    th = orc.theta_table(d, 5e5)
+    qr = orc.rope_cols(q, hq, d, T, d, th, start, style)
+    kr = orc.rope_cols(k, hkv, d, T, d, th, start, style)
+    ref = orc.attention_prefill(qr, kr, v, hq, hkv, d, T)
+    kc = torch.full((hkv * d, max_len), 7.0, device="cuda")
+    vc = torch.full((hkv * d, max_len), 7.0, device="cuda")
+    out = run_prefill(to_dev(q, 0), to_dev(k, 0), to_dev(v, 0), hq, hkv, d, T, apply_rope=True,
+                      rope_base=5e5, rope_style=style, k_cache=kc, v_cache=vc, max_len=max_len,
+                      start_pos=start)
+    assert rel_err(from_dev(out), ref) < TOL_F32 / 10
+    kch, vch = from_dev(kc), from_dev(vc)
+    assert np.array_equal(vch[:, start:start + T], v)
+    assert rel_err(kch[:, start:start + T], kr) < 1e-6
+    assert np.all(kch[:, :start] == 7.0) and np.all(kch[:, start + T:] == 7.0)
+    assert np.all(vch[:, :start] == 7.0) and np.all(vch[:, start + T:] == 7.0)
+
+
+@pytest.mark.parametrize("d", [64, 128])
 @pytest.mark.parametrize("where", ["k_tile", "v_tile", "q_row", "tiny"])
 def test_prefill_fp32_split_path_outliers(hl, orc, where, d):
     """T=300: values of 2^15 and beyond in one K tile, one V tile or one
