@@ -4,7 +4,8 @@ restatement of tensor.nim's matmul (tensor.nim:63-81), on both kernels:
 the decode GEMV (seq_len == 1) and the fp32-MFMA GEMM (seq_len > 1), with
 and without 16-byte loads (K or T not a multiple of 4, misaligned inputs),
 ragged tiles, and at the Llama-3-8B projection shapes against an fp64
-matmul of the same inputs.  Bar: 1e-4 relative (fp32)."""
+matmul of the same inputs; the 128 x 128-tile GEMM also over wide exponent
+ranges and with inf / NaN operands.  Bar: 1e-4 relative (fp32)."""
 import numpy as np
 import pytest
 import torch
@@ -88,3 +89,54 @@ def test_linear_col_linearity_and_repeat(hl, orc):
     comb = (0.5 * ys[0].double() - 2.0 * ys[1].double())
     assert ((ys[2].double() - comb).abs().max() / comb.abs().max()).item() < TOL_F32
     assert torch.equal(ys[0], ys[3])
+
+
+def _tile128_operands(seed):
+    """2048 x 4096 outputs (512 tiles: the 128 x 128-tile GEMM), K = 256."""
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    M, K, T = 2048, 256, 4096
+    w = torch.rand(M, K, device="cuda", generator=g) * 2 - 1
+    x = torch.randn(K, T, device="cuda", generator=g)
+    return M, K, T, w, x
+
+
+def test_linear_col_gemm_wide_range(hl):
+    """Rows of W scaled by 1e-18 .. 1e18 and columns of x by 1e-15 .. 1e15:
+    every output within 1e-4 of its own row/column scale against a float64
+    matmul."""
+    from hippo_leap_amd import attention as A
+    M, K, T, w, x = _tile128_operands(41)
+    rs = torch.logspace(-18, 18, M, device="cuda")
+    cs = torch.logspace(-15, 15, T, device="cuda")
+    w = w * rs[:, None]
+    x = x * cs[None, :]
+    y = torch.full((M, T), float("nan"), device="cuda")
+    A.gpu_linear_col(y, x, w, K, M, T)
+    ref = w.double() @ x.double()
+    scale = (w.double().abs() @ x.double().abs())  # |W| |x|: the sum's own scale
+    err = ((y.double() - ref).abs() / scale).max().item()
+    assert err < TOL_F32, err
+
+
+def test_linear_col_gemm_inf_nan(hl):
+    """inf and NaN through the GEMM: an inf weight gives inf where its x is
+    nonzero and NaN where it is 0 (inf x 0), a NaN weight NaN, as the
+    reference's fp32 products do; every other output matches a float64
+    matmul."""
+    from hippo_leap_amd import attention as A
+    M, K, T, w, x = _tile128_operands(42)
+    x = x.abs() + 0.5           # positive, so row 5's sum is +inf
+    x[3, 100] = 0.0             # ... except column 100: inf x 0
+    w[5, 3] = float("inf")
+    w[7, 10] = float("nan")
+    y = torch.full((M, T), 7.0, device="cuda")
+    A.gpu_linear_col(y, x, w, K, M, T)
+    yc = y.cpu()
+    assert torch.isnan(yc[7]).all()
+    assert torch.isnan(yc[5, 100])
+    assert torch.isinf(yc[5, :100]).all() and torch.isinf(yc[5, 101:]).all() and (yc[5, :100] > 0).all()
+    fin = torch.ones(M, dtype=torch.bool)
+    fin[5] = fin[7] = False
+    ref = (w.double() @ x.double()).cpu()
+    err = ((yc.double()[fin] - ref[fin]).abs().max() / ref[fin].abs().max()).item()
+    assert err < TOL_F32, err
